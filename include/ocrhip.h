@@ -1,0 +1,118 @@
+/*
+ * ocrhip: the GPU path of wgpu-ocr (huppiflupp/wgpu-ocr) rebuilt for AMD Instinct MI355X
+ * (gfx950) as HIP kernels behind a C ABI.
+ *
+ * Each entry point names the reference interface it replaces (file:line in the reference tree).
+ * Conventions: functions returning int give OCR_OK (0) or OCR_ERR (1); the message of the last
+ * failure on the calling thread is ocr_last_error(). Functions returning a pointer give NULL on
+ * failure. No exception or abort crosses this boundary. A context, and everything made from it,
+ * is used by one host thread at a time (the reference's Gpu is !Sync, src/gpu.rs:835). Output
+ * buffers belong to the caller and are sized with the *_dims queries.
+ */
+#ifndef OCRHIP_H
+#define OCRHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OCR_OK 0
+#define OCR_ERR 1
+
+typedef struct ocr_ctx ocr_ctx;
+typedef struct ocr_detector ocr_detector;
+typedef struct ocr_recognizer ocr_recognizer;
+typedef struct ocr_pipeline ocr_pipeline;
+
+/* Options of a context. lines: lines per GRU workgroup (LINES, src/bin/ocr-bench.rs:135; this
+ * build's recurrence always groups 8). pool_mb: the scratch pool's cap (POOLMB, src/gpu.rs:919).
+ * device: the HIP device index. */
+typedef struct ocr_opts {
+    uint32_t lines;
+    uint32_t pool_mb;
+    int32_t device;
+} ocr_opts;
+
+/* Message of the last failure on this thread ("" if none). */
+const char *ocr_last_error(void);
+const char *ocr_version(void);
+
+/* Gpu::new (src/gpu.rs:850-920): the device, its stream and the scratch pool. opts may be NULL. */
+ocr_ctx *ocr_create(const ocr_opts *opts);
+void ocr_destroy(ocr_ctx *ctx);
+/* Wait for all work queued on the context (the reference's submit_wait, src/gpu.rs:1005-1008). */
+int ocr_synchronize(ocr_ctx *ctx);
+
+/* Device memory of the context's GPU, for callers that keep inputs resident in HBM
+ * (the reference's upload / read, src/gpu.rs:922-936, 1039-1055). Copies are ordered on the
+ * context's stream; ocr_memcpy_d2h returns when the data is on the host. */
+void *ocr_device_alloc(ocr_ctx *ctx, size_t bytes);
+int ocr_device_free(ocr_ctx *ctx, void *p);
+int ocr_memcpy_h2d(ocr_ctx *ctx, void *dst, const void *src, size_t bytes);
+int ocr_memcpy_d2h(ocr_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* Detector::new (src/gpu.rs:1385-1387) from an ONNX file (Onnx::load, src/onnx.rs:88-123). */
+ocr_detector *ocr_detector_new(ocr_ctx *ctx, const char *onnx_path);
+void ocr_detector_free(ocr_detector *det);
+
+/* Detector::detect_page (src/gpu.rs:1393-1422): rgb is h x w x 3 bytes (host); bits receives
+ * h rows of ceil(w / 32) words, bit x % 32 of word x / 32 set where the page-size mask is above
+ * thr. Returns when bits is filled. */
+int ocr_detect_page(ocr_detector *det, const uint8_t *rgb, uint32_t w, uint32_t h, float thr, uint32_t *bits);
+
+/* The same for `count` pages whose RGB bytes are already in device memory; bits are device
+ * buffers too. The pages go through the model as one batch. Queued on the context's stream. */
+int ocr_detect_pages_device(ocr_detector *det, const uint8_t *const *d_rgb, const uint32_t *w, const uint32_t *h,
+                            uint32_t count, float thr, uint32_t *const *d_bits);
+
+/* Detector::detect (src/gpu.rs:1425-1430): the model's probability map for a [1, 1, h, w]
+ * float input (host); prob receives h * w floats. */
+int ocr_detect(ocr_detector *det, const float *input, uint32_t h, uint32_t w, float *prob);
+
+/* Graph::build (src/gpu.rs:1104-1240): a convolutional ONNX graph up to (not including) the
+ * first node of type stop_op (NULL: the whole graph). The same operator contract as Detector. */
+typedef struct ocr_graph ocr_graph;
+ocr_graph *ocr_graph_new(ocr_ctx *ctx, const char *onnx_path, const char *stop_op);
+void ocr_graph_free(ocr_graph *g);
+/* Output shape [n, c, h, w] of the graph for an input of shape [n, c, h, w]. */
+int ocr_graph_dims(ocr_graph *g, uint32_t n, uint32_t c, uint32_t h, uint32_t w, uint32_t *out_nchw);
+/* Graph::run (src/gpu.rs:1243-1377) on a host NCHW float input; out receives the NCHW output
+ * (size from ocr_graph_dims). */
+int ocr_graph_run(ocr_graph *g, const float *in, uint32_t n, uint32_t c, uint32_t h, uint32_t w, float *out);
+
+/* Recognizer::new (src/gpu.rs:1452-1506). lines as in ocr_opts. */
+ocr_recognizer *ocr_recognizer_new(ocr_ctx *ctx, const char *onnx_path, uint32_t lines);
+void ocr_recognizer_free(ocr_recognizer *rec);
+
+/* One batch of n line images [n][64][w] (float, the ocrs input convention). */
+typedef struct ocr_batch {
+    const float *data;
+    uint32_t n;
+    uint32_t w;
+} ocr_batch;
+
+/* Output sizes of ocr_recognize for these batches: tmax steps, ntot lines, classes. */
+int ocr_recognize_dims(ocr_recognizer *rec, const ocr_batch *batches, uint32_t count, uint32_t *tmax,
+                       uint32_t *ntot, uint32_t *classes);
+
+/* Recognizer::recognize (src/gpu.rs:1510-1602): batches' data on the host. logits receives the
+ * raw logits [tmax][ntot][classes] (rows t >= lens[line] are undefined, as in the reference),
+ * lens [ntot] every line's step count (its batch's trunk width, src/gpu.rs:1552). best, if not
+ * NULL, receives [tmax][ntot] arg-max class per step (the last index on ties, as
+ * src/bin/ocr-bench.rs:67 decodes). logits may be NULL when only best is wanted. */
+int ocr_recognize(ocr_recognizer *rec, const ocr_batch *batches, uint32_t count, float *logits, uint32_t *lens,
+                  uint32_t *best);
+
+/* The same with the batches' data, logits and best in device memory (either may be NULL);
+ * lens on the host. Queued on the context's stream. */
+int ocr_recognize_device(ocr_recognizer *rec, const ocr_batch *d_batches, uint32_t count, float *d_logits,
+                         uint32_t *d_best, uint32_t *lens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OCRHIP_H */

@@ -1,0 +1,278 @@
+"""ORACLE (test infrastructure only): runs an ONNX graph on the CPU in float32 with the C
+restatement in oracle.c for the heavy operators and numpy for the shape operators. Only tests,
+the smoke check and bench.py's cpu_baseline leg use it, always as the checker.
+
+ONNX operator semantics as rten (the reference's CPU engine, rten 0.26.0) implements them; the
+ocrs front and back ends follow the reference's GPU code where ocrs itself is not available:
+Detector::detect_page (src/gpu.rs:1393-1422) and the greedy CTC of src/bin/ocr-bench.rs:62-74.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+from . import onnx_read
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    """Compile oracle.c (gcc, OpenMP) into oracle/_build/liboracle.so."""
+    os.makedirs(os.path.dirname(LIB_PATH), exist_ok=True)
+    tmp = LIB_PATH + f".tmp{os.getpid()}"
+    subprocess.run(["gcc", "-O3", "-march=x86-64-v2", "-fopenmp", "-fPIC", "-shared", "-ffp-contract=off",
+                    "-o", tmp, os.path.join(HERE, "oracle.c"), "-lm"], check=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH) or os.path.getmtime(LIB_PATH) < os.path.getmtime(os.path.join(HERE, "oracle.c")):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        L.orc_conv2d.argtypes = [P, I, I, I, I, P, I, I, I, P, I, I, I, I, I, I, I, I, P, P]
+        L.orc_conv_transpose2d.argtypes = [P, I, I, I, I, P, I, I, I, P, I, I, I, P]
+        L.orc_pool2d.argtypes = [P, I, I, I, I, I, I, I, I, P]
+        L.orc_gru.argtypes = [P, I, I, I, P, P, P, I, I, P, P]
+        L.orc_grey_resize.argtypes = [P, I, I, I, I, I, I, F, F, P]
+        L.orc_mask_up_prob.argtypes = [P, I, I, I, I, I, F, F, P]
+        L.orc_pack_bits.argtypes = [P, I, I, F, P]
+        L.orc_activate.argtypes = [F, I]
+        L.orc_activate.restype = F
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype=np.float32):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ------------------------------------------------------------------------------------------
+# Operators (NCHW float32)
+# ------------------------------------------------------------------------------------------
+def conv2d(x, w, b=None, pads=(0, 0, 0, 0), strides=(1, 1), group=1, act=0, res=None):
+    x, w = _c(x), _c(w)
+    n, cin, h, wd = x.shape
+    cout, _, kh, kw = w.shape
+    pt, pl, pb, pr = pads
+    oh, ow = (h + pt + pb - kh) // strides[0] + 1, (wd + pl + pr - kw) // strides[1] + 1
+    y = np.empty((n, cout, oh, ow), np.float32)
+    b = None if b is None else _c(b)
+    res = None if res is None else _c(res)
+    lib().orc_conv2d(_p(x), n, cin, h, wd, _p(w), cout, kh, kw, _p(b), pt, pl, pb, pr, strides[0], strides[1],
+                     group, act, _p(res), _p(y))
+    return y
+
+
+def conv_transpose2d(x, w, b=None, strides=(2, 2), act=0):
+    x, w = _c(x), _c(w)
+    n, cin, h, wd = x.shape
+    _, cout, kh, kw = w.shape
+    y = np.empty((n, cout, (h - 1) * strides[0] + kh, (wd - 1) * strides[1] + kw), np.float32)
+    b = None if b is None else _c(b)
+    lib().orc_conv_transpose2d(_p(x), n, cin, h, wd, _p(w), cout, kh, kw, _p(b), strides[0], strides[1], act, _p(y))
+    return y
+
+
+def pool2d(x, kernel, strides, avg=False):
+    x = _c(x)
+    n, c, h, w = x.shape
+    oh, ow = (h - kernel[0]) // strides[0] + 1, (w - kernel[1]) // strides[1] + 1
+    y = np.empty((n, c, oh, ow), np.float32)
+    lib().orc_pool2d(_p(x), n * c, h, w, kernel[0], kernel[1], strides[0], strides[1], int(avg), _p(y))
+    return y
+
+
+def gru(X, W, R, B, lens=None):
+    X, W, R, B = _c(X), _c(W), _c(R), _c(B)
+    T, N, I = X.shape
+    D, H3, _ = W.shape
+    H = H3 // 3
+    Y = np.empty((T, D, N, H), np.float32)
+    lens_a = None if lens is None else _c(lens, np.int32)
+    lib().orc_gru(_p(X), T, N, I, _p(W), _p(R), _p(B), H, D, _p(lens_a), _p(Y))
+    return Y
+
+
+def activate(x, act):
+    f = {0: lambda v: v, 1: lambda v: np.maximum(v, np.float32(0)),
+         2: lambda v: np.float32(1) / (np.float32(1) + np.exp(-v))}
+    return f[act](np.asarray(x, np.float32)).astype(np.float32)
+
+
+# ------------------------------------------------------------------------------------------
+# Graph walker
+# ------------------------------------------------------------------------------------------
+def _attr(node, name, default=None):
+    return node.attrs.get(name, default)
+
+
+def run(model: onnx_read.Model, x: np.ndarray, want=()):
+    """Run the whole graph on input x; returns (output, {name: value for name in want})."""
+    vals = {model.input: np.asarray(x, np.float32)}
+    W, I = model.weights, model.ints
+
+    def get(name):
+        if name in vals:
+            return vals[name]
+        if name in W:
+            return W[name]
+        if name in I:
+            return I[name]
+        raise KeyError(name)
+
+    for nd in model.nodes:
+        ins = [get(i) if i else None for i in nd.inputs]
+        op = nd.op
+        if op == "Conv":
+            w = ins[1]
+            pads = _attr(nd, "pads", [0, 0, 0, 0])
+            pads = (pads[0], pads[1], pads[2], pads[3])
+            if any(d != 1 for d in _attr(nd, "dilations", [1, 1])):
+                raise ValueError("dilated conv")
+            y = conv2d(ins[0], w, ins[2] if len(ins) > 2 else None, pads, tuple(_attr(nd, "strides", [1, 1])),
+                       _attr(nd, "group", 1))
+        elif op == "ConvTranspose":
+            if any(_attr(nd, "pads", [0]) ) or any(_attr(nd, "output_padding", [0])) or _attr(nd, "group", 1) != 1:
+                raise ValueError("unsupported ConvTranspose")
+            y = conv_transpose2d(ins[0], ins[1], ins[2] if len(ins) > 2 else None, tuple(_attr(nd, "strides", [1, 1])))
+        elif op in ("MaxPool", "AveragePool"):
+            k = _attr(nd, "kernel_shape")
+            s = _attr(nd, "strides", [1] * len(k))
+            if any(_attr(nd, "pads", [0])) or _attr(nd, "ceil_mode", 0):
+                raise ValueError("padded/ceil pool")
+            y = pool2d(ins[0], k, s, avg=(op == "AveragePool"))
+        elif op == "Relu":
+            y = activate(ins[0], 1)
+        elif op == "Sigmoid":
+            y = activate(ins[0], 2)
+        elif op == "Concat":
+            y = np.concatenate(ins, axis=_attr(nd, "axis"))
+        elif op == "Squeeze":
+            y = np.squeeze(ins[0], axis=tuple(int(a) for a in ins[1]))
+        elif op == "Transpose":
+            y = np.ascontiguousarray(np.transpose(ins[0], _attr(nd, "perm")))
+        elif op == "Reshape":
+            shape = [int(s) if s != 0 else ins[0].shape[i] for i, s in enumerate(ins[1])]
+            y = ins[0].reshape(shape)
+        elif op == "GRU":
+            if _attr(nd, "linear_before_reset", 0) != 1:
+                raise ValueError("GRU linear_before_reset=0")
+            d = 2 if _attr(nd, "direction", "forward") == "bidirectional" else 1
+            assert ins[1].shape[0] == d
+            y = gru(ins[0], ins[1], ins[2], ins[3])
+            vals[nd.outputs[0]] = y
+            if len(nd.outputs) > 1 and nd.outputs[1]:
+                vals[nd.outputs[1]] = None
+            continue
+        elif op == "MatMul":
+            y = np.matmul(ins[0], ins[1]).astype(np.float32)
+        elif op == "Add":
+            y = (ins[0] + ins[1]).astype(np.float32)
+        elif op == "LogSoftmax":
+            ax = _attr(nd, "axis", -1)
+            v = ins[0].astype(np.float64)
+            m = v.max(axis=ax, keepdims=True)
+            y = (v - m - np.log(np.exp(v - m).sum(axis=ax, keepdims=True))).astype(np.float32)
+        elif op == "Pad":
+            if np.any(np.asarray(ins[1]) != 0):
+                raise ValueError("non-zero Pad")
+            y = ins[0]
+        elif op == "Slice":
+            y = ins[0]
+            axes = ins[3] if len(ins) > 3 and ins[3] is not None else range(len(ins[1]))
+            sl = [slice(None)] * y.ndim
+            for st, en, ax in zip(ins[1], ins[2], axes):
+                sl[int(ax)] = slice(int(st), int(en))
+            y = np.ascontiguousarray(y[tuple(sl)])
+        else:
+            raise ValueError(f"oracle: unsupported op {op}")
+        vals[nd.outputs[0]] = y
+    return vals[model.output], {k: vals[k] for k in want}
+
+
+def gru_nodes(model):
+    return [n for n in model.nodes if n.op == "GRU"]
+
+
+def rec_logits(model, batches):
+    """Per batch, the raw logits (the MatMul + bias Add output, before LogSoftmax) [T][n][C],
+    as rten computes them for each batch on its own (gpu.rs:1510-1602 returns these)."""
+    add = next(n for n in model.nodes if n.op == "Add")
+    out = []
+    for data, n, w in batches:
+        _, got = run(model, np.asarray(data, np.float32).reshape(n, 1, 64, w), want=[add.outputs[0]])
+        out.append(got[add.outputs[0]])
+    return out
+
+
+# ------------------------------------------------------------------------------------------
+# Detector front/back end (gpu.rs:1393-1422) and CTC (ocr-bench.rs:62-74)
+# ------------------------------------------------------------------------------------------
+MODEL_H, MODEL_W = 800, 600
+
+
+def grey_resize(rgb, w, h, mh=MODEL_H, mw=MODEL_W):
+    ph, pw = max(h, mh), max(w, mw)
+    y = np.empty((mh, mw), np.float32)
+    rgb = _c(rgb, np.uint8)
+    lib().orc_grey_resize(_p(rgb), w, h, pw, ph, mw, mh, np.float32(pw) / np.float32(mw),
+                          np.float32(ph) / np.float32(mh), _p(y))
+    return y
+
+
+def valid_region(w, h, mh=MODEL_H, mw=MODEL_W):
+    """gpu.rs:1414: the part of the model output that covers the page, not its padding."""
+    ph, pw = max(h, mh), max(w, mw)
+    return mh - (ph - h) * mh // ph, mw - (pw - w) * mw // pw
+
+
+def mask_up_prob(m, w, h, mh=MODEL_H, mw=MODEL_W):
+    vh, vw = valid_region(w, h, mh, mw)
+    prob = np.empty((h, w), np.float32)
+    m = _c(m)
+    lib().orc_mask_up_prob(_p(m), mw, vw, vh, w, h, np.float32(vw) / np.float32(w), np.float32(vh) / np.float32(h),
+                           _p(prob))
+    return prob
+
+
+def pack_bits(prob, thr):
+    h, w = prob.shape
+    bits = np.empty((h, (w + 31) // 32), np.uint32)
+    lib().orc_pack_bits(_p(_c(prob)), w, h, np.float32(thr), _p(bits))
+    return bits
+
+
+def detect_page(model, rgb, thr):
+    """Returns (bits [h][ceil(w/32)], pre-threshold prob [h][w], model output [800][600])."""
+    h, w = rgb.shape[:2]
+    inp = grey_resize(rgb, w, h)
+    out, _ = run(model, inp.reshape(1, 1, MODEL_H, MODEL_W))
+    m = out.reshape(MODEL_H, MODEL_W)
+    prob = mask_up_prob(m, w, h)
+    return pack_bits(prob, thr), prob, m
+
+
+def ctc_decode(logits_line, width, classes=97):
+    """ocr-bench.rs:62-74 on one line's [T][C] rows: arg-max with the LAST index on ties (Rust
+    `max_by`), emit when best != 0, best != prev and t * 4 < width."""
+    from_right = logits_line[:, ::-1]
+    best = classes - 1 - np.argmax(from_right, axis=1)
+    out, prev = [], 0
+    for t, b in enumerate(best):
+        if b != 0 and b != prev and t * 4 < width:
+            out.append(int(b))
+        prev = b
+    return out, best

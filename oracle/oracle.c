@@ -1,0 +1,222 @@
+/*
+ * ORACLE - test infrastructure only. A plain-C, float32 CPU restatement of the reference's
+ * GPU path (huppiflupp/wgpu-ocr, src/gpu.rs), used as the checker for the HIP kernels and, timed,
+ * as the CPU baseline. Nothing in the product links or calls this file.
+ *
+ * Layout is ONNX's: NCHW float32. Each function cites the reference code it restates.
+ * Pinning (which check fixes each function) is listed in oracle/README.md.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* gpu.rs:20-34: 0 none, 1 ReLU, 2 sigmoid, 3 GELU (A&S 7.1.26 erf), 4 SiLU. */
+static float erf_as(float v) {
+    float s = v < 0.f ? -1.f : (v > 0.f ? 1.f : 0.f);
+    float a = fabsf(v);
+    float t = 1.f / (1.f + 0.3275911f * a);
+    float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
+    return s * (1.f - poly * expf(-a * a));
+}
+
+float orc_activate(float v, int act) {
+    switch (act) {
+    case 1: return v > 0.f ? v : 0.f;
+    case 2: return 1.f / (1.f + expf(-v));
+    case 3: return 0.5f * v * (1.f + erf_as(v * 0.70710678118654752f));
+    case 4: return v / (1.f + expf(-v));
+    default: return v;
+    }
+}
+
+/* Conv (ONNX semantics; gpu.rs:37-69 and 1255-1265 for the epilogue y = act(acc + b[c]), then
+ * + res when given). Grouped: cin_g = cin / group input channels per group. pads are
+ * top, left, bottom, right. Output [n][cout][oh][ow]. */
+void orc_conv2d(const float *x, int n, int cin, int h, int w, const float *wt, int cout, int kh, int kw,
+                const float *b, int pt, int pl, int pb, int pr, int sh, int sw, int group, int act,
+                const float *res, float *y) {
+    int oh = (h + pt + pb - kh) / sh + 1, ow = (w + pl + pr - kw) / sw + 1;
+    int cin_g = cin / group, cout_g = cout / group;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int nb = 0; nb < n; nb++) {
+        for (int co = 0; co < cout; co++) {
+            int g = co / cout_g;
+            float *yo = y + ((size_t)nb * cout + co) * oh * ow;
+            for (int i = 0; i < oh * ow; i++) yo[i] = 0.f;
+            for (int cg = 0; cg < cin_g; cg++) {
+                int ci = g * cin_g + cg;
+                const float *xi = x + ((size_t)nb * cin + ci) * h * w;
+                for (int ky = 0; ky < kh; ky++) {
+                    for (int kx = 0; kx < kw; kx++) {
+                        float wv = wt[(((size_t)co * cin_g + cg) * kh + ky) * kw + kx];
+                        for (int oy = 0; oy < oh; oy++) {
+                            int iy = oy * sh - pt + ky;
+                            if (iy < 0 || iy >= h) continue;
+                            float *yr = yo + (size_t)oy * ow;
+                            const float *xr = xi + (size_t)iy * w;
+                            /* ox range with 0 <= ox * sw - pl + kx < w */
+                            int lo = pl - kx > 0 ? (pl - kx + sw - 1) / sw : 0;
+                            int hi = (w - 1 + pl - kx) >= 0 ? (w - 1 + pl - kx) / sw + 1 : 0;
+                            if (hi > ow) hi = ow;
+                            if (sw == 1) {
+                                const float *xs = xr - pl + kx;
+                                for (int ox = lo; ox < hi; ox++) yr[ox] += wv * xs[ox];
+                            } else {
+                                for (int ox = lo; ox < hi; ox++) yr[ox] += wv * xr[ox * sw - pl + kx];
+                            }
+                        }
+                    }
+                }
+            }
+            float bv = b ? b[co] : 0.f;
+            const float *ro = res ? res + ((size_t)nb * cout + co) * oh * ow : NULL;
+            for (int i = 0; i < oh * ow; i++) {
+                float r = orc_activate(yo[i] + bv, act);
+                yo[i] = ro ? r + ro[i] : r;
+            }
+        }
+    }
+}
+
+/* ConvTranspose, group 1, no pads or output padding (gpu.rs:424-460, 1184-1191, 1283-1290):
+ * oh = (h - 1) * s + kh. Weights [cin][cout][kh][kw]. y = act(sum + b). */
+void orc_conv_transpose2d(const float *x, int n, int cin, int h, int w, const float *wt, int cout, int kh,
+                          int kw, const float *b, int sh, int sw, int act, float *y) {
+    int oh = (h - 1) * sh + kh, ow = (w - 1) * sw + kw;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int nb = 0; nb < n; nb++) {
+        for (int co = 0; co < cout; co++) {
+            float *yo = y + ((size_t)nb * cout + co) * oh * ow;
+            for (int i = 0; i < oh * ow; i++) yo[i] = 0.f;
+            for (int ci = 0; ci < cin; ci++) {
+                const float *xi = x + ((size_t)nb * cin + ci) * h * w;
+                for (int ky = 0; ky < kh; ky++)
+                    for (int kx = 0; kx < kw; kx++) {
+                        float wv = wt[(((size_t)ci * cout + co) * kh + ky) * kw + kx];
+                        for (int iy = 0; iy < h; iy++)
+                            for (int ix = 0; ix < w; ix++)
+                                yo[(size_t)(iy * sh + ky) * ow + ix * sw + kx] += wv * xi[(size_t)iy * w + ix];
+                    }
+            }
+            float bv = b ? b[co] : 0.f;
+            for (int i = 0; i < oh * ow; i++) yo[i] = orc_activate(yo[i] + bv, act);
+        }
+    }
+}
+
+/* MaxPool / AveragePool without padding, floor output size (gpu.rs:462-482, 1291-1297;
+ * nd.rs:246-275 for avg). x is [nc][h][w]. */
+void orc_pool2d(const float *x, int nc, int h, int w, int kh, int kw, int sh, int sw, int avg, float *y) {
+    int oh = (h - kh) / sh + 1, ow = (w - kw) / sw + 1;
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < nc; c++)
+        for (int oy = 0; oy < oh; oy++)
+            for (int ox = 0; ox < ow; ox++) {
+                float m = -3.4e38f, s = 0.f;
+                for (int ky = 0; ky < kh; ky++)
+                    for (int kx = 0; kx < kw; kx++) {
+                        float v = x[((size_t)c * h + oy * sh + ky) * w + ox * sw + kx];
+                        m = v > m ? v : m;
+                        s += v;
+                    }
+                y[((size_t)c * oh + oy) * ow + ox] = avg ? s / (float)(kh * kw) : m;
+            }
+}
+
+static float sigm(float v) { return 1.f / (1.f + expf(-v)); }
+
+/* ONNX GRU with linear_before_reset = 1, gate order [z, r, h] (gpu.rs:680-819):
+ *   z = s(Wz x + Wbz + Rz h + Rbz), r = s(Wr x + Wbr + Rr h + Rbr),
+ *   c = tanh(Wh x + Wbh + r * (Rh h + Rbh)), h' = (1 - z) c + z h, h0 = 0.
+ * X [T][N][I], W [D][3H][I], R [D][3H][H], B [D][6H] = [Wb | Rb], Y [T][D][N][H].
+ * Direction 1 runs t = len - 1 - s (gpu.rs:692, 768). lens NULL means T for every line; steps
+ * at or past a line's length are written as 0 (ONNX). */
+void orc_gru(const float *X, int T, int N, int I, const float *W, const float *R, const float *B, int H, int D,
+             const int *lens, float *Y) {
+    memset(Y, 0, sizeof(float) * (size_t)T * D * N * H);
+#pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int d = 0; d < D; d++) {
+        for (int nb = 0; nb < N; nb++) {
+            const float *Wd = W + (size_t)d * 3 * H * I, *Rd = R + (size_t)d * 3 * H * H, *Bd = B + (size_t)d * 6 * H;
+            float *h = calloc((size_t)H, sizeof(float)), *hn = calloc((size_t)H, sizeof(float));
+            int len = lens ? lens[nb] : T;
+            for (int s = 0; s < len; s++) {
+                int t = d == 0 ? s : len - 1 - s;
+                const float *x = X + ((size_t)t * N + nb) * I;
+                for (int j = 0; j < H; j++) {
+                    float g[3], rh[3];
+                    for (int q = 0; q < 3; q++) {
+                        const float *wr = Wd + (size_t)(q * H + j) * I, *rr = Rd + (size_t)(q * H + j) * H;
+                        float a = 0.f, c = 0.f;
+                        for (int i = 0; i < I; i++) a += wr[i] * x[i];
+                        for (int k = 0; k < H; k++) c += rr[k] * h[k];
+                        g[q] = a + Bd[q * H + j];
+                        rh[q] = c + Bd[3 * H + q * H + j];
+                    }
+                    float z = sigm(g[0] + rh[0]), r = sigm(g[1] + rh[1]);
+                    float c = tanhf(g[2] + r * rh[2]);
+                    hn[j] = (1.f - z) * c + z * h[j];
+                }
+                memcpy(h, hn, sizeof(float) * (size_t)H);
+                memcpy(Y + (((size_t)t * D + d) * N + nb) * H, h, sizeof(float) * (size_t)H);
+            }
+            free(h);
+            free(hn);
+        }
+    }
+}
+
+/* WGSL mix(a, b, t) = a * (1 - t) + b * t. */
+static float mixf(float a, float b, float t) { return a * (1.f - t) + b * t; }
+
+/* gpu.rs:530-561: ocrs grey of the RGB page, black (-0.5) outside the w x h page inside the
+ * padded pw x ph canvas, resized bilinearly (half-pixel, clamped, x then y) to ow x oh. */
+static float grey_px(const uint8_t *rgb, int w, int h, int x, int yy) {
+    if (x >= w || yy >= h) return -0.5f;
+    const uint8_t *p = rgb + ((size_t)yy * w + x) * 3;
+    return -0.5f + (float)p[0] * (0.299f / 255.f) + (float)p[1] * (0.587f / 255.f) + (float)p[2] * (0.114f / 255.f);
+}
+
+void orc_grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, int ow, int oh, float sx, float sy, float *y) {
+#pragma omp parallel for schedule(static)
+    for (int oy = 0; oy < oh; oy++)
+        for (int ox = 0; ox < ow; ox++) {
+            float iy = fminf(fmaxf(sy * ((float)oy + 0.5f) - 0.5f, 0.f), (float)ph - 1.f);
+            float ix = fminf(fmaxf(sx * ((float)ox + 0.5f) - 0.5f, 0.f), (float)pw - 1.f);
+            int y1 = (int)iy, x1 = (int)ix;
+            int y2 = y1 + 1 < ph - 1 ? y1 + 1 : ph - 1, x2 = x1 + 1 < pw - 1 ? x1 + 1 : pw - 1;
+            float wy = iy - (float)y1, wx = ix - (float)x1;
+            float top = mixf(grey_px(rgb, w, h, x1, y1), grey_px(rgb, w, h, x2, y1), wx);
+            float bot = mixf(grey_px(rgb, w, h, x1, y2), grey_px(rgb, w, h, x2, y2), wx);
+            y[(size_t)oy * ow + ox] = mixf(top, bot, wy);
+        }
+}
+
+/* gpu.rs:563-593: the first mh x mw part of the model output m (row stride `stride`) resized
+ * to the page (w x h) bilinearly, before the threshold. */
+void orc_mask_up_prob(const float *m, int stride, int mw, int mh, int w, int h, float sx, float sy, float *prob) {
+#pragma omp parallel for schedule(static)
+    for (int oy = 0; oy < h; oy++) {
+        float iy = fminf(fmaxf(sy * ((float)oy + 0.5f) - 0.5f, 0.f), (float)mh - 1.f);
+        int y1 = (int)iy, y2 = y1 + 1 < mh - 1 ? y1 + 1 : mh - 1;
+        float fy = iy - (float)y1;
+        for (int ox = 0; ox < w; ox++) {
+            float ix = fminf(fmaxf(sx * ((float)ox + 0.5f) - 0.5f, 0.f), (float)mw - 1.f);
+            int x1 = (int)ix, x2 = x1 + 1 < mw - 1 ? x1 + 1 : mw - 1;
+            float fx = ix - (float)x1;
+            float top = mixf(m[(size_t)y1 * stride + x1], m[(size_t)y1 * stride + x2], fx);
+            float bot = mixf(m[(size_t)y2 * stride + x1], m[(size_t)y2 * stride + x2], fx);
+            prob[(size_t)oy * w + ox] = mixf(top, bot, fy);
+        }
+    }
+}
+
+/* gpu.rs:589-591: bit (x % 32) of word y * ceil(w / 32) + x / 32 is set when prob > thr. */
+void orc_pack_bits(const float *prob, int w, int h, float thr, uint32_t *bits) {
+    int words = (w + 31) / 32;
+    memset(bits, 0, sizeof(uint32_t) * (size_t)words * h);
+    for (int y = 0; y < h; y++)
+        for (int x = 0; x < w; x++)
+            if (prob[(size_t)y * w + x] > thr) bits[(size_t)y * words + x / 32] |= 1u << (x % 32);
+}

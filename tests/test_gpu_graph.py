@@ -1,0 +1,140 @@
+"""Every graph operator and kernel path on the GPU against the oracle, through the C ABI
+(ocr_graph_run), on small seeded inputs. Tolerance: the matrix-core path splits float32
+activations into float16 hi + lo (about 2^-22 relative) and accumulates in float32, so results
+agree with the float32 oracle to float32 rounding: |gpu - oracle| <= 1e-4 * (1 + |oracle|)."""
+import numpy as np
+import pytest
+
+from ocrhip import onnx_write as ow
+from oracle import graph as oracle_graph
+from oracle import onnx_read
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.Generator(np.random.PCG64(77))
+
+
+def f16x(a):
+    return a.astype(np.float16).astype(np.float32)
+
+
+def build(tmp_path, name, nodes_fn, in_shape):
+    g = ow.Graph(name)
+    out = nodes_fn(g, "x")
+    p = tmp_path / f"{name}.onnx"
+    p.write_bytes(g.model("x", list(in_shape), out, ["n", "c", "h", "w"]))
+    return str(p)
+
+
+def check(ctx, path, x, tol=1e-4):
+    import ocrhip
+    print(f"graph {path} input {x.shape}", flush=True)
+    got = ocrhip.Graph(ctx, path).run(x)
+    want, _ = oracle_graph.run(onnx_read.load(path), x)
+    assert got.shape == want.shape
+    err = np.abs(got - want) / (1 + np.abs(want))
+    assert err.max() <= tol, f"max rel err {err.max()}"
+    return got, want
+
+
+def conv(g, x, cin, cout, k=(3, 3), pads=(1, 1, 1, 1), strides=(1, 1), group=1, exact=True, act=None):
+    w = RNG.standard_normal((cout, cin // group, *k)).astype(np.float32) * np.float32(np.sqrt(2 / (cin * k[0] * k[1] / group)))
+    if exact:
+        w = f16x(w)
+    b = (RNG.standard_normal(cout) * 0.1).astype(np.float32)
+    y = g.add("Conv", [x, g.init(g.fresh("w"), w), g.init(g.fresh("b"), b)], kernel_shape=list(k), pads=list(pads),
+              strides=list(strides), group=group)
+    return g.add(act, [y]) if act else y
+
+
+@pytest.mark.parametrize("cin,cout,h,w", [(5, 7, 9, 11), (16, 32, 20, 33), (40, 70, 6, 21), (64, 64, 8, 50),
+                                          (128, 256, 4, 37), (32, 16, 33, 17)])
+def test_conv3x3_mfma(ctx, tmp_path, cin, cout, h, w):
+    p = build(tmp_path, "c", lambda g, x: conv(g, x, cin, cout, act="Relu"), (2, cin, h, w))
+    check(ctx, p, RNG.standard_normal((2, cin, h, w)).astype(np.float32))
+
+
+def test_conv1x1_and_sigmoid(ctx, tmp_path):
+    p = build(tmp_path, "c1", lambda g, x: conv(g, x, 16, 3, k=(1, 1), pads=(0, 0, 0, 0), act="Sigmoid"), (1, 16, 7, 130))
+    check(ctx, p, RNG.standard_normal((1, 16, 7, 130)).astype(np.float32))
+
+
+def test_conv_inexact_weights_third_pass(ctx, tmp_path):
+    # Weights that are not float16 values take the x_hi * w_lo pass as well.
+    p = build(tmp_path, "ci", lambda g, x: conv(g, x, 24, 40, exact=False), (1, 24, 10, 19))
+    check(ctx, p, RNG.standard_normal((1, 24, 10, 19)).astype(np.float32))
+
+
+def test_conv_asymmetric_pads(ctx, tmp_path):
+    p = build(tmp_path, "ca", lambda g, x: conv(g, x, 8, 12, k=(3, 2), pads=(0, 1, 2, 0)), (1, 8, 9, 10))
+    check(ctx, p, RNG.standard_normal((1, 8, 9, 10)).astype(np.float32))
+
+
+def test_conv_strided_generic(ctx, tmp_path):
+    p = build(tmp_path, "cs", lambda g, x: conv(g, x, 6, 5, strides=(2, 2), exact=False), (1, 6, 11, 12))
+    check(ctx, p, RNG.standard_normal((1, 6, 11, 12)).astype(np.float32))
+
+
+def test_depthwise(ctx, tmp_path):
+    p = build(tmp_path, "dw", lambda g, x: conv(g, x, 6, 6, group=6, act="Relu"), (2, 6, 9, 8))
+    check(ctx, p, RNG.standard_normal((2, 6, 9, 8)).astype(np.float32))
+
+
+@pytest.mark.parametrize("pool", [(2, 2), (2, 1)])
+def test_direct_conv_fused_pool(ctx, tmp_path, pool):
+    def net(g, x):
+        y = conv(g, x, 1, 32, act="Relu")
+        return g.add("MaxPool", [y], kernel_shape=list(pool), strides=list(pool))
+    p = build(tmp_path, "dp", net, (3, 1, 64, 37))
+    check(ctx, p, RNG.uniform(-0.5, 0.5, (3, 1, 64, 37)).astype(np.float32))
+
+
+def test_direct_conv_two_readers_and_concat(ctx, tmp_path):
+    # e0 is read by a MaxPool and a Concat (no fusion); the Concat takes the ConvTranspose output
+    # and the skip in its channel range, plus the graph input (a copy, not an alias).
+    def net(g, x):
+        e0 = conv(g, x, 1, 16, act="Relu")
+        p0 = g.add("MaxPool", [e0], kernel_shape=[2, 2], strides=[2, 2])
+        e1 = conv(g, p0, 16, 32, act="Relu")
+        wt = f16x(RNG.standard_normal((32, 16, 2, 2)).astype(np.float32) * 0.25)
+        u = g.add("ConvTranspose", [e1, g.init("ut", wt), g.init("ub", np.zeros(16, np.float32) + 0.05)],
+                  kernel_shape=[2, 2], strides=[2, 2])
+        u = g.add("Relu", [u])
+        c = g.add("Concat", [u, e0, x], axis=1)
+        return conv(g, c, 33, 8, act="Relu")
+    p = build(tmp_path, "cc", net, (1, 1, 24, 30))
+    check(ctx, p, RNG.uniform(-0.5, 0.5, (1, 1, 24, 30)).astype(np.float32))
+
+
+def test_conv_transpose_2x3(ctx, tmp_path):
+    def net(g, x):
+        wt = RNG.standard_normal((20, 9, 2, 3)).astype(np.float32) * 0.3
+        y = g.add("ConvTranspose", [x, g.init("w", wt), g.init("b", RNG.standard_normal(9).astype(np.float32))],
+                  kernel_shape=[2, 3], strides=[2, 2])
+        return g.add("Sigmoid", [y])
+    p = build(tmp_path, "t", net, (2, 20, 5, 7))
+    check(ctx, p, RNG.standard_normal((2, 20, 5, 7)).astype(np.float32))
+
+
+def test_maxpool_slice_pad(ctx, tmp_path):
+    def net(g, x):
+        y = g.add("MaxPool", [x], kernel_shape=[2, 1], strides=[2, 1])
+        y = g.add("Pad", [y, g.init("pads", np.zeros(8, np.int64))])
+        return g.add("Slice", [y, g.init("st", np.array([1, 2], np.int64)), g.init("en", np.array([-1, 100], np.int64)),
+                               g.init("ax", np.array([2, 3], np.int64))])
+    p = build(tmp_path, "mp", net, (2, 6, 13, 9))
+    check(ctx, p, RNG.standard_normal((2, 6, 13, 9)).astype(np.float32), tol=0)
+
+
+def test_unsupported_op_is_an_error(ctx, tmp_path):
+    import ocrhip
+    p = build(tmp_path, "bad", lambda g, x: g.add("Tanh", [x]), (1, 1, 4, 4))
+    with pytest.raises(ocrhip.OcrError, match="unsupported op Tanh"):
+        ocrhip.Graph(ctx, p)
+
+
+def test_shape_errors(ctx, tmp_path):
+    import ocrhip
+    p = build(tmp_path, "cs", lambda g, x: conv(g, x, 4, 4), (1, 4, 5, 5))
+    gr = ocrhip.Graph(ctx, p)
+    with pytest.raises(ocrhip.OcrError):
+        gr.run(np.zeros((1, 3, 5, 5), np.float32))  # wrong channel count

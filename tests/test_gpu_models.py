@@ -1,0 +1,106 @@
+"""The detector and recogniser on the GPU against the oracle, through the C ABI, on the
+benchmark's synthetic inputs (configs: ocrs recognition of 36 lines; ocrs detection of an
+800 x 600 image; whole synthetic 300-dpi pages).
+
+Parity bar (from the reference's own checks, stages.rs:129-147 and ppocr-bench.rs:94-125):
+- recognition: the same arg-max class at every valid CTC step, softmax probabilities within
+  1e-3, identical decoded strings;
+- detection: probability map within 1e-4 (the reference reports < 1e-5 vs rten, README:79),
+  page masks bit-exact except pixels whose pre-threshold probability is within 1e-4 of the
+  threshold."""
+import numpy as np
+import pytest
+
+from ocrhip import synth
+from oracle import graph as og
+
+pytestmark = pytest.mark.gpu
+
+
+def softmax(x):
+    x = x.astype(np.float64)
+    e = np.exp(x - x.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+@pytest.fixture(scope="module")
+def recognizer(ctx, rec_model_path):
+    import ocrhip
+    return ocrhip.Recognizer(ctx, rec_model_path)
+
+
+@pytest.fixture(scope="module")
+def detector(ctx, det_model_path):
+    import ocrhip
+    return ocrhip.Detector(ctx, det_model_path)
+
+
+def check_recognition(recognizer, rec_oracle, batches, widths):
+    print(f"recognize {[(n, w) for _, n, w in batches]}", flush=True)
+    logits, lens, best = recognizer.recognize([(d, n, w) for d, n, w in batches])
+    ref = og.rec_logits(rec_oracle, batches)
+    k0 = 0
+    steps = 0
+    for (d, n, w), rl in zip(batches, ref):
+        T = rl.shape[0]
+        assert np.all(lens[k0: k0 + n] == T)
+        g = logits[:T, k0: k0 + n]
+        # arg-max identical at every step (last index on ties, ocr-bench.rs:67)
+        want_best = rl.shape[2] - 1 - np.argmax(rl[..., ::-1], axis=2)
+        assert np.array_equal(best[:T, k0: k0 + n], want_best)
+        np.testing.assert_array_less(np.abs(softmax(g) - softmax(rl)), 1e-3)
+        for j in range(n):
+            s_gpu, _ = og.ctc_decode(g[:, j], widths[k0 + j])
+            s_ref, _ = og.ctc_decode(rl[:, j], widths[k0 + j])
+            assert s_gpu == s_ref
+        steps += T * n
+        k0 += n
+    return steps
+
+
+def test_recognition_config1(recognizer, rec_oracle):
+    lines = synth.rec_lines(36, seed=0)
+    batches, order, widths = synth.batch_lines(lines)
+    assert check_recognition(recognizer, rec_oracle, batches, widths) > 36 * 50
+
+
+def test_recognition_edge_shapes(recognizer, rec_oracle):
+    # one narrow line (T = 2), a width not a multiple of 4, and a single-line batch
+    rng = np.random.Generator(np.random.PCG64(9))
+    batches = [(rng.uniform(-0.5, 0.5, (1, 64, 8)).astype(np.float32), 1, 8),
+               (rng.uniform(-0.5, 0.5, (3, 64, 37)).astype(np.float32), 3, 37),
+               (rng.uniform(-0.5, 0.5, (9, 64, 203)).astype(np.float32), 9, 203)]
+    check_recognition(recognizer, rec_oracle, batches, [8, 37, 37, 37] + [203] * 9)
+
+
+def test_recognition_empty_batch_is_an_error(recognizer):
+    import ocrhip
+    with pytest.raises(ocrhip.OcrError):
+        recognizer.recognize([(np.zeros((0, 64, 50), np.float32), 0, 50)])
+
+
+def test_detection_config2(detector, det_oracle):
+    img = synth.det_input()
+    got = detector.detect(img)
+    want, _ = og.run(det_oracle, img.reshape(1, 1, 800, 600))
+    want = want.reshape(800, 600)
+    assert np.abs(got - want).max() <= 1e-4
+    band = np.abs(want - 0.5) < 1e-4
+    assert np.array_equal((got > 0.5)[~band], (want > 0.5)[~band])
+
+
+@pytest.mark.parametrize("h,w", [(3300, 2550), (1000, 700), (500, 420)])
+def test_detect_page_mask(detector, det_oracle, h, w):
+    page = synth.page(1)
+    if (h, w) != page.shape[:2]:
+        page = np.ascontiguousarray(page[:h, :w])
+    print(f"detect_page {h}x{w}", flush=True)
+    bits = detector.detect_page(page, 0.5)
+    want_bits, prob, _ = og.detect_page(det_oracle, page, 0.5)
+    ys, xs = np.nonzero(bits != want_bits)
+    # Unpack the differing words: every differing pixel must lie in the 1e-4 band.
+    for y, wx in zip(ys, xs):
+        diff = int(bits[y, wx]) ^ int(want_bits[y, wx])
+        for b in range(32):
+            if diff >> b & 1:
+                assert abs(prob[y, wx * 32 + b] - 0.5) < 1e-4

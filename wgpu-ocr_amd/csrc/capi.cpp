@@ -1,0 +1,319 @@
+// The C ABI (include/ocrhip.h): status codes and a thread-local message, nothing thrown across.
+#include "../../include/ocrhip.h"
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "models.h"
+
+using namespace ocr;
+
+struct ocr_ctx {
+    std::unique_ptr<Ctx> ctx;
+};
+struct ocr_detector {
+    ocr_ctx *owner;
+    std::unique_ptr<Detector> det;
+};
+struct ocr_graph {
+    ocr_ctx *owner;
+    Graph graph;
+};
+struct ocr_recognizer {
+    ocr_ctx *owner;
+    std::unique_ptr<Recognizer> rec;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+template <class F> int guard(F &&f) {
+    try {
+        f();
+        g_error.clear();
+        return OCR_OK;
+    } catch (const std::exception &e) {
+        g_error = e.what();
+    } catch (...) {
+        g_error = "unknown error";
+    }
+    return OCR_ERR;
+}
+
+template <class T, class F> T *guard_ptr(F &&f) {
+    T *out = nullptr;
+    guard([&] { out = f(); });
+    return out;
+}
+
+void need(const void *p, const char *what) {
+    if (!p) fail(std::string(what) + " is NULL");
+}
+
+std::vector<Recognizer::Batch> to_batches(const ocr_batch *b, uint32_t count) {
+    if (count) need(b, "batches");
+    std::vector<Recognizer::Batch> out(count);
+    for (uint32_t i = 0; i < count; i++) {
+        need(b[i].data, "batch data");
+        out[i] = {b[i].data, int(b[i].n), int(b[i].w)};
+    }
+    return out;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ocr_last_error(void) { return g_error.c_str(); }
+const char *ocr_version(void) { return "ocrhip 0.1 (gfx950)"; }
+
+ocr_ctx *ocr_create(const ocr_opts *opts) {
+    return guard_ptr<ocr_ctx>([&] {
+        ocr_opts o{8, 8192, 0};
+        if (opts) o = *opts;
+        if (o.lines == 0) o.lines = 8;
+        if (o.pool_mb == 0) o.pool_mb = 8192;
+        auto c = std::make_unique<ocr_ctx>();
+        c->ctx = std::make_unique<Ctx>(o.device, o.lines, size_t(o.pool_mb));
+        return c.release();
+    });
+}
+
+void ocr_destroy(ocr_ctx *ctx) { delete ctx; }
+
+int ocr_synchronize(ocr_ctx *ctx) {
+    return guard([&] {
+        need(ctx, "ctx");
+        ctx->ctx->bind();
+        ctx->ctx->sync();
+    });
+}
+
+void *ocr_device_alloc(ocr_ctx *ctx, size_t bytes) {
+    return guard_ptr<void>([&]() -> void * {
+        need(ctx, "ctx");
+        ctx->ctx->bind();
+        void *p = nullptr;
+        OCR_HIP(hipMalloc(&p, bytes ? bytes : 16));
+        return p;
+    });
+}
+
+int ocr_device_free(ocr_ctx *ctx, void *p) {
+    return guard([&] {
+        need(ctx, "ctx");
+        ctx->ctx->bind();
+        ctx->ctx->sync();
+        OCR_HIP(hipFree(p));
+    });
+}
+
+int ocr_memcpy_h2d(ocr_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return guard([&] {
+        need(ctx, "ctx");
+        ctx->ctx->bind();
+        ctx->ctx->h2d(dst, src, bytes);
+    });
+}
+
+int ocr_memcpy_d2h(ocr_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return guard([&] {
+        need(ctx, "ctx");
+        ctx->ctx->bind();
+        ctx->ctx->d2h(dst, src, bytes);
+    });
+}
+
+ocr_detector *ocr_detector_new(ocr_ctx *ctx, const char *onnx_path) {
+    return guard_ptr<ocr_detector>([&] {
+        need(ctx, "ctx");
+        need(onnx_path, "onnx_path");
+        ctx->ctx->bind();
+        Onnx m = Onnx::load(onnx_path);
+        auto d = std::make_unique<ocr_detector>();
+        d->owner = ctx;
+        d->det = std::make_unique<Detector>(*ctx->ctx, m);
+        return d.release();
+    });
+}
+
+void ocr_detector_free(ocr_detector *det) { delete det; }
+
+int ocr_detect_page(ocr_detector *det, const uint8_t *rgb, uint32_t w, uint32_t h, float thr, uint32_t *bits) {
+    return guard([&] {
+        need(det, "det");
+        need(rgb, "rgb");
+        need(bits, "bits");
+        Ctx &c = *det->owner->ctx;
+        c.bind();
+        const size_t bytes = size_t(w) * h * 3, words = size_t((w + 31) / 32) * h;
+        DBuf drgb(&c, bytes), dbits(&c, words * 4);
+        c.h2d(drgb.get(), rgb, bytes);
+        const uint8_t *pr = drgb.as<uint8_t>();
+        uint32_t *pb = dbits.as<uint32_t>();
+        const int wi = int(w), hi = int(h);
+        det->det->detect_pages_device(&pr, &wi, &hi, 1, thr, &pb);
+        c.d2h(bits, pb, words * 4);
+    });
+}
+
+int ocr_detect_pages_device(ocr_detector *det, const uint8_t *const *d_rgb, const uint32_t *w, const uint32_t *h,
+                            uint32_t count, float thr, uint32_t *const *d_bits) {
+    return guard([&] {
+        need(det, "det");
+        if (count == 0) return;
+        need(d_rgb, "d_rgb");
+        need(w, "w");
+        need(h, "h");
+        need(d_bits, "d_bits");
+        det->owner->ctx->bind();
+        std::vector<int> wi(count), hi(count);
+        for (uint32_t k = 0; k < count; k++) {
+            wi[k] = int(w[k]);
+            hi[k] = int(h[k]);
+        }
+        det->det->detect_pages_device(d_rgb, wi.data(), hi.data(), int(count), thr, d_bits);
+    });
+}
+
+int ocr_detect(ocr_detector *det, const float *input, uint32_t h, uint32_t w, float *prob) {
+    return guard([&] {
+        need(det, "det");
+        need(input, "input");
+        need(prob, "prob");
+        det->owner->ctx->bind();
+        std::vector<float> out = det->det->detect(input, int(h), int(w));
+        std::copy(out.begin(), out.end(), prob);
+    });
+}
+
+ocr_graph *ocr_graph_new(ocr_ctx *ctx, const char *onnx_path, const char *stop_op) {
+    return guard_ptr<ocr_graph>([&] {
+        need(ctx, "ctx");
+        need(onnx_path, "onnx_path");
+        ctx->ctx->bind();
+        Onnx m = Onnx::load(onnx_path);
+        auto g = std::make_unique<ocr_graph>();
+        g->owner = ctx;
+        g->graph = Graph::build(*ctx->ctx, m, stop_op, nullptr, nullptr);
+        return g.release();
+    });
+}
+
+void ocr_graph_free(ocr_graph *g) { delete g; }
+
+int ocr_graph_dims(ocr_graph *g, uint32_t n, uint32_t c, uint32_t h, uint32_t w, uint32_t *out_nchw) {
+    return guard([&] {
+        need(g, "graph");
+        need(out_nchw, "out");
+        Shape s = g->graph.infer({int(n), int(h), int(w), int(c)});
+        out_nchw[0] = uint32_t(s[0]);
+        out_nchw[1] = uint32_t(s[3]);
+        out_nchw[2] = uint32_t(s[1]);
+        out_nchw[3] = uint32_t(s[2]);
+    });
+}
+
+int ocr_graph_run(ocr_graph *g, const float *in, uint32_t n, uint32_t c, uint32_t h, uint32_t w, float *out) {
+    return guard([&] {
+        need(g, "graph");
+        need(in, "in");
+        need(out, "out");
+        Ctx &cx = *g->owner->ctx;
+        cx.bind();
+        const size_t hw = size_t(h) * w;
+        std::vector<float> nhwc(size_t(n) * c * hw);
+        for (size_t b = 0; b < n; b++)
+            for (size_t ch = 0; ch < c; ch++)
+                for (size_t p = 0; p < hw; p++) nhwc[(b * hw + p) * c + ch] = in[(b * c + ch) * hw + p];
+        Act x{nullptr, int(n), int(h), int(w), int(c), int(c)};
+        DBuf xb(&cx, nhwc.size() * sizeof(float));
+        x.p = xb.as<float>();
+        cx.h2d(x.p, nhwc.data(), nhwc.size() * sizeof(float));
+        Graph::Out o = g->graph.run(cx, x);
+        std::vector<float> res(o.act.count());
+        cx.d2h(res.data(), o.act.p, res.size() * sizeof(float));
+        const size_t ohw = size_t(o.act.h) * o.act.w;
+        for (size_t b = 0; b < size_t(o.act.n); b++)
+            for (size_t ch = 0; ch < size_t(o.act.c); ch++)
+                for (size_t p = 0; p < ohw; p++)
+                    out[(b * o.act.c + ch) * ohw + p] = res[(b * ohw + p) * o.act.c + ch];
+    });
+}
+
+ocr_recognizer *ocr_recognizer_new(ocr_ctx *ctx, const char *onnx_path, uint32_t lines) {
+    return guard_ptr<ocr_recognizer>([&] {
+        need(ctx, "ctx");
+        need(onnx_path, "onnx_path");
+        ctx->ctx->bind();
+        Onnx m = Onnx::load(onnx_path);
+        auto r = std::make_unique<ocr_recognizer>();
+        r->owner = ctx;
+        r->rec = std::make_unique<Recognizer>(*ctx->ctx, m, lines ? lines : 8);
+        return r.release();
+    });
+}
+
+void ocr_recognizer_free(ocr_recognizer *rec) { delete rec; }
+
+int ocr_recognize_dims(ocr_recognizer *rec, const ocr_batch *batches, uint32_t count, uint32_t *tmax, uint32_t *ntot,
+                       uint32_t *classes) {
+    return guard([&] {
+        need(rec, "rec");
+        auto bs = to_batches(batches, count);
+        Recognizer::Dims d = rec->rec->dims(bs.data(), int(bs.size()));
+        if (tmax) *tmax = uint32_t(d.tmax);
+        if (ntot) *ntot = uint32_t(d.ntot);
+        if (classes) *classes = uint32_t(d.classes);
+    });
+}
+
+int ocr_recognize(ocr_recognizer *rec, const ocr_batch *batches, uint32_t count, float *logits, uint32_t *lens,
+                  uint32_t *best) {
+    return guard([&] {
+        need(rec, "rec");
+        need(lens, "lens");
+        Ctx &c = *rec->owner->ctx;
+        c.bind();
+        auto bs = to_batches(batches, count);
+        Recognizer::Dims d = rec->rec->dims(bs.data(), int(bs.size()));
+        std::vector<DBuf> data;
+        std::vector<Recognizer::Batch> dev(bs.size());
+        for (size_t i = 0; i < bs.size(); i++) {
+            const size_t bytes = size_t(bs[i].n) * 64 * bs[i].w * sizeof(float);
+            data.emplace_back(&c, bytes);
+            c.h2d(data.back().get(), bs[i].data, bytes);
+            dev[i] = {data.back().as<float>(), bs[i].n, bs[i].w};
+        }
+        const size_t rows = size_t(d.tmax) * d.ntot;
+        DBuf dl(&c, rows * d.classes * sizeof(float)), db(&c, rows * sizeof(uint32_t));
+        rec->rec->recognize_device(dev.data(), int(dev.size()), dl.as<float>(), best ? db.as<uint32_t>() : nullptr,
+                                   lens);
+        if (logits) c.d2h(logits, dl.get(), rows * d.classes * sizeof(float));
+        if (best) c.d2h(best, db.get(), rows * sizeof(uint32_t));
+        c.sync();
+    });
+}
+
+int ocr_recognize_device(ocr_recognizer *rec, const ocr_batch *d_batches, uint32_t count, float *d_logits,
+                         uint32_t *d_best, uint32_t *lens) {
+    return guard([&] {
+        need(rec, "rec");
+        need(lens, "lens");
+        Ctx &c = *rec->owner->ctx;
+        c.bind();
+        auto bs = to_batches(d_batches, count);
+        Recognizer::Dims d = rec->rec->dims(bs.data(), int(bs.size()));
+        DBuf tmp;
+        float *logits = d_logits;
+        if (!logits) {
+            tmp = DBuf(&c, size_t(d.tmax) * d.ntot * d.classes * sizeof(float));
+            logits = tmp.as<float>();
+        }
+        rec->rec->recognize_device(bs.data(), int(bs.size()), logits, d_best, lens);
+    });
+}
+
+}  // extern "C"

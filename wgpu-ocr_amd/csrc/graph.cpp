@@ -1,0 +1,448 @@
+// Graph::build follows the reference's operator contract (src/gpu.rs:1101-1240): Conv (dense,
+// depthwise, one-input-channel direct with a fused MaxPool), ConvTranspose, MaxPool (kernel =
+// stride, no pad, no ceil), Slice (constant, step 1), Concat (channels), all-zero Pad, Relu and
+// Sigmoid (fused into the Conv / ConvTranspose before them when they are its only reader).
+// Graph::run differs in how it runs, not in what it computes: shapes are inferred first, every
+// Concat's inputs are written by their producers straight into the Concat's channel range (no
+// copy), and each buffer goes back to the stream-ordered pool after its last reader.
+#include "graph.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <map>
+#include <set>
+
+namespace ocr {
+
+namespace {
+
+int act_of(const std::string &op) {
+    if (op == "Relu") return ACT_RELU;
+    if (op == "Sigmoid") return ACT_SIGMOID;
+    return -1;
+}
+
+// One value for a symmetric 2-D attribute ([a, a] or [a, a, a, a]); `def` when absent (gpu.rs:1091-1099).
+int symmetric(const Node &n, const char *name, int def) {
+    auto v = n.ints(name);
+    if (!v || v->empty()) return def;
+    for (int64_t x : *v)
+        if (x != (*v)[0]) fail(n.op + ": asymmetric " + name);
+    if ((*v)[0] < 0) fail(n.op + ": negative " + name);
+    return int((*v)[0]);
+}
+
+bool env_set(const char *name) { return std::getenv(name) != nullptr; }
+
+}  // namespace
+
+Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node, bool *found_stop) {
+    Graph g;
+    g.input = onnx.input;
+    if (found_stop) *found_stop = false;
+    const auto &nodes = onnx.nodes;
+    const Node *stopn = nullptr;
+    for (size_t i = 0; i < nodes.size(); i++) {
+        const Node &n = nodes[i];
+        if (stop && n.op == stop) {
+            stopn = &n;
+            break;
+        }
+        Step s;
+        s.output = n.outputs.at(0);
+        // An activation right after, reading only this output, is fused into it (gpu.rs:1116-1127).
+        int fused = ACT_NONE;
+        if ((n.op == "Conv" || n.op == "ConvTranspose") && i + 1 < nodes.size() && act_of(nodes[i + 1].op) >= 0 &&
+            nodes[i + 1].inputs.at(0) == s.output && onnx.readers(s.output) == 1) {
+            fused = act_of(nodes[i + 1].op);
+            s.output = nodes[i + 1].outputs.at(0);
+            i++;
+        }
+        auto bias = [&](size_t idx, int count) -> const float * {
+            if (idx < n.inputs.size() && !n.inputs[idx].empty()) {
+                const Weight &b = onnx.weight(n.inputs[idx]);
+                if (int(b.data.size()) != count) fail(n.op + ": bias size");
+                return ctx.upload_weights(b.data.data(), b.data.size());
+            }
+            std::vector<float> z(size_t(count), 0.f);
+            return ctx.upload_weights(z.data(), z.size());
+        };
+        if (n.op == "Conv") {
+            const Weight &w = onnx.weight(n.inputs.at(1));
+            if (w.dims.size() != 4) fail("conv weight not 4D");
+            const int cout = int(w.dims[0]), cin_g = int(w.dims[1]), kh = int(w.dims[2]), kw = int(w.dims[3]);
+            const int group = int(n.int_("group").value_or(1));
+            if (symmetric(n, "dilations", 1) != 1) fail("dilated conv");
+            auto ap = n.str("auto_pad");
+            if (ap && *ap != "NOTSET") fail("Conv auto_pad " + *ap + " unsupported");
+            std::vector<int64_t> pads = n.ints("pads").value_or(std::vector<int64_t>{});
+            if (pads.empty()) pads = {0, 0, 0, 0};
+            if (pads.size() != 4) fail("Conv pads");
+            auto st = n.ints("strides").value_or(std::vector<int64_t>{1, 1});
+            if (st.size() != 2) fail("Conv strides");
+            s.cout = cout;
+            s.kh = kh;
+            s.kw = kw;
+            s.pt = int(pads[0]);
+            s.pl = int(pads[1]);
+            s.pb = int(pads[2]);
+            s.pr = int(pads[3]);
+            s.sh = int(st[0]);
+            s.sw = int(st[1]);
+            s.group = group;
+            s.act = fused;
+            s.b = bias(2, cout);
+            const bool square = s.pt == s.pb && s.pl == s.pr && s.pt == s.pl;
+            if (group == 1 && cin_g == 1 && s.sh == 1 && s.sw == 1 && square && !env_set("NODIRECT")) {
+                // A MaxPool right after, reading only this output, is fused in (gpu.rs:1144-1160).
+                s.kind = OpKind::Direct;
+                s.cin = 1;
+                if (i + 1 < nodes.size()) {
+                    const Node &nx = nodes[i + 1];
+                    auto k = nx.ints("kernel_shape");
+                    auto ks = nx.ints("strides");
+                    if (nx.op == "MaxPool" && nx.inputs.at(0) == s.output && onnx.readers(s.output) == 1 && k &&
+                        k->size() == 2 && (!ks || *ks == *k) && symmetric(nx, "pads", 0) == 0 &&
+                        nx.int_("ceil_mode").value_or(0) == 0) {
+                        s.ph = int((*k)[0]);
+                        s.pw = int((*k)[1]);
+                        s.output = nx.outputs.at(0);
+                        i++;
+                    }
+                }
+                s.w = ctx.upload_weights(w.data.data(), w.data.size());
+            } else if (group == 1) {
+                s.kind = OpKind::Conv;
+                s.cin = cin_g;
+                s.mfma = conv_mfma_supported(kh, kw, s.sh, s.sw);
+                if (s.mfma) {
+                    s.pk = plan_conv_pack(cin_g, cout, kh, kw);
+                    std::vector<uint16_t> hi(s.pk.halves()), lo(s.pk.halves());
+                    bool exact = true;
+                    pack_conv_weights(s.pk, w.data.data(), hi.data(), lo.data(), &exact);
+                    s.pk.exact = exact;
+                    s.whi = ctx.upload_weights(hi.data(), hi.size());
+                    if (!exact) s.wlo = ctx.upload_weights(lo.data(), lo.size());
+                } else {
+                    s.w = ctx.upload_weights(w.data.data(), w.data.size());
+                }
+            } else if (cin_g == 1 && group == cout) {
+                s.kind = OpKind::Conv;  // depthwise: the generic kernel with groups
+                s.cin = cout;
+                s.w = ctx.upload_weights(w.data.data(), w.data.size());
+            } else {
+                fail("grouped conv with group " + std::to_string(group));
+            }
+        } else if (n.op == "ConvTranspose") {
+            const Weight &w = onnx.weight(n.inputs.at(1));
+            if (w.dims.size() != 4) fail("convT weight not 4D");
+            if (n.int_("group").value_or(1) != 1 || symmetric(n, "pads", 0) != 0 ||
+                symmetric(n, "output_padding", 0) != 0)
+                fail("unsupported ConvTranspose attributes");
+            s.kind = OpKind::ConvT;
+            s.cin = int(w.dims[0]);
+            s.cout = int(w.dims[1]);
+            s.kh = int(w.dims[2]);
+            s.kw = int(w.dims[3]);
+            s.sh = s.sw = symmetric(n, "strides", 1);
+            s.act = fused;
+            s.b = bias(2, s.cout);
+            // [cin][cout][kh][kw] -> [ky][kx][cin][cout]
+            std::vector<float> t(w.data.size());
+            for (int ci = 0; ci < s.cin; ci++)
+                for (int co = 0; co < s.cout; co++)
+                    for (int ky = 0; ky < s.kh; ky++)
+                        for (int kx = 0; kx < s.kw; kx++)
+                            t[((size_t(ky) * s.kw + kx) * s.cin + ci) * s.cout + co] =
+                                w.data[((size_t(ci) * s.cout + co) * s.kh + ky) * s.kw + kx];
+            s.w = ctx.upload_weights(t.data(), t.size());
+        } else if (n.op == "MaxPool") {
+            auto k = n.ints("kernel_shape");
+            if (!k || k->size() != 2) fail("MaxPool without kernel_shape");
+            auto st = n.ints("strides").value_or(*k);
+            if (st != *k || symmetric(n, "pads", 0) != 0 || n.int_("ceil_mode").value_or(0) != 0)
+                fail("unsupported MaxPool attributes");
+            s.kind = OpKind::MaxPool;
+            s.ph = int((*k)[0]);
+            s.pw = int((*k)[1]);
+        } else if (n.op == "Slice") {
+            auto get = [&](size_t idx) -> const std::vector<int64_t> * {
+                if (idx >= n.inputs.size() || n.inputs[idx].empty()) return nullptr;
+                auto it = onnx.ints.find(n.inputs[idx]);
+                return it == onnx.ints.end() ? nullptr : &it->second;
+            };
+            if (auto steps = get(4))
+                for (int64_t v : *steps)
+                    if (v != 1) fail("Slice with steps");
+            if (!get(1)) fail("Slice starts not constant");
+            if (!get(2)) fail("Slice ends not constant");
+            s.kind = OpKind::Slice;
+            s.starts = *get(1);
+            s.ends = *get(2);
+            if (get(3)) s.axes = *get(3);
+            else for (size_t a = 0; a < s.starts.size(); a++) s.axes.push_back(int64_t(a));
+        } else if (n.op == "Concat") {
+            if (n.int_("axis") != std::optional<int64_t>(1)) fail("Concat not on channels");
+            s.kind = OpKind::Concat;
+        } else if (n.op == "Pad") {
+            std::vector<int64_t> pads;
+            if (n.inputs.size() > 1) {
+                auto it = onnx.ints.find(n.inputs[1]);
+                if (it != onnx.ints.end()) pads = it->second;
+                else if (onnx.weights.count(n.inputs[1]))
+                    for (float v : onnx.weights.at(n.inputs[1]).data) pads.push_back(int64_t(v));
+            }
+            for (int64_t v : pads)
+                if (v != 0) fail("non-zero Pad");
+            s.kind = OpKind::Identity;
+        } else if (act_of(n.op) >= 0) {
+            s.kind = OpKind::Act;
+            s.act = act_of(n.op);
+        } else {
+            fail("unsupported op " + n.op);
+        }
+        if (s.kind == OpKind::Concat) s.inputs = n.inputs;
+        else s.inputs = {n.inputs.at(0)};
+        g.steps.push_back(std::move(s));
+    }
+    if (stopn) {
+        if (stop_node) *stop_node = *stopn;
+        if (found_stop) *found_stop = true;
+        g.output = stopn->inputs.at(0);
+    } else {
+        g.output = onnx.output;
+    }
+    return g;
+}
+
+std::vector<Shape> Graph::shapes(const Shape &in) const {
+    std::map<std::string, Shape> sh;
+    sh[input] = in;
+    std::vector<Shape> out;
+    out.reserve(steps.size());
+    for (const Step &s : steps) {
+        auto it = sh.find(s.inputs[0]);
+        if (it == sh.end()) fail("missing value " + s.inputs[0]);
+        const auto [n, h, w, c] = it->second;
+        Shape o = it->second;
+        switch (s.kind) {
+        case OpKind::Conv:
+            if (c != s.cin)
+                fail("Conv input has " + std::to_string(c) + " channels, weights take " + std::to_string(s.cin));
+            o = {n, (h + s.pt + s.pb - s.kh) / s.sh + 1, (w + s.pl + s.pr - s.kw) / s.sw + 1, s.cout};
+            if (h + s.pt + s.pb < s.kh || w + s.pl + s.pr < s.kw) fail("Conv input smaller than its kernel");
+            break;
+        case OpKind::Direct: {
+            if (c != 1) fail("direct conv takes one channel");
+            const int ch = h + 2 * s.pt - s.kh + 1, cw = w + 2 * s.pt - s.kw + 1;
+            if (ch < 1 || cw < 1) fail("Conv input smaller than its kernel");
+            o = {n, ch / s.ph, cw / s.pw, s.cout};
+            break;
+        }
+        case OpKind::ConvT:
+            if (c != s.cin) fail("ConvTranspose input channels");
+            o = {n, (h - 1) * s.sh + s.kh, (w - 1) * s.sw + s.kw, s.cout};
+            break;
+        case OpKind::MaxPool: o = {n, h / s.ph, w / s.pw, c}; break;
+        case OpKind::Slice: {
+            // Starts / ends clamped ONNX-style on NCHW axes (gpu.rs:1299-1309).
+            int nchw[4] = {n, c, h, w}, lo[4] = {0, 0, 0, 0};
+            int dims[4] = {n, c, h, w};
+            for (size_t k = 0; k < s.starts.size() && k < s.ends.size() && k < s.axes.size(); k++) {
+                int64_t ax = s.axes[k] < 0 ? s.axes[k] + 4 : s.axes[k];
+                if (ax < 0 || ax > 3) fail("Slice axis");
+                int64_t dim = nchw[ax];
+                auto clampv = [&](int64_t v) { return std::clamp<int64_t>(v < 0 ? v + dim : v, 0, dim); };
+                int64_t s0 = clampv(s.starts[k]), e0 = clampv(s.ends[k]);
+                lo[ax] = int(s0);
+                dims[ax] = int(std::max<int64_t>(0, e0 - s0));
+            }
+            if (lo[0] != 0 || lo[1] != 0 || dims[0] != n || dims[1] != c) fail("Slice on batch or channels");
+            o = {n, dims[2], dims[3], c};
+            break;
+        }
+        case OpKind::Concat: {
+            int ctot = 0;
+            for (const std::string &nm : s.inputs) {
+                auto jt = sh.find(nm);
+                if (jt == sh.end()) fail("missing value " + nm);
+                if (jt->second[0] != n || jt->second[1] != h || jt->second[2] != w) fail("Concat shapes differ");
+                ctot += jt->second[3];
+            }
+            o = {n, h, w, ctot};
+            break;
+        }
+        case OpKind::Act:
+        case OpKind::Identity: break;
+        }
+        if (o[1] < 1 || o[2] < 1) fail("empty output shape");
+        sh[s.output] = o;
+        out.push_back(o);
+    }
+    return out;
+}
+
+Shape Graph::infer(const Shape &in) const {
+    auto sh = shapes(in);
+    for (size_t i = steps.size(); i-- > 0;)
+        if (steps[i].output == output) return sh[i];
+    if (output == input) return in;
+    fail("graph output " + output + " not computed");
+}
+
+Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
+    const std::vector<Shape> shp = shapes({x.n, x.h, x.w, x.c});
+    const hipStream_t st = ctx.stream();
+    // Last reader of every value, and the Concat each value is written into (if any).
+    std::map<std::string, size_t> last;
+    std::map<std::string, std::pair<size_t, int>> into;  // value -> (concat step, channel offset)
+    std::set<std::string> produced;
+    for (size_t i = 0; i < steps.size(); i++) {
+        for (const std::string &nm : steps[i].inputs) last[nm] = i;
+        if (steps[i].kind != OpKind::Identity) produced.insert(steps[i].output);
+    }
+    for (size_t i = 0; i < steps.size(); i++) {
+        const Step &s = steps[i];
+        if (s.kind != OpKind::Concat) continue;
+        int off = 0;
+        for (const std::string &nm : s.inputs) {
+            const int c = [&] {
+                for (size_t j = 0; j < i; j++)
+                    if (steps[j].output == nm) return shp[j][3];
+                return x.c;
+            }();
+            if (produced.count(nm) && !into.count(nm) && nm != output && nm != input) into[nm] = {i, off};
+            off += c;
+        }
+    }
+    // A value written into a Concat's buffer keeps that buffer alive until its own last reader.
+    for (const auto &kv : into) {
+        auto lv = last.find(kv.first);
+        if (lv == last.end()) continue;
+        size_t &lc = last[steps[kv.second.first].output];
+        lc = std::max(lc, lv->second);
+    }
+    std::map<std::string, Act> view;
+    std::map<std::string, DBuf> owned;  // buffers by the value that owns them
+    view[input] = x;
+    auto alloc = [&](const std::string &name, const Shape &sh) -> Act {
+        Act a{nullptr, sh[0], sh[1], sh[2], sh[3], sh[3]};
+        DBuf b(&ctx, a.count() * sizeof(float));
+        a.p = b.as<float>();
+        owned[name] = std::move(b);
+        return a;
+    };
+    // Where step i writes its output.
+    auto out_view = [&](size_t i) -> Act {
+        const Step &s = steps[i];
+        auto it = into.find(s.output);
+        if (it == into.end()) return alloc(s.output, shp[i]);
+        const size_t ci = it->second.first;
+        const std::string &cname = steps[ci].output;
+        if (!view.count(cname)) view[cname] = alloc(cname, shp[ci]);
+        Act whole = view[cname];
+        Act a{whole.p + it->second.second, shp[i][0], shp[i][1], shp[i][2], shp[i][3], whole.cs};
+        return a;
+    };
+    auto release = [&](size_t i) {
+        // Buffers whose last reader was step i go back to the pool (stream order keeps the reuse
+        // safe). A value inside a Concat's buffer is freed with that buffer, whose last use was
+        // extended above to cover it.
+        for (const auto &kv : last) {
+            if (kv.second != i || kv.first == output || into.count(kv.first)) continue;
+            owned.erase(kv.first);
+        }
+    };
+    for (size_t i = 0; i < steps.size(); i++) {
+        const Step &s = steps[i];
+        const Act a = view.at(s.inputs[0]);
+        Act y;
+        switch (s.kind) {
+        case OpKind::Conv: {
+            y = out_view(i);
+            if (s.mfma) {
+                ConvArgs ca;
+                ca.x = a;
+                ca.y = y;
+                ca.wt_hi = s.whi;
+                ca.wt_lo = s.wlo;
+                ca.bias = s.b;
+                ca.pt = s.pt;
+                ca.pl = s.pl;
+                ca.act = s.act;
+                ca.pk = s.pk;
+                conv_mfma(ca, st);
+            } else {
+                conv_generic(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.sw, s.pt, s.pl, s.group, s.act, st);
+            }
+            break;
+        }
+        case OpKind::Direct:
+            y = out_view(i);
+            conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st);
+            break;
+        case OpKind::ConvT:
+            y = out_view(i);
+            conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
+            break;
+        case OpKind::MaxPool:
+            y = out_view(i);
+            maxpool(a, y, s.ph, s.pw, st);
+            break;
+        case OpKind::Slice: {
+            y = out_view(i);
+            int y0 = 0, x0 = 0;
+            for (size_t k = 0; k < s.starts.size() && k < s.axes.size(); k++) {
+                int64_t ax = s.axes[k] < 0 ? s.axes[k] + 4 : s.axes[k];
+                int64_t dim = ax == 2 ? a.h : a.w;
+                int64_t v = s.starts[k] < 0 ? s.starts[k] + dim : s.starts[k];
+                v = std::clamp<int64_t>(v, 0, dim);
+                if (ax == 2) y0 = int(v);
+                if (ax == 3) x0 = int(v);
+            }
+            copy_act(a, y, y0, x0, st);
+            break;
+        }
+        case OpKind::Concat: {
+            if (!view.count(s.output)) view[s.output] = alloc(s.output, shp[i]);
+            y = view[s.output];
+            int off = 0;
+            for (const std::string &nm : s.inputs) {
+                const Act part = view.at(nm);
+                auto it = into.find(nm);
+                if (it == into.end() || it->second.first != i) {
+                    Act dst{y.p + off, part.n, part.h, part.w, part.c, y.cs};
+                    copy_act(part, dst, 0, 0, st);
+                }
+                off += part.c;
+            }
+            break;
+        }
+        case OpKind::Act:
+            y = out_view(i);
+            activate(a, y, s.act, st);
+            break;
+        case OpKind::Identity: y = a; break;
+        }
+        view[s.output] = y;
+        release(i);
+    }
+    Out out;
+    auto vit = view.find(output);
+    if (vit == view.end()) fail("graph output " + output + " not computed");
+    out.act = vit->second;
+    auto oit = owned.find(output);
+    if (oit != owned.end() && out.act.cs == out.act.c) {
+        out.buf = std::move(oit->second);
+    } else {
+        // The output is a view (a Concat slice or the input): give the caller its own copy.
+        Act dst{nullptr, out.act.n, out.act.h, out.act.w, out.act.c, out.act.c};
+        out.buf = DBuf(&ctx, dst.count() * sizeof(float));
+        dst.p = out.buf.as<float>();
+        copy_act(out.act, dst, 0, 0, st);
+        out.act = dst;
+    }
+    return out;
+}
+
+}  // namespace ocr

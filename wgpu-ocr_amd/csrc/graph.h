@@ -1,0 +1,57 @@
+// Executor for convolutional ONNX graphs (the reference's Graph, src/gpu.rs:1058-1378).
+#pragma once
+
+#include <array>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "onnx.h"
+#include "runtime.h"
+
+namespace ocr {
+
+enum class OpKind { Conv, Direct, ConvT, MaxPool, Slice, Concat, Act, Identity };
+
+struct Step {
+    OpKind kind = OpKind::Identity;
+    std::vector<std::string> inputs;
+    std::string output;
+    // Conv / Direct / ConvT
+    int cin = 0, cout = 0, kh = 0, kw = 0, pt = 0, pl = 0, pb = 0, pr = 0, sh = 1, sw = 1, group = 1;
+    int act = ACT_NONE;
+    bool mfma = false;        // dense conv on the matrix cores (else conv_generic)
+    ConvPack pk;
+    const uint16_t *whi = nullptr, *wlo = nullptr;
+    const float *w = nullptr, *b = nullptr;  // float32 weights (direct, transpose, generic) and bias
+    int ph = 1, pw = 1;                       // Direct's fused MaxPool, or MaxPool's kernel
+    std::vector<int64_t> starts, ends, axes;  // Slice
+};
+
+// Shape of an activation: n, h, w, c.
+using Shape = std::array<int, 4>;
+
+class Graph {
+  public:
+    // The graph of `onnx` up to (not including) the first node of type `stop`, if given
+    // (gpu.rs:1102-1240). The stop node, if found, is copied to *stop_node.
+    static Graph build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node, bool *found_stop);
+
+    // Output shape for an input of shape `in` (throws on an invalid shape).
+    Shape infer(const Shape &in) const;
+
+    struct Out {
+        DBuf buf;
+        Act act;
+    };
+    // Record the graph on `x` on the context's stream; returns the output (gpu.rs:1243-1377).
+    Out run(Ctx &ctx, const Act &x) const;
+
+    std::string input, output;
+    std::vector<Step> steps;
+
+  private:
+    std::vector<Shape> shapes(const Shape &in) const;  // output shape of every step
+};
+
+}  // namespace ocr

@@ -1,0 +1,75 @@
+// Host-side launchers of the HIP kernels (each defined next to its kernel in kernels/*.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.h"
+
+namespace ocr {
+
+// ---- MFMA implicit-GEMM convolution (kernels/conv.hip) ----------------------------------
+// Weights are packed once per layer by pack_conv_weights: float16 hi (exact when the model's
+// weights are float16 values) and, if not exact, the float16 remainder lo.
+struct ConvPack {
+    int cin = 0, cout = 0, kh = 0, kw = 0;
+    int bn = 0;       // output channels per workgroup: 16, 32 or 64
+    int chunks = 0;   // input channels in slices of 32
+    int nblocks = 0;  // ceil(cout / bn)
+    bool exact = true;
+    size_t halves() const { return size_t(nblocks) * chunks * kh * kw * bn * 32; }
+};
+
+// Layout of a packed weight set: [nblock][chunk][tap][bn][32 input channels], float16.
+// w is ONNX's [cout][cin][kh][kw]. Returns the pack description; hi/lo (host) are filled.
+ConvPack plan_conv_pack(int cin, int cout, int kh, int kw);
+void pack_conv_weights(const ConvPack &pk, const float *w, uint16_t *hi, uint16_t *lo, bool *exact);
+
+struct ConvArgs {
+    Act x, y;                       // input and output views (NHWC)
+    const uint16_t *wt_hi = nullptr, *wt_lo = nullptr;
+    const float *bias = nullptr;    // [cout] or null
+    const float *res = nullptr;     // residual added after the activation (gpu.rs:65), or null
+    int res_cs = 0;
+    int pt = 0, pl = 0;             // leading pads (stride 1)
+    int act = ACT_NONE;
+    ConvPack pk;
+};
+// True when the MFMA path takes this shape (stride 1, kernel at most 3 x 3).
+bool conv_mfma_supported(int kh, int kw, int sh, int sw);
+void conv_mfma(const ConvArgs &a, hipStream_t s);
+
+// ---- Everything else (kernels/ops.hip) ----------------------------------------------------
+// Any conv (grouped, strided) in float32, one thread per output: the fallback path.
+void conv_generic(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int sh, int sw,
+                  int pt, int pl, int group, int act, hipStream_t s);
+// One input channel, stride 1, act, and a fused MaxPool (ph, pw) (gpu.rs:385-422).
+void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int pad, int act,
+                 int ph, int pw, hipStream_t s);
+// ConvTranspose gather form (gpu.rs:424-460); w re-laid out as [ky][kx][cin][cout].
+void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride,
+                    int act, hipStream_t s);
+void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s);
+void copy_act(const Act &x, const Act &y, int y0, int x0, hipStream_t s);  // Slice / Concat copies
+void activate(const Act &x, const Act &y, int act, hipStream_t s);
+void fill(float *p, size_t count, float v, hipStream_t s);
+// RGB bytes -> ocrs grey, padded with black, bilinear to ow x oh (gpu.rs:530-561).
+void grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh, float sx, float sy,
+                 hipStream_t s);
+// Model output (row stride `stride`, valid mw x mh) -> page size bits (gpu.rs:563-593).
+void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, float sx, float sy,
+             float thr, hipStream_t s);
+// AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c] at
+// line offset noff (gpu.rs:595-614).
+void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s);
+// Per row of [rows][classes]: the arg-max, the last index on ties (ocr-bench.rs:67).
+void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s);
+
+// ---- GRU recurrence (kernels/gru.hip) -------------------------------------------------------
+// One layer, both directions, every line with its own length (gpu.rs:680-819). G [t][n][1536]
+// holds W x + Wb; R [2][768][256] float16 (exact values); Rb [2][768]; Y [t][n][512].
+void gru_recurrence(const float *G, const uint16_t *R, const float *Rb, float *Y, const uint32_t *lens, int ntot,
+                    int tmax, hipStream_t s);
+
+}  // namespace ocr

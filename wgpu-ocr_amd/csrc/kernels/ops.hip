@@ -1,0 +1,304 @@
+// Memory-bound kernels of the path, NHWC float32 activations. Semantics follow the reference's
+// WGSL programs in src/gpu.rs (line numbers at each kernel); the layouts are this library's own.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "../kernels.h"
+
+namespace ocr {
+
+namespace {
+
+__device__ inline float act_f(float v, int act) {
+    if (act == ACT_RELU) return fmaxf(v, 0.f);
+    if (act == ACT_SIGMOID) return 1.f / (1.f + expf(-v));
+    if (act == ACT_GELU) return 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+    if (act == ACT_SILU) return v / (1.f + expf(-v));
+    return v;
+}
+
+inline unsigned blocks_for(size_t n, int per = 256) {
+    size_t b = (n + per - 1) / per;
+    if (b > 0x7fffffff) fail("grid too large");
+    return unsigned(b ? b : 1);
+}
+
+// WGSL mix(a, b, t) = a * (1 - t) + b * t, unfused as the reference states it.
+__device__ inline float mixf(float a, float b, float t) { return __fadd_rn(__fmul_rn(a, 1.f - t), __fmul_rn(b, t)); }
+
+// ---- conv_generic: any group / stride, float32, one thread per output value -----------------
+__global__ void conv_generic_kernel(const float *x, int n, int h, int w, int cin, int xcs, float *y, int oh, int ow,
+                                    int cout, int ycs, const float *wt, const float *b, int kh, int kw, int sh,
+                                    int sw, int pt, int pl, int group, int act) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    size_t total = size_t(n) * oh * ow * cout;
+    if (i >= total) return;
+    int co = int(i % cout);
+    size_t pix = i / cout;
+    int ox = int(pix % ow), oy = int((pix / ow) % oh), img = int(pix / (size_t(ow) * oh));
+    int cin_g = cin / group, cout_g = cout / group, g0 = (co / cout_g) * cin_g;
+    float acc = 0.f;
+    for (int c = 0; c < cin_g; c++)
+        for (int ky = 0; ky < kh; ky++) {
+            int iy = oy * sh - pt + ky;
+            if (iy < 0 || iy >= h) continue;
+            for (int kx = 0; kx < kw; kx++) {
+                int ix = ox * sw - pl + kx;
+                if (ix < 0 || ix >= w) continue;
+                acc += x[((size_t(img) * h + iy) * w + ix) * xcs + g0 + c] * wt[((size_t(co) * cin_g + c) * kh + ky) * kw + kx];
+            }
+        }
+    y[pix * ycs + co] = act_f(acc + (b ? b[co] : 0.f), act);
+}
+
+// ---- conv_direct (gpu.rs:385-422): cin = 1, stride 1, act, MaxPool (ph, pw) fused ------------
+// One thread per pooled output pixel computes every output channel; weights [cout][kh][kw].
+__global__ void conv_direct_kernel(const float *x, int n, int h, int w, int xcs, float *y, int oh, int ow, int cout,
+                                   int ycs, const float *wt, const float *b, int kh, int kw, int pad, int act, int ph,
+                                   int pw) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(n) * oh * ow) return;
+    int ox = int(i % ow), oy = int((i / ow) % oh), img = int(i / (size_t(ow) * oh));
+    const float *xi = x + size_t(img) * h * w * xcs;
+    float *yo = y + i * ycs;
+    for (int co = 0; co < cout; co++) {
+        float best = -3.4e38f;
+        for (int py = 0; py < ph; py++)
+            for (int px = 0; px < pw; px++) {
+                int cy = oy * ph + py, cx = ox * pw + px;
+                float acc = 0.f;
+                for (int ky = 0; ky < kh; ky++) {
+                    int iy = cy + ky - pad;
+                    if (iy < 0 || iy >= h) continue;
+                    for (int kx = 0; kx < kw; kx++) {
+                        int ix = cx + kx - pad;
+                        if (ix < 0 || ix >= w) continue;
+                        acc += xi[(size_t(iy) * w + ix) * xcs] * wt[(co * kh + ky) * kw + kx];
+                    }
+                }
+                best = fmaxf(best, act_f(acc + b[co], act));
+            }
+        yo[co] = best;
+    }
+}
+
+// ---- conv_transpose (gpu.rs:424-460): gather form, taps with ky = oy mod s ------------------
+// Weights re-laid out as [ky][kx][cin][cout]; consecutive threads take consecutive channels.
+__global__ void convt_kernel(const float *x, int n, int h, int w, int cin, int xcs, float *y, int oh, int ow,
+                             int cout, int ycs, const float *wt, const float *b, int kh, int kw, int s, int act) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(n) * oh * ow * cout) return;
+    int co = int(i % cout);
+    size_t pix = i / cout;
+    int ox = int(pix % ow), oy = int((pix / ow) % oh), img = int(pix / (size_t(ow) * oh));
+    float acc = 0.f;
+    for (int ky = oy % s; ky < kh && ky <= oy; ky += s) {
+        int iy = (oy - ky) / s;
+        if (iy >= h) continue;
+        for (int kx = ox % s; kx < kw && kx <= ox; kx += s) {
+            int ix = (ox - kx) / s;
+            if (ix >= w) continue;
+            const float *xp = x + ((size_t(img) * h + iy) * w + ix) * xcs;
+            const float *wp = wt + (size_t(ky * kw + kx) * cin) * cout + co;
+            for (int ci = 0; ci < cin; ci++) acc += xp[ci] * wp[size_t(ci) * cout];
+        }
+    }
+    y[pix * ycs + co] = act_f(acc + b[co], act);
+}
+
+// ---- maxpool (gpu.rs:462-482): kernel = stride, no padding, floor ---------------------------
+__global__ void maxpool_kernel(const float *x, int n, int h, int w, int c, int xcs, float *y, int oh, int ow, int ycs,
+                               int kh, int kw) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(n) * oh * ow * c) return;
+    int ch = int(i % c);
+    size_t pix = i / c;
+    int ox = int(pix % ow), oy = int((pix / ow) % oh), img = int(pix / (size_t(ow) * oh));
+    float m = -3.4e38f;
+    for (int ky = 0; ky < kh; ky++)
+        for (int kx = 0; kx < kw; kx++)
+            m = fmaxf(m, x[((size_t(img) * h + oy * kh + ky) * w + ox * kw + kx) * xcs + ch]);
+    y[pix * ycs + ch] = m;
+}
+
+// ---- copy: out[n][y][x][c] = in[n][y + y0][x + x0][c] (gpu.rs:484-515, Slice and Concat) -----
+__global__ void copy_kernel(const float *x, int xh, int xw, int xcs, float *y, int n, int h, int w, int c, int ycs,
+                            int y0, int x0) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(n) * h * w * c) return;
+    int ch = int(i % c);
+    size_t pix = i / c;
+    int ox = int(pix % w), oy = int((pix / w) % h), img = int(pix / (size_t(w) * h));
+    y[pix * ycs + ch] = x[((size_t(img) * xh + oy + y0) * xw + ox + x0) * xcs + ch];
+}
+
+__global__ void activate_kernel(const float *x, int xcs, float *y, int ycs, size_t pixels, int c, int act) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= pixels * c) return;
+    size_t pix = i / c;
+    int ch = int(i % c);
+    y[pix * ycs + ch] = act_f(x[pix * xcs + ch], act);
+}
+
+__global__ void fill_kernel(float *p, size_t count, float v) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = v;
+}
+
+// ---- grey_resize (gpu.rs:530-561) -------------------------------------------------------------
+__device__ inline float grey_at(const uint8_t *rgb, int w, int h, int x, int yy) {
+    if (x >= w || yy >= h) return -0.5f;
+    const uint8_t *q = rgb + (size_t(yy) * w + x) * 3;
+    float g = __fadd_rn(-0.5f, __fmul_rn(float(q[0]), 0.299f / 255.f));
+    g = __fadd_rn(g, __fmul_rn(float(q[1]), 0.587f / 255.f));
+    return __fadd_rn(g, __fmul_rn(float(q[2]), 0.114f / 255.f));
+}
+
+__global__ void grey_resize_kernel(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh,
+                                   float sx, float sy) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= ow * oh) return;
+    int ox = i % ow, oy = i / ow;
+    float iy = fminf(fmaxf(__fsub_rn(__fmul_rn(sy, float(oy) + 0.5f), 0.5f), 0.f), float(ph) - 1.f);
+    float ix = fminf(fmaxf(__fsub_rn(__fmul_rn(sx, float(ox) + 0.5f), 0.5f), 0.f), float(pw) - 1.f);
+    int y1 = int(iy), x1 = int(ix);
+    int y2 = min(y1 + 1, ph - 1), x2 = min(x1 + 1, pw - 1);
+    float wy = iy - float(y1), wx = ix - float(x1);
+    float top = mixf(grey_at(rgb, w, h, x1, y1), grey_at(rgb, w, h, x2, y1), wx);
+    float bot = mixf(grey_at(rgb, w, h, x1, y2), grey_at(rgb, w, h, x2, y2), wx);
+    y[i] = mixf(top, bot, wy);
+}
+
+// ---- mask_up (gpu.rs:563-593): one thread per 32-pixel word ----------------------------------
+__global__ void mask_up_kernel(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, int words,
+                               float sx, float sy, float thr) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= words * h) return;
+    int wx = i % words, oy = i / words;
+    float iy = fminf(fmaxf(__fsub_rn(__fmul_rn(sy, float(oy) + 0.5f), 0.5f), 0.f), float(mh) - 1.f);
+    int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
+    float fy = iy - float(y1);
+    uint32_t out = 0;
+    for (int b = 0; b < 32; b++) {
+        int ox = wx * 32 + b;
+        if (ox >= w) break;
+        float ix = fminf(fmaxf(__fsub_rn(__fmul_rn(sx, float(ox) + 0.5f), 0.5f), 0.f), float(mw) - 1.f);
+        int x1 = int(ix), x2 = min(x1 + 1, mw - 1);
+        float fx = ix - float(x1);
+        float top = mixf(m[size_t(y1) * stride + x1], m[size_t(y1) * stride + x2], fx);
+        float bot = mixf(m[size_t(y2) * stride + x1], m[size_t(y2) * stride + x2], fx);
+        if (mixf(top, bot, fy) > thr) out |= 1u << b;
+    }
+    bits[i] = out;
+}
+
+// ---- avgpool_t (gpu.rs:595-614): [n][kh][T][c] -> X[t][ntot][c] at line offset noff ----------
+__global__ void avgpool_t_kernel(const float *x, int n, int h, int kh, int T, int c, int xcs, float *X, int ntot,
+                                 int noff) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(n) * T * c) return;
+    int ch = int(i % c);
+    int t = int((i / c) % T), img = int(i / (size_t(c) * T));
+    float s = 0.f;
+    for (int r = 0; r < kh; r++) s += x[((size_t(img) * h + r) * T + t) * xcs + ch];
+    X[(size_t(t) * ntot + noff + img) * c + ch] = s / float(kh);
+}
+
+// ---- argmax: one wavefront per row, the last index on ties ---------------------------------
+__global__ void argmax_kernel(const float *x, int rows, int classes, uint32_t *best) {
+    int row = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *r = x + size_t(row) * classes;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int j = lane; j < classes; j += 64) {
+        float v = r[j];
+        if (bi < 0 || v >= bv) { bv = v; bi = j; }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        float ov = __shfl_xor(bv, off);
+        int oi = __shfl_xor(bi, off);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) best[row] = uint32_t(bi < 0 ? 0 : bi);
+}
+
+}  // namespace
+
+void conv_generic(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int sh, int sw, int pt,
+                  int pl, int group, int act, hipStream_t s) {
+    size_t total = y.count();
+    hipLaunchKernelGGL(conv_generic_kernel, dim3(blocks_for(total)), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.c, x.cs,
+                       y.p, y.h, y.w, y.c, y.cs, w, b, kh, kw, sh, sw, pt, pl, group, act);
+    OCR_HIP(hipGetLastError());
+}
+
+void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int pad, int act, int ph,
+                 int pw, hipStream_t s) {
+    hipLaunchKernelGGL(conv_direct_kernel, dim3(blocks_for(y.pixels())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.cs,
+                       y.p, y.h, y.w, y.c, y.cs, w, b, kh, kw, pad, act, ph, pw);
+    OCR_HIP(hipGetLastError());
+}
+
+void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride, int act,
+                    hipStream_t s) {
+    hipLaunchKernelGGL(convt_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.c, x.cs, y.p,
+                       y.h, y.w, y.c, y.cs, w, b, kh, kw, stride, act);
+    OCR_HIP(hipGetLastError());
+}
+
+void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s) {
+    hipLaunchKernelGGL(maxpool_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.c, x.cs,
+                       y.p, y.h, y.w, y.cs, kh, kw);
+    OCR_HIP(hipGetLastError());
+}
+
+void copy_act(const Act &x, const Act &y, int y0, int x0, hipStream_t s) {
+    hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.h, x.w, x.cs, y.p, y.n, y.h,
+                       y.w, y.c, y.cs, y0, x0);
+    OCR_HIP(hipGetLastError());
+}
+
+void activate(const Act &x, const Act &y, int act, hipStream_t s) {
+    hipLaunchKernelGGL(activate_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.cs, y.p, y.cs, y.pixels(),
+                       y.c, act);
+    OCR_HIP(hipGetLastError());
+}
+
+void fill(float *p, size_t count, float v, hipStream_t s) {
+    if (!count) return;
+    hipLaunchKernelGGL(fill_kernel, dim3(blocks_for(count)), dim3(256), 0, s, p, count, v);
+    OCR_HIP(hipGetLastError());
+}
+
+void grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh, float sx, float sy,
+                 hipStream_t s) {
+    hipLaunchKernelGGL(grey_resize_kernel, dim3(blocks_for(size_t(ow) * oh)), dim3(256), 0, s, rgb, w, h, pw, ph, y,
+                       ow, oh, sx, sy);
+    OCR_HIP(hipGetLastError());
+}
+
+void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, float sx, float sy, float thr,
+             hipStream_t s) {
+    int words = (w + 31) / 32;
+    hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t(words) * h)), dim3(256), 0, s, m, stride, mw, mh, bits,
+                       w, h, words, sx, sy, thr);
+    OCR_HIP(hipGetLastError());
+}
+
+void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s) {
+    if (kh < 1 || kh > x.h) fail("avgpool_t: pool height");
+    hipLaunchKernelGGL(avgpool_t_kernel, dim3(blocks_for(size_t(x.n) * x.w * x.c)), dim3(256), 0, s, x.p, x.n, x.h,
+                       kh, x.w, x.c, x.cs, X, ntot, noff);
+    OCR_HIP(hipGetLastError());
+}
+
+void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s) {
+    if (rows <= 0) return;
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks_for(size_t(rows), 4)), dim3(256), 0, s, x, rows, classes, best);
+    OCR_HIP(hipGetLastError());
+}
+
+}  // namespace ocr

@@ -1,0 +1,224 @@
+#include "models.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+namespace ocr {
+
+// ---------------------------------------------------------------------------------------------
+// Detector
+// ---------------------------------------------------------------------------------------------
+Detector::Detector(Ctx &ctx, const Onnx &onnx) : ctx_(ctx) {
+    graph_ = Graph::build(ctx, onnx, nullptr, nullptr, nullptr);
+}
+
+void Detector::detect_pages_device(const uint8_t *const *rgb, const int *w, const int *h, int count, float thr,
+                                   uint32_t *const *bits) {
+    if (count <= 0) return;
+    const hipStream_t st = ctx_.stream();
+    Act in{nullptr, count, DET_MH, DET_MW, 1, 1};
+    DBuf inbuf(&ctx_, in.count() * sizeof(float));
+    in.p = inbuf.as<float>();
+    for (int k = 0; k < count; k++) {
+        if (w[k] <= 0 || h[k] <= 0) fail("empty page");
+        const int ph = std::max(h[k], DET_MH), pw = std::max(w[k], DET_MW);
+        grey_resize(rgb[k], w[k], h[k], pw, ph, in.p + size_t(k) * DET_MH * DET_MW, DET_MW, DET_MH,
+                    float(pw) / float(DET_MW), float(ph) / float(DET_MH), st);
+    }
+    Graph::Out out = graph_.run(ctx_, in);
+    if (out.act.h != DET_MH || out.act.w != DET_MW || out.act.c != 1)
+        fail("detection model output is not [n, 1, 800, 600]");
+    for (int k = 0; k < count; k++) {
+        const int ph = std::max(h[k], DET_MH), pw = std::max(w[k], DET_MW);
+        // The part of the mask that covers the page, not the padding (gpu.rs:1413-1414).
+        const int vh = DET_MH - (ph - h[k]) * DET_MH / ph, vw = DET_MW - (pw - w[k]) * DET_MW / pw;
+        mask_up(out.act.p + size_t(k) * DET_MH * DET_MW, DET_MW, vw, vh, bits[k], w[k], h[k],
+                float(vw) / float(w[k]), float(vh) / float(h[k]), thr, st);
+    }
+}
+
+std::vector<float> Detector::detect(const float *input, int h, int w) {
+    Act in{nullptr, 1, h, w, 1, 1};
+    DBuf inbuf(&ctx_, in.count() * sizeof(float));
+    in.p = inbuf.as<float>();
+    ctx_.h2d(in.p, input, in.count() * sizeof(float));
+    Graph::Out out = graph_.run(ctx_, in);
+    std::vector<float> prob(out.act.count());
+    // The output is NHWC; for one channel that is NCHW too.
+    if (out.act.c != 1) {
+        std::vector<float> nhwc(out.act.count());
+        ctx_.d2h(nhwc.data(), out.act.p, nhwc.size() * sizeof(float));
+        const size_t hw = size_t(out.act.h) * out.act.w;
+        for (size_t p = 0; p < hw; p++)
+            for (int c = 0; c < out.act.c; c++) prob[c * hw + p] = nhwc[p * out.act.c + c];
+        return prob;
+    }
+    ctx_.d2h(prob.data(), out.act.p, prob.size() * sizeof(float));
+    return prob;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Recognizer
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+void pack_linear(Ctx &ctx, const std::vector<float> &w_rows, int rows, int cols, ConvPack &pk, const uint16_t *&hi,
+                 const uint16_t *&lo) {
+    // w_rows is [rows = outputs][cols = inputs]: a 1 x 1 convolution's [cout][cin][1][1].
+    pk = plan_conv_pack(cols, rows, 1, 1);
+    std::vector<uint16_t> h(pk.halves()), l(pk.halves());
+    bool exact = true;
+    pack_conv_weights(pk, w_rows.data(), h.data(), l.data(), &exact);
+    pk.exact = exact;
+    hi = ctx.upload_weights(h.data(), h.size());
+    lo = exact ? nullptr : ctx.upload_weights(l.data(), l.size());
+}
+
+}  // namespace
+
+Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), lines_(lines) {
+    Node pool;
+    bool found = false;
+    trunk_ = Graph::build(ctx, onnx, "AveragePool", &pool, &found);
+    if (!found) fail("no AveragePool in the recognition model");
+    auto k = pool.ints("kernel_shape");
+    if (!k) fail("AveragePool without kernel_shape");
+    auto s = pool.ints("strides");
+    if (k->size() != 2 || (*k)[1] != 1 || !s || *s != *k) fail("unsupported AveragePool");
+    pool_kh_ = int((*k)[0]);
+    int nl = 0;
+    for (const Node &n : onnx.nodes) {
+        if (n.op != "GRU") continue;
+        if (nl >= 2) fail("more than 2 GRU layers");
+        if (n.int_("hidden_size") != std::optional<int64_t>(256) ||
+            n.int_("linear_before_reset") != std::optional<int64_t>(1) ||
+            n.str("direction") != std::optional<std::string>("bidirectional"))
+            fail("unsupported GRU attributes");
+        const Weight &w = onnx.weight(n.inputs.at(1)), &r = onnx.weight(n.inputs.at(2)),
+                     &b = onnx.weight(n.inputs.at(3));
+        if (w.dims.size() != 3 || w.dims[0] != 2 || w.dims[1] != 768) fail("GRU W shape");
+        if (r.dims != std::vector<int64_t>{2, 768, 256}) fail("GRU R shape");
+        if (b.data.size() != 2 * 1536) fail("GRU B shape");
+        Layer &L = layers_[nl++];
+        L.input = int(w.dims[2]);
+        // W [2][768][in] is already the projection's [1536 outputs][in] (gpu.rs:1466-1472).
+        pack_linear(ctx, w.data, 1536, L.input, L.pk, L.w_hi, L.w_lo);
+        std::vector<float> wb, rb;
+        for (int d = 0; d < 2; d++) {
+            wb.insert(wb.end(), b.data.begin() + d * 1536, b.data.begin() + d * 1536 + 768);
+            rb.insert(rb.end(), b.data.begin() + d * 1536 + 768, b.data.begin() + d * 1536 + 1536);
+        }
+        L.wb = ctx.upload_weights(wb.data(), wb.size());
+        L.rb = ctx.upload_weights(rb.data(), rb.size());
+        // R in float16 (gpu.rs:1478-1484). Exact for float16-valued weights; otherwise rounded,
+        // as the reference does with F16 (F16=0 refuses such a model here).
+        std::vector<uint16_t> rh(r.data.size());
+        for (size_t i = 0; i < r.data.size(); i++) {
+            _Float16 v = (_Float16)r.data[i];
+            if ((float)v != r.data[i]) r_exact_ = false;
+            std::memcpy(&rh[i], &v, 2);
+        }
+        const char *f16 = std::getenv("F16");
+        if (!r_exact_ && f16 && std::string(f16) == "0")
+            fail("GRU recurrent weights are not float16 values and F16=0 forbids rounding them");
+        L.r = ctx.upload_weights(rh.data(), rh.size());
+    }
+    if (nl != 2) fail(std::to_string(nl) + " GRU layers");
+    const Node *mm = nullptr;
+    for (const Node &n : onnx.nodes)
+        if (n.op == "MatMul") { mm = &n; break; }
+    if (!mm) fail("no MatMul");
+    const Weight &lin = onnx.weight(mm->inputs.at(1));  // [512][classes]: [in][out]
+    if (lin.dims.size() != 2 || lin.dims[0] != 512) fail("output MatMul weight shape");
+    classes_ = int(lin.dims[1]);
+    const Node *add = nullptr;
+    for (const Node &n : onnx.nodes)
+        if (n.op == "Add" && std::find(n.inputs.begin(), n.inputs.end(), mm->outputs.at(0)) != n.inputs.end()) {
+            add = &n;
+            break;
+        }
+    if (!add) fail("no bias Add");
+    const Weight *bias = nullptr;
+    for (const std::string &i : add->inputs)
+        if (onnx.weights.count(i)) bias = &onnx.weights.at(i);
+    if (!bias || int(bias->data.size()) != classes_) fail("no bias weight");
+    std::vector<float> t(size_t(classes_) * 512);
+    for (int i = 0; i < 512; i++)
+        for (int c = 0; c < classes_; c++) t[size_t(c) * 512 + i] = lin.data[size_t(i) * classes_ + c];
+    pack_linear(ctx, t, classes_, 512, lin_pk_, lin_hi_, lin_lo_);
+    lin_b_ = ctx.upload_weights(bias->data.data(), bias->data.size());
+}
+
+Recognizer::Dims Recognizer::dims(const Batch *batches, int count) const {
+    Dims d{0, 0, classes_};
+    for (int b = 0; b < count; b++) {
+        if (batches[b].n <= 0 || batches[b].w <= 0) fail("empty recognition batch");
+        const Shape s = trunk_.infer({batches[b].n, 64, batches[b].w, 1});
+        d.tmax = std::max(d.tmax, s[2]);
+        d.ntot += batches[b].n;
+    }
+    return d;
+}
+
+void Recognizer::recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens) {
+    const hipStream_t st = ctx_.stream();
+    const Dims d = dims(batches, count);
+    if (d.ntot == 0) return;
+    // The trunks first (gpu.rs:1516-1526), all on the stream.
+    std::vector<Graph::Out> trunks;
+    trunks.reserve(size_t(count));
+    for (int b = 0; b < count; b++) {
+        Act x{const_cast<float *>(batches[b].data), batches[b].n, 64, batches[b].w, 1, 1};
+        trunks.push_back(trunk_.run(ctx_, x));
+        const Act &t = trunks.back().act;
+        if (t.c != layers_[0].input)
+            fail("trunk gives " + std::to_string(t.c) + " features, GRU takes " + std::to_string(layers_[0].input));
+        if ((t.h - pool_kh_) / pool_kh_ + 1 != 1)
+            fail("trunk height " + std::to_string(t.h) + " does not pool to one row");
+    }
+    const int tmax = d.tmax, ntot = d.ntot, M = tmax * ntot;
+    DBuf X(&ctx_, size_t(M) * 256 * sizeof(float));
+    fill(X.as<float>(), size_t(M) * 256, 0.f, st);
+    int noff = 0;
+    for (int b = 0; b < count; b++) {
+        const Act &t = trunks[b].act;
+        avgpool_t(t, pool_kh_, X.as<float>(), ntot, noff, st);
+        for (int i = 0; i < t.n; i++) lens[noff + i] = uint32_t(t.w);
+        noff += t.n;
+    }
+    trunks.clear();
+    DBuf lensd(&ctx_, size_t(ntot) * sizeof(uint32_t));
+    ctx_.h2d(lensd.get(), lens, size_t(ntot) * sizeof(uint32_t));
+    DBuf G(&ctx_, size_t(M) * 1536 * sizeof(float));
+    DBuf Y[2] = {DBuf(&ctx_, size_t(M) * 512 * sizeof(float)), DBuf(&ctx_, size_t(M) * 512 * sizeof(float))};
+    const float *in = X.as<float>();
+    int in_c = 256;
+    for (int l = 0; l < 2; l++) {
+        const Layer &L = layers_[l];
+        if (in_c != L.input) fail("GRU layer input size");
+        ConvArgs ca;
+        ca.x = Act{const_cast<float *>(in), 1, 1, M, in_c, in_c};
+        ca.y = Act{G.as<float>(), 1, 1, M, 1536, 1536};
+        ca.wt_hi = L.w_hi;
+        ca.wt_lo = L.w_lo;
+        ca.bias = L.wb;
+        ca.pk = L.pk;
+        conv_mfma(ca, st);
+        fill(Y[l].as<float>(), size_t(M) * 512, 0.f, st);
+        gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd.as<uint32_t>(), ntot, tmax, st);
+        in = Y[l].as<float>();
+        in_c = 512;
+    }
+    ConvArgs ca;
+    ca.x = Act{const_cast<float *>(in), 1, 1, M, 512, 512};
+    ca.y = Act{logits, 1, 1, M, classes_, classes_};
+    ca.wt_hi = lin_hi_;
+    ca.wt_lo = lin_lo_;
+    ca.bias = lin_b_;
+    ca.pk = lin_pk_;
+    conv_mfma(ca, st);
+    if (best) argmax_rows(logits, M, classes_, best, st);
+}
+
+}  // namespace ocr

@@ -1,0 +1,138 @@
+#include "runtime.h"
+
+#include <cstdio>
+
+namespace ocr {
+
+void fail(const std::string &msg) { throw Error(msg); }
+
+size_t Pool::size_class(size_t bytes) {
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes <= (64u << 10)) return bytes ? bytes : 256;
+    size_t p = 1;
+    while (p < bytes) p <<= 1;
+    size_t mid = p / 2 + p / 4;  // 1.5 * 2^(k-1)
+    return mid >= bytes ? mid : p;
+}
+
+Pool::~Pool() { trim(); }
+
+void *Pool::get(size_t bytes) {
+    size_t sz = size_class(bytes);
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        auto it = free_.find(sz);
+        if (it != free_.end() && !it->second.empty()) {
+            void *p = it->second.back();
+            it->second.pop_back();
+            held_ -= sz;
+            live_ += sz;
+            return p;
+        }
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess) {
+        // Out of memory: give back what the pool holds and try once more.
+        trim();
+        OCR_HIP(hipMalloc(&p, sz));
+    }
+    std::lock_guard<std::mutex> lk(mu_);
+    size_of_[p] = sz;
+    live_ += sz;
+    return p;
+}
+
+void Pool::put(void *p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = size_of_.find(p);
+    if (it == size_of_.end()) return;
+    size_t sz = it->second;
+    live_ -= sz;
+    if (held_ + sz > cap_) {
+        size_of_.erase(it);
+        // hipFree waits for the device to finish with the buffer.
+        (void)hipFree(p);
+        return;
+    }
+    held_ += sz;
+    free_[sz].push_back(p);
+}
+
+void Pool::trim() {
+    std::lock_guard<std::mutex> lk(mu_);
+    for (auto &kv : free_)
+        for (void *p : kv.second) {
+            (void)hipFree(p);
+            size_of_.erase(p);
+        }
+    free_.clear();
+    held_ = 0;
+}
+
+DBuf::DBuf(Ctx *ctx, size_t bytes) : ctx_(ctx), bytes_(bytes) { p_ = ctx->pool().get(bytes); }
+
+DBuf &DBuf::operator=(DBuf &&o) noexcept {
+    if (this != &o) {
+        reset();
+        ctx_ = o.ctx_;
+        p_ = o.p_;
+        bytes_ = o.bytes_;
+        o.p_ = nullptr;
+        o.ctx_ = nullptr;
+        o.bytes_ = 0;
+    }
+    return *this;
+}
+
+void DBuf::reset() {
+    if (p_ && ctx_) ctx_->pool().put(p_);
+    p_ = nullptr;
+    ctx_ = nullptr;
+    bytes_ = 0;
+}
+
+Ctx::Ctx(int device, uint32_t lines, size_t pool_mb) : device_(device), lines_(lines), pool_(pool_mb << 20) {
+    int count = 0;
+    OCR_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count)
+        fail("device " + std::to_string(device) + " not present (" + std::to_string(count) + " visible)");
+    OCR_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    OCR_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
+        fail(std::string("this library is built for gfx950; device is ") + prop.gcnArchName);
+    OCR_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+}
+
+Ctx::~Ctx() {
+    (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    pool_.trim();
+    for (void *p : weights_) (void)hipFree(p);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Ctx::bind() const { OCR_HIP(hipSetDevice(device_)); }
+
+void Ctx::sync() { OCR_HIP(hipStreamSynchronize(stream_)); }
+
+const void *Ctx::upload_raw(const void *data, size_t bytes) {
+    void *p = nullptr;
+    OCR_HIP(hipMalloc(&p, bytes ? bytes : 16));
+    weights_.push_back(p);
+    if (bytes) OCR_HIP(hipMemcpy(p, data, bytes, hipMemcpyHostToDevice));
+    return p;
+}
+
+void Ctx::h2d(void *dst, const void *src, size_t bytes) {
+    if (bytes) OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_));
+}
+
+void Ctx::d2h(void *dst, const void *src, size_t bytes) {
+    if (bytes) OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream_));
+    OCR_HIP(hipStreamSynchronize(stream_));
+}
+
+}  // namespace ocr

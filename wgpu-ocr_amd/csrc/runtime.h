@@ -1,0 +1,97 @@
+// Device context: the GPU, its stream and the scratch pool (the reference's Gpu, src/gpu.rs:825-1056).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "common.h"
+
+namespace ocr {
+
+// Size-classed, stream-ordered pool of device buffers (gpu.rs:938-966). hipMalloc is slow and
+// synchronising, so scratch buffers are reused: a buffer given back is handed out again for
+// later work on the same stream, which stream order makes safe without any wait. Sizes are
+// rounded up to classes (2^k and 1.5 * 2^k above 64 KiB) so varied batch shapes share buffers;
+// the pool keeps at most `cap` bytes and frees the rest (POOLMB, gpu.rs:919).
+class Pool {
+  public:
+    explicit Pool(size_t cap_bytes) : cap_(cap_bytes) {}
+    ~Pool();
+    void *get(size_t bytes);
+    void put(void *p);
+    void trim();  // free everything held
+    size_t held() const { return held_; }
+    size_t live() const { return live_; }
+    static size_t size_class(size_t bytes);
+
+  private:
+    std::map<size_t, std::vector<void *>> free_;
+    std::unordered_map<void *, size_t> size_of_;
+    size_t cap_, held_ = 0, live_ = 0;
+    std::mutex mu_;
+};
+
+class Ctx;
+
+// A pooled device buffer owned by one holder; goes back to the pool when destroyed.
+class DBuf {
+  public:
+    DBuf() = default;
+    DBuf(Ctx *ctx, size_t bytes);
+    DBuf(DBuf &&o) noexcept { *this = std::move(o); }
+    DBuf &operator=(DBuf &&o) noexcept;
+    DBuf(const DBuf &) = delete;
+    DBuf &operator=(const DBuf &) = delete;
+    ~DBuf() { reset(); }
+    void reset();
+    template <class T> T *as() const { return static_cast<T *>(p_); }
+    void *get() const { return p_; }
+    size_t bytes() const { return bytes_; }
+    explicit operator bool() const { return p_ != nullptr; }
+
+  private:
+    Ctx *ctx_ = nullptr;
+    void *p_ = nullptr;
+    size_t bytes_ = 0;
+};
+
+// A weight buffer uploaded once at load time (not pooled).
+struct DevWeights {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+
+class Ctx {
+  public:
+    Ctx(int device, uint32_t lines, size_t pool_mb);
+    ~Ctx();
+    int device() const { return device_; }
+    hipStream_t stream() const { return stream_; }
+    uint32_t lines() const { return lines_; }
+    Pool &pool() { return pool_; }
+    void bind() const;  // make this context's device current on the calling thread
+    void sync();
+
+    // Weights live until the context is destroyed.
+    template <class T> const T *upload_weights(const T *data, size_t count) {
+        return static_cast<const T *>(upload_raw(data, count * sizeof(T)));
+    }
+    void h2d(void *dst, const void *src, size_t bytes);  // async on the stream (pageable src is staged)
+    void d2h(void *dst, const void *src, size_t bytes);  // synchronous: waits for the stream
+
+  private:
+    const void *upload_raw(const void *data, size_t bytes);
+    int device_;
+    uint32_t lines_;
+    hipStream_t stream_ = nullptr;
+    Pool pool_;
+    std::vector<void *> weights_;
+};
+
+}  // namespace ocr
