@@ -1,0 +1,158 @@
+"""Benchmark of the ocrs whole-page pipeline on one MI355X.
+
+Workload (one step): 12 synthetic 300-dpi US Letter RGB pages (2550 x 3300, ~36 text lines each,
+Gaussian noise sigma 4) through the whole pipeline: GPU grey conversion, pad and resize to
+800 x 600, the detection U-Net, the page-size mask; host words, lines and line padding; GPU line
+images (64 high); the CNN + 2 x BiGRU recogniser; host CTC. The pages are resident in HBM when
+the timed region starts (the PCIe-inclusive rate is a separate field). Models are random-init
+(Kaiming, seed 0) with the ocrs architecture; data are synthetic.
+
+Prints one JSON line: value = pages/s over K timed steps, plus recognition lines/s, the
+dominant kernel's roofline (HIP events on the kernel's own stream over the timed region), and a
+CPU baseline (the oracle: a C / numpy restatement of the same path, on a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "wgpu-ocr_amd")]
+
+import numpy as np  # noqa: E402
+
+METRIC = "pages/sec + ms/page (ocrs det+rec) on 1 MI355X; rec lines/sec; % roofline"
+HBM_PEAK_GBS = 8000.0
+F16_PEAK_TFLOPS = 2500.0
+
+
+def roofline(kernels):
+    """The kernel family with the most time in the timed region, against its bound."""
+    fam, k = max(kernels.items(), key=lambda kv: kv[1]["ms"])
+    secs = k["ms"] / 1e3
+    intensity = k["flops"] / max(k["bytes"], 1.0)
+    ridge = F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    if k["flops"] > 0 and intensity >= ridge:
+        achieved = k["flops"] / secs / 1e12
+        out = {"bound": "mfma", "achieved": achieved, "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+               "frac": achieved / F16_PEAK_TFLOPS}
+    else:
+        achieved = k["bytes"] / secs / 1e9
+        out = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+               "frac": achieved / HBM_PEAK_GBS}
+    out.update({"kernel": fam, "calls": k["calls"], "avg_us": 1e3 * k["ms"] / max(k["calls"], 1),
+                "traffic": None})
+    return out
+
+
+def cpu_baseline(det_path, rec_path, page, sample_pages=1):
+    """The oracle (C restatement, OpenMP on all host cores) on `sample_pages` page(s): oracle
+    detection, the library's host layout, oracle line images and recognition, greedy CTC."""
+    import ocrhip
+    from oracle import graph as og
+    from oracle import onnx_read
+
+    det, rec = onnx_read.load(det_path), onnx_read.load(rec_path)
+    og.lib()
+    t = time.perf_counter()
+    for _ in range(sample_pages):
+        og.page_pipeline(det, rec, page, 0.5, lambda b, w: ocrhip.Layout(b, w))
+    secs = time.perf_counter() - t
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": sample_pages / secs, "unit": "pages/s", "cores": cores, "kind": "port",
+            "sample": f"{sample_pages} synthetic page(s) of the same workload, whole pipeline, "
+                      f"{secs:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--pages", type=int, default=12)
+    ap.add_argument("--merge", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the pipeline shards by page with no exchange, so N GPUs run N "
+              "independent copies (see DESIGN.md); run it with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import ocrhip
+    from ocrhip import synth
+
+    det_path, rec_path = synth.model_path("det"), synth.model_path("rec")
+    pages = [synth.page(i) for i in range(args.pages)]
+    ctx = ocrhip.Context()
+    det = ocrhip.Detector(ctx, det_path)
+    rec = ocrhip.Recognizer(ctx, rec_path)
+    pipe = ocrhip.Pipeline(det, rec, merge=args.merge)
+    h, w = pages[0].shape[:2]
+    d_pages = []
+    for p in pages:
+        b = ctx.alloc(p.nbytes)
+        b.upload(p)
+        d_pages.append(b)
+    ws, hs = [w] * len(pages), [h] * len(pages)
+    for _ in range(args.warmup):
+        pipe.run_device(d_pages, ws, hs)
+    ctx.synchronize()
+
+    for fam in ocrhip.FAMILIES:
+        ocrhip.probe_start(fam)
+    lines = 0
+    rec_steps = 0
+    cpu_busy = 0.0
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        pipe.run_device(d_pages, ws, hs)
+        st = pipe.stats()
+        lines += st["lines"]
+        rec_steps += st["rec_steps"]
+        cpu_busy += st["cpu_busy_ms"]
+    ctx.synchronize()
+    secs = time.perf_counter() - t0
+    kernels = {f: ocrhip.probe_stop(f) for f in ocrhip.FAMILIES}
+    kernels = {f: k for f, k in kernels.items() if k["calls"]}
+
+    # PCIe-inclusive rate: the same pages handed over from host memory (reported, not the value).
+    t1 = time.perf_counter()
+    pipe.run(pages)
+    host_secs = time.perf_counter() - t1
+
+    n_pages = args.steps * len(pages)
+    out = {
+        "metric": METRIC,
+        "value": n_pages / secs,
+        "unit": "pages/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": 1e3 * secs / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"ocrs whole-page pipeline, {len(pages)} synthetic 300-dpi US Letter RGB pages "
+                               f"(2550x3300) per step: det U-Net 16-256 + CNN/2xBiGRU(256) rec, merge {args.merge}",
+                   "pages_per_step": len(pages), "page": [h, w], "models": "random-init ocrs architecture"},
+        "ms_per_page": 1e3 * secs / n_pages,
+        "rec_lines_per_sec": lines / secs,
+        "lines_per_page": lines / n_pages,
+        "gru_steps_per_page": rec_steps / n_pages,
+        "host_busy_ms_per_page": cpu_busy / n_pages,
+        "pcie_inclusive_pages_per_sec": len(pages) / host_secs,
+        "roofline": roofline(kernels),
+        "kernels_ms_per_page": {f: round(k["ms"] / n_pages, 4) for f, k in
+                                sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(det_path, rec_path, pages[0])
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -111,6 +111,77 @@ int ocr_recognize(ocr_recognizer *rec, const ocr_batch *batches, uint32_t count,
 int ocr_recognize_device(ocr_recognizer *rec, const ocr_batch *d_batches, uint32_t count, float *d_logits,
                          uint32_t *d_best, uint32_t *lens);
 
+/* Kernel timing for measurement (the role of the reference's OPPROFILE, src/gpu.rs:1247-1368,
+ * without its waits): between start and stop, every launch of the kernel family (process-wide:
+ * "conv_mfma", "gru", "conv_transpose", "conv_direct", "conv_generic", "maxpool", "mask_up",
+ * "grey_resize", "line_crop", "avgpool_t", "argmax", "copy") is bracketed by HIP events on its
+ * own stream. stop waits for them and returns the launches, their summed duration in ms and
+ * their summed algorithmic FLOPs and bytes. */
+int ocr_probe_start(const char *family);
+int ocr_probe_stop(const char *family, uint32_t *calls, double *ms, double *flops, double *bytes);
+
+/* ---- Host geometry of the page pipeline (no GPU involved) ------------------------------ */
+
+/* A rotated rectangle: centre, unit up axis (y down), width across it, height along it. */
+typedef struct ocr_rrect {
+    float cx, cy, ux, uy, w, h;
+} ocr_rrect;
+
+/* word_rects (src/bin/ocr-bench.rs:40-60): the words of a page mask (h rows of ceil(w / 32)
+ * words): 8-connected components, minimum-area rectangles grown by 3 px, area >= 100. Writes
+ * at most cap rectangles; *count receives the number found. */
+int ocr_word_rects(const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out, uint32_t cap, uint32_t *count);
+
+/* The page layout before recognition (src/bin/ocr-bench.rs:503-559): words, text lines in
+ * reading order, line padding (relv, relend), every line's crop box, polygon spans and resized
+ * width, and the batches (ocr-bench.rs:385-407). */
+typedef struct ocr_layout ocr_layout;
+ocr_layout *ocr_layout_page(const uint32_t *bits, uint32_t w, uint32_t h, float relv, float relend);
+void ocr_layout_free(ocr_layout *lay);
+/* Counts: words, lines, batches. */
+int ocr_layout_counts(ocr_layout *lay, uint32_t *words, uint32_t *lines, uint32_t *batches);
+/* Line i: box = {left, top, width, height, resized width}; row_off (height + 1 entries) and
+ * spans (pairs of crop columns [x0, x1)) may be NULL to query nspans first. */
+int ocr_layout_line(ocr_layout *lay, uint32_t i, int32_t *box, int32_t *row_off, int32_t *spans, uint32_t *nspans);
+/* Batch i: its width and members (line indices, at most 20). */
+int ocr_layout_batch(ocr_layout *lay, uint32_t i, uint32_t *width, uint32_t *lines, uint32_t *count);
+
+/* ---- The page pipeline (src/bin/ocr-bench.rs:133-310, 458-585) ------------------------- */
+
+/* merge: pages per recognition pass (MERGE); relv / relend: line padding (RELV, RELEND);
+ * thr: detection threshold; threads: host worker threads (0 = up to 16); det_batch: pages per
+ * detection pass. Zeros take the defaults 2, 0.15, 0.1, 0.5, 0, 4. */
+typedef struct ocr_pipeline_opts {
+    uint32_t merge;
+    float relv;
+    float relend;
+    float thr;
+    uint32_t threads;
+    uint32_t det_batch;
+} ocr_pipeline_opts;
+
+typedef struct ocr_pipeline_stats {
+    double ms;           /* wall time of the last run */
+    double cpu_busy_ms;  /* host worker time spent on layout and decoding */
+    uint32_t pages, lines, words, batches, rec_passes;
+    uint64_t rec_steps;  /* GRU steps summed over lines */
+} ocr_pipeline_stats;
+
+ocr_pipeline *ocr_pipeline_new(ocr_detector *det, ocr_recognizer *rec, const ocr_pipeline_opts *opts);
+void ocr_pipeline_free(ocr_pipeline *pipe);
+/* Runs every page: RGB bytes (h x w x 3) already in device memory. Returns when all text is
+ * decoded. */
+int ocr_pipeline_run_device(ocr_pipeline *pipe, const uint8_t *const *d_rgb, const uint32_t *w, const uint32_t *h,
+                            uint32_t npages);
+/* The same with the pages in host memory (uploaded first, inside the call). */
+int ocr_pipeline_run(ocr_pipeline *pipe, const uint8_t *const *rgb, const uint32_t *w, const uint32_t *h,
+                     uint32_t npages);
+int ocr_pipeline_stats_get(ocr_pipeline *pipe, ocr_pipeline_stats *out);
+/* Lines and words found on a page of the last run. */
+int ocr_pipeline_page(ocr_pipeline *pipe, uint32_t page, uint32_t *lines, uint32_t *words);
+/* Text of one line (UTF-8, NUL-terminated, truncated to cap bytes); *len receives its length. */
+int ocr_pipeline_line_text(ocr_pipeline *pipe, uint32_t page, uint32_t line, char *buf, uint32_t cap, uint32_t *len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ def lib():
         L.orc_grey_resize.argtypes = [P, I, I, I, I, I, I, F, F, P]
         L.orc_mask_up_prob.argtypes = [P, I, I, I, I, I, F, F, P]
         L.orc_pack_bits.argtypes = [P, I, I, F, P]
+        L.orc_line_crop.argtypes = [P, I, I, I, I, I, I, I, P, P, I, P]
         L.orc_activate.argtypes = [F, I]
         L.orc_activate.restype = F
         _lib = L
@@ -276,3 +277,40 @@ def ctc_decode(logits_line, width, classes=97):
             out.append(int(b))
         prev = b
     return out, best
+
+
+def line_crop(rgb, box, row_off, spans, wb):
+    """One line image [64][wb] (see orc_line_crop); box = (left, top, bw, bh, out_w)."""
+    rgb = _c(rgb, np.uint8)
+    h, w = rgb.shape[:2]
+    out = np.empty((64, wb), np.float32)
+    ro = _c(row_off, np.int32)
+    sp = _c(np.asarray(spans).reshape(-1), np.int32)
+    if sp.size == 0:
+        sp = np.zeros(2, np.int32)
+    lib().orc_line_crop(_p(rgb), w, h, int(box[0]), int(box[1]), int(box[2]), int(box[3]), int(box[4]), _p(ro),
+                        _p(sp), wb, _p(out))
+    return out
+
+
+def page_pipeline(det_model, rec_model, page, thr, layout_of):
+    """The whole page on the CPU: detection (oracle), the layout (given: layout_of(bits, w)
+    returns an object with nlines, nbatches, line(i) and batch(i) as the product's host layout
+    does), line images (oracle), recognition (oracle), greedy CTC. Returns (texts by line,
+    words, bits)."""
+    bits, _, _ = detect_page(det_model, page, thr)
+    lay = layout_of(bits, page.shape[1])
+    texts = [""] * lay.nlines
+    for b in range(lay.nbatches):
+        wb, members = lay.batch(b)
+        data = np.stack([line_crop(page, *lay.line(i), wb) for i in members])
+        (logits,) = rec_logits(rec_model, [(data, len(members), wb)])
+        for k, i in enumerate(members):
+            out_w = int(lay.line(i)[0][4])
+            cls, _ = ctc_decode(logits[:, k], out_w)
+            texts[i] = "".join(ALPHABET[c - 1] for c in cls)
+    return texts, lay.words, bits
+
+
+# ocr-bench.rs:31: class k > 0 is ALPHABET[k - 1].
+ALPHABET = " 0123456789!\"#$%&'()*+,-./:;<=>?@[\\]^_`{|}~EABCDEFGHIJKLMNOPQRSTUVWXYZabcdefghijklmnopqrstuvwxyz"

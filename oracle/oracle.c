@@ -220,3 +220,43 @@ void orc_pack_bits(const float *prob, int w, int h, float thr, uint32_t *bits) {
         for (int x = 0; x < w; x++)
             if (prob[(size_t)y * w + x] > thr) bits[(size_t)y * words + x / 32] |= 1u << (x % 32);
 }
+
+/* Line image of the page pipeline (the role of ocrs' prepare_recognition_input, called at
+ * src/bin/ocr-bench.rs:378, and the batch assembly of ocr-bench.rs:388-404): crop pixel
+ * (cx, cy) is the ocrs grey value of page pixel (left + cx, top + cy) when cx lies in one of the
+ * row's spans [x0, x1) and the pixel is on the page, else black (-0.5); the crop (bh x bw) is
+ * resized bilinearly (half-pixel, clamped) to 64 x out_w and written into dst [64][wb], padded
+ * with black. */
+static float crop_px(const uint8_t *rgb, int pw, int ph, int left, int top, const int *row_off, const int *spans,
+                     int cx, int cy) {
+    for (int s = row_off[cy]; s < row_off[cy + 1]; s += 2)
+        if (cx >= spans[s] && cx < spans[s + 1]) {
+            int x = left + cx, y = top + cy;
+            if (x < 0 || y < 0 || x >= pw || y >= ph) return -0.5f;
+            return grey_px(rgb, pw, ph, x, y);
+        }
+    return -0.5f;
+}
+
+void orc_line_crop(const uint8_t *rgb, int pw, int ph, int left, int top, int bw, int bh, int out_w,
+                   const int *row_off, const int *spans, int wb, float *dst) {
+    const int H = 64;
+    float sy = (float)bh / (float)H, sx = (float)bw / (float)out_w;
+    for (int oy = 0; oy < H; oy++)
+        for (int ox = 0; ox < wb; ox++) {
+            float v = -0.5f;
+            if (ox < out_w) {
+                float iy = fminf(fmaxf(sy * ((float)oy + 0.5f) - 0.5f, 0.f), (float)bh - 1.f);
+                float ix = fminf(fmaxf(sx * ((float)ox + 0.5f) - 0.5f, 0.f), (float)bw - 1.f);
+                int y1 = (int)iy, x1 = (int)ix;
+                int y2 = y1 + 1 < bh - 1 ? y1 + 1 : bh - 1, x2 = x1 + 1 < bw - 1 ? x1 + 1 : bw - 1;
+                float fy = iy - (float)y1, fx = ix - (float)x1;
+                float t0 = mixf(crop_px(rgb, pw, ph, left, top, row_off, spans, x1, y1),
+                                crop_px(rgb, pw, ph, left, top, row_off, spans, x2, y1), fx);
+                float b0 = mixf(crop_px(rgb, pw, ph, left, top, row_off, spans, x1, y2),
+                                crop_px(rgb, pw, ph, left, top, row_off, spans, x2, y2), fx);
+                v = mixf(t0, b0, fy);
+            }
+            dst[(size_t)oy * wb + ox] = v;
+        }
+}

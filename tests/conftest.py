@@ -43,3 +43,15 @@ def ctx():
     c = ocrhip.Context()
     yield c
     c.close()
+
+
+@pytest.fixture(scope="session")
+def recognizer(ctx, rec_model_path):
+    import ocrhip
+    return ocrhip.Recognizer(ctx, rec_model_path)
+
+
+@pytest.fixture(scope="session")
+def detector(ctx, det_model_path):
+    import ocrhip
+    return ocrhip.Detector(ctx, det_model_path)

@@ -23,18 +23,6 @@ def softmax(x):
     return e / e.sum(axis=-1, keepdims=True)
 
 
-@pytest.fixture(scope="module")
-def recognizer(ctx, rec_model_path):
-    import ocrhip
-    return ocrhip.Recognizer(ctx, rec_model_path)
-
-
-@pytest.fixture(scope="module")
-def detector(ctx, det_model_path):
-    import ocrhip
-    return ocrhip.Detector(ctx, det_model_path)
-
-
 def check_recognition(recognizer, rec_oracle, batches, widths):
     print(f"recognize {[(n, w) for _, n, w in batches]}", flush=True)
     logits, lens, best = recognizer.recognize([(d, n, w) for d, n, w in batches])

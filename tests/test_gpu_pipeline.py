@@ -1,0 +1,74 @@
+"""The whole-page pipeline on the GPU (ocr-bench.rs:133-310, 458-585) against the same pipeline
+on the CPU: oracle detection, line images and recognition on the same host layout. Text must be
+identical line by line (the arg-max parity of the recogniser, carried through the GPU line
+crops and the host CTC)."""
+import numpy as np
+import pytest
+
+import ocrhip
+from ocrhip import synth
+from oracle import graph as og
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def pipeline(detector, recognizer):
+    return ocrhip.Pipeline(detector, recognizer, merge=2)
+
+
+def layout_of(bits, w):
+    return ocrhip.Layout(bits, w)
+
+
+def test_pipeline_text_matches_cpu(pipeline, detector, det_oracle, rec_oracle):
+    page = synth.page(3)
+    print("pipeline page 3", flush=True)
+    pipeline.run([page])
+    texts, words = pipeline.texts(0)
+    st = pipeline.stats()
+    assert st["pages"] == 1 and st["lines"] == len(texts) > 20
+    # The page mask must agree with the oracle (band excepted); the CPU pipeline then runs on
+    # the GPU's mask so that both use one layout.
+    bits = detector.detect_page(page, 0.5)
+    want_bits, prob, _ = og.detect_page(det_oracle, page, 0.5)
+    diff = np.unpackbits((bits ^ want_bits).view(np.uint8), bitorder="little").reshape(bits.shape[0], -1)
+    diff = diff[:, : page.shape[1]].astype(bool)
+    assert np.all(np.abs(prob[diff] - 0.5) < 1e-4)
+    cpu_texts, cpu_words, _ = og.page_pipeline(det_oracle, rec_oracle, page, 0.5, lambda b, w: layout_of(bits, w))
+    assert words == cpu_words
+    assert texts == cpu_texts
+    assert sum(len(t) for t in texts) > 0
+
+
+def test_pipeline_merge_and_device_entry(detector, recognizer, ctx):
+    pages = [synth.page(s) for s in (4, 5, 6)]
+    a = ocrhip.Pipeline(detector, recognizer, merge=1, det_batch=1)
+    a.run(pages)
+    b = ocrhip.Pipeline(detector, recognizer, merge=3, det_batch=2)
+    d_pages = []
+    for p in pages:
+        buf = ctx.alloc(p.nbytes)
+        buf.upload(p)
+        d_pages.append(buf)
+    b.run_device(d_pages, [p.shape[1] for p in pages], [p.shape[0] for p in pages])
+    for k in range(3):
+        assert a.texts(k) == b.texts(k)
+    assert a.stats()["lines"] == b.stats()["lines"]
+
+
+def test_pipeline_blank_and_small_pages(detector, recognizer):
+    blank = np.full((3300, 2550, 3), 255, np.uint8)
+    small = np.ascontiguousarray(synth.page(7)[150:400, 100:900])
+    p = ocrhip.Pipeline(detector, recognizer)
+    p.run([blank, small])
+    t0, w0 = p.texts(0)
+    assert t0 == [] and w0 == 0
+    t1, _ = p.texts(1)
+    assert isinstance(t1, list)
+
+
+def test_pipeline_rejects_empty_page(detector, recognizer):
+    p = ocrhip.Pipeline(detector, recognizer)
+    with pytest.raises(ocrhip.OcrError):
+        p.run([np.zeros((0, 10, 3), np.uint8)])

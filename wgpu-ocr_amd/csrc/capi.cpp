@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "models.h"
+#include "pipeline.h"
 
 using namespace ocr;
 
@@ -23,6 +24,13 @@ struct ocr_graph {
 struct ocr_recognizer {
     ocr_ctx *owner;
     std::unique_ptr<Recognizer> rec;
+};
+struct ocr_layout {
+    PageLayout layout;
+};
+struct ocr_pipeline {
+    ocr_ctx *owner;
+    std::unique_ptr<Pipeline> pipe;
 };
 
 namespace {
@@ -313,6 +321,172 @@ int ocr_recognize_device(ocr_recognizer *rec, const ocr_batch *d_batches, uint32
             logits = tmp.as<float>();
         }
         rec->rec->recognize_device(bs.data(), int(bs.size()), logits, d_best, lens);
+    });
+}
+
+int ocr_probe_start(const char *family) {
+    return guard([&] {
+        need(family, "family");
+        Probe::get().start(family);
+    });
+}
+
+int ocr_probe_stop(const char *family, uint32_t *calls, double *ms, double *flops, double *bytes) {
+    return guard([&] {
+        need(family, "family");
+        if (!Probe::get().stop(family, calls, ms, flops, bytes)) fail(std::string("not probing ") + family);
+    });
+}
+
+int ocr_word_rects(const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out, uint32_t cap, uint32_t *count) {
+    return guard([&] {
+        need(bits, "bits");
+        need(count, "count");
+        std::vector<RRect> r = word_rects(bits, int(w), int(h));
+        *count = uint32_t(r.size());
+        for (size_t i = 0; i < r.size() && i < cap; i++) out[i] = {r[i].cx, r[i].cy, r[i].ux, r[i].uy, r[i].w, r[i].h};
+    });
+}
+
+ocr_layout *ocr_layout_page(const uint32_t *bits, uint32_t w, uint32_t h, float relv, float relend) {
+    return guard_ptr<ocr_layout>([&] {
+        need(bits, "bits");
+        auto l = std::make_unique<ocr_layout>();
+        l->layout = layout_page(bits, int(w), int(h), relv, relend);
+        return l.release();
+    });
+}
+
+void ocr_layout_free(ocr_layout *lay) { delete lay; }
+
+int ocr_layout_counts(ocr_layout *lay, uint32_t *words, uint32_t *lines, uint32_t *batches) {
+    return guard([&] {
+        need(lay, "layout");
+        if (words) *words = uint32_t(lay->layout.words);
+        if (lines) *lines = uint32_t(lay->layout.lines.size());
+        if (batches) *batches = uint32_t(lay->layout.plan.lines.size());
+    });
+}
+
+int ocr_layout_line(ocr_layout *lay, uint32_t i, int32_t *box, int32_t *row_off, int32_t *spans, uint32_t *nspans) {
+    return guard([&] {
+        need(lay, "layout");
+        if (i >= lay->layout.lines.size()) fail("line index out of range");
+        const LineGeom &g = lay->layout.lines[i];
+        if (box) {
+            box[0] = g.left, box[1] = g.top, box[2] = g.bw, box[3] = g.bh, box[4] = g.out_w;
+        }
+        if (nspans) *nspans = uint32_t(g.spans.size() / 2);
+        if (row_off) std::copy(g.row_off.begin(), g.row_off.end(), row_off);
+        if (spans) std::copy(g.spans.begin(), g.spans.end(), spans);
+    });
+}
+
+int ocr_layout_batch(ocr_layout *lay, uint32_t i, uint32_t *width, uint32_t *lines, uint32_t *count) {
+    return guard([&] {
+        need(lay, "layout");
+        if (i >= lay->layout.plan.lines.size()) fail("batch index out of range");
+        const auto &m = lay->layout.plan.lines[i];
+        if (width) *width = uint32_t(lay->layout.plan.width[i]);
+        if (count) *count = uint32_t(m.size());
+        if (lines)
+            for (size_t k = 0; k < m.size(); k++) lines[k] = uint32_t(m[k]);
+    });
+}
+
+ocr_pipeline *ocr_pipeline_new(ocr_detector *det, ocr_recognizer *rec, const ocr_pipeline_opts *opts) {
+    return guard_ptr<ocr_pipeline>([&] {
+        need(det, "det");
+        need(rec, "rec");
+        if (det->owner != rec->owner) fail("detector and recogniser belong to different contexts");
+        PipelineOpts o;
+        if (opts) {
+            if (opts->merge) o.merge = int(opts->merge);
+            if (opts->relv != 0.f) o.relv = opts->relv;
+            if (opts->relend != 0.f) o.relend = opts->relend;
+            if (opts->thr != 0.f) o.thr = opts->thr;
+            o.threads = int(opts->threads);
+            if (opts->det_batch) o.det_batch = int(opts->det_batch);
+        }
+        det->owner->ctx->bind();
+        auto p = std::make_unique<ocr_pipeline>();
+        p->owner = det->owner;
+        p->pipe = std::make_unique<Pipeline>(*det->owner->ctx, *det->det, *rec->rec, o);
+        return p.release();
+    });
+}
+
+void ocr_pipeline_free(ocr_pipeline *pipe) { delete pipe; }
+
+int ocr_pipeline_run_device(ocr_pipeline *pipe, const uint8_t *const *d_rgb, const uint32_t *w, const uint32_t *h,
+                            uint32_t npages) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        if (npages) {
+            need(d_rgb, "d_rgb");
+            need(w, "w");
+            need(h, "h");
+        }
+        pipe->owner->ctx->bind();
+        std::vector<int> wi(npages), hi(npages);
+        for (uint32_t k = 0; k < npages; k++) wi[k] = int(w[k]), hi[k] = int(h[k]);
+        pipe->pipe->run(d_rgb, wi.data(), hi.data(), int(npages));
+    });
+}
+
+int ocr_pipeline_run(ocr_pipeline *pipe, const uint8_t *const *rgb, const uint32_t *w, const uint32_t *h,
+                     uint32_t npages) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        Ctx &c = *pipe->owner->ctx;
+        c.bind();
+        std::vector<DBuf> bufs;
+        std::vector<const uint8_t *> ptrs;
+        std::vector<int> wi(npages), hi(npages);
+        for (uint32_t k = 0; k < npages; k++) {
+            need(rgb[k], "page");
+            const size_t bytes = size_t(w[k]) * h[k] * 3;
+            bufs.emplace_back(&c, bytes);
+            c.h2d(bufs.back().get(), rgb[k], bytes);
+            ptrs.push_back(bufs.back().as<uint8_t>());
+            wi[k] = int(w[k]), hi[k] = int(h[k]);
+        }
+        pipe->pipe->run(ptrs.data(), wi.data(), hi.data(), int(npages));
+    });
+}
+
+int ocr_pipeline_stats_get(ocr_pipeline *pipe, ocr_pipeline_stats *out) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        need(out, "out");
+        const PipelineStats &s = pipe->pipe->stats();
+        *out = {s.ms, s.cpu_busy_ms, uint32_t(s.pages), uint32_t(s.lines), uint32_t(s.words), uint32_t(s.batches),
+                uint32_t(s.rec_passes), uint64_t(s.rec_steps)};
+    });
+}
+
+int ocr_pipeline_page(ocr_pipeline *pipe, uint32_t page, uint32_t *lines, uint32_t *words) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        const auto &pages = pipe->pipe->pages();
+        if (page >= pages.size()) fail("page index out of range");
+        if (lines) *lines = uint32_t(pages[page].lines.size());
+        if (words) *words = uint32_t(pages[page].words);
+    });
+}
+
+int ocr_pipeline_line_text(ocr_pipeline *pipe, uint32_t page, uint32_t line, char *buf, uint32_t cap, uint32_t *len) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        const auto &pages = pipe->pipe->pages();
+        if (page >= pages.size() || line >= pages[page].lines.size()) fail("line index out of range");
+        const std::string &s = pages[page].lines[line];
+        if (len) *len = uint32_t(s.size());
+        if (buf && cap) {
+            const size_t n = std::min<size_t>(s.size(), cap - 1);
+            std::copy(s.begin(), s.begin() + long(n), buf);
+            buf[n] = 0;
+        }
     });
 }
 

@@ -1,0 +1,336 @@
+#include "geometry.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <string>
+
+namespace ocr {
+
+// ocr-bench.rs:31: class k > 0 is this string's character k - 1 (96 characters; class 0 blank).
+const char *const OCRS_ALPHABET =
+    " 0123456789!\"#$%&'()*+,-./:;<=>?@[\\]^_`{|}~EABCDEFGHIJKLMNOPQRSTUVWXYZabcdefghijklmnopqrstuvwxyz";
+
+void RRect::corners(float xs[4], float ys[4]) const {
+    const float hx = ux * h / 2, hy = uy * h / 2, wx = rx() * w / 2, wy = ry() * w / 2;
+    xs[0] = cx + hx - wx, ys[0] = cy + hy - wy;  // top-left
+    xs[1] = cx + hx + wx, ys[1] = cy + hy + wy;  // top-right
+    xs[2] = cx - hx + wx, ys[2] = cy - hy + wy;  // bottom-right
+    xs[3] = cx - hx - wx, ys[3] = cy - hy - wy;  // bottom-left
+}
+
+void RRect::bbox(float &l, float &t, float &r, float &b) const {
+    float xs[4], ys[4];
+    corners(xs, ys);
+    l = *std::min_element(xs, xs + 4);
+    r = *std::max_element(xs, xs + 4);
+    t = *std::min_element(ys, ys + 4);
+    b = *std::max_element(ys, ys + 4);
+}
+
+bool RRect::upright() const { return std::fabs(uy) >= std::fabs(ux); }
+
+namespace {
+
+struct Pt {
+    float x, y;
+};
+
+float cross(const Pt &o, const Pt &a, const Pt &b) { return (a.x - o.x) * (b.y - o.y) - (a.y - o.y) * (b.x - o.x); }
+
+// Andrew's monotone chain; returns the hull counter-clockwise without repeating the first point.
+std::vector<Pt> hull(std::vector<Pt> p) {
+    std::sort(p.begin(), p.end(), [](const Pt &a, const Pt &b) { return a.x < b.x || (a.x == b.x && a.y < b.y); });
+    p.erase(std::unique(p.begin(), p.end(), [](const Pt &a, const Pt &b) { return a.x == b.x && a.y == b.y; }),
+            p.end());
+    if (p.size() < 3) return p;
+    std::vector<Pt> h(2 * p.size());
+    size_t k = 0;
+    for (size_t i = 0; i < p.size(); i++) {
+        while (k >= 2 && cross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
+        h[k++] = p[i];
+    }
+    for (size_t i = p.size() - 1, t = k + 1; i-- > 0;) {
+        while (k >= t && cross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
+        h[k++] = p[i];
+    }
+    h.resize(k - 1);
+    return h;
+}
+
+// Minimum-area enclosing rectangle of a convex polygon: the best of the rectangles with a side
+// on one of its edges (rotating calipers). The up axis is the rectangle axis pointing most
+// towards -y, so near-horizontal boxes come out upright.
+RRect min_area_rect(const std::vector<Pt> &h) {
+    RRect best;
+    if (h.empty()) return best;
+    if (h.size() == 1) {
+        best.cx = h[0].x, best.cy = h[0].y, best.w = best.h = 0;
+        return best;
+    }
+    float best_area = INFINITY;
+    for (size_t i = 0; i < h.size(); i++) {
+        const Pt &a = h[i], &b = h[(i + 1) % h.size()];
+        float ex = b.x - a.x, ey = b.y - a.y, len = std::sqrt(ex * ex + ey * ey);
+        if (len == 0) continue;
+        ex /= len, ey /= len;
+        const float nx = -ey, ny = ex;
+        float e0 = INFINITY, e1 = -INFINITY, n0 = INFINITY, n1 = -INFINITY;
+        for (const Pt &p : h) {
+            const float pe = p.x * ex + p.y * ey, pn = p.x * nx + p.y * ny;
+            e0 = std::min(e0, pe), e1 = std::max(e1, pe), n0 = std::min(n0, pn), n1 = std::max(n1, pn);
+        }
+        const float area = (e1 - e0) * (n1 - n0);
+        if (area < best_area) {
+            best_area = area;
+            const float me = (e0 + e1) / 2, mn = (n0 + n1) / 2;
+            RRect r;
+            r.cx = ex * me + nx * mn, r.cy = ey * me + ny * mn;
+            // Candidate up axes: +-e (height = e extent) and +-n (height = n extent).
+            const float cand[4][3] = {{ex, ey, e1 - e0}, {-ex, -ey, e1 - e0}, {nx, ny, n1 - n0}, {-nx, -ny, n1 - n0}};
+            int k = 0;
+            for (int c = 1; c < 4; c++)
+                if (cand[c][1] < cand[k][1] - 1e-6f) k = c;
+            r.ux = cand[k][0], r.uy = cand[k][1], r.h = cand[k][2];
+            r.w = (k < 2) ? (n1 - n0) : (e1 - e0);
+            best = r;
+        }
+    }
+    return best;
+}
+
+struct Run {
+    int y, x0, x1;  // inclusive pixel range in row y
+};
+
+int find(std::vector<int> &parent, int a) {
+    while (parent[a] != a) a = parent[a] = parent[parent[a]];
+    return a;
+}
+
+}  // namespace
+
+std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area) {
+    const int words = (w + 31) / 32;
+    std::vector<Run> runs;
+    std::vector<int> row_start(size_t(h) + 1, 0);
+    for (int y = 0; y < h; y++) {
+        row_start[y] = int(runs.size());
+        const uint32_t *row = bits + size_t(y) * words;
+        int x = 0;
+        while (x < w) {
+            // next set bit at or after x
+            int wi = x >> 5;
+            uint32_t word = row[wi] & (~0u << (x & 31));
+            while (!word && ++wi < words) word = row[wi];
+            if (!word) break;
+            const int start = (wi << 5) + __builtin_ctz(word);
+            if (start >= w) break;
+            // next clear bit at or after start
+            int wj = start >> 5;
+            uint32_t inv = ~row[wj] & (~0u << (start & 31));
+            while (!inv && ++wj < words) inv = ~row[wj];
+            int end = inv ? (wj << 5) + __builtin_ctz(inv) : words * 32;
+            end = std::min(end, w);
+            runs.push_back({y, start, end - 1});
+            x = end;
+        }
+    }
+    row_start[h] = int(runs.size());
+    // Union the runs of neighbouring rows that touch with 8-connectivity.
+    std::vector<int> parent(runs.size());
+    std::iota(parent.begin(), parent.end(), 0);
+    for (int y = 1; y < h; y++) {
+        int i = row_start[y - 1], j = row_start[y];
+        const int ie = row_start[y], je = row_start[y + 1];
+        while (i < ie && j < je) {
+            const Run &a = runs[size_t(i)], &b = runs[size_t(j)];
+            if (a.x1 + 1 >= b.x0 && b.x1 + 1 >= a.x0) {
+                int ra = find(parent, i), rb = find(parent, j);
+                if (ra != rb) parent[size_t(std::max(ra, rb))] = std::min(ra, rb);
+            }
+            if (a.x1 < b.x1) i++;
+            else j++;
+        }
+    }
+    // Hull points of each component: both ends of each run (pixel coordinates).
+    std::vector<int> comp(runs.size(), -1);
+    std::vector<std::vector<Pt>> pts;
+    for (size_t r = 0; r < runs.size(); r++) {
+        const int root = find(parent, int(r));
+        if (comp[size_t(root)] < 0) {
+            comp[size_t(root)] = int(pts.size());
+            pts.emplace_back();
+        }
+        auto &v = pts[size_t(comp[size_t(root)])];
+        v.push_back({float(runs[r].x0), float(runs[r].y)});
+        if (runs[r].x1 != runs[r].x0) v.push_back({float(runs[r].x1), float(runs[r].y)});
+    }
+    std::vector<RRect> out;
+    for (auto &v : pts) {
+        RRect r = min_area_rect(hull(std::move(v)));
+        r.resize(r.w + 2 * expand, r.h + 2 * expand);
+        if (r.area() >= min_area) out.push_back(r);
+    }
+    return out;
+}
+
+std::vector<std::vector<RRect>> find_text_lines(const std::vector<RRect> &words) {
+    struct Box {
+        float l, t, r, b;
+        int i;
+    };
+    std::vector<Box> boxes;
+    for (size_t i = 0; i < words.size(); i++) {
+        Box b;
+        words[i].bbox(b.l, b.t, b.r, b.b);
+        b.i = int(i);
+        boxes.push_back(b);
+    }
+    std::stable_sort(boxes.begin(), boxes.end(), [](const Box &a, const Box &b) { return a.l < b.l; });
+    // A word joins the line whose last word ends nearest before it, when the two overlap
+    // vertically by at least half the smaller height and the gap is at most twice the taller.
+    std::vector<std::vector<int>> lines;
+    std::vector<Box> last;
+    for (const Box &b : boxes) {
+        int best = -1;
+        float best_gap = INFINITY;
+        const float hb = b.b - b.t;
+        for (size_t k = 0; k < lines.size(); k++) {
+            const Box &a = last[k];
+            const float ha = a.b - a.t;
+            const float overlap = std::min(a.b, b.b) - std::max(a.t, b.t);
+            const float gap = b.l - a.r;
+            if (overlap < 0.5f * std::min(ha, hb) || gap > 2.f * std::max(ha, hb) || gap < -0.5f * std::min(ha, hb))
+                continue;
+            if (gap < best_gap) best_gap = gap, best = int(k);
+        }
+        if (best < 0) {
+            lines.push_back({b.i});
+            last.push_back(b);
+        } else {
+            lines[size_t(best)].push_back(b.i);
+            last[size_t(best)] = b;
+        }
+    }
+    // Reading order: lines by the top of their first word, then left.
+    std::vector<size_t> order(lines.size());
+    std::iota(order.begin(), order.end(), 0);
+    auto top_left = [&](size_t k) {
+        float l, t, r, b;
+        words[size_t(lines[k][0])].bbox(l, t, r, b);
+        return std::make_pair(t, l);
+    };
+    std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return top_left(a) < top_left(b); });
+    std::vector<std::vector<RRect>> out;
+    for (size_t k : order) {
+        std::vector<RRect> line;
+        for (int i : lines[k]) line.push_back(words[size_t(i)]);
+        out.push_back(std::move(line));
+    }
+    return out;
+}
+
+void pad_lines(std::vector<std::vector<RRect>> &lines, float relv, float relend) {
+    if (relv <= 0 && relend <= 0) return;
+    for (auto &line : lines) {
+        std::vector<float> hs;
+        for (const RRect &r : line) hs.push_back(r.upright() ? r.h : r.w);
+        std::sort(hs.begin(), hs.end());
+        const float h = hs.empty() ? 0.f : hs[hs.size() / 2];
+        const size_t n = line.size();
+        for (size_t i = 0; i < n; i++) {
+            RRect &r = line[i];
+            const float along = (i == 0 || i + 1 == n) ? relend * h : 0.f, across = relv * h;
+            if (r.upright()) r.resize(r.w + 2 * along, r.h + 2 * across);
+            else r.resize(r.w + 2 * across, r.h + 2 * along);
+        }
+    }
+}
+
+LineGeom line_geometry(const std::vector<RRect> &words) {
+    // Polygon: top edges left to right, then bottom edges right to left, floored.
+    std::vector<Pt> poly;
+    for (const RRect &r : words) {
+        float xs[4], ys[4];
+        r.corners(xs, ys);
+        poly.push_back({std::floor(xs[0]), std::floor(ys[0])});
+        poly.push_back({std::floor(xs[1]), std::floor(ys[1])});
+    }
+    for (size_t i = words.size(); i-- > 0;) {
+        float xs[4], ys[4];
+        words[i].corners(xs, ys);
+        poly.push_back({std::floor(xs[2]), std::floor(ys[2])});
+        poly.push_back({std::floor(xs[3]), std::floor(ys[3])});
+    }
+    LineGeom g;
+    if (poly.empty()) return g;
+    float l = INFINITY, t = INFINITY, r = -INFINITY, b = -INFINITY;
+    for (const Pt &p : poly) l = std::min(l, p.x), r = std::max(r, p.x), t = std::min(t, p.y), b = std::max(b, p.y);
+    g.left = int(l), g.top = int(t);
+    g.bw = std::max(1, int(r - l)), g.bh = std::max(1, int(b - t));
+    const float aspect = float(g.bw) / float(g.bh);
+    g.out_w = int(std::min(std::max(float(LINE_H) * aspect, float(LINE_MIN_W)), float(LINE_MAX_W)));
+    // Row spans: crossings of the line y + 0.5 with the polygon's edges (even-odd rule).
+    g.row_off.assign(size_t(g.bh) + 1, 0);
+    std::vector<float> xs;
+    for (int cy = 0; cy < g.bh; cy++) {
+        g.row_off[size_t(cy)] = int(g.spans.size());
+        const float Y = float(g.top + cy) + 0.5f;
+        xs.clear();
+        for (size_t i = 0; i < poly.size(); i++) {
+            const Pt &a = poly[i], &c = poly[(i + 1) % poly.size()];
+            if ((a.y <= Y && c.y > Y) || (c.y <= Y && a.y > Y))
+                xs.push_back(a.x + (Y - a.y) * (c.x - a.x) / (c.y - a.y));
+        }
+        std::sort(xs.begin(), xs.end());
+        for (size_t k = 0; k + 1 < xs.size(); k += 2) {
+            // pixels whose centre x + 0.5 lies in [xs[k], xs[k+1])
+            const int x0 = std::max(0, int(std::ceil(xs[k] - 0.5f)) - g.left);
+            const int x1 = std::min(g.bw, int(std::ceil(xs[k + 1] - 0.5f)) - g.left);
+            if (x1 > x0) {
+                g.spans.push_back(x0);
+                g.spans.push_back(x1);
+            }
+        }
+    }
+    g.row_off[size_t(g.bh)] = int(g.spans.size());
+    return g;
+}
+
+BatchPlan plan_batches(const std::vector<int> &out_w, int round_to, int per_batch) {
+    std::vector<std::pair<int, int>> keyed;  // (rounded width, line)
+    for (size_t i = 0; i < out_w.size(); i++)
+        keyed.push_back({(out_w[i] + round_to - 1) / round_to * round_to, int(i)});
+    std::stable_sort(keyed.begin(), keyed.end(),
+                     [](const std::pair<int, int> &a, const std::pair<int, int> &b) { return a.first < b.first; });
+    BatchPlan plan;
+    size_t i = 0;
+    while (i < keyed.size()) {
+        size_t j = i;
+        while (j < keyed.size() && keyed[j].first == keyed[i].first) j++;
+        for (size_t c = i; c < j; c += size_t(per_batch)) {
+            std::vector<int> members;
+            for (size_t k = c; k < std::min(j, c + size_t(per_batch)); k++) members.push_back(keyed[k].second);
+            plan.lines.push_back(std::move(members));
+            plan.width.push_back(keyed[i].first);
+        }
+        i = j;
+    }
+    return plan;
+}
+
+std::string ctc_decode(const uint32_t *best, int steps, int stride, int width) {
+    std::string s;
+    uint32_t prev = 0;
+    const int nalpha = int(std::strlen(OCRS_ALPHABET));
+    for (int t = 0; t < steps; t++) {
+        const uint32_t b = best[size_t(t) * stride];
+        if (b != 0 && b != prev && t * 4 < width && int(b) <= nalpha) s.push_back(OCRS_ALPHABET[b - 1]);
+        prev = b;
+    }
+    return s;
+}
+
+}  // namespace ocr

@@ -1,0 +1,64 @@
+// Host geometry of the page pipeline: words from the detection mask, text lines, line padding
+// and the line-image layout. The reference takes these from ocrs 0.13.1 and rten-imageproc
+// 0.26.0 (src/bin/ocr-bench.rs:40-60, 516, 534-558, 366-408), which are not available here;
+// this is the library's own restatement of the same steps (see each function).
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+namespace ocr {
+
+// A rotated rectangle: centre, unit "up" axis (image coordinates, y down), width across the up
+// axis and height along it (rten-imageproc's RotatedRect).
+struct RRect {
+    float cx = 0, cy = 0, ux = 0, uy = -1, w = 0, h = 0;
+    float rx() const { return -uy; }  // the width axis: up rotated a quarter turn clockwise
+    float ry() const { return ux; }
+    void corners(float xs[4], float ys[4]) const;  // top-left, top-right, bottom-right, bottom-left
+    void bbox(float &l, float &t, float &r, float &b) const;
+    float area() const { return w * h; }
+    bool upright() const;  // up axis closer to vertical (ocr-bench.rs:544)
+    void resize(float nw, float nh) { w = nw; h = nh; }
+};
+
+// word_rects (ocr-bench.rs:40-60): 8-connected components of the mask (h rows of ceil(w/32)
+// words), each component's minimum-area rectangle over its pixels, grown by `expand` on every
+// side, kept when its area is at least min_area.
+std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand = 3.f, float min_area = 100.f);
+
+// Text lines from words, left to right within a line, lines top to bottom (the role of ocrs'
+// find_text_lines, ocr-bench.rs:516).
+std::vector<std::vector<RRect>> find_text_lines(const std::vector<RRect> &words);
+
+// Line padding (ocr-bench.rs:534-558): every word grows by relv * h across the line, the first
+// and last by relend * h along it, h the line's median word height.
+void pad_lines(std::vector<std::vector<RRect>> &lines, float relv, float relend);
+
+// The image of one text line: the polygon of its words' top edges (left to right) and bottom
+// edges (right to left), floored to pixels; its bounding box [left, left + bw) x [top, top + bh)
+// on the page; the pixels inside it as spans per row (even-odd rule at pixel centres); and the
+// width the 64-high line image is resized to (aspect ratio kept, clamped to [10, 800]).
+struct LineGeom {
+    int left = 0, top = 0, bw = 0, bh = 0, out_w = 0;
+    std::vector<int32_t> row_off;  // bh + 1 offsets into spans
+    std::vector<int32_t> spans;    // pairs [x0, x1) of crop columns
+};
+LineGeom line_geometry(const std::vector<RRect> &words);
+
+constexpr int LINE_H = 64, LINE_MIN_W = 10, LINE_MAX_W = 800;
+
+// ocrs batching (ocr-bench.rs:385-407): lines grouped by their width rounded up to 50, in order
+// of that width, at most 20 a batch. Returns for every batch its line indices and width.
+struct BatchPlan {
+    std::vector<std::vector<int>> lines;
+    std::vector<int> width;
+};
+BatchPlan plan_batches(const std::vector<int> &out_w, int round_to = 50, int per_batch = 20);
+
+// Greedy CTC over per-step arg-max classes (ocr-bench.rs:62-74): emit when best != 0,
+// best != prev and t * 4 < width. Classes index the 96-character ocrs alphabet (class 0 blank).
+std::string ctc_decode(const uint32_t *best, int steps, int stride, int width);
+extern const char *const OCRS_ALPHABET;
+
+}  // namespace ocr

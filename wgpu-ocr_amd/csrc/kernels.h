@@ -69,7 +69,8 @@ void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStrea
 // ---- GRU recurrence (kernels/gru.hip) -------------------------------------------------------
 // One layer, both directions, every line with its own length (gpu.rs:680-819). G [t][n][1536]
 // holds W x + Wb; R [2][768][256] float16 (exact values); Rb [2][768]; Y [t][n][512].
+// steps: the sum of lens (for the probe's work count only).
 void gru_recurrence(const float *G, const uint16_t *R, const float *Rb, float *Y, const uint32_t *lens, int ntot,
-                    int tmax, hipStream_t s);
+                    int tmax, long long steps, hipStream_t s);
 
 }  // namespace ocr

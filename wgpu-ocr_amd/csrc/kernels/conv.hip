@@ -21,6 +21,7 @@
 #include <cmath>
 
 #include "../kernels.h"
+#include "../runtime.h"
 
 namespace ocr {
 
@@ -266,6 +267,10 @@ void conv_mfma(const ConvArgs &a, hipStream_t s) {
     const size_t blocks = size_t(p.tiles_x) * p.tiles_y * p.n;
     if (blocks > 0x7fffffff) fail("conv_mfma: grid too large");
     dim3 grid(unsigned(blocks), unsigned(pk.nblocks));
+    const double flops = 2.0 * p.n * p.oh * p.ow * p.cout * p.cin * pk.kh * pk.kw;
+    const double bytes = 4.0 * (double(p.n) * p.h * p.w * p.cin + double(p.n) * p.oh * p.ow * p.cout) +
+                         2.0 * double(pk.halves()) * (lo ? 2 : 1);
+    ProbeScope probe("conv_mfma", s, flops, bytes);
     if (ks == 1) launch2<128, 1>(p, pk.bn, lo, grid, s);
     else if (tw == 16) launch2<16, 3>(p, pk.bn, lo, grid, s);
     else if (tw == 32) launch2<32, 3>(p, pk.bn, lo, grid, s);

@@ -19,6 +19,7 @@
 #include <cmath>
 
 #include "../kernels.h"
+#include "../runtime.h"
 
 namespace ocr {
 
@@ -133,10 +134,13 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
 }  // namespace
 
 void gru_recurrence(const float *G, const uint16_t *R, const float *Rb, float *Y, const uint32_t *lens, int ntot,
-                    int tmax, hipStream_t s) {
+                    int tmax, long long steps, hipStream_t s) {
     (void)tmax;
     if (ntot <= 0) return;
     dim3 grid(unsigned((ntot + LINES - 1) / LINES), 2);
+    // Per line step and direction: R h (768 x 256), G read (768 floats), Y written (256 floats).
+    ProbeScope probe("gru", s, 2.0 * 2.0 * double(steps) * 768 * 256,
+                     2.0 * double(steps) * (768 + 256) * 4 + 2.0 * 768 * 256 * 2);
     hipLaunchKernelGGL((gru_kernel<32>), grid, dim3(H / 32 * 64), 0, s, G, reinterpret_cast<const half8 *>(R), Rb, Y,
                        lens, ntot);
     OCR_HIP(hipGetLastError());

@@ -5,6 +5,7 @@
 #include <cmath>
 
 #include "../kernels.h"
+#include "../runtime.h"
 
 namespace ocr {
 
@@ -230,6 +231,8 @@ __global__ void argmax_kernel(const float *x, int rows, int classes, uint32_t *b
 void conv_generic(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int sh, int sw, int pt,
                   int pl, int group, int act, hipStream_t s) {
     size_t total = y.count();
+    ProbeScope probe("conv_generic", s, 2.0 * double(total) * (x.c / group) * kh * kw,
+                     4.0 * double(x.count() + y.count()));
     hipLaunchKernelGGL(conv_generic_kernel, dim3(blocks_for(total)), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.c, x.cs,
                        y.p, y.h, y.w, y.c, y.cs, w, b, kh, kw, sh, sw, pt, pl, group, act);
     OCR_HIP(hipGetLastError());
@@ -237,6 +240,8 @@ void conv_generic(const Act &x, const Act &y, const float *w, const float *b, in
 
 void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int pad, int act, int ph,
                  int pw, hipStream_t s) {
+    ProbeScope probe("conv_direct", s, 2.0 * double(y.pixels()) * ph * pw * y.c * kh * kw,
+                     4.0 * double(x.count() + y.count()));
     hipLaunchKernelGGL(conv_direct_kernel, dim3(blocks_for(y.pixels())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.cs,
                        y.p, y.h, y.w, y.c, y.cs, w, b, kh, kw, pad, act, ph, pw);
     OCR_HIP(hipGetLastError());
@@ -244,18 +249,22 @@ void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int
 
 void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride, int act,
                     hipStream_t s) {
+    ProbeScope probe("conv_transpose", s, 2.0 * double(x.pixels()) * x.c * y.c * kh * kw,
+                     4.0 * double(x.count() + y.count()));
     hipLaunchKernelGGL(convt_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.c, x.cs, y.p,
                        y.h, y.w, y.c, y.cs, w, b, kh, kw, stride, act);
     OCR_HIP(hipGetLastError());
 }
 
 void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s) {
+    ProbeScope probe("maxpool", s, double(x.count()), 4.0 * double(x.count() + y.count()));
     hipLaunchKernelGGL(maxpool_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.c, x.cs,
                        y.p, y.h, y.w, y.cs, kh, kw);
     OCR_HIP(hipGetLastError());
 }
 
 void copy_act(const Act &x, const Act &y, int y0, int x0, hipStream_t s) {
+    ProbeScope probe("copy", s, 0, 8.0 * double(y.count()));
     hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.h, x.w, x.cs, y.p, y.n, y.h,
                        y.w, y.c, y.cs, y0, x0);
     OCR_HIP(hipGetLastError());
@@ -275,6 +284,7 @@ void fill(float *p, size_t count, float v, hipStream_t s) {
 
 void grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh, float sx, float sy,
                  hipStream_t s) {
+    ProbeScope probe("grey_resize", s, 0, 16.0 * double(ow) * oh);
     hipLaunchKernelGGL(grey_resize_kernel, dim3(blocks_for(size_t(ow) * oh)), dim3(256), 0, s, rgb, w, h, pw, ph, y,
                        ow, oh, sx, sy);
     OCR_HIP(hipGetLastError());
@@ -283,6 +293,7 @@ void grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int
 void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, float sx, float sy, float thr,
              hipStream_t s) {
     int words = (w + 31) / 32;
+    ProbeScope probe("mask_up", s, 0, 4.0 * double(mw) * mh + 4.0 * double(words) * h);
     hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t(words) * h)), dim3(256), 0, s, m, stride, mw, mh, bits,
                        w, h, words, sx, sy, thr);
     OCR_HIP(hipGetLastError());
@@ -290,6 +301,7 @@ void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, 
 
 void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s) {
     if (kh < 1 || kh > x.h) fail("avgpool_t: pool height");
+    ProbeScope probe("avgpool_t", s, 0, 4.0 * double(x.n) * x.w * x.c * (kh + 1));
     hipLaunchKernelGGL(avgpool_t_kernel, dim3(blocks_for(size_t(x.n) * x.w * x.c)), dim3(256), 0, s, x.p, x.n, x.h,
                        kh, x.w, x.c, x.cs, X, ntot, noff);
     OCR_HIP(hipGetLastError());
@@ -297,6 +309,7 @@ void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s
 
 void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s) {
     if (rows <= 0) return;
+    ProbeScope probe("argmax", s, 0, 4.0 * double(rows) * (classes + 1));
     hipLaunchKernelGGL(argmax_kernel, dim3(blocks_for(size_t(rows), 4)), dim3(256), 0, s, x, rows, classes, best);
     OCR_HIP(hipGetLastError());
 }

@@ -188,6 +188,8 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         noff += t.n;
     }
     trunks.clear();
+    long long steps = 0;
+    for (int i = 0; i < ntot; i++) steps += lens[i];
     DBuf lensd(&ctx_, size_t(ntot) * sizeof(uint32_t));
     ctx_.h2d(lensd.get(), lens, size_t(ntot) * sizeof(uint32_t));
     DBuf G(&ctx_, size_t(M) * 1536 * sizeof(float));
@@ -206,7 +208,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         ca.pk = L.pk;
         conv_mfma(ca, st);
         fill(Y[l].as<float>(), size_t(M) * 512, 0.f, st);
-        gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd.as<uint32_t>(), ntot, tmax, st);
+        gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd.as<uint32_t>(), ntot, tmax, steps, st);
         in = Y[l].as<float>();
         in_c = 512;
     }

@@ -1,0 +1,337 @@
+#include "pipeline.h"
+
+#include <algorithm>
+#include <chrono>
+#include <condition_variable>
+#include <deque>
+#include <functional>
+#include <mutex>
+#include <thread>
+
+#include "crop.h"
+
+namespace ocr {
+
+PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend) {
+    PageLayout L;
+    std::vector<RRect> words = word_rects(bits, w, h);
+    L.words = int(words.size());
+    auto lines = find_text_lines(words);
+    pad_lines(lines, relv, relend);
+    std::vector<int> out_w;
+    for (const auto &line : lines) {
+        if (line.empty()) continue;
+        L.lines.push_back(line_geometry(line));
+        out_w.push_back(L.lines.back().out_w);
+    }
+    L.plan = plan_batches(out_w);
+    return L;
+}
+
+namespace {
+
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point t) { return std::chrono::duration<double, std::milli>(Clock::now() - t).count(); }
+
+// A fixed pool of host worker threads with a FIFO of tasks.
+class Workers {
+  public:
+    explicit Workers(int n) {
+        for (int i = 0; i < n; i++) threads_.emplace_back([this] { loop(); });
+    }
+    ~Workers() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto &t : threads_) t.join();
+    }
+    void submit(std::function<void()> f) {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            q_.push_back(std::move(f));
+        }
+        cv_.notify_one();
+    }
+
+  private:
+    void loop() {
+        for (;;) {
+            std::function<void()> f;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [this] { return stop_ || !q_.empty(); });
+                if (q_.empty()) return;
+                f = std::move(q_.front());
+                q_.pop_front();
+            }
+            f();
+        }
+    }
+    std::vector<std::thread> threads_;
+    std::deque<std::function<void()>> q_;
+    std::mutex mu_;
+    std::condition_variable cv_;
+    bool stop_ = false;
+};
+
+// Page-locked host memory, reused across runs.
+struct Pinned {
+    void *p = nullptr;
+    size_t bytes = 0;
+    Pinned() = default;
+    Pinned(const Pinned &) = delete;
+    Pinned &operator=(const Pinned &) = delete;
+    Pinned(Pinned &&o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr, o.bytes = 0; }
+    Pinned &operator=(Pinned &&o) noexcept {
+        std::swap(p, o.p);
+        std::swap(bytes, o.bytes);
+        return *this;
+    }
+    void ensure(size_t n) {
+        if (n <= bytes) return;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        OCR_HIP(hipHostMalloc(&p, n, hipHostMallocDefault));
+        bytes = n;
+    }
+    ~Pinned() {
+        if (p) (void)hipHostFree(p);
+    }
+};
+
+}  // namespace
+
+struct Pipeline::Impl {
+    Ctx &ctx;
+    Detector &det;
+    Recognizer &rec;
+    PipelineOpts opts;
+    Workers workers;
+    std::vector<Pinned> bits_host, best_host;
+    explicit Impl(Ctx &c, Detector &d, Recognizer &r, const PipelineOpts &o, int nthreads)
+        : ctx(c), det(d), rec(r), opts(o), workers(nthreads) {}
+};
+
+static int worker_count(int requested) {
+    if (requested > 0) return requested;
+    int hc = int(std::thread::hardware_concurrency());
+    return std::max(1, std::min(hc > 0 ? hc : 4, 16));
+}
+
+Pipeline::Pipeline(Ctx &ctx, Detector &det, Recognizer &rec, const PipelineOpts &opts)
+    : impl_(new Impl(ctx, det, rec, opts, worker_count(opts.threads))) {
+    if (opts.merge < 1 || opts.det_batch < 1) fail("pipeline: merge and det_batch must be at least 1");
+}
+
+Pipeline::~Pipeline() { delete impl_; }
+
+void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages) {
+    Impl &I = *impl_;
+    Ctx &ctx = I.ctx;
+    const hipStream_t st = ctx.stream();
+    const auto t0 = Clock::now();
+    pages_.assign(size_t(std::max(npages, 0)), PageText{});
+    stats_ = PipelineStats{};
+    stats_.pages = npages;
+    if (npages <= 0) return;
+    for (int p = 0; p < npages; p++)
+        if (w[p] <= 0 || h[p] <= 0) fail("pipeline: empty page " + std::to_string(p));
+
+    std::mutex mu;
+    std::condition_variable cv;
+    std::vector<int> layout_ready(size_t(npages), 0);
+    std::vector<PageLayout> layouts(static_cast<size_t>(npages));
+    std::string error;
+    double cpu_busy = 0;
+    int pending_tasks = 0;
+    auto task_done = [&](double busy, const std::string &err) {
+        std::lock_guard<std::mutex> lk(mu);
+        cpu_busy += busy;
+        if (!err.empty() && error.empty()) error = err;
+        pending_tasks--;
+        cv.notify_all();
+    };
+
+    // 1. Detection of every page, det_batch pages a pass; the bit masks come back asynchronously.
+    const int ngroups = (npages + I.opts.det_batch - 1) / I.opts.det_batch;
+    std::vector<hipEvent_t> det_ev(size_t(ngroups), nullptr);
+    const int nrec = (npages + I.opts.merge - 1) / I.opts.merge;
+    std::vector<hipEvent_t> rec_ev(size_t(nrec), nullptr);
+    struct RecPass {
+        std::vector<std::pair<int, int>> rows;  // (page, line in page) of every recogniser line
+        std::vector<uint32_t> lens;
+        std::vector<int> widths;
+        int tmax = 0, ntot = 0;
+        std::vector<CropLine> crops;
+        std::vector<int32_t> row_off, spans;
+    };
+    std::vector<RecPass> passes(static_cast<size_t>(nrec));
+    // Worker tasks refer to the locals above: whatever happens, wait for them before returning.
+    try {
+    if (I.bits_host.size() < size_t(npages)) I.bits_host.resize(size_t(npages));
+    std::vector<size_t> words_of(static_cast<size_t>(npages));
+    for (int p = 0; p < npages; p++) {
+        words_of[size_t(p)] = size_t((w[p] + 31) / 32) * h[p];
+        I.bits_host[size_t(p)].ensure(words_of[size_t(p)] * 4);
+    }
+    for (int g = 0; g < ngroups; g++) {
+        const int p0 = g * I.opts.det_batch, p1 = std::min(npages, p0 + I.opts.det_batch);
+        std::vector<DBuf> bits;
+        std::vector<uint32_t *> bp;
+        for (int p = p0; p < p1; p++) {
+            bits.emplace_back(&ctx, words_of[size_t(p)] * 4);
+            bp.push_back(bits.back().as<uint32_t>());
+        }
+        I.det.detect_pages_device(d_rgb + p0, w + p0, h + p0, p1 - p0, I.opts.thr, bp.data());
+        for (int p = p0; p < p1; p++)
+            OCR_HIP(hipMemcpyAsync(I.bits_host[size_t(p)].p, bp[size_t(p - p0)], words_of[size_t(p)] * 4,
+                                   hipMemcpyDeviceToHost, st));
+        OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(det_ev[size_t(g)], st));
+    }
+    // 2. Host layout of each page as soon as its mask is on the host.
+    const int dev = ctx.device();
+    for (int p = 0; p < npages; p++) {
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            pending_tasks++;
+        }
+        hipEvent_t ev = det_ev[size_t(p / I.opts.det_batch)];
+        const uint32_t *bits = static_cast<const uint32_t *>(I.bits_host[size_t(p)].p);
+        const int pw = w[p], ph = h[p];
+        I.workers.submit([&, p, ev, bits, pw, ph, dev] {
+            std::string err;
+            double busy = 0;
+            try {
+                (void)hipSetDevice(dev);
+                OCR_HIP(hipEventSynchronize(ev));
+                const auto tc = Clock::now();
+                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend);
+                busy = ms_since(tc);
+                std::lock_guard<std::mutex> lk(mu);
+                layouts[size_t(p)] = std::move(L);
+                layout_ready[size_t(p)] = 1;
+            } catch (const std::exception &e) {
+                err = e.what();
+                std::lock_guard<std::mutex> lk(mu);
+                layout_ready[size_t(p)] = -1;
+            }
+            task_done(busy, err);
+        });
+    }
+    // 3. Recognition, `merge` pages a pass, in page order.
+    if (I.best_host.size() < size_t(nrec)) I.best_host.resize(size_t(nrec));
+    for (int r = 0; r < nrec; r++) {
+        const int p0 = r * I.opts.merge, p1 = std::min(npages, p0 + I.opts.merge);
+        {
+            std::unique_lock<std::mutex> lk(mu);
+            cv.wait(lk, [&] {
+                for (int p = p0; p < p1; p++)
+                    if (!layout_ready[size_t(p)]) return false;
+                return true;
+            });
+            if (!error.empty()) break;
+        }
+        RecPass &R = passes[size_t(r)];
+        std::vector<Recognizer::Batch> batches;
+        std::vector<DBuf> batch_bufs;
+        int max_wb = 0;
+        for (int p = p0; p < p1; p++) {
+            const PageLayout &L = layouts[size_t(p)];
+            pages_[size_t(p)].words = L.words;
+            pages_[size_t(p)].lines.assign(L.lines.size(), std::string());
+            for (size_t b = 0; b < L.plan.lines.size(); b++) {
+                const int wb = L.plan.width[b], n = int(L.plan.lines[b].size());
+                batch_bufs.emplace_back(&ctx, size_t(n) * LINE_H * wb * sizeof(float));
+                float *base = batch_bufs.back().as<float>();
+                batches.push_back({base, n, wb});
+                max_wb = std::max(max_wb, wb);
+                for (int k = 0; k < n; k++) {
+                    const int li = L.plan.lines[b][size_t(k)];
+                    const LineGeom &g = L.lines[size_t(li)];
+                    CropLine c{d_rgb[p], w[p], h[p], g.left, g.top, g.bw, g.bh, g.out_w,
+                               int(R.row_off.size()), base + size_t(k) * LINE_H * wb, wb};
+                    const int sbase = int(R.spans.size());
+                    for (int32_t o : g.row_off) R.row_off.push_back(o + sbase);
+                    R.spans.insert(R.spans.end(), g.spans.begin(), g.spans.end());
+                    R.crops.push_back(c);
+                    R.rows.push_back({p, li});
+                    R.widths.push_back(g.out_w);
+                }
+            }
+        }
+        stats_.batches += int(batches.size());
+        if (batches.empty()) continue;
+        DBuf dcrops(&ctx, R.crops.size() * sizeof(CropLine)), droff(&ctx, R.row_off.size() * 4),
+            dspans(&ctx, std::max<size_t>(R.spans.size(), 1) * 4);
+        ctx.h2d(dcrops.get(), R.crops.data(), R.crops.size() * sizeof(CropLine));
+        ctx.h2d(droff.get(), R.row_off.data(), R.row_off.size() * 4);
+        if (!R.spans.empty()) ctx.h2d(dspans.get(), R.spans.data(), R.spans.size() * 4);
+        line_crop(dcrops.as<CropLine>(), int(R.crops.size()), droff.as<int>(), dspans.as<int>(), max_wb, st);
+        const Recognizer::Dims d = I.rec.dims(batches.data(), int(batches.size()));
+        R.tmax = d.tmax;
+        R.ntot = d.ntot;
+        R.lens.assign(size_t(d.ntot), 0);
+        DBuf logits(&ctx, size_t(d.tmax) * d.ntot * d.classes * sizeof(float));
+        DBuf best(&ctx, size_t(d.tmax) * d.ntot * sizeof(uint32_t));
+        I.rec.recognize_device(batches.data(), int(batches.size()), logits.as<float>(), best.as<uint32_t>(),
+                               R.lens.data());
+        I.best_host[size_t(r)].ensure(size_t(d.tmax) * d.ntot * sizeof(uint32_t));
+        OCR_HIP(hipMemcpyAsync(I.best_host[size_t(r)].p, best.get(), size_t(d.tmax) * d.ntot * sizeof(uint32_t),
+                               hipMemcpyDeviceToHost, st));
+        OCR_HIP(hipEventCreateWithFlags(&rec_ev[size_t(r)], hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(rec_ev[size_t(r)], st));
+        stats_.rec_passes++;
+        // 4. Greedy CTC on the host once the arg-max is back.
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            pending_tasks++;
+        }
+        hipEvent_t ev = rec_ev[size_t(r)];
+        const uint32_t *bh = static_cast<const uint32_t *>(I.best_host[size_t(r)].p);
+        I.workers.submit([&, ev, bh, r, dev] {
+            std::string err;
+            double busy = 0;
+            try {
+                (void)hipSetDevice(dev);
+                OCR_HIP(hipEventSynchronize(ev));
+                const auto tc = Clock::now();
+                const RecPass &R2 = passes[size_t(r)];
+                for (size_t j = 0; j < R2.rows.size(); j++) {
+                    std::string s = ctc_decode(bh + j, int(R2.lens[j]), R2.ntot, R2.widths[j]);
+                    pages_[size_t(R2.rows[j].first)].lines[size_t(R2.rows[j].second)] = std::move(s);
+                }
+                busy = ms_since(tc);
+            } catch (const std::exception &e) {
+                err = e.what();
+            }
+            task_done(busy, err);
+        });
+    }
+    } catch (const std::exception &e) {
+        std::lock_guard<std::mutex> lk(mu);
+        if (error.empty()) error = e.what();
+    }
+    {
+        std::unique_lock<std::mutex> lk(mu);
+        cv.wait(lk, [&] { return pending_tasks == 0; });
+    }
+    for (hipEvent_t e : det_ev)
+        if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : rec_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (!error.empty()) fail("pipeline: " + error);
+    ctx.sync();
+    stats_.ms = ms_since(t0);
+    stats_.cpu_busy_ms = cpu_busy;
+    for (const PageText &pt : pages_) {
+        stats_.lines += int(pt.lines.size());
+        stats_.words += pt.words;
+    }
+    for (const RecPass &R : passes)
+        for (uint32_t l : R.lens) stats_.rec_steps += l;
+}
+
+}  // namespace ocr

@@ -1,0 +1,59 @@
+// The whole-page pipeline (the reference's ocr-bench gpu_thread and run, src/bin/ocr-bench.rs:
+// 133-310 and 458-585): GPU detection, host words and lines, GPU line images and recognition,
+// host CTC, with the GPU and the host cores working on different pages at once.
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "geometry.h"
+#include "models.h"
+
+namespace ocr {
+
+struct PipelineOpts {
+    int merge = 2;        // pages per recognition pass (MERGE, ocr-bench.rs:164; README tuned value 2)
+    float relv = 0.15f;   // line padding across, fraction of the median word height (RELV)
+    float relend = 0.1f;  // line padding at the ends (RELEND)
+    float thr = 0.5f;     // detection threshold
+    int threads = 0;      // host worker threads (0: hardware concurrency, at most 16)
+    int det_batch = 4;    // pages per detection pass
+};
+
+struct PageText {
+    std::vector<std::string> lines;  // reading order
+    int words = 0;
+};
+
+struct PipelineStats {
+    double ms = 0, cpu_busy_ms = 0;
+    int pages = 0, lines = 0, words = 0, batches = 0, rec_passes = 0;
+    long long rec_steps = 0;  // sum over lines of their GRU steps
+};
+
+// Words -> lines -> padding -> line images -> batches for one page (all host work before the
+// recogniser), as ocr-bench.rs:503-559 does it per page.
+struct PageLayout {
+    int words = 0;
+    std::vector<LineGeom> lines;
+    BatchPlan plan;
+};
+PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend);
+
+class Pipeline {
+  public:
+    Pipeline(Ctx &ctx, Detector &det, Recognizer &rec, const PipelineOpts &opts);
+    ~Pipeline();
+    // All pages' RGB bytes already in device memory.
+    void run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages);
+    const std::vector<PageText> &pages() const { return pages_; }
+    const PipelineStats &stats() const { return stats_; }
+
+  private:
+    struct Impl;
+    Impl *impl_;
+    std::vector<PageText> pages_;
+    PipelineStats stats_;
+};
+
+}  // namespace ocr

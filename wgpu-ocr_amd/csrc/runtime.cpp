@@ -6,6 +6,76 @@ namespace ocr {
 
 void fail(const std::string &msg) { throw Error(msg); }
 
+Probe &Probe::get() {
+    static Probe p;
+    return p;
+}
+
+hipEvent_t Probe::take() {
+    if (!spare_.empty()) {
+        hipEvent_t e = spare_.back();
+        spare_.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    OCR_HIP(hipEventCreate(&e));
+    return e;
+}
+
+void Probe::start(const std::string &family) {
+    std::lock_guard<std::mutex> lk(mu_);
+    Fam &f = fams_[family];
+    for (auto &pr : f.ev) spare_.push_back(pr.first), spare_.push_back(pr.second);
+    f = Fam{};
+    any_ = true;
+}
+
+bool Probe::active(const char *family) {
+    if (!any_) return false;
+    std::lock_guard<std::mutex> lk(mu_);
+    return fams_.count(family) > 0;
+}
+
+void Probe::record(const char *family, hipStream_t s, bool begin, double flops, double bytes) {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = fams_.find(family);
+    if (it == fams_.end()) return;
+    Fam &f = it->second;
+    hipEvent_t e = take();
+    OCR_HIP(hipEventRecord(e, s));
+    if (begin) {
+        f.open = e;
+        f.flops += flops;
+        f.bytes += bytes;
+    } else if (f.open) {
+        f.ev.push_back({f.open, e});
+        f.open = nullptr;
+    }
+}
+
+bool Probe::stop(const std::string &family, uint32_t *calls, double *ms, double *flops, double *bytes) {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = fams_.find(family);
+    if (it == fams_.end()) return false;
+    Fam &f = it->second;
+    double total = 0;
+    for (auto &pr : f.ev) {
+        OCR_HIP(hipEventSynchronize(pr.second));
+        float t = 0;
+        OCR_HIP(hipEventElapsedTime(&t, pr.first, pr.second));
+        total += t;
+        spare_.push_back(pr.first);
+        spare_.push_back(pr.second);
+    }
+    if (calls) *calls = uint32_t(f.ev.size());
+    if (ms) *ms = total;
+    if (flops) *flops = f.flops;
+    if (bytes) *bytes = f.bytes;
+    fams_.erase(it);
+    any_ = !fams_.empty();
+    return true;
+}
+
 size_t Pool::size_class(size_t bytes) {
     bytes = (bytes + 255) & ~size_t(255);
     if (bytes <= (64u << 10)) return bytes ? bytes : 256;

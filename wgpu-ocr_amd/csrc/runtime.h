@@ -3,10 +3,12 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <map>
 #include <mutex>
+#include <string>
 #include <unordered_map>
 #include <vector>
 
@@ -38,6 +40,50 @@ class Pool {
 };
 
 class Ctx;
+
+// Kernel timing with HIP events, for measurement (the role of the reference's OPPROFILE,
+// src/gpu.rs:1247-1368, without its waits): while a kernel family is being probed, each launch
+// of it is bracketed by two events recorded on the launch's own stream, and its algorithmic
+// FLOPs and bytes are added up. Process-wide; families are "conv_mfma", "gru", "conv_transpose",
+// "conv_direct", "maxpool", "mask_up", "grey_resize", "line_crop", "avgpool_t", "argmax", "copy".
+class Probe {
+  public:
+    static Probe &get();
+    void start(const std::string &family);
+    // Waits for the recorded events; returns false if the family was not being probed.
+    bool stop(const std::string &family, uint32_t *calls, double *ms, double *flops, double *bytes);
+    bool active(const char *family);
+    void record(const char *family, hipStream_t s, bool begin, double flops, double bytes);
+
+  private:
+    struct Fam {
+        std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+        double flops = 0, bytes = 0;
+        hipEvent_t open = nullptr;
+    };
+    std::map<std::string, Fam> fams_;
+    std::vector<hipEvent_t> spare_;
+    std::mutex mu_;
+    std::atomic<bool> any_{false};
+    hipEvent_t take();
+};
+
+// Brackets one launch when its family is probed (no cost otherwise beyond a flag check).
+class ProbeScope {
+  public:
+    ProbeScope(const char *family, hipStream_t s, double flops, double bytes) : fam_(family), s_(s) {
+        on_ = Probe::get().active(family);
+        if (on_) Probe::get().record(fam_, s_, true, flops, bytes);
+    }
+    ~ProbeScope() {
+        if (on_) Probe::get().record(fam_, s_, false, 0, 0);
+    }
+
+  private:
+    const char *fam_;
+    hipStream_t s_;
+    bool on_ = false;
+};
 
 // A pooled device buffer owned by one holder; goes back to the pool when destroyed.
 class DBuf {

@@ -56,7 +56,33 @@ SIGNATURES = {
     "ocr_recognize_dims": (ctypes.c_int, [P, P, U32, PU32, PU32, PU32]),
     "ocr_recognize": (ctypes.c_int, [P, P, U32, P, P, P]),
     "ocr_recognize_device": (ctypes.c_int, [P, P, U32, P, P, P]),
+    "ocr_probe_start": (ctypes.c_int, [ctypes.c_char_p]),
+    "ocr_probe_stop": (ctypes.c_int, [ctypes.c_char_p, PU32, P, P, P]),
+    "ocr_word_rects": (ctypes.c_int, [P, U32, U32, P, U32, PU32]),
+    "ocr_layout_page": (P, [P, U32, U32, F32, F32]),
+    "ocr_layout_free": (None, [P]),
+    "ocr_layout_counts": (ctypes.c_int, [P, PU32, PU32, PU32]),
+    "ocr_layout_line": (ctypes.c_int, [P, U32, P, P, P, PU32]),
+    "ocr_layout_batch": (ctypes.c_int, [P, U32, PU32, P, PU32]),
+    "ocr_pipeline_new": (P, [P, P, P]),
+    "ocr_pipeline_free": (None, [P]),
+    "ocr_pipeline_run_device": (ctypes.c_int, [P, P, P, P, U32]),
+    "ocr_pipeline_run": (ctypes.c_int, [P, P, P, P, U32]),
+    "ocr_pipeline_stats_get": (ctypes.c_int, [P, P]),
+    "ocr_pipeline_page": (ctypes.c_int, [P, U32, PU32, PU32]),
+    "ocr_pipeline_line_text": (ctypes.c_int, [P, U32, U32, ctypes.c_char_p, U32, PU32]),
 }
+
+
+class ocr_pipeline_opts(ctypes.Structure):
+    _fields_ = [("merge", ctypes.c_uint32), ("relv", ctypes.c_float), ("relend", ctypes.c_float),
+                ("thr", ctypes.c_float), ("threads", ctypes.c_uint32), ("det_batch", ctypes.c_uint32)]
+
+
+class ocr_pipeline_stats(ctypes.Structure):
+    _fields_ = [("ms", ctypes.c_double), ("cpu_busy_ms", ctypes.c_double), ("pages", ctypes.c_uint32),
+                ("lines", ctypes.c_uint32), ("words", ctypes.c_uint32), ("batches", ctypes.c_uint32),
+                ("rec_passes", ctypes.c_uint32), ("rec_steps", ctypes.c_uint64)]
 
 
 def lib():
@@ -263,6 +289,123 @@ class Recognizer:
         try:
             if self.handle:
                 lib().ocr_recognizer_free(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+FAMILIES = ("conv_mfma", "gru", "conv_transpose", "conv_direct", "conv_generic", "maxpool", "mask_up",
+            "grey_resize", "line_crop", "avgpool_t", "argmax", "copy")
+
+
+def probe_start(family: str):
+    _check(lib().ocr_probe_start(family.encode()))
+
+
+def probe_stop(family: str) -> dict:
+    calls = ctypes.c_uint32()
+    ms, flops, nbytes = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    _check(lib().ocr_probe_stop(family.encode(), ctypes.byref(calls), ctypes.byref(ms), ctypes.byref(flops),
+                                ctypes.byref(nbytes)))
+    return {"calls": calls.value, "ms": ms.value, "flops": flops.value, "bytes": nbytes.value}
+
+
+# ---- host geometry (no GPU) -----------------------------------------------------------------
+def word_rects(bits: np.ndarray, w: int):
+    """Words of a page mask (ocr-bench.rs:40-60) as an [n, 6] array (cx, cy, ux, uy, w, h)."""
+    bits = np.ascontiguousarray(bits, np.uint32)
+    h = bits.shape[0]
+    count = ctypes.c_uint32()
+    _check(lib().ocr_word_rects(_ptr(bits), w, h, None, 0, ctypes.byref(count)))
+    out = np.zeros((count.value, 6), np.float32)
+    _check(lib().ocr_word_rects(_ptr(bits), w, h, _ptr(out), count.value, ctypes.byref(count)))
+    return out
+
+
+class Layout:
+    """The layout of one page before recognition: words, lines, crop geometry, batches."""
+
+    def __init__(self, bits: np.ndarray, w: int, relv: float = 0.15, relend: float = 0.1):
+        bits = np.ascontiguousarray(bits, np.uint32)
+        self.handle = lib().ocr_layout_page(_ptr(bits), w, bits.shape[0], relv, relend)
+        if not self.handle:
+            raise OcrError(lib().ocr_last_error().decode())
+        nw, nl, nb = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+        _check(lib().ocr_layout_counts(self.handle, ctypes.byref(nw), ctypes.byref(nl), ctypes.byref(nb)))
+        self.words, self.nlines, self.nbatches = nw.value, nl.value, nb.value
+
+    def line(self, i: int):
+        """(box [left, top, bw, bh, out_w], row_off [bh + 1], spans [n, 2])"""
+        box = np.zeros(5, np.int32)
+        ns = ctypes.c_uint32()
+        _check(lib().ocr_layout_line(self.handle, i, _ptr(box), None, None, ctypes.byref(ns)))
+        row_off = np.zeros(box[3] + 1, np.int32)
+        spans = np.zeros((ns.value, 2), np.int32)
+        _check(lib().ocr_layout_line(self.handle, i, None, _ptr(row_off), _ptr(spans), ctypes.byref(ns)))
+        return box, row_off, spans
+
+    def batch(self, i: int):
+        """(width, [line indices])"""
+        w, n = ctypes.c_uint32(), ctypes.c_uint32()
+        members = np.zeros(64, np.uint32)
+        _check(lib().ocr_layout_batch(self.handle, i, ctypes.byref(w), _ptr(members), ctypes.byref(n)))
+        return w.value, [int(v) for v in members[: n.value]]
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().ocr_layout_free(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+class Pipeline:
+    """The whole-page pipeline (ocr-bench.rs:133-310, 458-585)."""
+
+    def __init__(self, det: Detector, rec: Recognizer, merge=2, relv=0.15, relend=0.1, thr=0.5, threads=0,
+                 det_batch=4):
+        self.ctx = det.ctx
+        self._keep = (det, rec)
+        opts = ocr_pipeline_opts(merge, relv, relend, thr, threads, det_batch)
+        self.handle = lib().ocr_pipeline_new(det.handle, rec.handle, ctypes.byref(opts))
+        if not self.handle:
+            raise OcrError(lib().ocr_last_error().decode())
+
+    def run_device(self, d_pages, ws, hs):
+        n = len(d_pages)
+        arr = (ctypes.c_void_p * n)(*[b.ptr for b in d_pages])
+        w, h = np.asarray(ws, np.uint32), np.asarray(hs, np.uint32)
+        _check(lib().ocr_pipeline_run_device(self.handle, arr, _ptr(w), _ptr(h), n))
+
+    def run(self, pages):
+        pages = [np.ascontiguousarray(p, np.uint8) for p in pages]
+        n = len(pages)
+        arr = (ctypes.c_void_p * n)(*[p.ctypes.data for p in pages])
+        w = np.asarray([p.shape[1] for p in pages], np.uint32)
+        h = np.asarray([p.shape[0] for p in pages], np.uint32)
+        _check(lib().ocr_pipeline_run(self.handle, arr, _ptr(w), _ptr(h), n))
+
+    def stats(self) -> dict:
+        s = ocr_pipeline_stats()
+        _check(lib().ocr_pipeline_stats_get(self.handle, ctypes.byref(s)))
+        return {k: getattr(s, k) for k, _ in ocr_pipeline_stats._fields_}
+
+    def texts(self, page: int):
+        nl, nw = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(lib().ocr_pipeline_page(self.handle, page, ctypes.byref(nl), ctypes.byref(nw)))
+        out = []
+        buf = ctypes.create_string_buffer(4096)
+        n = ctypes.c_uint32()
+        for i in range(nl.value):
+            _check(lib().ocr_pipeline_line_text(self.handle, page, i, buf, 4096, ctypes.byref(n)))
+            out.append(buf.value.decode())
+        return out, nw.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().ocr_pipeline_free(self.handle)
                 self.handle = None
         except Exception:
             pass

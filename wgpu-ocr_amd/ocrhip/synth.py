@@ -183,7 +183,11 @@ def det_model(seed: int = 0) -> bytes:
     edge = np.zeros_like(label)
     edge[:4], edge[-4:], edge[:, :4], edge[:, -4:] = True, True, True, True
     wt = np.sqrt(np.where(edge, 50.0 * wt, wt)).reshape(-1)  # the zero-padded border is paper too
-    sol = np.linalg.lstsq(x * wt[:, None], y * wt, rcond=None)[0] * 4.0  # logits of about +-4
+    sol = np.linalg.lstsq(x * wt[:, None], y * wt, rcond=None)[0]
+    # Bias: at most 0.5 % of the paper pixels of the fit page above the threshold (logit 0).
+    paper_logits = (x[:, :-1] @ sol[:-1])[~label.reshape(-1)]
+    sol[-1] = -np.quantile(paper_logits, 0.995)
+    sol *= 4.0  # logits of about +-4
     p["head.w"] = _f16_exact(sol[:-1].astype(np.float32).reshape(1, DET_ENC[0], 1, 1))
     p["head.b"] = _f16_exact(sol[-1:].astype(np.float32))
 
@@ -298,7 +302,7 @@ def page(seed: int, lines: int = 36, noise: float = 4.0, with_blocks: bool = Fal
     top, bottom, left = 180, PAGE_H - 180, 150
     pitch = (bottom - top) / lines
     for i in range(lines):
-        lh = int(rng.integers(34, 50))
+        lh = int(rng.integers(24, 37))
         y0 = int(top + i * pitch + rng.integers(0, max(1, int(pitch) - lh)))
         x = left + int(rng.integers(0, 60))
         xend = PAGE_W - 150 - int(rng.integers(0, 900))
@@ -307,10 +311,10 @@ def page(seed: int, lines: int = 36, noise: float = 4.0, with_blocks: bool = Fal
             x1 = min(x + ww, xend)
             ink = float(rng.uniform(0, 60))
             sx = x
-            while sx < x1:  # vertical strokes 3-7 px wide, gaps 1-3 px
-                s = int(rng.integers(3, 8))
+            while sx < x1:  # vertical strokes 4-9 px wide, gaps 1-2 px
+                s = int(rng.integers(4, 10))
                 grey[y0: y0 + lh, sx: min(sx + s, x1)] = ink
-                sx += s + int(rng.integers(1, 4))
+                sx += s + int(rng.integers(1, 3))
             if with_blocks:
                 blocks[y0: y0 + lh, x: x1] = True
             x = x1 + int(rng.integers(22, 40))
