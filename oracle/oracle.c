@@ -4,7 +4,17 @@
  * as the CPU baseline. Nothing in the product links or calls this file.
  *
  * Layout is ONNX's: NCHW float32. Each function cites the reference code it restates.
- * Pinning (which check fixes each function) is listed in oracle/README.md.
+ * Pinning (the check in tests/test_oracle.py that fixes each function):
+ *   orc_conv2d            torch conv2d golden vectors (pads, strides, groups, cin = 1, wide)
+ *   orc_conv_transpose2d  torch conv_transpose2d golden vectors (2x2, 2x3, 3x3 stride 1)
+ *   orc_pool2d            torch max_pool2d / avg_pool2d golden vectors
+ *   orc_gru               torch GRU golden vectors (gates reordered), truncated-run lengths,
+ *                         and a planted gate swap that must fail
+ *   orc_grey_resize       torch bilinear (half-pixel) golden of the padded grey page
+ *   orc_mask_up_prob      torch bilinear golden of the valid region; valid-region closed form
+ *   orc_pack_bits         bit layout closed form
+ *   orc_line_crop         torch bilinear golden of span-masked grey crops
+ *   orc_activate          sigmoid closed form via the conv golden; ReLU by the conv goldens
  */
 #include <math.h>
 #include <stdint.h>

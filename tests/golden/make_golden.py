@@ -112,6 +112,38 @@ def resize_cases():
     return cases
 
 
+def line_crop_cases():
+    """Line images: the ocrs grey value inside the line polygon (row spans), black (-0.5) outside
+    it and off the page, resized to 64 rows x out_w columns (F.interpolate, half-pixel), padded
+    on the right to the batch width wb with black."""
+    cases = {}
+    for name, (ph, pw, left, top, bh, bw, out_w, wb) in [("inside", (40, 90, 5, 3, 30, 70, 150, 200)),
+                                                         ("edge", (30, 50, -4, 20, 16, 60, 240, 250))]:
+        rgb = rng.integers(0, 256, (ph, pw, 3), dtype=np.uint8)
+        grey = (-0.5 + rgb[..., 0].astype(np.float32) * np.float32(0.299 / 255)
+                + rgb[..., 1].astype(np.float32) * np.float32(0.587 / 255)
+                + rgb[..., 2].astype(np.float32) * np.float32(0.114 / 255)).astype(np.float32)
+        row_off, spans = [0], []
+        crop = np.full((bh, bw), -0.5, np.float32)
+        for cy in range(bh):
+            a = int(rng.integers(0, bw // 3))
+            b = int(rng.integers(bw // 2, bw + 1))
+            runs = [(a, b)] if cy % 3 else [(a, a + (b - a) // 3), (a + (b - a) // 2, b)]
+            for x0, x1 in runs:
+                spans += [x0, x1]
+                for cx in range(x0, x1):
+                    x, y = left + cx, top + cy
+                    if 0 <= x < pw and 0 <= y < ph:
+                        crop[cy, cx] = grey[y, x]
+            row_off.append(len(spans))
+        img = F.interpolate(t(crop)[None, None], size=(64, out_w), mode="bilinear", align_corners=False)[0, 0]
+        out = np.full((64, wb), -0.5, np.float32)
+        out[:, :out_w] = img.numpy()
+        cases[name] = dict(rgb=rgb, box=np.array([left, top, bw, bh, out_w]), row_off=np.array(row_off, np.int32),
+                           spans=np.array(spans, np.int32), wb=np.array(wb), y=out)
+    return cases
+
+
 def softmax_cases():
     x = f32(4, 3, 97, scale=3.0)
     return {"ls": dict(x=x, y=F.log_softmax(t(x), dim=2).numpy())}
@@ -129,4 +161,5 @@ if __name__ == "__main__":
     save("gru", gru_cases())
     save("resize", resize_cases())
     save("logsoftmax", softmax_cases())
+    save("line_crop", line_crop_cases())
     print("written to", OUT)

@@ -89,6 +89,14 @@ def test_mask_up_golden(case):
     np.testing.assert_allclose(prob, c["prob"], rtol=0, atol=2e-6)
 
 
+@pytest.mark.parametrize("case", sorted(cases("line_crop")))
+def test_line_crop_golden(case):
+    c = cases("line_crop")[case]
+    y = graph.line_crop(c["rgb"], c["box"], c["row_off"], c["spans"], int(c["wb"]))
+    # torch interpolates as a + (b - a) t, the reference's mix as a (1 - t) + b t: a few ulp apart.
+    np.testing.assert_allclose(y, c["y"], rtol=0, atol=1e-5)
+
+
 def test_logsoftmax_golden():
     c = cases("logsoftmax")["ls"]
     m = onnx_read.Model([onnx_read.Node("LogSoftmax", ["x"], ["y"], {"axis": 2})], {}, {}, "x", "y")

@@ -11,9 +11,14 @@
 // 0-7 its float16 "hi" part and columns 8-15 the float16 remainder "lo" (h = hi + lo to about
 // 2^-22), so one v_mfma_f32_16x16x32_f16 per 16 rows and 32 hidden units gives R h for all 8
 // lines at float32-class accuracy. Each wavefront owns UPW hidden units (all three gate rows of
-// them), so the gate nonlinearity needs no exchange: after adding the hi and lo columns, lane
-// (r < 8) holds 4 units of line r for z, r and h and keeps that line's state in registers. The
-// new state goes to a double-buffered LDS copy of the B operand: one barrier per step.
+// them), so the gate nonlinearity needs no exchange across wavefronts.
+//
+// Per step, after the MFMAs, lane (g, r) of a 16-lane row holds rows 4g..4g+3 of column r. The
+// hi and lo columns of a line are summed with one DPP rotation by 8, arranged so that lane r < 8
+// ends with units 4g, 4g+1 of line r and lane r + 8 with units 4g+2, 4g+3 of the same line:
+// every lane does gate arithmetic for two units. The step's G values are loaded at the end of
+// the previous step, so the HBM latency hides behind the barrier and the MFMA phase. The new state
+// goes to a double-buffered LDS copy of the B operand: one barrier per step.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -30,46 +35,75 @@ namespace {
 
 constexpr int H = 256, LINES = 8, HROW = H + 8;  // LDS row of the B operand: 256 units + padding
 
-__device__ inline float sigm(float v) { return 1.f / (1.f + expf(-v)); }
+// exp through the hardware base-2 exponential; 1/x through the hardware reciprocal (1 ulp).
+__device__ inline float fast_exp(float v) { return __builtin_amdgcn_exp2f(v * 1.4426950408889634f); }
+__device__ inline float sigm(float v) { return __builtin_amdgcn_rcpf(1.f + fast_exp(-v)); }
+__device__ inline float tanh_f(float v) { return 1.f - 2.f * __builtin_amdgcn_rcpf(1.f + fast_exp(2.f * v)); }
+
+// Lane r of each 16-lane row receives the value of lane (r + 8) mod 16 (DPP row_ror:8).
+__device__ inline float ror8(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));
+}
 
 template <int UPW>
 __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restrict__ G, const half8 *__restrict__ R,
                                                            const float *__restrict__ Rb, float *__restrict__ Y,
                                                            const uint32_t *__restrict__ lens, int ntot) {
     constexpr int RT = UPW / 16;  // 16-row tiles per gate per wavefront
+    constexpr int KL = 2;         // k-slices of the h gate's R kept in LDS
     __shared__ __align__(16) _Float16 hbuf[2][16][HROW];
+    __shared__ float s_rb[768];  // this direction's recurrent bias [z | r | h]
+    __shared__ half8 s_rf[H / UPW][RT * KL][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r = lane & 15;
     const int dir = blockIdx.y, n0 = blockIdx.x * LINES;
 
     // R fragments: rows gate * 256 + unit, unit = wave * UPW + rt * 16 + r; k = kt * 32 + 8g .. +7.
+    // All are held in VGPRs except the last KL k-slices of the h gate, which live in LDS (the
+    // register file holds the rest of the step's state without spilling).
     half8 rf[3][RT][8];
 #pragma unroll
     for (int q = 0; q < 3; q++)
 #pragma unroll
         for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (int kt = 0; kt < 8; kt++)
-                rf[q][rt][kt] = R[(size_t(dir) * 768 + q * 256 + wave * UPW + rt * 16 + r) * 32 + kt * 4 + g];
+            for (int kt = 0; kt < 8; kt++) {
+                const half8 v = R[(size_t(dir) * 768 + q * 256 + wave * UPW + rt * 16 + r) * 32 + kt * 4 + g];
+                if (q == 2 && kt >= 8 - KL) s_rf[wave][rt * KL + kt - (8 - KL)][lane] = v;
+                else rf[q][rt][kt] = v;
+            }
 
     for (int i = tid; i < 2 * 16 * HROW; i += blockDim.x) (&hbuf[0][0][0])[i] = (_Float16)0.f;
+    for (int i = tid; i < 768; i += blockDim.x) s_rb[i] = Rb[dir * 768 + i];
 
     int maxlen = 0;
     for (int j = 0; j < LINES; j++)
         if (n0 + j < ntot) maxlen = max(maxlen, int(lens[n0 + j]));
-    const int line = n0 + r;
-    const bool owner = r < LINES;
-    const int len = (owner && line < ntot) ? int(lens[line]) : 0;
-    float h[RT][4];
+    // This lane's line and the two units (of each 16-row tile) it updates: lane r < 8 takes
+    // units 4g, 4g+1 of line r, lane r >= 8 units 4g+2, 4g+3 of line r - 8.
+    const bool upper = r >= LINES;
+    const int lr = upper ? r - LINES : r;
+    const int line = n0 + lr;
+    const int len = line < ntot ? int(lens[line]) : 0;
+    const int usub = upper ? 2 : 0;
+    float h[RT][2];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
+    for (int rt = 0; rt < RT; rt++) h[rt][0] = h[rt][1] = 0.f;
+    __syncthreads();
+    // G of the step about to run, [gate][rt] pairs of units; loaded one step ahead.
+    auto load_g = [&](int s, float2 (&gv)[3][RT]) {
+        const int t = dir == 0 ? s : len - 1 - s;
+        if (s < len) {
+            const float *gb = G + (size_t(t) * ntot + line) * 1536 + dir * 768 + wave * UPW + 4 * g + usub;
 #pragma unroll
-        for (int i = 0; i < 4; i++) h[rt][i] = 0.f;
-    __syncthreads();
-
-    __shared__ float s_rb[768];  // this direction's recurrent bias [z | r | h]
-    for (int i = tid; i < 768; i += blockDim.x) s_rb[i] = Rb[dir * 768 + i];
-    __syncthreads();
+            for (int q = 0; q < 3; q++)
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++)
+                    gv[q][rt] = *reinterpret_cast<const float2 *>(gb + q * 256 + rt * 16);
+        }
+    };
+    float2 gcur[3][RT];
+    load_g(0, gcur);
 
     for (int s = 0; s < maxlen; s++) {
         const int cur = s & 1;
@@ -85,48 +119,55 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
 #pragma unroll
             for (int q = 0; q < 3; q++)
 #pragma unroll
-                for (int rt = 0; rt < RT; rt++)
-                    acc[q][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(rf[q][rt][kt], b, acc[q][rt], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
+                for (int rt = 0; rt < RT; rt++) {
+                    const half8 a = (q == 2 && kt >= 8 - KL) ? s_rf[wave][rt * KL + kt - (8 - KL)][lane] : rf[q][rt][kt];
+                    acc[q][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[q][rt], 0, 0, 0);
+                }
         }
-        // Column r + 8 holds the lo contribution of line r: add it in (DPP row_ror:8 brings lane
-        // r + 8 of each 16-lane row to lane r).
+        // hi + lo: lane r < 8 keeps rows 0, 1 and sends rows 2, 3 to lane r + 8 (and the reverse).
+        float rh[3][RT][2];
 #pragma unroll
         for (int q = 0; q < 3; q++)
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[q][rt][i] += __int_as_float(
-                        __builtin_amdgcn_mov_dpp(__float_as_int(acc[q][rt][i]), 0x128, 0xf, 0xf, false));
-        if (owner) {
-            const bool on = s < len;
-            const int t = dir == 0 ? s : len - 1 - s;
-#pragma unroll
             for (int rt = 0; rt < RT; rt++) {
-                const int u0 = wave * UPW + rt * 16 + 4 * g;
-                if (on) {
-                    const float *gb = G + (size_t(t) * ntot + line) * 1536 + dir * 768 + u0;
-                    float *yo = Y + (size_t(t) * ntot + line) * 512 + dir * 256 + u0;
+                const float send0 = upper ? acc[q][rt][0] : acc[q][rt][2];
+                const float send1 = upper ? acc[q][rt][1] : acc[q][rt][3];
+                const float keep0 = upper ? acc[q][rt][2] : acc[q][rt][0];
+                const float keep1 = upper ? acc[q][rt][3] : acc[q][rt][1];
+                rh[q][rt][0] = keep0 + ror8(send0);
+                rh[q][rt][1] = keep1 + ror8(send1);
+            }
+        const bool on = s < len;
+        const int t = dir == 0 ? s : len - 1 - s;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float z = sigm(gb[i] + (acc[0][rt][i] + s_rb[u0 + i]));
-                        const float rr = sigm(gb[256 + i] + (acc[1][rt][i] + s_rb[256 + u0 + i]));
-                        const float c = tanhf(gb[512 + i] + rr * (acc[2][rt][i] + s_rb[512 + u0 + i]));
-                        h[rt][i] = (1.f - z) * c + z * h[rt][i];
-                        yo[i] = h[rt][i];
-                    }
-                }
-                // The next step's B operand (the unchanged state when this line has ended).
+        for (int rt = 0; rt < RT; rt++) {
+            const int u0 = wave * UPW + rt * 16 + 4 * g + usub;
+            if (on) {
+                float hn[2];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const _Float16 hi = (_Float16)h[rt][i];
-                    hbuf[cur ^ 1][r][u0 + i] = hi;
-                    hbuf[cur ^ 1][r + 8][u0 + i] = (_Float16)(h[rt][i] - (float)hi);
+                for (int i = 0; i < 2; i++) {
+                    const float gz = i ? gcur[0][rt].y : gcur[0][rt].x;
+                    const float gr = i ? gcur[1][rt].y : gcur[1][rt].x;
+                    const float gh = i ? gcur[2][rt].y : gcur[2][rt].x;
+                    const float z = sigm(gz + (rh[0][rt][i] + s_rb[u0 + i]));
+                    const float rr = sigm(gr + (rh[1][rt][i] + s_rb[256 + u0 + i]));
+                    const float c = tanh_f(gh + rr * (rh[2][rt][i] + s_rb[512 + u0 + i]));
+                    hn[i] = (1.f - z) * c + z * h[rt][i];
+                    h[rt][i] = hn[i];
                 }
-                __builtin_amdgcn_sched_barrier(0);
+                *reinterpret_cast<float2 *>(Y + (size_t(t) * ntot + line) * 512 + dir * 256 + u0) =
+                    make_float2(hn[0], hn[1]);
+            }
+            // The next step's B operand (the unchanged state when this line has ended).
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const _Float16 hi = (_Float16)h[rt][i];
+                hbuf[cur ^ 1][lr][u0 + i] = hi;
+                hbuf[cur ^ 1][lr + LINES][u0 + i] = (_Float16)(h[rt][i] - (float)hi);
             }
         }
+        // The next step's G, in flight across the barrier and the next MFMA phase.
+        load_g(s + 1, gcur);
         __syncthreads();
     }
 }

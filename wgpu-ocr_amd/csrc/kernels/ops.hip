@@ -54,33 +54,54 @@ __global__ void conv_generic_kernel(const float *x, int n, int h, int w, int cin
 }
 
 // ---- conv_direct (gpu.rs:385-422): cin = 1, stride 1, act, MaxPool (ph, pw) fused ------------
-// One thread per pooled output pixel computes every output channel; weights [cout][kh][kw].
-__global__ void conv_direct_kernel(const float *x, int n, int h, int w, int xcs, float *y, int oh, int ow, int cout,
-                                   int ycs, const float *wt, const float *b, int kh, int kw, int pad, int act, int ph,
-                                   int pw) {
-    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(n) * oh * ow) return;
-    int ox = int(i % ow), oy = int((i / ow) % oh), img = int(i / (size_t(ow) * oh));
+// A workgroup owns a tile of DTY x DTX pooled outputs of one image and every output channel. The
+// input window of the tile and all weights are staged in LDS; thread i takes channel i % cout
+// of successive pixels, so the NHWC stores of a row of the tile are contiguous. Template
+// arguments fix the kernel and pool sizes of the common cases (0: taken from the arguments).
+constexpr int DTY = 8, DTX = 32, DMAXK = 7, DMAXP = 4, DMAXC = 64;
+constexpr int DIN_ROWS = DTY * DMAXP + DMAXK - 1, DIN_COLS = DTX * DMAXP + DMAXK - 1;
+
+template <int KS, int PS>
+__global__ __launch_bounds__(256) void conv_direct_kernel(const float *__restrict__ x, int h, int w, int xcs,
+                                                          float *__restrict__ y, int oh, int ow, int cout, int ycs,
+                                                          const float *__restrict__ wt, const float *__restrict__ b,
+                                                          int kh_, int kw_, int pad, int act, int ph_, int pw_,
+                                                          int tiles_x) {
+    const int kh = KS ? KS : kh_, kw = KS ? KS : kw_, ph = PS ? PS : ph_, pw = PS ? PS : pw_;
+    __shared__ float s_in[DIN_ROWS * DIN_COLS];
+    __shared__ float s_w[DMAXC * DMAXK * DMAXK];
+    __shared__ float s_b[DMAXC];
+    const int tid = threadIdx.x;
+    const int tx = blockIdx.x % tiles_x, ty = blockIdx.x / tiles_x, img = blockIdx.y;
+    const int oy0 = ty * DTY, ox0 = tx * DTX;
+    const int rows = DTY * ph + kh - 1, cols = DTX * pw + kw - 1;
+    const int iy0 = oy0 * ph - pad, ix0 = ox0 * pw - pad;
     const float *xi = x + size_t(img) * h * w * xcs;
-    float *yo = y + i * ycs;
-    for (int co = 0; co < cout; co++) {
-        float best = -3.4e38f;
-        for (int py = 0; py < ph; py++)
-            for (int px = 0; px < pw; px++) {
-                int cy = oy * ph + py, cx = ox * pw + px;
+    for (int i = tid; i < rows * cols; i += 256) {
+        const int r = i / cols, c = i - r * cols;
+        const int iy = iy0 + r, ix = ix0 + c;
+        s_in[i] = (iy >= 0 && iy < h && ix >= 0 && ix < w) ? xi[(size_t(iy) * w + ix) * xcs] : 0.f;
+    }
+    for (int i = tid; i < cout * kh * kw; i += 256) s_w[i] = wt[i];
+    for (int i = tid; i < cout; i += 256) s_b[i] = b[i];
+    __syncthreads();
+    for (int idx = tid; idx < DTY * DTX * cout; idx += 256) {
+        const int co = idx % cout, p = idx / cout;
+        const int py = p / DTX, px = p - py * DTX;
+        const int oy = oy0 + py, ox = ox0 + px;
+        if (oy >= oh || ox >= ow) continue;
+        const float *wc = s_w + co * kh * kw;
+        const float bias = s_b[co];
+        float best = -INFINITY;
+        for (int qy = 0; qy < ph; qy++)
+            for (int qx = 0; qx < pw; qx++) {
+                const float *src = s_in + (py * ph + qy) * cols + px * pw + qx;
                 float acc = 0.f;
-                for (int ky = 0; ky < kh; ky++) {
-                    int iy = cy + ky - pad;
-                    if (iy < 0 || iy >= h) continue;
-                    for (int kx = 0; kx < kw; kx++) {
-                        int ix = cx + kx - pad;
-                        if (ix < 0 || ix >= w) continue;
-                        acc += xi[(size_t(iy) * w + ix) * xcs] * wt[(co * kh + ky) * kw + kx];
-                    }
-                }
-                best = fmaxf(best, act_f(acc + b[co], act));
+                for (int ky = 0; ky < kh; ky++)
+                    for (int kx = 0; kx < kw; kx++) acc = __fmaf_rn(src[ky * cols + kx], wc[ky * kw + kx], acc);
+                best = fmaxf(best, act_f(acc + bias, act));
             }
-        yo[co] = best;
+        y[((size_t(img) * oh + oy) * ow + ox) * ycs + co] = best;
     }
 }
 
@@ -240,10 +261,23 @@ void conv_generic(const Act &x, const Act &y, const float *w, const float *b, in
 
 void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int pad, int act, int ph,
                  int pw, hipStream_t s) {
+    if (kh > DMAXK || kw > DMAXK || ph > DMAXP || pw > DMAXP || y.c > DMAXC)
+        fail("conv_direct: kernel above 7 x 7, pool above 4 x 4 or more than 64 channels");
+    if (x.c != 1) fail("conv_direct: one input channel");
     ProbeScope probe("conv_direct", s, 2.0 * double(y.pixels()) * ph * pw * y.c * kh * kw,
-                     4.0 * double(x.count() + y.count()));
-    hipLaunchKernelGGL(conv_direct_kernel, dim3(blocks_for(y.pixels())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.cs,
-                       y.p, y.h, y.w, y.c, y.cs, w, b, kh, kw, pad, act, ph, pw);
+                     4.0 * double(x.pixels() + y.count()));
+    const int tiles_x = (y.w + DTX - 1) / DTX, tiles_y = (y.h + DTY - 1) / DTY;
+    if (size_t(tiles_x) * tiles_y > 0x7fffffff || y.n > 65535) fail("conv_direct: grid too large");
+    dim3 grid(unsigned(tiles_x * tiles_y), unsigned(y.n));
+    if (kh == 3 && kw == 3 && ph == 2 && pw == 2)
+        hipLaunchKernelGGL((conv_direct_kernel<3, 2>), grid, dim3(256), 0, s, x.p, x.h, x.w, x.cs, y.p, y.h, y.w, y.c,
+                           y.cs, w, b, kh, kw, pad, act, ph, pw, tiles_x);
+    else if (kh == 3 && kw == 3 && ph == 1 && pw == 1)
+        hipLaunchKernelGGL((conv_direct_kernel<3, 1>), grid, dim3(256), 0, s, x.p, x.h, x.w, x.cs, y.p, y.h, y.w, y.c,
+                           y.cs, w, b, kh, kw, pad, act, ph, pw, tiles_x);
+    else
+        hipLaunchKernelGGL((conv_direct_kernel<0, 0>), grid, dim3(256), 0, s, x.p, x.h, x.w, x.cs, y.p, y.h, y.w, y.c,
+                           y.cs, w, b, kh, kw, pad, act, ph, pw, tiles_x);
     OCR_HIP(hipGetLastError());
 }
 
