@@ -182,6 +182,42 @@ int ocr_pipeline_page(ocr_pipeline *pipe, uint32_t page, uint32_t *lines, uint32
 /* Text of one line (UTF-8, NUL-terminated, truncated to cap bytes); *len receives its length. */
 int ocr_pipeline_line_text(ocr_pipeline *pipe, uint32_t page, uint32_t line, char *buf, uint32_t cap, uint32_t *len);
 
+/* ---- The N-D executor for the PP-OCRv6 models (src/nd.rs) ----------------------------------- */
+
+typedef struct ocr_nd ocr_nd;
+
+/* NdGraph::new (src/nd.rs:505-817): any ONNX graph of the reference's N-D operator set, with its
+ * load-time fusions. stop_before_softmax: the run returns the logits a final Softmax would read
+ * (the arg-max needs no Softmax). */
+ocr_nd *ocr_nd_new(ocr_ctx *ctx, const char *onnx_path, int stop_before_softmax);
+void ocr_nd_free(ocr_nd *g);
+/* Output shape (rank <= 6) for an input shape, without running the graph. */
+int ocr_nd_dims(ocr_nd *g, const int64_t *in_shape, uint32_t rank, int64_t *out_shape, uint32_t *out_rank);
+/* NdGraph::run (src/nd.rs:834-1195) on a row-major float input (host); out receives the output
+ * (its size from ocr_nd_dims). */
+int ocr_nd_run(ocr_nd *g, const float *in, const int64_t *in_shape, uint32_t rank, float *out);
+/* The same with input and output in device memory, queued on the context's stream. */
+int ocr_nd_run_device(ocr_nd *g, const float *d_in, const int64_t *in_shape, uint32_t rank, float *d_out);
+/* NdGraph::argmax_record / argmax (src/nd.rs:1373-1392): the arg-max over the output's last axis
+ * per row, the first index on ties (nd.rs:383); best has one entry per row. A graph that ends in
+ * a Linear (the CTC head) never writes its logits: the GEMM keeps per-block maxima. */
+int ocr_nd_argmax(ocr_nd *g, const float *in, const int64_t *in_shape, uint32_t rank, uint32_t *best);
+int ocr_nd_argmax_device(ocr_nd *g, const float *d_in, const int64_t *in_shape, uint32_t rank, uint32_t *d_best);
+/* NdGraph::det_input (src/nd.rs:1353-1369): the size of the PP-OCR detection input for a page
+ * (long side at most max_side, sides rounded to multiples of 32) and the factors back to the
+ * page (to_page may be NULL). */
+int ocr_nd_det_input_dims(uint32_t w, uint32_t h, uint32_t max_side, uint32_t *ow, uint32_t *oh, float *to_page);
+/* The detection input itself: rgb h x w x 3 bytes -> out [1][3][oh][ow] floats, bilinear
+ * half-pixel, BGR, ImageNet mean and deviation. Host buffers; the _device form takes device
+ * buffers and is queued on the context's stream. */
+int ocr_nd_det_input(ocr_ctx *ctx, const uint8_t *rgb, uint32_t w, uint32_t h, uint32_t max_side, float *out);
+int ocr_nd_det_input_device(ocr_ctx *ctx, const uint8_t *d_rgb, uint32_t w, uint32_t h, uint32_t max_side,
+                            float *d_out);
+/* DB thresholding (the first step of ppdet::boxes, src/ppdet.rs:88) on the GPU: prob (h rows of
+ * w floats) > thr as h rows of ceil(w / 32) bit words. */
+int ocr_db_threshold(ocr_ctx *ctx, const float *prob, uint32_t w, uint32_t h, float thr, uint32_t *bits);
+int ocr_db_threshold_device(ocr_ctx *ctx, const float *d_prob, uint32_t w, uint32_t h, float thr, uint32_t *d_bits);
+
 #ifdef __cplusplus
 }
 #endif

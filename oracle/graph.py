@@ -46,6 +46,7 @@ def lib():
         L.orc_mask_up_prob.argtypes = [P, I, I, I, I, I, F, F, P]
         L.orc_pack_bits.argtypes = [P, I, I, F, P]
         L.orc_line_crop.argtypes = [P, I, I, I, I, I, I, I, P, P, I, P]
+        L.orc_det_prep.argtypes = [P, I, I, I, I, P]
         L.orc_activate.argtypes = [F, I]
         L.orc_activate.restype = F
         _lib = L
@@ -96,6 +97,23 @@ def pool2d(x, kernel, strides, avg=False):
     return y
 
 
+def pool2d_padded(x, kernel, strides, pads, avg=False):
+    """Max / average pool with leading and trailing padding that is never counted (ONNX with
+    count_include_pad = 0), numpy."""
+    x = np.asarray(x, np.float32)
+    n, c, h, w = x.shape
+    pt, pl, pb, pr = pads
+    oh, ow = (h + pt + pb - kernel[0]) // strides[0] + 1, (w + pl + pr - kernel[1]) // strides[1] + 1
+    y = np.empty((n, c, oh, ow), np.float32)
+    for oy in range(oh):
+        y0, y1 = max(oy * strides[0] - pt, 0), min(oy * strides[0] - pt + kernel[0], h)
+        for ox in range(ow):
+            x0, x1 = max(ox * strides[1] - pl, 0), min(ox * strides[1] - pl + kernel[1], w)
+            win = x[:, :, y0:y1, x0:x1].astype(np.float64)
+            y[:, :, oy, ox] = win.mean(axis=(2, 3)) if avg else win.max(axis=(2, 3))
+    return y
+
+
 def gru(X, W, R, B, lens=None):
     X, W, R, B = _c(X), _c(W), _c(R), _c(B)
     T, N, I = X.shape
@@ -120,6 +138,20 @@ def _attr(node, name, default=None):
     return node.attrs.get(name, default)
 
 
+def _is_int(a):
+    return isinstance(a, np.ndarray) and np.issubdtype(a.dtype, np.integer)
+
+
+def _erf(v):
+    """The error function in float64 (scipy's, else the math module's, element by element)."""
+    try:
+        from scipy.special import erf
+        return erf(v)
+    except ImportError:  # pragma: no cover
+        import math
+        return np.vectorize(math.erf)(v)
+
+
 def run(model: onnx_read.Model, x: np.ndarray, want=()):
     """Run the whole graph on input x; returns (output, {name: value for name in want})."""
     vals = {model.input: np.asarray(x, np.float32)}
@@ -139,6 +171,8 @@ def run(model: onnx_read.Model, x: np.ndarray, want=()):
         op = nd.op
         if op == "Conv":
             w = ins[1]
+            if _attr(nd, "auto_pad", "NOTSET") not in ("NOTSET", b"NOTSET"):
+                raise ValueError("Conv auto_pad")
             pads = _attr(nd, "pads", [0, 0, 0, 0])
             pads = (pads[0], pads[1], pads[2], pads[3])
             if any(d != 1 for d in _attr(nd, "dilations", [1, 1])):
@@ -152,22 +186,89 @@ def run(model: onnx_read.Model, x: np.ndarray, want=()):
         elif op in ("MaxPool", "AveragePool"):
             k = _attr(nd, "kernel_shape")
             s = _attr(nd, "strides", [1] * len(k))
-            if any(_attr(nd, "pads", [0])) or _attr(nd, "ceil_mode", 0):
-                raise ValueError("padded/ceil pool")
-            y = pool2d(ins[0], k, s, avg=(op == "AveragePool"))
+            pads = _attr(nd, "pads", [0, 0, 0, 0])
+            if _attr(nd, "ceil_mode", 0) or _attr(nd, "count_include_pad", 0) or \
+                    _attr(nd, "auto_pad", "NOTSET") not in ("NOTSET", b"NOTSET"):
+                raise ValueError("ceil_mode / count_include_pad / auto_pad pool")
+            if any(pads):
+                y = pool2d_padded(ins[0], k, s, pads, avg=(op == "AveragePool"))
+            else:
+                y = pool2d(ins[0], k, s, avg=(op == "AveragePool"))
         elif op == "Relu":
             y = activate(ins[0], 1)
         elif op == "Sigmoid":
-            y = activate(ins[0], 2)
+            y = (1.0 / (1.0 + np.exp(-ins[0].astype(np.float64)))).astype(np.float32)
+        elif op == "HardSigmoid":
+            a, b = _attr(nd, "alpha", 0.2), _attr(nd, "beta", 0.5)
+            y = np.clip(np.float32(a) * ins[0] + np.float32(b), 0, 1).astype(np.float32)
+        elif op == "Erf":
+            y = _erf(ins[0].astype(np.float64)).astype(np.float32)
+        elif op == "Sqrt":
+            y = np.sqrt(ins[0]).astype(np.float32)
+        elif op in ("Add", "Sub", "Mul", "Div", "Pow"):
+            a, b = ins
+            if _is_int(a) and _is_int(b):
+                y = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply,
+                     "Div": lambda u, v: np.where(v == 0, 0, u // np.where(v == 0, 1, v)),
+                     "Pow": lambda u, v: u}[op](a, b).astype(np.int64)
+            else:
+                a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+                if op == "Pow":
+                    y = (a * a) if (b.size == 1 and float(b.reshape(-1)[0]) == 2.0) else np.power(a, b)
+                else:
+                    y = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply, "Div": np.divide}[op](a, b)
+                y = y.astype(np.float32)
+        elif op == "BatchNormalization":
+            g, b, m, v = (np.asarray(t, np.float64) for t in ins[1:5])
+            eps = _attr(nd, "epsilon", 1e-5)
+            sh = (1, -1) + (1,) * (ins[0].ndim - 2)
+            y = ((ins[0] - m.reshape(sh)) / np.sqrt(v.reshape(sh) + eps) * g.reshape(sh) + b.reshape(sh)).astype(np.float32)
+        elif op in ("ReduceMean", "GlobalAveragePool"):
+            xv = ins[0].astype(np.float64)
+            axes = tuple(range(2, xv.ndim)) if op == "GlobalAveragePool" else \
+                tuple(int(a) % xv.ndim for a in _attr(nd, "axes", range(xv.ndim)))
+            keep = op == "GlobalAveragePool" or bool(_attr(nd, "keepdims", 1))
+            y = xv.mean(axis=axes, keepdims=keep).astype(np.float32)
+        elif op == "Softmax":
+            ax = _attr(nd, "axis", -1)
+            v = ins[0].astype(np.float64)
+            e = np.exp(v - v.max(axis=ax, keepdims=True))
+            y = (e / e.sum(axis=ax, keepdims=True)).astype(np.float32)
+        elif op == "Resize":
+            if _attr(nd, "mode") != "nearest" or _attr(nd, "coordinate_transformation_mode") != "asymmetric":
+                raise ValueError("Resize other than nearest / asymmetric")
+            sc = np.asarray(ins[2], np.float32)
+            xv = ins[0]
+            oh, ow = int(np.floor(xv.shape[2] * sc[2])), int(np.floor(xv.shape[3] * sc[3]))
+            iy = np.minimum(np.floor(np.arange(oh, dtype=np.float32) / sc[2]).astype(int), xv.shape[2] - 1)
+            ix = np.minimum(np.floor(np.arange(ow, dtype=np.float32) / sc[3]).astype(int), xv.shape[3] - 1)
+            y = np.ascontiguousarray(xv[:, :, iy][:, :, :, ix])
         elif op == "Concat":
-            y = np.concatenate(ins, axis=_attr(nd, "axis"))
-        elif op == "Squeeze":
-            y = np.squeeze(ins[0], axis=tuple(int(a) for a in ins[1]))
+            if all(_is_int(t) for t in ins):
+                y = np.concatenate([np.asarray(t, np.int64).reshape(-1) for t in ins])
+            else:
+                y = np.concatenate(ins, axis=_attr(nd, "axis"))
+        elif op in ("Squeeze", "Unsqueeze"):
+            axes = _attr(nd, "axes") if _attr(nd, "axes") is not None else [int(a) for a in ins[1]]
+            if op == "Squeeze":
+                y = np.squeeze(ins[0], axis=tuple(int(a) % ins[0].ndim for a in axes))
+            else:
+                y = ins[0]
+                r = y.ndim + len(axes)
+                for a in sorted(int(a) % r for a in axes):
+                    y = np.expand_dims(y, a)
         elif op == "Transpose":
             y = np.ascontiguousarray(np.transpose(ins[0], _attr(nd, "perm")))
         elif op == "Reshape":
-            shape = [int(s) if s != 0 else ins[0].shape[i] for i, s in enumerate(ins[1])]
+            target = [int(v) for v in ins[1]]
+            shape = [ins[0].shape[i] if s == 0 else s for i, s in enumerate(target)]
             y = ins[0].reshape(shape)
+        elif op == "Shape":
+            y = np.array(np.shape(ins[0]), np.int64)
+        elif op == "Gather":
+            if _attr(nd, "axis", 0) != 0 or not _is_int(ins[0]):
+                raise ValueError("Gather other than of integers on axis 0")
+            y = np.asarray(ins[0], np.int64)[np.asarray(ins[1], np.int64)]
         elif op == "GRU":
             if _attr(nd, "linear_before_reset", 0) != 1:
                 raise ValueError("GRU linear_before_reset=0")
@@ -179,9 +280,7 @@ def run(model: onnx_read.Model, x: np.ndarray, want=()):
                 vals[nd.outputs[1]] = None
             continue
         elif op == "MatMul":
-            y = np.matmul(ins[0], ins[1]).astype(np.float32)
-        elif op == "Add":
-            y = (ins[0] + ins[1]).astype(np.float32)
+            y = np.matmul(ins[0].astype(np.float64), np.asarray(ins[1], np.float64)).astype(np.float32)
         elif op == "LogSoftmax":
             ax = _attr(nd, "axis", -1)
             v = ins[0].astype(np.float64)
@@ -193,11 +292,15 @@ def run(model: onnx_read.Model, x: np.ndarray, want=()):
             y = ins[0]
         elif op == "Slice":
             y = ins[0]
+            if len(ins) > 4 and ins[4] is not None and np.any(np.asarray(ins[4]) != 1):
+                raise ValueError("Slice with steps")
             axes = ins[3] if len(ins) > 3 and ins[3] is not None else range(len(ins[1]))
             sl = [slice(None)] * y.ndim
             for st, en, ax in zip(ins[1], ins[2], axes):
                 sl[int(ax)] = slice(int(st), int(en))
             y = np.ascontiguousarray(y[tuple(sl)])
+        elif op in ("Cast", "Identity"):
+            y = ins[0]
         else:
             raise ValueError(f"oracle: unsupported op {op}")
         vals[nd.outputs[0]] = y
@@ -314,3 +417,31 @@ def page_pipeline(det_model, rec_model, page, thr, layout_of):
 
 # ocr-bench.rs:31: class k > 0 is ALPHABET[k - 1].
 ALPHABET = " 0123456789!\"#$%&'()*+,-./:;<=>?@[\\]^_`{|}~EABCDEFGHIJKLMNOPQRSTUVWXYZabcdefghijklmnopqrstuvwxyz"
+
+
+# ------------------------------------------------------------------------------------------
+# PP-OCR front and back ends (src/nd.rs:1353-1369, src/ppdet.rs:29-44, 87-132)
+# ------------------------------------------------------------------------------------------
+def det_input_size(w, h, max_side):
+    """nd.rs:1356-1358: long side at most max_side, each side rounded to the nearest multiple of
+    32 (at least 32; halves away from zero, as Rust's f32::round)."""
+    ratio = np.float32(max_side) / np.float32(max(w, h)) if max(w, h) > max_side else np.float32(1.0)
+    def round32(v):
+        q = np.float32(v) / np.float32(32.0)
+        return max(int(np.floor(q + np.float32(0.5))) * 32, 32)
+    return round32(np.float32(w) * ratio), round32(np.float32(h) * ratio)
+
+
+def det_prep(rgb, max_side):
+    """The detection input [1, 3, oh, ow] (see orc_det_prep)."""
+    rgb = _c(rgb, np.uint8)
+    h, w = rgb.shape[:2]
+    ow, oh = det_input_size(w, h, max_side)
+    y = np.empty((1, 3, oh, ow), np.float32)
+    lib().orc_det_prep(_p(rgb), w, h, ow, oh, _p(y))
+    return y
+
+
+def threshold_bits(prob, thr):
+    """ppdet.rs:88 as bit rows: prob [h, w] > thr, bit x % 32 of word x / 32."""
+    return pack_bits(np.asarray(prob, np.float32), thr)

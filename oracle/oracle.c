@@ -15,6 +15,7 @@
  *   orc_pack_bits         bit layout closed form
  *   orc_line_crop         torch bilinear golden of span-masked grey crops
  *   orc_activate          sigmoid closed form via the conv golden; ReLU by the conv goldens
+ *   orc_det_prep          torch bilinear (half-pixel) golden of the BGR-normalised page
  */
 #include <math.h>
 #include <stdint.h>
@@ -268,5 +269,28 @@ void orc_line_crop(const uint8_t *rgb, int pw, int ph, int left, int top, int bw
                 v = mixf(t0, b0, fy);
             }
             dst[(size_t)oy * wb + ox] = v;
+        }
+}
+
+/* PP-OCR detection input (src/nd.rs:172-204, NdGraph::det_input nd.rs:1353-1369): the page's RGB
+ * bytes resized bilinearly (half-pixel, clamped, x then y with the reference's mix) to ow x oh,
+ * channels in BGR order, each (v / 255 - mean) / dev with ImageNet's mean and deviation.
+ * Output [3][oh][ow]. */
+void orc_det_prep(const uint8_t *rgb, int w, int h, int ow, int oh, float *y) {
+    const float mean[3] = {0.485f, 0.456f, 0.406f}, dev[3] = {0.229f, 0.224f, 0.225f};
+    const float sx = (float)w / (float)ow, sy = (float)h / (float)oh;
+    for (int oy = 0; oy < oh; oy++)
+        for (int ox = 0; ox < ow; ox++) {
+            float ix = fminf(fmaxf(sx * ((float)ox + 0.5f) - 0.5f, 0.f), (float)w - 1.f);
+            float iy = fminf(fmaxf(sy * ((float)oy + 0.5f) - 0.5f, 0.f), (float)h - 1.f);
+            int x1 = (int)ix, y1 = (int)iy;
+            int x2 = x1 + 1 < w - 1 ? x1 + 1 : w - 1, y2 = y1 + 1 < h - 1 ? y1 + 1 : h - 1;
+            float fx = ix - (float)x1, fy = iy - (float)y1;
+            for (int c = 0; c < 3; c++) {
+                int k = 2 - c;
+                float a = mixf((float)rgb[((size_t)y1 * w + x1) * 3 + k], (float)rgb[((size_t)y1 * w + x2) * 3 + k], fx);
+                float b = mixf((float)rgb[((size_t)y2 * w + x1) * 3 + k], (float)rgb[((size_t)y2 * w + x2) * 3 + k], fx);
+                y[((size_t)c * oh + oy) * ow + ox] = (mixf(a, b, fy) / 255.f - mean[c]) / dev[c];
+            }
         }
 }

@@ -149,6 +149,41 @@ def softmax_cases():
     return {"ls": dict(x=x, y=F.log_softmax(t(x), dim=2).numpy())}
 
 
+def nd_cases():
+    """Operators of the N-D (PP-OCR) graphs: LayerNorm, attention, BatchNormalization, GELU, SiLU,
+    nearest resize x2, padded strided pools, a depthwise conv with stride (2, 1) and the PP-OCR
+    detection input (bilinear half-pixel of the page's bytes, BGR, ImageNet normalisation)."""
+    c = {}
+    x = f32(3, 7, 120)
+    g, b = f32(120, scale=0.2) + 1, f32(120, scale=0.1)
+    c["ln"] = dict(x=x, g=g, b=b, y=F.layer_norm(t(x), (120,), t(g), t(b), eps=1e-6).numpy())
+    q, k, v = f32(2, 8, 9, 15), f32(2, 8, 9, 15), f32(2, 8, 9, 15)
+    att = torch.softmax((t(q) * 15 ** -0.5) @ t(k).transpose(2, 3).contiguous(), dim=-1)
+    c["attn"] = dict(q=q, k=k, v=v, y=(att @ t(v)).numpy())
+    x = f32(2, 5, 6, 7)
+    gm, bt, mu, var = f32(5, scale=0.2) + 1, f32(5, scale=0.1), f32(5, scale=0.1), np.abs(f32(5)) + 0.5
+    c["bn"] = dict(x=x, g=gm, b=bt, m=mu, v=var,
+                   y=F.batch_norm(t(x), t(mu), t(var), t(gm), t(bt), training=False, eps=1e-5).numpy())
+    x = f32(4, 33, scale=2.0)
+    c["gelu"] = dict(x=x, y=F.gelu(t(x)).numpy())
+    c["silu"] = dict(x=x, y=F.silu(t(x)).numpy())
+    x = f32(1, 3, 5, 7)
+    c["resize2"] = dict(x=x, y=F.interpolate(t(x), scale_factor=2.0, mode="nearest").numpy())
+    x = f32(2, 3, 9, 10)
+    c["avgpool_pad"] = dict(x=x, y=F.avg_pool2d(t(x), 3, 2, padding=1, count_include_pad=False).numpy())
+    c["maxpool_pad"] = dict(x=x, y=F.max_pool2d(t(x), 3, 2, padding=1).numpy())
+    x, wd = f32(1, 6, 9, 8), f32(6, 1, 3, 3, scale=0.3)
+    c["dw_s21"] = dict(x=x, w=wd, y=F.conv2d(F.pad(t(x), (1, 1, 1, 1)), t(wd), stride=(2, 1), groups=6).numpy())
+    rgb = rng.integers(0, 256, (53, 70, 3), dtype=np.uint8)
+    bgr = t(rgb[..., ::-1].astype(np.float32).transpose(2, 0, 1).copy())[None]
+    ow, oh = 64, 64  # 70 x 53 with max side 64: ratio 64 / 70 gives 64 x 48.5, rounded to multiples of 32
+    img = F.interpolate(bgr, size=(oh, ow), mode="bilinear", align_corners=False)[0]
+    mean = torch.tensor([0.485, 0.456, 0.406]).reshape(3, 1, 1)
+    dev = torch.tensor([0.229, 0.224, 0.225]).reshape(3, 1, 1)
+    c["det_prep"] = dict(rgb=rgb, max_side=np.array(64), y=((img / 255.0 - mean) / dev).numpy()[None])
+    return c
+
+
 def save(name, cases):
     flat = {f"{c}__{k}": v for c, d in cases.items() for k, v in d.items()}
     np.savez_compressed(os.path.join(OUT, f"{name}.npz"), **flat)
@@ -162,4 +197,5 @@ if __name__ == "__main__":
     save("resize", resize_cases())
     save("logsoftmax", softmax_cases())
     save("line_crop", line_crop_cases())
+    save("nd", nd_cases())
     print("written to", OUT)

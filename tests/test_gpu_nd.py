@@ -1,0 +1,237 @@
+"""The N-D executor (NdGraph, src/nd.rs) on the GPU against the oracle, through the C ABI
+(ocr_nd_*): every fusion pattern and operator on small graphs, then the PP-OCRv6-architecture
+recogniser (36 lines, widths in [160, 960]) and the DB detector's front end and map.
+
+Tolerances: float32 activations go through the matrix cores as float16 hi + lo (about 2^-22
+relative), so results agree with the float32 oracle to float32 rounding:
+|gpu - oracle| <= 1e-4 * (1 + |oracle|) per operator. Recognition: the identical arg-max at every
+CTC step and probabilities within 1e-3. Detection: probabilities within 1e-4, so the thresholded
+mask is bit-exact outside the 1e-4 band around the threshold."""
+import numpy as np
+import pytest
+
+from ocrhip import onnx_write as ow
+from ocrhip import synth_pp
+from oracle import graph as og
+from oracle import onnx_read
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.Generator(np.random.PCG64(91))
+
+
+def f16x(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def build(tmp_path, name, fn, in_shape):
+    g = ow.Graph(name)
+    out = fn(g, "x")
+    p = tmp_path / f"{name}.onnx"
+    p.write_bytes(g.model("x", list(in_shape), out, ["a"] * 1))
+    return str(p)
+
+
+def check(ctx, path, x, tol=1e-4, stop=False):
+    import ocrhip
+    print(f"nd graph {path} input {x.shape}", flush=True)
+    got = ocrhip.NdGraph(ctx, path, stop).run(x)
+    want, _ = og.run(onnx_read.load(path), x)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    err = np.abs(got - want) / (1 + np.abs(want))
+    assert err.max() <= tol, f"max rel err {err.max()}"
+    return got, want
+
+
+def w(g, shape, fan, exact=True):
+    a = RNG.standard_normal(shape).astype(np.float32) * np.float32(np.sqrt(2 / fan))
+    return g.init(g.fresh("w"), f16x(a) if exact else a)
+
+
+def conv(g, x, cin, cout, k=3, stride=(1, 1), group=1, bias=True, exact=True):
+    ins = [x, w(g, (cout, cin // group, k, k), cin // group * k * k, exact)]
+    if bias:
+        ins.append(g.init(g.fresh("b"), (RNG.standard_normal(cout) * 0.1).astype(np.float32)))
+    return g.add("Conv", ins, kernel_shape=[k, k], pads=[k // 2] * 4, strides=list(stride), group=group)
+
+
+def bn(g, x, c):
+    vals = [RNG.uniform(0.8, 1.2, c), RNG.uniform(-.1, .1, c), RNG.uniform(-.1, .1, c), RNG.uniform(.5, 1.5, c)]
+    return g.add("BatchNormalization", [x] + [g.init(g.fresh("bn"), v.astype(np.float32)) for v in vals], epsilon=1e-5)
+
+
+def const(g, v):
+    return g.init(g.fresh("c"), np.array([v], np.float32))
+
+
+def ints(g, v):
+    return g.init(g.fresh("i"), np.array(v, np.int64))
+
+
+def test_conv_bn_relu_nchw_mfma(ctx, tmp_path):
+    p = build(tmp_path, "cbr", lambda g, x: g.add("Relu", [bn(g, conv(g, x, 24, 40, bias=False), 40)]), (2, 24, 11, 29))
+    check(ctx, p, RNG.standard_normal((2, 24, 11, 29)).astype(np.float32))
+
+
+def test_conv_bias_add_and_1x1(ctx, tmp_path):
+    def fn(g, x):
+        y = conv(g, x, 16, 32, k=1, bias=False)
+        y = g.add("Add", [y, g.init("ab", (RNG.standard_normal((1, 32, 1, 1)) * 0.1).astype(np.float32))])
+        return g.add("Relu", [y])
+    p = build(tmp_path, "cba", fn, (1, 16, 6, 45))
+    check(ctx, p, RNG.standard_normal((1, 16, 6, 45)).astype(np.float32))
+
+
+def test_strided_and_depthwise_convs(ctx, tmp_path):
+    def fn(g, x):
+        y = g.add("Relu", [bn(g, conv(g, x, 3, 16, stride=(2, 2), bias=False), 16)])
+        y = g.add("Relu", [conv(g, y, 16, 16, group=16)])
+        return g.add("Relu", [bn(g, conv(g, y, 16, 16, stride=(2, 1), group=16, bias=False), 16)])
+    p = build(tmp_path, "sd", fn, (2, 3, 24, 40))
+    check(ctx, p, RNG.standard_normal((2, 3, 24, 40)).astype(np.float32))
+
+
+def test_se_gate_gelu_residual(ctx, tmp_path):
+    def fn(g, x):
+        se = g.add("GlobalAveragePool", [x])
+        se = g.add("Relu", [conv(g, se, 32, 8, k=1)])
+        se = g.add("HardSigmoid", [conv(g, se, 8, 32, k=1)], alpha=0.2, beta=0.5)
+        y = g.add("Mul", [x, se])
+        y = conv(g, y, 32, 32, k=1)
+        d = g.add("Div", [y, const(g, np.float32(np.sqrt(2.0)))])
+        e = g.add("Erf", [d])
+        a = g.add("Add", [e, const(g, 1.0)])
+        m = g.add("Mul", [y, a])
+        y = g.add("Mul", [m, const(g, 0.5)])
+        return g.add("Add", [y, x])
+    p = build(tmp_path, "seg", fn, (2, 32, 3, 17))
+    check(ctx, p, RNG.standard_normal((2, 32, 3, 17)).astype(np.float32))
+
+
+def test_linear_silu_and_inexact_weights(ctx, tmp_path):
+    def fn(g, x):
+        y = g.add("MatMul", [x, w(g, (120, 240), 120)])
+        y = g.add("Add", [y, g.init("lb", (RNG.standard_normal(240) * 0.1).astype(np.float32))])
+        s = g.add("Sigmoid", [y])
+        y = g.add("Mul", [y, s])
+        return g.add("MatMul", [y, w(g, (240, 50), 240, exact=False)])
+    p = build(tmp_path, "lin", fn, (3, 37, 120))
+    check(ctx, p, RNG.standard_normal((3, 37, 120)).astype(np.float32))
+
+
+def test_layer_norm_and_attention(ctx, tmp_path):
+    def fn(g, x):
+        b = synth_pp._B("t", 5)
+        b.g = g
+        return synth_pp._svtr_block(b, x)
+    p = build(tmp_path, "svtr", fn, (2, 23, 120))
+    check(ctx, p, RNG.standard_normal((2, 23, 120)).astype(np.float32))
+
+
+def test_pools_resize_convt_concat(ctx, tmp_path):
+    def fn(g, x):
+        a = g.add("AveragePool", [x], kernel_shape=[3, 3], strides=[2, 2], pads=[1, 1, 1, 1])
+        m = g.add("MaxPool", [x], kernel_shape=[3, 3], strides=[2, 2], pads=[1, 1, 1, 1])
+        y = g.add("Concat", [a, m], axis=1)
+        y = g.add("Resize", [y, "", g.init("sc", np.array([1, 1, 2, 2], np.float32))], mode="nearest",
+                  coordinate_transformation_mode="asymmetric", nearest_mode="floor")
+        t = g.add("ConvTranspose", [y, w(g, (12, 5, 2, 2), 12), g.init("tb", np.full(5, 0.05, np.float32))],
+                  kernel_shape=[2, 2], strides=[2, 2])
+        t = g.add("Sigmoid", [t])
+        r = g.add("ReduceMean", [t], axes=[2, 3], keepdims=0)
+        return g.add("Concat", [r, g.add("Sqrt", [g.add("Mul", [r, r])])], axis=1)
+    p = build(tmp_path, "prc", fn, (2, 6, 9, 10))
+    check(ctx, p, RNG.standard_normal((2, 6, 9, 10)).astype(np.float32))
+
+
+def test_binary_broadcast_and_shape_ops(ctx, tmp_path):
+    def fn(g, x):
+        sh = g.add("Shape", [x])
+        nt = g.add("Gather", [sh, ints(g, [0, 1])], axis=0)
+        s5 = g.add("Concat", [nt, ints(g, [2, 3])], axis=0)
+        y = g.add("Reshape", [x, s5])                       # [2, 5, 2, 3]
+        y = g.add("Transpose", [y], perm=[0, 2, 1, 3])      # [2, 2, 5, 3]
+        z = g.add("Sub", [y, g.init("row", RNG.standard_normal(3).astype(np.float32))])
+        z = g.add("Div", [z, g.init("col", (RNG.uniform(1, 2, (1, 2, 5, 1))).astype(np.float32))])
+        z = g.add("Pow", [z, const(g, 2.0)])
+        z = g.add("Slice", [z, ints(g, [1, 0]), ints(g, [4, 2]), ints(g, [2, 3])])
+        return g.add("Unsqueeze", [g.add("Squeeze", [g.add("Unsqueeze", [z, ints(g, [0])]), ints(g, [0])]), ints(g, [1])])
+    p = build(tmp_path, "bin", fn, (2, 5, 6))
+    check(ctx, p, RNG.standard_normal((2, 5, 6)).astype(np.float32))
+
+
+def test_unsupported_and_bad_shapes_raise(ctx, tmp_path):
+    import ocrhip
+    p = build(tmp_path, "bad", lambda g, x: g.add("Tanh", [x]), (1, 4))
+    g = ocrhip.NdGraph(ctx, p)
+    with pytest.raises(ocrhip.OcrError, match="unsupported op Tanh"):
+        g.run(np.zeros((1, 4), np.float32))
+    p = build(tmp_path, "c", lambda g, x: conv(g, x, 8, 8), (1, 8, 5, 5))
+    with pytest.raises(ocrhip.OcrError, match="channels"):
+        ocrhip.NdGraph(ctx, p).run(np.zeros((1, 6, 5, 5), np.float32))
+
+
+# ---- the PP-OCRv6-architecture models ------------------------------------------------------------
+@pytest.fixture(scope="module")
+def pp_rec_path():
+    return synth_pp.model_path("rec")
+
+
+@pytest.fixture(scope="module")
+def pp_lines():
+    return synth_pp.batch_lines(synth_pp.rec_lines(36))
+
+
+def test_pp_recognition_config4(ctx, pp_rec_path, pp_lines):
+    """36 lines, widths in [160, 960], batches sorted by width (16 a batch): the GPU's softmax
+    within 1e-3 of the oracle's and the identical arg-max (the fused head) at every step."""
+    import ocrhip
+    full = ocrhip.NdGraph(ctx, pp_rec_path)
+    head = ocrhip.NdGraph(ctx, pp_rec_path, stop_before_softmax=True)
+    model = onnx_read.load(pp_rec_path)
+    batches, _ = pp_lines
+    steps = 0
+    for data, n, wd in batches:
+        print(f"pp rec batch n={n} w={wd}", flush=True)
+        want, _ = og.run(model, data)
+        got = full.run(data)
+        assert got.shape == want.shape == (n, wd // 8, synth_pp.PP_CLASSES)
+        assert np.abs(got - want).max() <= 1e-3
+        best = head.argmax(data)
+        want_best = np.argmax(want, axis=-1)  # first index on ties, as nd.rs:383
+        assert np.array_equal(best, want_best), f"{int((best != want_best).sum())} steps differ"
+        steps += best.size
+    assert steps == sum(n * wd // 8 for _, n, wd in batches)
+
+
+def test_pp_head_argmax_matches_materialised_logits(ctx, pp_rec_path, pp_lines):
+    """The fused head arg-max equals the arg-max over the head's own logits on the GPU."""
+    import ocrhip
+    head = ocrhip.NdGraph(ctx, pp_rec_path, stop_before_softmax=True)
+    data, n, wd = pp_lines[0][0]
+    logits = head.run(data)
+    assert np.array_equal(head.argmax(data), np.argmax(logits, axis=-1))
+
+
+def test_pp_det_input_matches_oracle(ctx):
+    import ocrhip
+    from ocrhip import synth
+    page = np.ascontiguousarray(synth.page(1)[:1700, :1300])
+    got = ocrhip.det_input(ctx, page, synth_pp.DET_MAX_SIDE)
+    want = og.det_prep(page, synth_pp.DET_MAX_SIDE)
+    assert got.shape == want.shape
+    # The same float32 operations in the same order, none fused, on both sides: bit-exact.
+    np.testing.assert_array_equal(got, want)
+
+
+def test_pp_detection_map_and_threshold(ctx):
+    """The DB detector on a 960 x 736 input: probabilities within 1e-4 of the oracle; the GPU
+    threshold (0.3) bit-exact against the oracle's on the same map."""
+    import ocrhip
+    path = synth_pp.model_path("det")
+    x = RNG.standard_normal((1, 3, 960, 736)).astype(np.float32)
+    got, want = check(ctx, path, x)
+    assert np.abs(got - want).max() <= 1e-4
+    bits = ocrhip.db_threshold(ctx, got[0, 0], 0.3)
+    assert np.array_equal(bits, og.threshold_bits(got[0, 0], 0.3))
+    band = np.abs(want[0, 0] - 0.3) < 1e-4
+    assert np.array_equal((got[0, 0] > 0.3)[~band], (want[0, 0] > 0.3)[~band])

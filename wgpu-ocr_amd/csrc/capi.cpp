@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "models.h"
+#include "nd.h"
 #include "pipeline.h"
 
 using namespace ocr;
@@ -31,6 +32,10 @@ struct ocr_layout {
 struct ocr_pipeline {
     ocr_ctx *owner;
     std::unique_ptr<Pipeline> pipe;
+};
+struct ocr_nd {
+    ocr_ctx *owner;
+    NdGraph graph;
 };
 
 namespace {
@@ -487,6 +492,206 @@ int ocr_pipeline_line_text(ocr_pipeline *pipe, uint32_t page, uint32_t line, cha
             std::copy(s.begin(), s.begin() + long(n), buf);
             buf[n] = 0;
         }
+    });
+}
+
+
+}  // extern "C"
+
+// ---- N-D executor (PP-OCRv6) -------------------------------------------------------------------
+
+namespace {
+
+std::vector<int64_t> shape_in(const int64_t *shape, uint32_t rank) {
+    if (rank == 0 || rank > uint32_t(ND_RANK)) fail("rank must be 1 to 6");
+    need(shape, "shape");
+    std::vector<int64_t> s(shape, shape + rank);
+    for (int64_t d : s)
+        if (d <= 0) fail("shape with a zero or negative dimension");
+    return s;
+}
+
+size_t count_of(const std::vector<int64_t> &s) {
+    size_t c = 1;
+    for (int64_t d : s) c *= size_t(d);
+    return c;
+}
+
+// PP-OCR detection input size (src/nd.rs:1356-1358): long side at most max_side, each side
+// rounded to the nearest multiple of 32 (at least 32).
+void det_input_size(uint32_t w, uint32_t h, uint32_t max_side, int *ow, int *oh) {
+    if (w == 0 || h == 0 || max_side == 0) fail("det input: empty page or max_side 0");
+    const float ratio = std::max(w, h) > max_side ? float(max_side) / float(std::max(w, h)) : 1.f;
+    auto round32 = [](float v) { return std::max(int(std::lround(v / 32.f)) * 32, 32); };
+    *ow = round32(float(w) * ratio);
+    *oh = round32(float(h) * ratio);
+}
+
+}  // namespace
+
+extern "C" {
+
+ocr_nd *ocr_nd_new(ocr_ctx *ctx, const char *onnx_path, int stop_before_softmax) {
+    return guard_ptr<ocr_nd>([&] {
+        need(ctx, "ctx");
+        need(onnx_path, "onnx_path");
+        ctx->ctx->bind();
+        Onnx m = Onnx::load(onnx_path);
+        auto g = std::make_unique<ocr_nd>();
+        g->owner = ctx;
+        g->graph = NdGraph::build(*ctx->ctx, m, stop_before_softmax != 0);
+        return g.release();
+    });
+}
+
+void ocr_nd_free(ocr_nd *g) { delete g; }
+
+int ocr_nd_dims(ocr_nd *g, const int64_t *in_shape, uint32_t rank, int64_t *out_shape, uint32_t *out_rank) {
+    return guard([&] {
+        need(g, "graph");
+        need(out_shape, "out_shape");
+        need(out_rank, "out_rank");
+        auto s = g->graph.output_shape(shape_in(in_shape, rank));
+        if (s.size() > size_t(ND_RANK)) fail("output rank above 6");
+        std::copy(s.begin(), s.end(), out_shape);
+        *out_rank = uint32_t(s.size());
+    });
+}
+
+int ocr_nd_run_device(ocr_nd *g, const float *d_in, const int64_t *in_shape, uint32_t rank, float *d_out) {
+    return guard([&] {
+        need(g, "graph");
+        need(d_in, "input");
+        need(d_out, "output");
+        Ctx &c = *g->owner->ctx;
+        c.bind();
+        NdTensor x;
+        x.p = const_cast<float *>(d_in);
+        x.shape = shape_in(in_shape, rank);
+        NdTensor y = g->graph.run(c, x);
+        OCR_HIP(hipMemcpyAsync(d_out, y.p, y.count() * sizeof(float), hipMemcpyDeviceToDevice, c.stream()));
+    });
+}
+
+int ocr_nd_run(ocr_nd *g, const float *in, const int64_t *in_shape, uint32_t rank, float *out) {
+    return guard([&] {
+        need(g, "graph");
+        need(in, "input");
+        need(out, "output");
+        Ctx &c = *g->owner->ctx;
+        c.bind();
+        NdTensor x;
+        x.shape = shape_in(in_shape, rank);
+        DBuf din(&c, count_of(x.shape) * sizeof(float));
+        x.p = din.as<float>();
+        c.h2d(x.p, in, count_of(x.shape) * sizeof(float));
+        NdTensor y = g->graph.run(c, x);
+        c.d2h(out, y.p, y.count() * sizeof(float));
+    });
+}
+
+int ocr_nd_argmax_device(ocr_nd *g, const float *d_in, const int64_t *in_shape, uint32_t rank, uint32_t *d_best) {
+    return guard([&] {
+        need(g, "graph");
+        need(d_in, "input");
+        need(d_best, "best");
+        Ctx &c = *g->owner->ctx;
+        c.bind();
+        NdTensor x;
+        x.p = const_cast<float *>(d_in);
+        x.shape = shape_in(in_shape, rank);
+        g->graph.run_argmax(c, x, d_best, nullptr);
+    });
+}
+
+int ocr_nd_argmax(ocr_nd *g, const float *in, const int64_t *in_shape, uint32_t rank, uint32_t *best) {
+    return guard([&] {
+        need(g, "graph");
+        need(in, "input");
+        need(best, "best");
+        Ctx &c = *g->owner->ctx;
+        c.bind();
+        NdTensor x;
+        x.shape = shape_in(in_shape, rank);
+        auto os = g->graph.output_shape(x.shape);
+        if (os.empty()) fail("arg-max of a scalar output");
+        const size_t rows = count_of(os) / size_t(os.back());
+        DBuf din(&c, count_of(x.shape) * sizeof(float)), dbest(&c, std::max<size_t>(rows, 1) * 4);
+        x.p = din.as<float>();
+        c.h2d(x.p, in, count_of(x.shape) * sizeof(float));
+        g->graph.run_argmax(c, x, dbest.as<uint32_t>(), nullptr);
+        c.d2h(best, dbest.get(), rows * 4);
+    });
+}
+
+int ocr_nd_det_input_dims(uint32_t w, uint32_t h, uint32_t max_side, uint32_t *ow, uint32_t *oh, float *to_page) {
+    return guard([&] {
+        need(ow, "ow");
+        need(oh, "oh");
+        int a = 0, b = 0;
+        det_input_size(w, h, max_side, &a, &b);
+        *ow = uint32_t(a);
+        *oh = uint32_t(b);
+        if (to_page) {
+            to_page[0] = float(w) / float(a);
+            to_page[1] = float(h) / float(b);
+        }
+    });
+}
+
+int ocr_nd_det_input_device(ocr_ctx *ctx, const uint8_t *d_rgb, uint32_t w, uint32_t h, uint32_t max_side,
+                            float *d_out) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(d_rgb, "rgb");
+        need(d_out, "output");
+        ctx->ctx->bind();
+        int ow = 0, oh = 0;
+        det_input_size(w, h, max_side, &ow, &oh);
+        nd_det_prep(d_rgb, int(w), int(h), d_out, ow, oh, ctx->ctx->stream());
+    });
+}
+
+int ocr_nd_det_input(ocr_ctx *ctx, const uint8_t *rgb, uint32_t w, uint32_t h, uint32_t max_side, float *out) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(rgb, "rgb");
+        need(out, "output");
+        Ctx &c = *ctx->ctx;
+        c.bind();
+        int ow = 0, oh = 0;
+        det_input_size(w, h, max_side, &ow, &oh);
+        DBuf drgb(&c, size_t(w) * h * 3), dout(&c, size_t(3) * ow * oh * sizeof(float));
+        c.h2d(drgb.get(), rgb, size_t(w) * h * 3);
+        nd_det_prep(drgb.as<uint8_t>(), int(w), int(h), dout.as<float>(), ow, oh, c.stream());
+        c.d2h(out, dout.get(), size_t(3) * ow * oh * sizeof(float));
+    });
+}
+
+int ocr_db_threshold_device(ocr_ctx *ctx, const float *d_prob, uint32_t w, uint32_t h, float thr, uint32_t *d_bits) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(d_prob, "prob");
+        need(d_bits, "bits");
+        if (w == 0 || h == 0) fail("empty probability map");
+        ctx->ctx->bind();
+        nd_threshold_bits(d_prob, int(w), int(h), thr, d_bits, ctx->ctx->stream());
+    });
+}
+
+int ocr_db_threshold(ocr_ctx *ctx, const float *prob, uint32_t w, uint32_t h, float thr, uint32_t *bits) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(prob, "prob");
+        need(bits, "bits");
+        if (w == 0 || h == 0) fail("empty probability map");
+        Ctx &c = *ctx->ctx;
+        c.bind();
+        const size_t words = size_t((w + 31) / 32) * h;
+        DBuf dp(&c, size_t(w) * h * sizeof(float)), db(&c, words * 4);
+        c.h2d(dp.get(), prob, size_t(w) * h * sizeof(float));
+        nd_threshold_bits(dp.as<float>(), int(w), int(h), thr, db.as<uint32_t>(), c.stream());
+        c.d2h(bits, db.get(), words * 4);
     });
 }
 

@@ -27,13 +27,20 @@ ConvPack plan_conv_pack(int cin, int cout, int kh, int kw);
 void pack_conv_weights(const ConvPack &pk, const float *w, uint16_t *hi, uint16_t *lo, bool *exact);
 
 struct ConvArgs {
-    Act x, y;                       // input and output views (NHWC)
+    Act x, y;                       // input and output views (NHWC, or NCHW with nchw set)
     const uint16_t *wt_hi = nullptr, *wt_lo = nullptr;
     const float *bias = nullptr;    // [cout] or null
     const float *res = nullptr;     // residual added after the activation (gpu.rs:65), or null
     int res_cs = 0;
     int pt = 0, pl = 0;             // leading pads (stride 1)
     int act = ACT_NONE;
+    bool nchw = false;              // x and y (and res) are NCHW tensors (the N-D executor)
+    const float *affine = nullptr;  // BatchNormalization folded: scale[cout] then shift[cout]
+    const float *in_scale = nullptr;  // [n][cin] input scale (the SE gate), or null
+    // When set, no output is written: for every output pixel (GEMM row) and block of BN
+    // channels, (max value, index as float bits) of acc + bias, first index on ties, at
+    // amax_part[pixel * nblocks + block] (float2 pairs).
+    float *amax_part = nullptr;
     ConvPack pk;
 };
 // True when the MFMA path takes this shape (stride 1, kernel at most 3 x 3).

@@ -39,9 +39,10 @@ struct ConvParams {
     float *y;
     int oh, ow, cout, ycs;
     const half8 *wt_hi, *wt_lo;
-    const float *bias, *res;
+    const float *bias, *res, *affine, *in_scale;
+    float2 *amax;  // arg-max partials [pixels][nblocks] instead of y, or null
     int rcs;
-    int kh, kw, pt, pl, act, chunks, tiles_x, tiles_y, vec;
+    int kh, kw, pt, pl, act, chunks, tiles_x, tiles_y, vec, nchw;
 };
 
 __device__ inline float activate_dev(float v, int act) {
@@ -83,28 +84,53 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
     const int g = lane >> 4, r = lane & 15;
     for (int chunk = 0; chunk < p.chunks; chunk++) {
         const int ci0 = chunk * 32;
-        // Stage the halo as hi/lo float16, zero outside the image and past cin.
-        for (int i = tid; i < HALO * 8; i += 256) {
-            const int hp = i >> 3, q = i & 7;
-            const int hy = hp / HWD, hx = hp - hy * HWD;
-            const int iy = iy0 + hy, ix = ix0 + hx, ci = ci0 + 4 * q;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w && ci < p.cin) {
-                const float *src = xim + (size_t(iy) * p.w + ix) * p.xcs + ci;
-                if (p.vec) {
-                    v = *reinterpret_cast<const float4 *>(src);
-                } else {
-                    v.x = src[0];
-                    if (ci + 1 < p.cin) v.y = src[1];
-                    if (ci + 2 < p.cin) v.z = src[2];
-                    if (ci + 3 < p.cin) v.w = src[3];
+        // Stage the halo as hi/lo float16, zero outside the image and past cin; the SE gate
+        // (in_scale) multiplies the input first.
+        if (p.nchw) {
+            // NCHW: consecutive threads take consecutive pixels of one channel.
+            for (int i = tid; i < HALO * 32; i += 256) {
+                const int cl = i / HALO, hp = i - cl * HALO;
+                const int hy = hp / HWD, hx = hp - hy * HWD;
+                const int iy = iy0 + hy, ix = ix0 + hx, ci = ci0 + cl;
+                float v = 0.f;
+                if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w && ci < p.cin) {
+                    v = p.x[((size_t(img) * p.cin + ci) * p.h + iy) * p.w + ix];
+                    if (p.in_scale) v *= p.in_scale[size_t(img) * p.cin + ci];
                 }
+                const _Float16 hi = (_Float16)v;
+                s_hi[hp][cl] = hi;
+                s_lo[hp][cl] = (_Float16)(v - (float)hi);
             }
-            half4 hi = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-            half4 lo = {(_Float16)(v.x - (float)hi[0]), (_Float16)(v.y - (float)hi[1]),
-                        (_Float16)(v.z - (float)hi[2]), (_Float16)(v.w - (float)hi[3])};
-            *reinterpret_cast<half4 *>(&s_hi[hp][4 * q]) = hi;
-            *reinterpret_cast<half4 *>(&s_lo[hp][4 * q]) = lo;
+        } else {
+            for (int i = tid; i < HALO * 8; i += 256) {
+                const int hp = i >> 3, q = i & 7;
+                const int hy = hp / HWD, hx = hp - hy * HWD;
+                const int iy = iy0 + hy, ix = ix0 + hx, ci = ci0 + 4 * q;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w && ci < p.cin) {
+                    const float *src = xim + (size_t(iy) * p.w + ix) * p.xcs + ci;
+                    if (p.vec) {
+                        v = *reinterpret_cast<const float4 *>(src);
+                    } else {
+                        v.x = src[0];
+                        if (ci + 1 < p.cin) v.y = src[1];
+                        if (ci + 2 < p.cin) v.z = src[2];
+                        if (ci + 3 < p.cin) v.w = src[3];
+                    }
+                    if (p.in_scale) {
+                        const float *sc = p.in_scale + size_t(img) * p.cin + ci;
+                        v.x *= sc[0];
+                        if (ci + 1 < p.cin) v.y *= sc[1];
+                        if (ci + 2 < p.cin) v.z *= sc[2];
+                        if (ci + 3 < p.cin) v.w *= sc[3];
+                    }
+                }
+                half4 hi = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+                half4 lo = {(_Float16)(v.x - (float)hi[0]), (_Float16)(v.y - (float)hi[1]),
+                            (_Float16)(v.z - (float)hi[2]), (_Float16)(v.w - (float)hi[3])};
+                *reinterpret_cast<half4 *>(&s_hi[hp][4 * q]) = hi;
+                *reinterpret_cast<half4 *>(&s_lo[hp][4 * q]) = lo;
+            }
         }
         // Stage this slice's weights for every tap: [tap][BN][32] halves, contiguous in HBM.
         {
@@ -146,6 +172,37 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
         __syncthreads();
     }
     // Epilogue: lane holds rows 4g..4g+3 (pixels) of column r (channel) of each 16 x 16 tile.
+    // y = act(affine(acc + b)) + res, in the order the fused nodes run.
+    if (p.amax) {
+        // Arg-max partials of a GEMM row (1 x 1, NHWC): the best of this block's channels, the
+        // first index on ties, reduced over the 16 lanes that share the rows.
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float bv = -INFINITY;
+                int bi = 0x7fffffff;
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const int co = co0 + t * 16 + r;
+                    if (co >= p.cout) continue;
+                    const float v = acc[m][t][i] + (p.bias ? p.bias[co] : 0.f);
+                    if (v > bv) { bv = v; bi = co; }
+                }
+                for (int off = 8; off > 0; off >>= 1) {
+                    const float ov = __shfl_xor(bv, off);
+                    const int oi = __shfl_xor(bi, off);
+                    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+                }
+                const int pix = wave * 32 + m * 16 + 4 * g + i;
+                const int oy = oy0 + pix / TW, ox = ox0 + pix % TW;
+                if (r == 0 && oy < p.oh && ox < p.ow) {
+                    const size_t o = (size_t(img) * p.oh + oy) * p.ow + ox;
+                    p.amax[o * gridDim.y + nb] = make_float2(bv, __int_as_float(bi));
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int m = 0; m < 2; m++) {
 #pragma unroll
@@ -153,15 +210,24 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
             const int co = co0 + t * 16 + r;
             if (co >= p.cout) continue;
             const float bv = p.bias ? p.bias[co] : 0.f;
+            const float as = p.affine ? p.affine[co] : 1.f, at = p.affine ? p.affine[p.cout + co] : 0.f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int pix = wave * 32 + m * 16 + 4 * g + i;
                 const int oy = oy0 + pix / TW, ox = ox0 + pix % TW;
                 if (oy >= p.oh || ox >= p.ow) continue;
-                const size_t o = (size_t(img) * p.oh + oy) * p.ow + ox;
-                float v = activate_dev(acc[m][t][i] + bv, p.act);
-                if (p.res) v += p.res[o * p.rcs + co];
-                p.y[o * p.ycs + co] = v;
+                float v = acc[m][t][i] + bv;
+                if (p.affine) v = v * as + at;
+                v = activate_dev(v, p.act);
+                if (p.nchw) {
+                    const size_t o = ((size_t(img) * p.cout + co) * p.oh + oy) * p.ow + ox;
+                    if (p.res) v += p.res[o];
+                    p.y[o] = v;
+                } else {
+                    const size_t o = (size_t(img) * p.oh + oy) * p.ow + ox;
+                    if (p.res) v += p.res[o * p.rcs + co];
+                    p.y[o * p.ycs + co] = v;
+                }
             }
         }
     }
@@ -238,6 +304,10 @@ void conv_mfma(const ConvArgs &a, hipStream_t s) {
     p.wt_lo = reinterpret_cast<const half8 *>(a.wt_lo);
     p.bias = a.bias;
     p.res = a.res;
+    p.affine = a.affine;
+    p.in_scale = a.in_scale;
+    p.amax = reinterpret_cast<float2 *>(a.amax_part);
+    p.nchw = a.nchw ? 1 : 0;
     p.rcs = a.res_cs;
     p.kh = pk.kh;
     p.kw = pk.kw;
@@ -246,6 +316,7 @@ void conv_mfma(const ConvArgs &a, hipStream_t s) {
     p.act = a.act;
     p.chunks = pk.chunks;
     p.vec = (p.cin % 4 == 0 && p.xcs % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) & 15) == 0) ? 1 : 0;
+    if (a.amax_part && (a.nchw || pk.kh != 1 || pk.kw != 1)) fail("conv_mfma: arg-max partials need a 1 x 1 NHWC GEMM");
     if (pk.cin != a.x.c || pk.cout != a.y.c) fail("conv_mfma: channel counts differ from the packed weights");
     if (a.y.n != a.x.n) fail("conv_mfma: batch mismatch");
     const bool lo = !pk.exact;

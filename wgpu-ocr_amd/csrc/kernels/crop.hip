@@ -14,14 +14,19 @@ namespace ocr {
 
 namespace {
 
-__device__ inline float mixf(float a, float b, float t) { return __fadd_rn(__fmul_rn(a, 1.f - t), __fmul_rn(b, t)); }
+// mix as the reference states it, each operation rounded on its own (no contraction).
+__device__ inline float mixf(float a, float b, float t) {
+#pragma clang fp contract(off)
+    return a * (1.f - t) + b * t;
+}
 
 __device__ inline float grey_px(const uint8_t *rgb, int w, int h, int x, int y) {
+#pragma clang fp contract(off)
     if (x < 0 || y < 0 || x >= w || y >= h) return -0.5f;
     const uint8_t *q = rgb + (size_t(y) * w + x) * 3;
-    float g = __fadd_rn(-0.5f, __fmul_rn(float(q[0]), 0.299f / 255.f));
-    g = __fadd_rn(g, __fmul_rn(float(q[1]), 0.587f / 255.f));
-    return __fadd_rn(g, __fmul_rn(float(q[2]), 0.114f / 255.f));
+    float g = -0.5f + float(q[0]) * (0.299f / 255.f);
+    g = g + float(q[1]) * (0.587f / 255.f);
+    return g + float(q[2]) * (0.114f / 255.f);
 }
 
 __device__ inline float crop_px(const CropLine &L, const int *row_off, const int *spans, int cx, int cy) {
@@ -32,6 +37,7 @@ __device__ inline float crop_px(const CropLine &L, const int *row_off, const int
 }
 
 __global__ void line_crop_kernel(const CropLine *lines, const int *row_off, const int *spans) {
+#pragma clang fp contract(off)
     const CropLine L = lines[blockIdx.y];
     const int total = LINE_H * L.wb;
     const float sy = float(L.bh) / float(LINE_H), sx = float(L.bw) / float(L.out_w);
@@ -39,8 +45,8 @@ __global__ void line_crop_kernel(const CropLine *lines, const int *row_off, cons
         const int ox = i % L.wb, oy = i / L.wb;
         float v = -0.5f;
         if (ox < L.out_w) {
-            const float iy = fminf(fmaxf(__fsub_rn(__fmul_rn(sy, float(oy) + 0.5f), 0.5f), 0.f), float(L.bh) - 1.f);
-            const float ix = fminf(fmaxf(__fsub_rn(__fmul_rn(sx, float(ox) + 0.5f), 0.5f), 0.f), float(L.bw) - 1.f);
+            const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(L.bh) - 1.f);
+            const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(L.bw) - 1.f);
             const int y1 = int(iy), x1 = int(ix);
             const int y2 = min(y1 + 1, L.bh - 1), x2 = min(x1 + 1, L.bw - 1);
             const float fy = iy - float(y1), fx = ix - float(x1);

@@ -25,8 +25,12 @@ inline unsigned blocks_for(size_t n, int per = 256) {
     return unsigned(b ? b : 1);
 }
 
-// WGSL mix(a, b, t) = a * (1 - t) + b * t, unfused as the reference states it.
-__device__ inline float mixf(float a, float b, float t) { return __fadd_rn(__fmul_rn(a, 1.f - t), __fmul_rn(b, t)); }
+// WGSL mix(a, b, t) = a * (1 - t) + b * t, unfused as the reference states it: contraction into
+// fused multiply-adds is off in the front- and back-end kernels below.
+__device__ inline float mixf(float a, float b, float t) {
+#pragma clang fp contract(off)
+    return a * (1.f - t) + b * t;
+}
 
 // ---- conv_generic: any group / stride, float32, one thread per output value -----------------
 __global__ void conv_generic_kernel(const float *x, int n, int h, int w, int cin, int xcs, float *y, int oh, int ow,
@@ -170,20 +174,22 @@ __global__ void fill_kernel(float *p, size_t count, float v) {
 
 // ---- grey_resize (gpu.rs:530-561) -------------------------------------------------------------
 __device__ inline float grey_at(const uint8_t *rgb, int w, int h, int x, int yy) {
+#pragma clang fp contract(off)
     if (x >= w || yy >= h) return -0.5f;
     const uint8_t *q = rgb + (size_t(yy) * w + x) * 3;
-    float g = __fadd_rn(-0.5f, __fmul_rn(float(q[0]), 0.299f / 255.f));
-    g = __fadd_rn(g, __fmul_rn(float(q[1]), 0.587f / 255.f));
-    return __fadd_rn(g, __fmul_rn(float(q[2]), 0.114f / 255.f));
+    float g = -0.5f + float(q[0]) * (0.299f / 255.f);
+    g = g + float(q[1]) * (0.587f / 255.f);
+    return g + float(q[2]) * (0.114f / 255.f);
 }
 
 __global__ void grey_resize_kernel(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh,
                                    float sx, float sy) {
+#pragma clang fp contract(off)
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= ow * oh) return;
     int ox = i % ow, oy = i / ow;
-    float iy = fminf(fmaxf(__fsub_rn(__fmul_rn(sy, float(oy) + 0.5f), 0.5f), 0.f), float(ph) - 1.f);
-    float ix = fminf(fmaxf(__fsub_rn(__fmul_rn(sx, float(ox) + 0.5f), 0.5f), 0.f), float(pw) - 1.f);
+    float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(ph) - 1.f);
+    float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(pw) - 1.f);
     int y1 = int(iy), x1 = int(ix);
     int y2 = min(y1 + 1, ph - 1), x2 = min(x1 + 1, pw - 1);
     float wy = iy - float(y1), wx = ix - float(x1);
@@ -195,17 +201,18 @@ __global__ void grey_resize_kernel(const uint8_t *rgb, int w, int h, int pw, int
 // ---- mask_up (gpu.rs:563-593): one thread per 32-pixel word ----------------------------------
 __global__ void mask_up_kernel(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, int words,
                                float sx, float sy, float thr) {
+#pragma clang fp contract(off)
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= words * h) return;
     int wx = i % words, oy = i / words;
-    float iy = fminf(fmaxf(__fsub_rn(__fmul_rn(sy, float(oy) + 0.5f), 0.5f), 0.f), float(mh) - 1.f);
+    float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(mh) - 1.f);
     int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
     float fy = iy - float(y1);
     uint32_t out = 0;
     for (int b = 0; b < 32; b++) {
         int ox = wx * 32 + b;
         if (ox >= w) break;
-        float ix = fminf(fmaxf(__fsub_rn(__fmul_rn(sx, float(ox) + 0.5f), 0.5f), 0.f), float(mw) - 1.f);
+        float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(mw) - 1.f);
         int x1 = int(ix), x2 = min(x1 + 1, mw - 1);
         float fx = ix - float(x1);
         float top = mixf(m[size_t(y1) * stride + x1], m[size_t(y1) * stride + x2], fx);

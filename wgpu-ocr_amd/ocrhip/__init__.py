@@ -71,6 +71,18 @@ SIGNATURES = {
     "ocr_pipeline_stats_get": (ctypes.c_int, [P, P]),
     "ocr_pipeline_page": (ctypes.c_int, [P, U32, PU32, PU32]),
     "ocr_pipeline_line_text": (ctypes.c_int, [P, U32, U32, ctypes.c_char_p, U32, PU32]),
+    "ocr_nd_new": (P, [P, ctypes.c_char_p, ctypes.c_int]),
+    "ocr_nd_free": (None, [P]),
+    "ocr_nd_dims": (ctypes.c_int, [P, P, U32, P, PU32]),
+    "ocr_nd_run": (ctypes.c_int, [P, P, P, U32, P]),
+    "ocr_nd_run_device": (ctypes.c_int, [P, P, P, U32, P]),
+    "ocr_nd_argmax": (ctypes.c_int, [P, P, P, U32, P]),
+    "ocr_nd_argmax_device": (ctypes.c_int, [P, P, P, U32, P]),
+    "ocr_nd_det_input_dims": (ctypes.c_int, [U32, U32, U32, PU32, PU32, P]),
+    "ocr_nd_det_input": (ctypes.c_int, [P, P, U32, U32, U32, P]),
+    "ocr_nd_det_input_device": (ctypes.c_int, [P, P, U32, U32, U32, P]),
+    "ocr_db_threshold": (ctypes.c_int, [P, P, U32, U32, F32, P]),
+    "ocr_db_threshold_device": (ctypes.c_int, [P, P, U32, U32, F32, P]),
 }
 
 
@@ -240,6 +252,74 @@ class Graph:
             pass
 
 
+class NdGraph:
+    """NdGraph (src/nd.rs:428-1394): an ONNX graph of the N-D operator set on the GPU."""
+
+    def __init__(self, ctx: Context, onnx_path: str, stop_before_softmax: bool = False):
+        self.ctx = ctx
+        self.handle = lib().ocr_nd_new(ctx.handle, onnx_path.encode(), int(bool(stop_before_softmax)))
+        if not self.handle:
+            raise OcrError(lib().ocr_last_error().decode())
+
+    def dims(self, shape):
+        s = np.asarray(shape, np.int64)
+        out = np.zeros(6, np.int64)
+        rank = ctypes.c_uint32()
+        _check(lib().ocr_nd_dims(self.handle, _ptr(s), len(s), _ptr(out), ctypes.byref(rank)))
+        return tuple(int(v) for v in out[: rank.value])
+
+    def run(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        s = np.asarray(x.shape, np.int64)
+        y = np.empty(self.dims(x.shape), np.float32)
+        _check(lib().ocr_nd_run(self.handle, _ptr(x), _ptr(s), len(s), _ptr(y)))
+        return y
+
+    def argmax(self, x: np.ndarray) -> np.ndarray:
+        """Arg-max over the output's last axis (first index on ties), shape = output shape[:-1]."""
+        x = np.ascontiguousarray(x, np.float32)
+        s = np.asarray(x.shape, np.int64)
+        shape = self.dims(x.shape)[:-1]
+        best = np.empty(shape, np.uint32)
+        _check(lib().ocr_nd_argmax(self.handle, _ptr(x), _ptr(s), len(s), _ptr(best)))
+        return best
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().ocr_nd_free(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+def det_input_dims(w: int, h: int, max_side: int):
+    """(ow, oh, to_page) of the PP-OCR detection input (src/nd.rs:1356-1358)."""
+    ow, oh = ctypes.c_uint32(), ctypes.c_uint32()
+    tp = np.zeros(2, np.float32)
+    _check(lib().ocr_nd_det_input_dims(w, h, max_side, ctypes.byref(ow), ctypes.byref(oh), _ptr(tp)))
+    return ow.value, oh.value, (float(tp[0]), float(tp[1]))
+
+
+def det_input(ctx: Context, rgb: np.ndarray, max_side: int) -> np.ndarray:
+    """The PP-OCR detection input [1, 3, oh, ow] of an RGB page (src/nd.rs:1353-1369)."""
+    rgb = np.ascontiguousarray(rgb, np.uint8)
+    h, w = rgb.shape[:2]
+    ow, oh, _ = det_input_dims(w, h, max_side)
+    out = np.empty((1, 3, oh, ow), np.float32)
+    _check(lib().ocr_nd_det_input(ctx.handle, _ptr(rgb), w, h, max_side, _ptr(out)))
+    return out
+
+
+def db_threshold(ctx: Context, prob: np.ndarray, thr: float) -> np.ndarray:
+    """prob [h, w] > thr as [h, ceil(w / 32)] bit words (src/ppdet.rs:88)."""
+    prob = np.ascontiguousarray(prob, np.float32)
+    h, w = prob.shape
+    bits = np.empty((h, (w + 31) // 32), np.uint32)
+    _check(lib().ocr_db_threshold(ctx.handle, _ptr(prob), w, h, thr, _ptr(bits)))
+    return bits
+
+
 class Recognizer:
     """Recognizer (src/gpu.rs:1441-1603)."""
 
@@ -296,6 +376,9 @@ class Recognizer:
 
 FAMILIES = ("conv_mfma", "gru", "conv_transpose", "conv_direct", "conv_generic", "maxpool", "mask_up",
             "grey_resize", "line_crop", "avgpool_t", "argmax", "copy")
+ND_FAMILIES = ("conv_mfma", "nd_bgemm", "nd_conv_generic", "nd_conv_transpose", "nd_elementwise", "nd_copy",
+               "nd_reduce", "nd_layer_norm", "nd_softmax", "nd_argmax", "nd_pool", "nd_resize", "nd_det_prep",
+               "nd_threshold")
 
 
 def probe_start(family: str):
