@@ -218,6 +218,61 @@ int ocr_nd_det_input_device(ocr_ctx *ctx, const uint8_t *d_rgb, uint32_t w, uint
 int ocr_db_threshold(ocr_ctx *ctx, const float *prob, uint32_t w, uint32_t h, float thr, uint32_t *bits);
 int ocr_db_threshold_device(ocr_ctx *ctx, const float *d_prob, uint32_t w, uint32_t h, float thr, uint32_t *d_bits);
 
+/* ---- The PP-OCR page pipeline (src/bin/ocr-bench.rs with DET=ppocr REC=ppocr) --------------- */
+
+typedef struct ocr_pp_pipeline ocr_pp_pipeline;
+
+/* merge: pages per recognition pass (MERGE); thr: DB threshold (ppdet.rs:58; 0.3 here);
+ * relv: box padding across (RELV, 0.1 with DET=ppocr, ocr-bench.rs:540); max_side: detection
+ * input's long side (DETMAX); per_batch: lines per batch (PPBATCH); threads: host workers;
+ * det_batch: same-size pages per detection pass; box_thresh, unclip_ratio, min_size: DB
+ * post-processing (ppdet.rs:55-60). Zeros take the defaults 2, 0.3, 0.1, 960, 16, 0, 4, 0.45,
+ * 1.4, 3. */
+typedef struct ocr_pp_opts {
+    uint32_t merge;
+    float thr;
+    float relv;
+    uint32_t max_side;
+    uint32_t per_batch;
+    uint32_t threads;
+    uint32_t det_batch;
+    float box_thresh;
+    float unclip_ratio;
+    float min_size;
+} ocr_pp_opts;
+
+/* det: the DB detector; rec: the SVTR recogniser, best built with stop_before_softmax (its head
+ * arg-max then never writes logits). Both from the same context. */
+ocr_pp_pipeline *ocr_pp_pipeline_new(ocr_nd *det, ocr_nd *rec, const ocr_pp_opts *opts);
+void ocr_pp_pipeline_free(ocr_pp_pipeline *pipe);
+/* Every page: detection input and map on the GPU, DB boxes on the host, line images and
+ * recognition on the GPU, CTC on the host, pages overlapped (ocr-bench.rs:186-284, 500-560).
+ * RGB bytes (h x w x 3) in device memory; the second form takes host memory. */
+int ocr_pp_pipeline_run_device(ocr_pp_pipeline *pipe, const uint8_t *const *d_rgb, const uint32_t *w, const uint32_t *h,
+                               uint32_t npages);
+int ocr_pp_pipeline_run(ocr_pp_pipeline *pipe, const uint8_t *const *rgb, const uint32_t *w, const uint32_t *h,
+                        uint32_t npages);
+int ocr_pp_pipeline_stats_get(ocr_pp_pipeline *pipe, ocr_pipeline_stats *out);
+/* Lines (DB boxes) of a page of the last run, and the text of one (UTF-8; the synthetic
+ * dictionary maps class k >= 1 to U+4E00 + k - 1 and the last class to a space). */
+int ocr_pp_pipeline_page(ocr_pp_pipeline *pipe, uint32_t page, uint32_t *lines);
+int ocr_pp_pipeline_line_text(ocr_pp_pipeline *pipe, uint32_t page, uint32_t line, char *buf, uint32_t cap,
+                              uint32_t *len);
+
+/* ppdet::boxes (src/ppdet.rs:87-132) on the host from a thresholded map (bits, h rows of
+ * ceil(w / 32) words) and the map (prob, h x w): the boxes in page coordinates and reading order.
+ * Zeros take the defaults 0.45, 1.4, 3. Writes at most cap boxes; *count receives the number. */
+int ocr_db_boxes(const uint32_t *bits, const float *prob, uint32_t w, uint32_t h, float to_page_x, float to_page_y,
+                 float box_thresh, float unclip_ratio, float min_size, ocr_rrect *out, uint32_t cap, uint32_t *count);
+/* One box as a PP-OCR line image (ocr-bench.rs:538-555, ppocr.rs:42-53): out = {left, top,
+ * width, height, resized width at height 48} on a page_w x page_h page. */
+int ocr_pp_line_box(const ocr_rrect *box, float relv, uint32_t page_w, uint32_t page_h, int32_t *out);
+/* ppocr::line_input + ppocr::batch (src/ppocr.rs:42-78) on the GPU: count line images of an RGB
+ * page (host), lines = count x {left, top, width, height, resized width}, into out
+ * [count][3][48][wb] (host), zero past each line's width. */
+int ocr_pp_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t page_h, const int32_t *lines,
+                       uint32_t count, uint32_t wb, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,7 @@ def lib():
         L.orc_pack_bits.argtypes = [P, I, I, F, P]
         L.orc_line_crop.argtypes = [P, I, I, I, I, I, I, I, P, P, I, P]
         L.orc_det_prep.argtypes = [P, I, I, I, I, P]
+        L.orc_pp_line_input.argtypes = [P, I, I, I, I, I, I, I, I, P]
         L.orc_activate.argtypes = [F, I]
         L.orc_activate.restype = F
         _lib = L
@@ -445,3 +446,60 @@ def det_prep(rgb, max_side):
 def threshold_bits(prob, thr):
     """ppdet.rs:88 as bit rows: prob [h, w] > thr, bit x % 32 of word x / 32."""
     return pack_bits(np.asarray(prob, np.float32), thr)
+
+
+PP_H = 48
+
+
+def pp_line_input(rgb, line, wb):
+    """One PP-OCR line image [3, 48, wb] (see orc_pp_line_input); line = (left, top, cw, ch, out_w)."""
+    rgb = _c(rgb, np.uint8)
+    ph, pw = rgb.shape[:2]
+    out = np.empty((3, PP_H, wb), np.float32)
+    lib().orc_pp_line_input(_p(rgb), pw, ph, *[int(v) for v in line], wb, _p(out))
+    return out
+
+
+def pp_batches(lines, per_batch=16):
+    """ocr-bench.rs:330-345: line indices sorted by resized width (stable), per_batch a batch,
+    each as wide as its widest line rounded up to a multiple of 8."""
+    order = sorted(range(len(lines)), key=lambda i: lines[i][4])
+    out = []
+    for c in range(0, len(order), per_batch):
+        part = order[c: c + per_batch]
+        out.append((part, -(-max(max(lines[i][4] for i in part), 8) // 8) * 8))
+    return out
+
+
+def pp_decode(best):
+    """ppocr.rs:23-33 with the synthetic dictionary: class k in [1, 18706] is U+4E00 + k - 1,
+    class 18707 a space, 0 the blank; repeats merged, blanks dropped."""
+    out, prev = [], 0
+    for c in best:
+        c = int(c)
+        if c != 0 and c != prev:
+            out.append(" " if c == 18707 else chr(0x4E00 + c - 1))
+        prev = c
+    return "".join(out)
+
+
+def pp_page_pipeline(det_model, rec_model, page, boxes_of, thr=0.3, max_side=960, per_batch=16):
+    """The PP-OCR page on the CPU: detection input, DB map and threshold (oracle); the boxes and
+    their line geometry (given: boxes_of(bits, prob, to_page) returns (left, top, cw, ch, out_w)
+    per line in reading order, as the product's host code does); line images, recognition and
+    CTC (oracle). Returns (texts by line, lines, bits, prob)."""
+    h, w = page.shape[:2]
+    x = det_prep(page, max_side)
+    prob, _ = run(det_model, x)
+    prob = prob[0, 0]
+    bits = pack_bits(prob, thr)
+    ow, oh = x.shape[3], x.shape[2]
+    lines = boxes_of(bits, prob, (np.float32(w) / np.float32(ow), np.float32(h) / np.float32(oh)))
+    texts = [""] * len(lines)
+    for part, wb in pp_batches(lines, per_batch):
+        data = np.stack([pp_line_input(page, lines[i], wb) for i in part])
+        y, _ = run(rec_model, data)
+        best = np.argmax(y, axis=-1)  # the first index on ties (nd.rs:383)
+        for k, i in enumerate(part):
+            texts[i] = pp_decode(best[k])
+    return texts, lines, bits, prob

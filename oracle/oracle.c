@@ -16,6 +16,7 @@
  *   orc_line_crop         torch bilinear golden of span-masked grey crops
  *   orc_activate          sigmoid closed form via the conv golden; ReLU by the conv goldens
  *   orc_det_prep          torch bilinear (half-pixel) golden of the BGR-normalised page
+ *   orc_pp_line_input     torch bilinear golden of a page box, rounded to bytes and normalised
  */
 #include <math.h>
 #include <stdint.h>
@@ -291,6 +292,39 @@ void orc_det_prep(const uint8_t *rgb, int w, int h, int ow, int oh, float *y) {
                 float a = mixf((float)rgb[((size_t)y1 * w + x1) * 3 + k], (float)rgb[((size_t)y1 * w + x2) * 3 + k], fx);
                 float b = mixf((float)rgb[((size_t)y2 * w + x1) * 3 + k], (float)rgb[((size_t)y2 * w + x2) * 3 + k], fx);
                 y[((size_t)c * oh + oy) * ow + ox] = (mixf(a, b, fy) / 255.f - mean[c]) / dev[c];
+            }
+        }
+}
+
+/* PP-OCR line image (ppocr::line_input, src/ppocr.rs:42-62, batched as ppocr::batch,
+ * ppocr.rs:64-78): the page box [left, left + cw) x [top, top + ch) resized to 48 rows and out_w
+ * columns bilinearly (half-pixel, clamped; pixels off the page read 0), rounded to bytes (half
+ * away from zero) as an 8-bit resize gives them, then (v / 255 - 0.5) / 0.5 per RGB channel;
+ * dst [3][48][wb], zero past out_w. The reference resizes with the image crate's Triangle filter,
+ * which this does not restate (parity with it is unpinned). */
+static float pp_px(const uint8_t *rgb, int pw, int ph, int x, int y, int c) {
+    if (x < 0 || y < 0 || x >= pw || y >= ph) return 0.f;
+    return (float)rgb[((size_t)y * pw + x) * 3 + c];
+}
+
+void orc_pp_line_input(const uint8_t *rgb, int pw, int ph, int left, int top, int cw, int ch, int out_w, int wb,
+                       float *dst) {
+    const int H = 48;
+    float sy = (float)ch / (float)H, sx = (float)cw / (float)out_w;
+    for (int oy = 0; oy < H; oy++)
+        for (int ox = 0; ox < wb; ox++) {
+            for (int c = 0; c < 3; c++) dst[((size_t)c * H + oy) * wb + ox] = 0.f;
+            if (ox >= out_w) continue;
+            float iy = fminf(fmaxf(sy * ((float)oy + 0.5f) - 0.5f, 0.f), (float)ch - 1.f);
+            float ix = fminf(fmaxf(sx * ((float)ox + 0.5f) - 0.5f, 0.f), (float)cw - 1.f);
+            int y1 = (int)iy, x1 = (int)ix;
+            int y2 = y1 + 1 < ch - 1 ? y1 + 1 : ch - 1, x2 = x1 + 1 < cw - 1 ? x1 + 1 : cw - 1;
+            float fy = iy - (float)y1, fx = ix - (float)x1;
+            for (int c = 0; c < 3; c++) {
+                float t0 = mixf(pp_px(rgb, pw, ph, left + x1, top + y1, c), pp_px(rgb, pw, ph, left + x2, top + y1, c), fx);
+                float b0 = mixf(pp_px(rgb, pw, ph, left + x1, top + y2, c), pp_px(rgb, pw, ph, left + x2, top + y2, c), fx);
+                float q = floorf(mixf(t0, b0, fy) + 0.5f);
+                dst[((size_t)c * H + oy) * wb + ox] = (q / 255.f - 0.5f) / 0.5f;
             }
         }
 }

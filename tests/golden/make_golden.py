@@ -181,6 +181,20 @@ def nd_cases():
     mean = torch.tensor([0.485, 0.456, 0.406]).reshape(3, 1, 1)
     dev = torch.tensor([0.229, 0.224, 0.225]).reshape(3, 1, 1)
     c["det_prep"] = dict(rgb=rgb, max_side=np.array(64), y=((img / 255.0 - mean) / dev).numpy()[None])
+    # PP-OCR line images: page boxes (one reaching past the page's right and bottom edges, where
+    # pixels read 0) resized to 48 rows, rounded to bytes, (v / 255 - 0.5) / 0.5, padded to wb.
+    page = rng.integers(0, 256, (40, 90, 3), dtype=np.uint8)
+    for name, (left, top, cw, ch, out_w, wb) in [("pp_line_in", (7, 5, 60, 22, 131, 136)),
+                                                 ("pp_line_edge", (70, 30, 25, 14, 86, 88))]:
+        crop = np.zeros((ch, cw, 3), np.float32)
+        sub = page[top: top + ch, left: left + cw].astype(np.float32)
+        crop[: sub.shape[0], : sub.shape[1]] = sub
+        img = F.interpolate(t(crop.transpose(2, 0, 1).copy())[None], size=(48, out_w), mode="bilinear",
+                            align_corners=False)[0].numpy()
+        q = np.floor(img + 0.5)
+        y = np.zeros((3, 48, wb), np.float32)
+        y[:, :, :out_w] = (q / 255.0 - 0.5) / 0.5
+        c[name] = dict(rgb=page, line=np.array([left, top, cw, ch, out_w]), wb=np.array(wb), y=y)
     return c
 
 

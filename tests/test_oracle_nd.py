@@ -135,3 +135,19 @@ def test_planted_layer_norm_mistake_is_caught():
               {"two": f32(2.0), "eps": f32(1e-6), "g": c["g"], "b": c["b"]})
     y, _ = graph.run(m, c["x"])
     assert np.abs(y - c["y"]).max() > 1e-2
+
+
+@pytest.mark.parametrize("case", ["pp_line_in", "pp_line_edge"])
+def test_pp_line_input_golden(case):
+    c = nd(case)
+    y = graph.pp_line_input(c["rgb"], c["line"], int(c["wb"]))
+    d = np.abs(y - c["y"])
+    # Both round the interpolated value to a byte; a value within an ulp of .5 may round to the
+    # neighbouring byte (2 / 255 after normalisation) on one side only.
+    assert d.max() <= 2 / 255 + 1e-6
+    assert (d > 1e-6).mean() < 0.005
+
+
+def test_pp_decode_rules():
+    assert graph.pp_decode([0, 5, 5, 0, 5, 18707, 18707, 1]) == "\u4e04\u4e04 \u4e00"
+    assert graph.pp_decode([]) == ""

@@ -8,6 +8,8 @@
 #include "models.h"
 #include "nd.h"
 #include "pipeline.h"
+#include "crop.h"
+#include "pp_pipeline.h"
 
 using namespace ocr;
 
@@ -36,6 +38,10 @@ struct ocr_pipeline {
 struct ocr_nd {
     ocr_ctx *owner;
     NdGraph graph;
+};
+struct ocr_pp_pipeline {
+    ocr_ctx *owner;
+    std::unique_ptr<PpPipeline> pipe;
 };
 
 namespace {
@@ -692,6 +698,172 @@ int ocr_db_threshold(ocr_ctx *ctx, const float *prob, uint32_t w, uint32_t h, fl
         c.h2d(dp.get(), prob, size_t(w) * h * sizeof(float));
         nd_threshold_bits(dp.as<float>(), int(w), int(h), thr, db.as<uint32_t>(), c.stream());
         c.d2h(bits, db.get(), words * 4);
+    });
+}
+
+
+ocr_pp_pipeline *ocr_pp_pipeline_new(ocr_nd *det, ocr_nd *rec, const ocr_pp_opts *opts) {
+    return guard_ptr<ocr_pp_pipeline>([&] {
+        need(det, "det");
+        need(rec, "rec");
+        if (det->owner != rec->owner) fail("detector and recogniser belong to different contexts");
+        PpPipelineOpts o;
+        if (opts) {
+            if (opts->merge) o.merge = int(opts->merge);
+            if (opts->thr > 0) o.thr = opts->thr;
+            if (opts->relv > 0) o.relv = opts->relv;
+            if (opts->max_side) o.max_side = int(opts->max_side);
+            if (opts->per_batch) o.per_batch = int(opts->per_batch);
+            if (opts->threads) o.threads = int(opts->threads);
+            if (opts->det_batch) o.det_batch = int(opts->det_batch);
+            if (opts->box_thresh > 0) o.db.box_thresh = opts->box_thresh;
+            if (opts->unclip_ratio > 0) o.db.unclip_ratio = opts->unclip_ratio;
+            if (opts->min_size > 0) o.db.min_size = opts->min_size;
+        }
+        det->owner->ctx->bind();
+        auto p = std::make_unique<ocr_pp_pipeline>();
+        p->owner = det->owner;
+        p->pipe = std::make_unique<PpPipeline>(*det->owner->ctx, det->graph, rec->graph, o);
+        return p.release();
+    });
+}
+
+void ocr_pp_pipeline_free(ocr_pp_pipeline *pipe) { delete pipe; }
+
+int ocr_pp_pipeline_run_device(ocr_pp_pipeline *pipe, const uint8_t *const *d_rgb, const uint32_t *w, const uint32_t *h,
+                               uint32_t npages) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        if (npages) {
+            need(d_rgb, "d_rgb");
+            need(w, "w");
+            need(h, "h");
+        }
+        pipe->owner->ctx->bind();
+        std::vector<int> wi(npages), hi(npages);
+        for (uint32_t k = 0; k < npages; k++) wi[k] = int(w[k]), hi[k] = int(h[k]);
+        pipe->pipe->run(d_rgb, wi.data(), hi.data(), int(npages));
+    });
+}
+
+int ocr_pp_pipeline_run(ocr_pp_pipeline *pipe, const uint8_t *const *rgb, const uint32_t *w, const uint32_t *h,
+                        uint32_t npages) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        if (npages) {
+            need(rgb, "rgb");
+            need(w, "w");
+            need(h, "h");
+        }
+        Ctx &c = *pipe->owner->ctx;
+        c.bind();
+        std::vector<DBuf> bufs;
+        std::vector<const uint8_t *> ptrs;
+        std::vector<int> wi(npages), hi(npages);
+        for (uint32_t k = 0; k < npages; k++) {
+            need(rgb[k], "page");
+            wi[k] = int(w[k]), hi[k] = int(h[k]);
+            const size_t bytes = size_t(w[k]) * h[k] * 3;
+            bufs.emplace_back(&c, std::max<size_t>(bytes, 1));
+            c.h2d(bufs.back().get(), rgb[k], bytes);
+            ptrs.push_back(bufs.back().as<uint8_t>());
+        }
+        pipe->pipe->run(ptrs.data(), wi.data(), hi.data(), int(npages));
+    });
+}
+
+int ocr_pp_pipeline_stats_get(ocr_pp_pipeline *pipe, ocr_pipeline_stats *out) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        need(out, "out");
+        const PipelineStats &s = pipe->pipe->stats();
+        *out = ocr_pipeline_stats{s.ms, s.cpu_busy_ms, uint32_t(s.pages), uint32_t(s.lines), uint32_t(s.words),
+                                  uint32_t(s.batches), uint32_t(s.rec_passes), uint64_t(s.rec_steps)};
+    });
+}
+
+int ocr_pp_pipeline_line_text(ocr_pp_pipeline *pipe, uint32_t page, uint32_t line, char *buf, uint32_t cap,
+                              uint32_t *len) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        const auto &pages = pipe->pipe->pages();
+        if (page >= pages.size() || line >= pages[page].lines.size()) fail("line index out of range");
+        const std::string &s = pages[page].lines[line];
+        if (len) *len = uint32_t(s.size());
+        if (buf && cap) {
+            const size_t n = std::min<size_t>(s.size(), cap - 1);
+            std::copy(s.begin(), s.begin() + long(n), buf);
+            buf[n] = 0;
+        }
+    });
+}
+
+int ocr_pp_pipeline_page(ocr_pp_pipeline *pipe, uint32_t page, uint32_t *lines) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        const auto &pages = pipe->pipe->pages();
+        if (page >= pages.size()) fail("page index out of range");
+        if (lines) *lines = uint32_t(pages[page].lines.size());
+    });
+}
+
+int ocr_db_boxes(const uint32_t *bits, const float *prob, uint32_t w, uint32_t h, float to_page_x, float to_page_y,
+                 float box_thresh, float unclip_ratio, float min_size, ocr_rrect *out, uint32_t cap, uint32_t *count) {
+    return guard([&] {
+        need(bits, "bits");
+        need(prob, "prob");
+        need(count, "count");
+        DbParams db;
+        if (box_thresh > 0) db.box_thresh = box_thresh;
+        if (unclip_ratio > 0) db.unclip_ratio = unclip_ratio;
+        if (min_size > 0) db.min_size = min_size;
+        auto boxes = db_boxes(bits, prob, int(w), int(h), to_page_x, to_page_y, db);
+        *count = uint32_t(boxes.size());
+        for (size_t i = 0; i < boxes.size() && i < cap; i++) {
+            need(out, "out");
+            const RRect &r = boxes[i];
+            out[i] = ocr_rrect{r.cx, r.cy, r.ux, r.uy, r.w, r.h};
+        }
+    });
+}
+
+int ocr_pp_line_box(const ocr_rrect *box, float relv, uint32_t page_w, uint32_t page_h, int32_t *out) {
+    return guard([&] {
+        need(box, "box");
+        need(out, "out");
+        RRect r;
+        r.cx = box->cx, r.cy = box->cy, r.ux = box->ux, r.uy = box->uy, r.w = box->w, r.h = box->h;
+        const PpLine l = pp_line_box(r, relv, int(page_w), int(page_h));
+        out[0] = l.left, out[1] = l.top, out[2] = l.cw, out[3] = l.ch, out[4] = l.out_w;
+    });
+}
+
+
+int ocr_pp_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t page_h, const int32_t *lines,
+                       uint32_t count, uint32_t wb, float *out) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(rgb, "rgb");
+        need(lines, "lines");
+        need(out, "out");
+        if (count == 0) return;
+        if (wb == 0 || page_w == 0 || page_h == 0) fail("empty page or batch width");
+        Ctx &c = *ctx->ctx;
+        c.bind();
+        const size_t slot = size_t(3) * PP_LINE_H * wb;
+        DBuf drgb(&c, size_t(page_w) * page_h * 3), dout(&c, size_t(count) * slot * sizeof(float));
+        c.h2d(drgb.get(), rgb, size_t(page_w) * page_h * 3);
+        std::vector<PpCropLine> crops;
+        for (uint32_t i = 0; i < count; i++) {
+            const int32_t *l = lines + size_t(i) * 5;
+            if (l[2] < 1 || l[3] < 1 || l[4] < 1 || uint32_t(l[4]) > wb) fail("line box or width out of range");
+            crops.push_back({drgb.as<uint8_t>(), int(page_w), int(page_h), l[0], l[1], l[2], l[3], l[4],
+                             dout.as<float>() + size_t(i) * slot, int(wb)});
+        }
+        DBuf dc(&c, crops.size() * sizeof(PpCropLine));
+        c.h2d(dc.get(), crops.data(), crops.size() * sizeof(PpCropLine));
+        pp_line_crop(dc.as<PpCropLine>(), int(count), int(wb), c.stream());
+        c.d2h(out, dout.get(), size_t(count) * slot * sizeof(float));
     });
 }
 

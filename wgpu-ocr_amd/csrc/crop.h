@@ -24,4 +24,14 @@ struct CropLine {
 void line_crop(const CropLine *d_lines, int nlines, const int *d_row_off, const int *d_spans, int max_wb,
                hipStream_t s);
 
+// One PP-OCR line image (ppocr::line_input, src/ppocr.rs:42-62, and ppocr::batch, ppocr.rs:64-78).
+struct PpCropLine {
+    const uint8_t *rgb;  // the page's RGB bytes (device)
+    int pw, ph;          // page size
+    int left, top, cw, ch, out_w;  // crop box and resized width (PpLine)
+    float *dst;          // the line's slot in its batch: [3][48][wb] floats (device)
+    int wb;              // batch width
+};
+void pp_line_crop(const PpCropLine *d_lines, int nlines, int max_wb, hipStream_t s);
+
 }  // namespace ocr

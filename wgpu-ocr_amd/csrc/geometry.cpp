@@ -111,7 +111,9 @@ int find(std::vector<int> &parent, int a) {
 
 }  // namespace
 
-std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area) {
+// Pixel coordinates of every 8-connected component of a bit mask (h rows of ceil(w / 32) words),
+// reduced to the ends of its row runs (enough for the convex hull).
+static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w, int h) {
     const int words = (w + 31) / 32;
     std::vector<Run> runs;
     std::vector<int> row_start(size_t(h) + 1, 0);
@@ -154,7 +156,7 @@ std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, 
             else j++;
         }
     }
-    // Hull points of each component: both ends of each run (pixel coordinates).
+    // Both ends of each run, per component (components in order of their first run).
     std::vector<int> comp(runs.size(), -1);
     std::vector<std::vector<Pt>> pts;
     for (size_t r = 0; r < runs.size(); r++) {
@@ -167,13 +169,133 @@ std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, 
         v.push_back({float(runs[r].x0), float(runs[r].y)});
         if (runs[r].x1 != runs[r].x0) v.push_back({float(runs[r].x1), float(runs[r].y)});
     }
+    return pts;
+}
+
+std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area) {
     std::vector<RRect> out;
-    for (auto &v : pts) {
+    for (auto &v : component_points(bits, w, h)) {
         RRect r = min_area_rect(hull(std::move(v)));
         r.resize(r.w + 2 * expand, r.h + 2 * expand);
         if (r.area() >= min_area) out.push_back(r);
     }
     return out;
+}
+
+// ppdet.rs:65-85: the mean probability of the map's pixels whose position lies inside r (its
+// height along the up axis, its width across it), scanning r's bounding box.
+static float db_score(const float *prob, int w, int h, const RRect &r) {
+    float l, t, rr, b;
+    r.bbox(l, t, rr, b);
+    const int x0 = int(std::max(std::floor(l), 0.f)), y0 = int(std::max(std::floor(t), 0.f));
+    const int x1 = std::min(int(std::ceil(rr)), w - 1), y1 = std::min(int(std::ceil(b)), h - 1);
+    const float hw = r.w / 2, hh = r.h / 2;
+    double sum = 0;
+    long n = 0;
+    for (int y = y0; y <= y1; y++)
+        for (int x = x0; x <= x1; x++) {
+            const float dx = float(x) - r.cx, dy = float(y) - r.cy;
+            const float along_up = dx * r.ux + dy * r.uy, across = dx * -r.uy + dy * r.ux;
+            if (std::fabs(along_up) <= hh && std::fabs(across) <= hw) {
+                sum += prob[size_t(y) * w + x];
+                n++;
+            }
+        }
+    return n ? float(sum / double(n)) : 0.f;
+}
+
+std::vector<RRect> db_boxes(const uint32_t *bits, const float *prob, int w, int h, float to_page_x, float to_page_y,
+                            const DbParams &db) {
+    std::vector<RRect> out;
+    for (auto &v : component_points(bits, w, h)) {
+        const RRect r = min_area_rect(hull(std::move(v)));
+        if (std::min(r.w, r.h) < db.min_size || db_score(prob, w, h, r) < db.box_thresh) continue;
+        // Unclip: grown by area * ratio / perimeter on every side (ppdet.rs:104-109).
+        const float d = r.w * r.h * db.unclip_ratio / std::max(2.f * (r.w + r.h), 1e-6f);
+        const float nw = r.w + 2 * d, nh = r.h + 2 * d;
+        if (std::min(nw, nh) < db.min_size + 2) continue;
+        const float s = (to_page_x + to_page_y) / 2;
+        RRect p = r;
+        p.cx = r.cx * to_page_x, p.cy = r.cy * to_page_y;
+        p.w = nw * s, p.h = nh * s;
+        out.push_back(p);
+    }
+    // Reading order (ppdet.rs:118-131): by the top edge; a box within 10 px of the previous one's
+    // top moves before it when it starts further left.
+    auto top = [](const RRect &r) {
+        float l, t, rr, b;
+        r.bbox(l, t, rr, b);
+        return t;
+    };
+    auto left = [](const RRect &r) {
+        float l, t, rr, b;
+        r.bbox(l, t, rr, b);
+        return l;
+    };
+    std::stable_sort(out.begin(), out.end(), [&](const RRect &a, const RRect &b) { return top(a) < top(b); });
+    for (size_t i = 0; i < out.size(); i++)
+        for (size_t j = i; j > 0; j--) {
+            if (std::fabs(top(out[j]) - top(out[j - 1])) < 10.f && left(out[j]) < left(out[j - 1]))
+                std::swap(out[j - 1], out[j]);
+            else
+                break;
+        }
+    return out;
+}
+
+PpLine pp_line_box(const RRect &box, float relv, int page_w, int page_h) {
+    // ocr-bench.rs:538-555 with one box a line: grown by relv * its height across.
+    std::vector<std::vector<RRect>> line{{box}};
+    pad_lines(line, relv, 0.f);
+    float l, t, r, b;
+    line[0][0].bbox(l, t, r, b);
+    // ppocr.rs:42-53: the clamped box, at least 1 x 1, resized to 48 rows keeping its aspect.
+    auto clampf = [](float v, int hi) { return int(std::min(std::max(v, 0.f), float(hi))); };
+    PpLine p;
+    p.left = clampf(l, page_w), p.top = clampf(t, page_h);
+    const int rr = clampf(r, page_w), bb = clampf(b, page_h);
+    p.cw = std::max(rr - p.left, 1), p.ch = std::max(bb - p.top, 1);
+    p.out_w = std::min(std::max(int(std::ceil(float(PP_LINE_H) * float(p.cw) / float(p.ch))), 8), 3200);
+    return p;
+}
+
+BatchPlan plan_pp_batches(const std::vector<int> &out_w, int per_batch) {
+    // ocr-bench.rs:330-345 (PPGROUP = 0): sorted by width, cut into batches of per_batch, each as
+    // wide as its widest line rounded up to a multiple of 8.
+    std::vector<int> order(out_w.size());
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return out_w[size_t(a)] < out_w[size_t(b)]; });
+    BatchPlan plan;
+    for (size_t c = 0; c < order.size(); c += size_t(per_batch)) {
+        std::vector<int> members(order.begin() + long(c), order.begin() + long(std::min(order.size(), c + size_t(per_batch))));
+        int wmax = 8;
+        for (int i : members) wmax = std::max(wmax, out_w[size_t(i)]);
+        plan.lines.push_back(std::move(members));
+        plan.width.push_back((wmax + 7) / 8 * 8);
+    }
+    return plan;
+}
+
+std::string pp_ctc_decode(const uint32_t *best, int steps) {
+    // ppocr.rs:23-33: repeats merged, blanks dropped; class k >= 1 is dictionary entry k - 1,
+    // here the synthetic dictionary (code point U+4E00 + k - 1), the last class a space.
+    std::string s;
+    uint32_t prev = 0;
+    for (int t = 0; t < steps; t++) {
+        const uint32_t c = best[t];
+        if (c != 0 && c != prev) {
+            if (c + 1 == PP_CLASSES) {
+                s.push_back(' ');
+            } else {
+                const uint32_t cp = 0x4E00u + c - 1;  // 3-byte UTF-8
+                s.push_back(char(0xE0 | (cp >> 12)));
+                s.push_back(char(0x80 | ((cp >> 6) & 0x3F)));
+                s.push_back(char(0x80 | (cp & 0x3F)));
+            }
+        }
+        prev = c;
+    }
+    return s;
 }
 
 std::vector<std::vector<RRect>> find_text_lines(const std::vector<RRect> &words) {

@@ -56,6 +56,39 @@ struct BatchPlan {
 };
 BatchPlan plan_batches(const std::vector<int> &out_w, int round_to = 50, int per_batch = 20);
 
+// ---- PP-OCR (DB detection, SVTR recognition) ----------------------------------------------
+// DB post-processing parameters (ppdet.rs:48-61; the threshold itself runs on the GPU).
+struct DbParams {
+    float box_thresh = 0.45f, unclip_ratio = 1.4f, min_size = 3.f;
+};
+
+// ppdet::boxes (ppdet.rs:87-132) from the thresholded map (bits) and the map itself (prob, for
+// the box scores), both w x h: each 8-connected component's minimum-area rectangle, kept when
+// its shorter side is at least min_size and its mean probability at least box_thresh, grown by
+// the DB unclip offset, scaled to the page and put in reading order. The reference simplifies
+// each contour (Douglas-Peucker, 2 px) before its rectangle; here the rectangle encloses the
+// component's convex hull.
+std::vector<RRect> db_boxes(const uint32_t *bits, const float *prob, int w, int h, float to_page_x, float to_page_y,
+                            const DbParams &db = DbParams{});
+
+constexpr int PP_LINE_H = 48, PP_CLASSES = 18708;
+
+// One PP-OCR line image: the page box [left, left + cw) x [top, top + ch) and the width it is
+// resized to at height 48.
+struct PpLine {
+    int left = 0, top = 0, cw = 1, ch = 1, out_w = 8;
+};
+// A DB box as a line (ocr-bench.rs:538-555 with relv, relend 0) and its crop (ppocr.rs:42-53).
+PpLine pp_line_box(const RRect &box, float relv, int page_w, int page_h);
+
+// PP-OCR batching (ocr-bench.rs:330-345): sorted by width, per_batch a batch, each padded to its
+// widest line rounded up to a multiple of 8.
+BatchPlan plan_pp_batches(const std::vector<int> &out_w, int per_batch = 16);
+
+// Greedy CTC for the PP-OCR head (ppocr.rs:23-33) with a synthetic dictionary: class k in
+// [1, 18706] is code point U+4E00 + k - 1 (UTF-8), class 18707 the space, 0 the blank.
+std::string pp_ctc_decode(const uint32_t *best, int steps);
+
 // Greedy CTC over per-step arg-max classes (ocr-bench.rs:62-74): emit when best != 0,
 // best != prev and t * 4 < width. Classes index the 96-character ocrs alphabet (class 0 blank).
 std::string ctc_decode(const uint32_t *best, int steps, int stride, int width);

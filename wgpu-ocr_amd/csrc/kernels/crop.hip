@@ -58,7 +58,50 @@ __global__ void line_crop_kernel(const CropLine *lines, const int *row_off, cons
     }
 }
 
+// PP-OCR line images: the crop resized to 48 rows x out_w columns bilinearly (half-pixel,
+// clamped) and rounded to bytes (the reference resizes to an 8-bit image), then per channel
+// (v / 255 - 0.5) / 0.5 in RGB order, zero past out_w. Page pixels outside the page read as 0.
+__global__ void pp_line_crop_kernel(const PpCropLine *lines) {
+#pragma clang fp contract(off)
+    const PpCropLine L = lines[blockIdx.y];
+    const int total = PP_LINE_H * L.wb;
+    const float sy = float(L.ch) / float(PP_LINE_H), sx = float(L.cw) / float(L.out_w);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int ox = i % L.wb, oy = i / L.wb;
+        float v[3] = {0.f, 0.f, 0.f};
+        if (ox < L.out_w) {
+            const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(L.ch) - 1.f);
+            const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(L.cw) - 1.f);
+            const int y1 = int(iy), x1 = int(ix);
+            const int y2 = min(y1 + 1, L.ch - 1), x2 = min(x1 + 1, L.cw - 1);
+            const float fy = iy - float(y1), fx = ix - float(x1);
+            auto px = [&](int cx, int cy, int c) -> float {
+                const int x = L.left + cx, y = L.top + cy;
+                if (x < 0 || y < 0 || x >= L.pw || y >= L.ph) return 0.f;
+                return float(L.rgb[(size_t(y) * L.pw + x) * 3 + c]);
+            };
+            for (int c = 0; c < 3; c++) {
+                const float top = mixf(px(x1, y1, c), px(x2, y1, c), fx);
+                const float bot = mixf(px(x1, y2, c), px(x2, y2, c), fx);
+                const float q = floorf(mixf(top, bot, fy) + 0.5f);
+                v[c] = (q / 255.f - 0.5f) / 0.5f;
+            }
+        }
+        for (int c = 0; c < 3; c++) L.dst[(size_t(c) * PP_LINE_H + oy) * L.wb + ox] = v[c];
+    }
+}
+
 }  // namespace
+
+void pp_line_crop(const PpCropLine *d_lines, int nlines, int max_wb, hipStream_t s) {
+    if (nlines <= 0) return;
+    if (nlines > 65535) fail("pp_line_crop: more than 65535 lines");
+    const int per_line = (PP_LINE_H * max_wb + 255) / 256;
+    dim3 grid(unsigned(per_line < 64 ? per_line : 64), unsigned(nlines));
+    ProbeScope probe("line_crop", s, 0, 12.0 * double(nlines) * PP_LINE_H * max_wb);
+    hipLaunchKernelGGL(pp_line_crop_kernel, grid, dim3(256), 0, s, d_lines);
+    OCR_HIP(hipGetLastError());
+}
 
 void line_crop(const CropLine *d_lines, int nlines, const int *d_row_off, const int *d_spans, int max_wb,
                hipStream_t s) {

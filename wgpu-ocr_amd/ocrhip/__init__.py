@@ -83,6 +83,16 @@ SIGNATURES = {
     "ocr_nd_det_input_device": (ctypes.c_int, [P, P, U32, U32, U32, P]),
     "ocr_db_threshold": (ctypes.c_int, [P, P, U32, U32, F32, P]),
     "ocr_db_threshold_device": (ctypes.c_int, [P, P, U32, U32, F32, P]),
+    "ocr_pp_pipeline_new": (P, [P, P, P]),
+    "ocr_pp_pipeline_free": (None, [P]),
+    "ocr_pp_pipeline_run_device": (ctypes.c_int, [P, P, P, P, U32]),
+    "ocr_pp_pipeline_run": (ctypes.c_int, [P, P, P, P, U32]),
+    "ocr_pp_pipeline_stats_get": (ctypes.c_int, [P, P]),
+    "ocr_pp_pipeline_page": (ctypes.c_int, [P, U32, PU32]),
+    "ocr_pp_pipeline_line_text": (ctypes.c_int, [P, U32, U32, ctypes.c_char_p, U32, PU32]),
+    "ocr_db_boxes": (ctypes.c_int, [P, P, U32, U32, F32, F32, F32, F32, F32, P, U32, PU32]),
+    "ocr_pp_line_box": (ctypes.c_int, [P, F32, U32, U32, P]),
+    "ocr_pp_line_images": (ctypes.c_int, [P, P, U32, U32, P, U32, U32, P]),
 }
 
 
@@ -492,3 +502,95 @@ class Pipeline:
                 self.handle = None
         except Exception:
             pass
+
+
+class ocr_pp_opts(ctypes.Structure):
+    _fields_ = [("merge", ctypes.c_uint32), ("thr", ctypes.c_float), ("relv", ctypes.c_float),
+                ("max_side", ctypes.c_uint32), ("per_batch", ctypes.c_uint32), ("threads", ctypes.c_uint32),
+                ("det_batch", ctypes.c_uint32), ("box_thresh", ctypes.c_float), ("unclip_ratio", ctypes.c_float),
+                ("min_size", ctypes.c_float)]
+
+
+class PpPipeline:
+    """The PP-OCR page pipeline (ocr-bench.rs with DET=ppocr REC=ppocr): DB detection, host boxes,
+    SVTR recognition with the fused arg-max head, host CTC."""
+
+    def __init__(self, det: NdGraph, rec: NdGraph, merge=2, thr=0.3, relv=0.1, max_side=960, per_batch=16,
+                 threads=0, det_batch=4):
+        self.ctx = det.ctx
+        self._keep = (det, rec)
+        opts = ocr_pp_opts(merge, thr, relv, max_side, per_batch, threads, det_batch, 0.0, 0.0, 0.0)
+        self.handle = lib().ocr_pp_pipeline_new(det.handle, rec.handle, ctypes.byref(opts))
+        if not self.handle:
+            raise OcrError(lib().ocr_last_error().decode())
+
+    def run_device(self, d_pages, ws, hs):
+        n = len(d_pages)
+        arr = (ctypes.c_void_p * n)(*[b.ptr for b in d_pages])
+        w, h = np.asarray(ws, np.uint32), np.asarray(hs, np.uint32)
+        _check(lib().ocr_pp_pipeline_run_device(self.handle, arr, _ptr(w), _ptr(h), n))
+
+    def run(self, pages):
+        pages = [np.ascontiguousarray(p, np.uint8) for p in pages]
+        n = len(pages)
+        arr = (ctypes.c_void_p * n)(*[p.ctypes.data for p in pages])
+        w = np.asarray([p.shape[1] for p in pages], np.uint32)
+        h = np.asarray([p.shape[0] for p in pages], np.uint32)
+        _check(lib().ocr_pp_pipeline_run(self.handle, arr, _ptr(w), _ptr(h), n))
+
+    def stats(self) -> dict:
+        s = ocr_pipeline_stats()
+        _check(lib().ocr_pp_pipeline_stats_get(self.handle, ctypes.byref(s)))
+        return {k: getattr(s, k) for k, _ in ocr_pipeline_stats._fields_}
+
+    def texts(self, page: int):
+        nl = ctypes.c_uint32()
+        _check(lib().ocr_pp_pipeline_page(self.handle, page, ctypes.byref(nl)))
+        out = []
+        buf = ctypes.create_string_buffer(1 << 16)
+        n = ctypes.c_uint32()
+        for i in range(nl.value):
+            _check(lib().ocr_pp_pipeline_line_text(self.handle, page, i, buf, 1 << 16, ctypes.byref(n)))
+            out.append(buf.value.decode())
+        return out
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().ocr_pp_pipeline_free(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+def db_boxes(bits: np.ndarray, prob: np.ndarray, to_page=(1.0, 1.0), box_thresh=0.45, unclip_ratio=1.4,
+             min_size=3.0):
+    """ppdet::boxes (ppdet.rs:87-132) on the host: [n, 6] (cx, cy, ux, uy, w, h) in page units."""
+    prob = np.ascontiguousarray(prob, np.float32)
+    bits = np.ascontiguousarray(bits, np.uint32)
+    h, w = prob.shape
+    count = ctypes.c_uint32()
+    _check(lib().ocr_db_boxes(_ptr(bits), _ptr(prob), w, h, to_page[0], to_page[1], box_thresh, unclip_ratio,
+                              min_size, None, 0, ctypes.byref(count)))
+    out = np.zeros((max(count.value, 1), 6), np.float32)
+    _check(lib().ocr_db_boxes(_ptr(bits), _ptr(prob), w, h, to_page[0], to_page[1], box_thresh, unclip_ratio,
+                              min_size, _ptr(out), count.value, ctypes.byref(count)))
+    return out[: count.value]
+
+
+def pp_line_box(box, relv: float, page_w: int, page_h: int):
+    """(left, top, width, height, resized width) of a box's PP-OCR line image."""
+    b = np.ascontiguousarray(box, np.float32)
+    out = np.zeros(5, np.int32)
+    _check(lib().ocr_pp_line_box(_ptr(b), relv, page_w, page_h, _ptr(out)))
+    return tuple(int(v) for v in out)
+
+
+def pp_line_images(ctx: Context, rgb: np.ndarray, lines, wb: int) -> np.ndarray:
+    """PP-OCR line images [n, 3, 48, wb] of an RGB page on the GPU (ppocr.rs:42-78)."""
+    rgb = np.ascontiguousarray(rgb, np.uint8)
+    ln = np.ascontiguousarray(np.asarray(lines, np.int32).reshape(-1, 5))
+    out = np.empty((len(ln), 3, 48, wb), np.float32)
+    _check(lib().ocr_pp_line_images(ctx.handle, _ptr(rgb), rgb.shape[1], rgb.shape[0], _ptr(ln), len(ln), wb,
+                                    _ptr(out)))
+    return out

@@ -17,7 +17,7 @@ Detector: [1, 3, H, W] (multiples of 32) -> stem + 4 depthwi
 stages (strides 4, 8, 16, 32; 32-256 channels) -> a DB FPN (1x1 laterals to 64, nearest x2
 top-down adds, 3x3 convs to 16, nearest upsampling to H/4, Concat) -> the DB head (3x3 conv,
 BatchNormalization, Relu, ConvTranspose x2 with Relu, ConvTranspose x2 with Sigmoid) -> the
-probability map [1, 1, H, W].
+probability map [1, 1, H, W]. Its last layer is fitted so the map follows the ink (det_model).
 
 Every weight is Kaiming-normal from a seeded PCG64 stream, rounded to a float16 value.
 """
@@ -190,34 +190,150 @@ def rec_model(seed: int = 0, classes: int = PP_CLASSES) -> bytes:
 # ---------------------------------------------------------------------------------------------
 # DB detector
 # ---------------------------------------------------------------------------------------------
-def det_model(seed: int = 0) -> bytes:
-    b = _B("ppocr_det_synth", seed + 700)
-    x = "pp_page"
-    x = b.relu(b.bn(b.conv(x, 3, 16, stride=(2, 2), bias=False), 16))                    # /2
+class _Eager:
+    """numpy evaluation of the detector's layers, for the calibration of its last layer only."""
+
+    @staticmethod
+    def conv(x, w, b, stride, group):
+        n, c, h, wd = x.shape
+        cout, cin_g, kh, kw = w.shape
+        xp = np.pad(x, ((0, 0), (0, 0), (kh // 2, kh // 2), (kw // 2, kw // 2)))
+        oh, ow = (h + 2 * (kh // 2) - kh) // stride[0] + 1, (wd + 2 * (kw // 2) - kw) // stride[1] + 1
+        taps = [xp[:, :, ky: ky + stride[0] * (oh - 1) + 1: stride[0], kx: kx + stride[1] * (ow - 1) + 1: stride[1]]
+                for ky in range(kh) for kx in range(kw)]
+        if group == c and cin_g == 1:  # depthwise
+            y = sum(t * w[:, 0, k // kw, k % kw][None, :, None, None] for k, t in enumerate(taps))
+        else:
+            cols = np.stack(taps, axis=2).reshape(n, c * kh * kw, oh * ow)  # channel-major like w
+            y = np.einsum("ok,nkp->nop", w.reshape(cout, -1), cols).reshape(n, cout, oh, ow)
+        return (y + (0 if b is None else b[None, :, None, None])).astype(np.float32)
+
+    @staticmethod
+    def bn(x, g, b, m, v, eps=1e-5):
+        s = g / np.sqrt(v + eps)
+        return (x * s[None, :, None, None] + (b - m * s)[None, :, None, None]).astype(np.float32)
+
+    @staticmethod
+    def up(x, f):
+        f = int(f)
+        return np.repeat(np.repeat(x, f, axis=2), f, axis=3)
+
+    @staticmethod
+    def convt2(x, w, b):
+        n, c, h, wd = x.shape
+        y = np.zeros((n, w.shape[1], 2 * h, 2 * wd), np.float32)
+        for dy in range(2):
+            for dx in range(2):
+                y[:, :, dy::2, dx::2] = np.einsum("co,nchw->nohw", w[:, :, dy, dx], x)
+        return y + b[None, :, None, None]
+
+
+def _det_layers(b: _B, x_name: str, x_val):
+    """The detector up to the features the last ConvTranspose reads: graph nodes into b, and the
+    same layers evaluated with numpy on x_val (None: graph only). Returns (name, value)."""
+    E = _Eager
+    v = x_val
+
+    def cbr(x, v, cin, cout, k=3, stride=(1, 1), group=1, blur=False, signed=False):
+        fan = cin // group * k * k
+        wt = kaiming(b.rng, (cout, cin // group, k, k), fan)
+        if blur or signed:
+            # Random positive kernels normalised to sum 1 (a random blur), with a random sign per
+            # output channel for the stem: the features keep how dark each region is.
+            wt = np.abs(wt) / np.abs(wt).reshape(cout, -1).sum(axis=1)[:, None, None, None]
+            if signed:
+                wt *= np.where(b.rng.random(cout) < 0.5, -1.0, 1.0).astype(np.float32)[:, None, None, None] * 4
+            wt = _f16_exact(wt)
+        gamma = _f16_exact(b.rng.uniform(0.8, 1.2, cout).astype(np.float32))
+        beta = _f16_exact(b.rng.uniform(-0.1, 0.1, cout).astype(np.float32))
+        mean = _f16_exact(b.rng.uniform(-0.1, 0.1, cout).astype(np.float32))
+        var = _f16_exact(b.rng.uniform(0.5, 1.5, cout).astype(np.float32))
+        y = b.g.add("Conv", [x, b.w("cw", wt)], kernel_shape=[k, k], pads=[k // 2] * 4, strides=list(stride),
+                    group=group)
+        y = b.g.add("BatchNormalization", [y] + [b.w(nm, a) for nm, a in
+                                                 (("g", gamma), ("b", beta), ("m", mean), ("v", var))], epsilon=1e-5)
+        y = b.relu(y)
+        if v is not None:
+            v = np.maximum(E.bn(E.conv(v, wt, None, stride, group), gamma, beta, mean, var), 0)
+        return y, v
+
+    def conv(x, v, cin, cout, k):
+        wt = kaiming(b.rng, (cout, cin, k, k), cin * k * k)
+        y = b.g.add("Conv", [x, b.w("cw", wt)], kernel_shape=[k, k], pads=[k // 2] * 4, strides=[1, 1])
+        return y, (None if v is None else E.conv(v, wt, None, (1, 1), 1))
+
+    def add(a, va, c, vc):
+        return b.g.add("Add", [a, c]), (None if va is None else va + vc)
+
+    def up(x, vx, f):
+        return b.resize(x, float(f)), (None if vx is None else E.up(vx, f))
+
+    x, v = cbr(x_name, v, 3, 16, stride=(2, 2), signed=True)                             # /2
     feats = []
     cin = 16
     for cout in (32, 64, 128, 256):                                                      # /4 .. /32
-        x = b.relu(b.bn(b.conv(x, cin, cin, stride=(2, 2), group=cin, bias=False), cin))
-        x = b.relu(b.bn(b.conv(x, cin, cout, k=1, bias=False), cout))
-        feats.append(x)
+        x, v = cbr(x, v, cin, cin, stride=(2, 2), group=cin, blur=True)
+        x, v = cbr(x, v, cin, cout, k=1)
+        feats.append((x, v, cout))
         cin = cout
-    c2, c3, c4, c5 = feats
-    in2, in3, in4, in5 = (b.conv(f, c, 64, k=1, bias=False) for f, c in zip(feats, (32, 64, 128, 256)))
-    out4 = b.g.add("Add", [in4, b.resize(in5, 2.0)])
-    out3 = b.g.add("Add", [in3, b.resize(out4, 2.0)])
-    out2 = b.g.add("Add", [in2, b.resize(out3, 2.0)])
-    p5 = b.resize(b.conv(in5, 64, 16, bias=False), 8.0)
-    p4 = b.resize(b.conv(out4, 64, 16, bias=False), 4.0)
-    p3 = b.resize(b.conv(out3, 64, 16, bias=False), 2.0)
-    p2 = b.conv(out2, 64, 16, bias=False)
-    fuse = b.g.add("Concat", [p5, p4, p3, p2], axis=1)                                    # [1, 64, H/4, W/4]
-    x = b.relu(b.bn(b.conv(fuse, 64, 16, bias=False), 16))
-    w1 = b.w("tw", kaiming(b.rng, (16, 16, 2, 2), 16))
-    x = b.g.add("ConvTranspose", [x, w1, b.w("tb", uniform_bias(b.rng, 16, 16))], kernel_shape=[2, 2], strides=[2, 2])
+    lat = [conv(f, fv, c, 64, 1) for f, fv, c in feats]
+    (in2, v2), (in3, v3), (in4, v4), (in5, v5) = lat
+    out4 = add(in4, v4, *up(in5, v5, 2))
+    out3 = add(in3, v3, *up(*out4, 2))
+    out2 = add(in2, v2, *up(*out3, 2))
+    p5 = up(*conv(in5, v5, 64, 16, 3), 8)
+    p4 = up(*conv(*out4, 64, 16, 3), 4)
+    p3 = up(*conv(*out3, 64, 16, 3), 2)
+    p2 = conv(*out2, 64, 16, 3)
+    fuse = b.g.add("Concat", [p5[0], p4[0], p3[0], p2[0]], axis=1)                       # [1, 64, H/4, W/4]
+    fv = None if v is None else np.concatenate([p5[1], p4[1], p3[1], p2[1]], axis=1)
+    x, v = cbr(fuse, fv, 64, 16)
+    w1 = kaiming(b.rng, (16, 16, 2, 2), 16)
+    b1 = uniform_bias(b.rng, 16, 16)
+    x = b.g.add("ConvTranspose", [x, b.w("tw", w1), b.w("tb", b1)], kernel_shape=[2, 2], strides=[2, 2])
     x = b.relu(x)
-    w2 = b.w("tw", kaiming(b.rng, (16, 1, 2, 2), 16))
-    x = b.g.add("ConvTranspose", [x, w2], kernel_shape=[2, 2], strides=[2, 2])
-    x = b.g.add("Add", [x, b.w("tb", np.zeros(1, np.float32))])
+    if v is not None:
+        v = np.maximum(E.convt2(v, w1, b1), 0)
+    return x, v
+
+
+def _det_calibration_input(seed: int = 999):
+    """A synthetic page as the detector sees it (about [1, 3, 960, 736]: page pixels sampled at
+    the resize's source positions, BGR, ImageNet-normalised) and its word-block mask at H/2."""
+    from . import synth
+    rgb, blocks = synth.page(seed, with_blocks=True)
+    h, w = rgb.shape[:2]
+    ow, oh = 736, 960
+    ys = np.minimum(((np.arange(oh) + 0.5) * h / oh).astype(int), h - 1)
+    xs = np.minimum(((np.arange(ow) + 0.5) * w / ow).astype(int), w - 1)
+    small = rgb[np.ix_(ys, xs)].astype(np.float32)[..., ::-1]
+    mean, dev = np.array([0.485, 0.456, 0.406], np.float32), np.array([0.229, 0.224, 0.225], np.float32)
+    x = ((small / 255.0 - mean) / dev).transpose(2, 0, 1)[None].astype(np.float32)
+    label = blocks[np.ix_(ys[1::2], xs[1::2])]
+    return x, label
+
+
+def det_model(seed: int = 0) -> bytes:
+    """The DB detector. Its last layer (ConvTranspose 16 -> 1 with Sigmoid) is not random: its
+    four taps share one weight vector (a 1 x 1 projection upsampled by 2, as the ocrs synthetic
+    detector's heads are tied) fitted by least squares on a held-out synthetic page (seed 999)
+    against its word blocks, so that the probability map follows the ink."""
+    x_in, label = _det_calibration_input()
+    b = _B("ppocr_det_synth", seed + 700)
+    x, feats = _det_layers(b, "pp_page", x_in)
+    f = feats[0].reshape(16, -1).T.astype(np.float64)                                    # [pixels, 16]
+    a = np.concatenate([f, np.ones((f.shape[0], 1))], axis=1)
+    y = np.where(label.reshape(-1), 1.0, -1.0)
+    wt = np.sqrt(np.where(label, 0.5 / label.mean(), 0.5 / (1 - label.mean()))).reshape(-1)
+    sol = np.linalg.lstsq(a * wt[:, None], y * wt, rcond=None)[0]
+    # Logits of about +-4; the bias puts 10 % of the fit page's paper pixels (most of them next to
+    # the ink) above 0.3.
+    sol *= 4.0
+    paper = (f @ sol[:-1])[~label.reshape(-1)]
+    sol[-1] = np.log(0.3 / 0.7) - np.quantile(paper, 0.90)
+    w2 = np.repeat(np.repeat(sol[:-1].reshape(16, 1, 1, 1), 2, axis=2), 2, axis=3).astype(np.float32)
+    x = b.g.add("ConvTranspose", [x, b.w("tw", _f16_exact(w2))], kernel_shape=[2, 2], strides=[2, 2])
+    x = b.g.add("Add", [x, b.w("tb", _f16_exact(np.array([sol[-1]], np.float32)))])
     out = b.g.add("Sigmoid", [x])
     return b.g.model("pp_page", [1, 3, "height", "width"], out, [1, 1, "height", "width"])
 
