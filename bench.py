@@ -70,14 +70,40 @@ def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
                       f"(oracle: C restatement with OpenMP, float32)"}
 
 
+def pp_pipeline(ctx, d_pages, ws, hs, merge, steps=2):
+    """The PP-OCR whole-page pipeline on the same resident pages (DB detector at long side 960,
+    threshold 0.3, host boxes, SVTR recogniser with the 18 708-class head): a supplementary
+    figure, not the headline value."""
+    import ocrhip
+    from ocrhip import synth_pp
+
+    det = ocrhip.NdGraph(ctx, synth_pp.model_path("det"))
+    rec = ocrhip.NdGraph(ctx, synth_pp.model_path("rec"), stop_before_softmax=True)
+    pipe = ocrhip.PpPipeline(det, rec, merge=merge)
+    pipe.run_device(d_pages, ws, hs)
+    ctx.synchronize()
+    lines = 0
+    t = time.perf_counter()
+    for _ in range(steps):
+        pipe.run_device(d_pages, ws, hs)
+        lines += pipe.stats()["lines"]
+    ctx.synchronize()
+    secs = time.perf_counter() - t
+    n = steps * len(d_pages)
+    return {"workload": f"PP-OCRv6-architecture DB det + SVTR rec, {len(d_pages)} synthetic 2550x3300 pages per step",
+            "pages_per_sec": n / secs, "ms_per_page": 1e3 * secs / n, "lines_per_page": lines / n,
+            "rec_lines_per_sec": lines / secs, "steps": steps}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--pages", type=int, default=12)
-    ap.add_argument("--merge", type=int, default=2)
+    ap.add_argument("--merge", type=int, default=6)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-pp", action="store_true", help="skip the PP-OCR pipeline measurement")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the pipeline shards by page with no exchange, so N GPUs run N "
@@ -154,6 +180,8 @@ def main():
         "kernels_ms_per_page": {f: round(k["ms"] / n_pages, 4) for f, k in
                                 sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])},
     }
+    if not args.no_pp:
+        out["pp_pipeline"] = pp_pipeline(ctx, d_pages, ws, hs, args.merge)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(det_path, rec_path, pages)
     print(json.dumps(out))

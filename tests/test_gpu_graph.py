@@ -115,6 +115,35 @@ def test_conv_transpose_2x3(ctx, tmp_path):
     check(ctx, p, RNG.standard_normal((2, 20, 5, 7)).astype(np.float32))
 
 
+@pytest.mark.parametrize("k,stride,cin,cout", [((3, 3), 1, 8, 5), ((2, 2), 2, 40, 16), ((3, 3), 2, 12, 7),
+                                               ((1, 1), 2, 6, 4)])
+def test_conv_transpose_phases(ctx, tmp_path, k, stride, cin, cout):
+    """Sub-pixel phases on the matrix cores (any kernel at least the stride), and the scalar
+    kernel when a phase has no taps (1 x 1 with stride 2)."""
+    def net(g, x):
+        wt = RNG.standard_normal((cin, cout, *k)).astype(np.float32) * 0.3
+        y = g.add("ConvTranspose", [x, g.init("w", wt), g.init("b", RNG.standard_normal(cout).astype(np.float32))],
+                  kernel_shape=list(k), strides=[stride, stride])
+        return g.add("Relu", [y])
+    p = build(tmp_path, "tp", net, (2, cin, 6, 9))
+    check(ctx, p, RNG.standard_normal((2, cin, 6, 9)).astype(np.float32))
+
+
+def test_conv_pool_fusion_single_and_dual(ctx, tmp_path):
+    """A MaxPool after a 3 x 3 conv runs in its epilogue: alone, and next to the full output
+    when a Concat also reads the conv."""
+    def net(g, x):
+        a = conv(g, x, 16, 32, act="Relu")
+        pa = g.add("MaxPool", [a], kernel_shape=[2, 2], strides=[2, 2])
+        b = conv(g, pa, 32, 32, act="Relu")
+        pb = g.add("MaxPool", [b], kernel_shape=[2, 2], strides=[2, 2])
+        up = g.add("ConvTranspose", [pb, g.init("wu", RNG.standard_normal((32, 32, 2, 3)).astype(np.float32) * 0.2)],
+                   kernel_shape=[2, 3], strides=[2, 2])
+        return g.add("Concat", [up, b], axis=1)
+    p = build(tmp_path, "pf", net, (2, 16, 20, 34))
+    check(ctx, p, RNG.standard_normal((2, 16, 20, 34)).astype(np.float32))
+
+
 def test_maxpool_slice_pad(ctx, tmp_path):
     def net(g, x):
         y = g.add("MaxPool", [x], kernel_shape=[2, 1], strides=[2, 1])

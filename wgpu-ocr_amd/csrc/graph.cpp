@@ -115,6 +115,27 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                 s.kind = OpKind::Conv;
                 s.cin = cin_g;
                 s.mfma = conv_mfma_supported(kh, kw, s.sh, s.sw);
+                // A MaxPool right after (kernel = stride, no padding) runs in the conv's epilogue:
+                // alone when it is the conv's only reader, next to the full output otherwise.
+                if (s.mfma && kh == 3 && kw == 3 && i + 1 < nodes.size() && !env_set("NOPOOLFUSE")) {
+                    const Node &nx = nodes[i + 1];
+                    auto k = nx.ints("kernel_shape");
+                    auto ks = nx.ints("strides");
+                    const int rd = onnx.readers(s.output);
+                    if (nx.op == "MaxPool" && nx.inputs.at(0) == s.output && k && k->size() == 2 && (!ks || *ks == *k) &&
+                        symmetric(nx, "pads", 0) == 0 && nx.int_("ceil_mode").value_or(0) == 0 && (*k)[0] >= 1 &&
+                        (*k)[0] <= 8 && (*k)[1] >= 1 && (*k)[1] <= 16 && s.output != onnx.output && (rd == 1 || rd == 2)) {
+                        s.ph = int((*k)[0]);
+                        s.pw = int((*k)[1]);
+                        if (rd == 1) {
+                            s.pool_only = true;
+                            s.output = nx.outputs.at(0);
+                        } else {
+                            s.pool_output = nx.outputs.at(0);
+                        }
+                        i++;
+                    }
+                }
                 if (s.mfma) {
                     s.pk = plan_conv_pack(cin_g, cout, kh, kw);
                     std::vector<uint16_t> hi(s.pk.halves()), lo(s.pk.halves());
@@ -156,6 +177,39 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                             t[((size_t(ky) * s.kw + kx) * s.cin + ci) * s.cout + co] =
                                 w.data[((size_t(ci) * s.cout + co) * s.kh + ky) * s.kw + kx];
             s.w = ctx.upload_weights(t.data(), t.size());
+            // Sub-pixel phases for the matrix cores: y[s*i + py][s*j + px] sums the taps
+            // ky = py + s*m, kx = px + s*q of x[i - m][j - q]; as a conv with leading pads
+            // (ty - 1, tx - 1), tap (a, b) reads x[i - ty + 1 + a][j - tx + 1 + b], i.e. m = ty-1-a.
+            const int st2 = s.sh;
+            bool ok = st2 >= 1 && s.kh >= st2 && s.kw >= st2 && !env_set("NOCONVTMFMA");
+            for (int py = 0; ok && py < st2; py++)
+                for (int px = 0; ok && px < st2; px++) {
+                    Step::TPhase ph;
+                    ph.py = py, ph.px = px;
+                    ph.ty = (s.kh - py + st2 - 1) / st2, ph.tx = (s.kw - px + st2 - 1) / st2;
+                    if (ph.ty < 1 || ph.tx < 1 || ph.ty > 3 || ph.tx > 3) {
+                        ok = false;
+                        break;
+                    }
+                    std::vector<float> cw(size_t(s.cout) * s.cin * ph.ty * ph.tx);
+                    for (int co = 0; co < s.cout; co++)
+                        for (int ci = 0; ci < s.cin; ci++)
+                            for (int a2 = 0; a2 < ph.ty; a2++)
+                                for (int b2 = 0; b2 < ph.tx; b2++) {
+                                    const int ky = py + st2 * (ph.ty - 1 - a2), kx = px + st2 * (ph.tx - 1 - b2);
+                                    cw[((size_t(co) * s.cin + ci) * ph.ty + a2) * ph.tx + b2] =
+                                        w.data[((size_t(ci) * s.cout + co) * s.kh + ky) * s.kw + kx];
+                                }
+                    ph.pk = plan_conv_pack(s.cin, s.cout, ph.ty, ph.tx);
+                    std::vector<uint16_t> hi(ph.pk.halves()), lo(ph.pk.halves());
+                    bool exact = true;
+                    pack_conv_weights(ph.pk, cw.data(), hi.data(), lo.data(), &exact);
+                    ph.pk.exact = exact;
+                    ph.whi = ctx.upload_weights(hi.data(), hi.size());
+                    if (!exact) ph.wlo = ctx.upload_weights(lo.data(), lo.size());
+                    s.phases.push_back(std::move(ph));
+                }
+            if (!ok) s.phases.clear();
         } else if (n.op == "MaxPool") {
             auto k = n.ints("kernel_shape");
             if (!k || k->size() != 2) fail("MaxPool without kernel_shape");
@@ -231,6 +285,12 @@ std::vector<Shape> Graph::shapes(const Shape &in) const {
                 fail("Conv input has " + std::to_string(c) + " channels, weights take " + std::to_string(s.cin));
             o = {n, (h + s.pt + s.pb - s.kh) / s.sh + 1, (w + s.pl + s.pr - s.kw) / s.sw + 1, s.cout};
             if (h + s.pt + s.pb < s.kh || w + s.pl + s.pr < s.kw) fail("Conv input smaller than its kernel");
+            if (s.pool_only || !s.pool_output.empty()) {
+                const Shape pooled{o[0], o[1] / s.ph, o[2] / s.pw, o[3]};
+                if (pooled[1] < 1 || pooled[2] < 1) fail("empty output shape");
+                if (s.pool_only) o = pooled;
+                else sh[s.pool_output] = pooled;
+            }
             break;
         case OpKind::Direct: {
             if (c != 1) fail("direct conv takes one channel");
@@ -300,6 +360,7 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
     for (size_t i = 0; i < steps.size(); i++) {
         for (const std::string &nm : steps[i].inputs) last[nm] = i;
         if (steps[i].kind != OpKind::Identity) produced.insert(steps[i].output);
+        if (!steps[i].pool_output.empty()) produced.insert(steps[i].pool_output);
     }
     for (size_t i = 0; i < steps.size(); i++) {
         const Step &s = steps[i];
@@ -308,7 +369,7 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
         for (const std::string &nm : s.inputs) {
             const int c = [&] {
                 for (size_t j = 0; j < i; j++)
-                    if (steps[j].output == nm) return shp[j][3];
+                    if (steps[j].output == nm || steps[j].pool_output == nm) return shp[j][3];
                 return x.c;
             }();
             if (produced.count(nm) && !into.count(nm) && nm != output && nm != input) into[nm] = {i, off};
@@ -332,18 +393,18 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
         owned[name] = std::move(b);
         return a;
     };
-    // Where step i writes its output.
-    auto out_view = [&](size_t i) -> Act {
-        const Step &s = steps[i];
-        auto it = into.find(s.output);
-        if (it == into.end()) return alloc(s.output, shp[i]);
+    // Where a value of shape sh is written: its own buffer, or its channel range of a Concat's.
+    auto view_for = [&](const std::string &name, const Shape &sh) -> Act {
+        auto it = into.find(name);
+        if (it == into.end()) return alloc(name, sh);
         const size_t ci = it->second.first;
         const std::string &cname = steps[ci].output;
         if (!view.count(cname)) view[cname] = alloc(cname, shp[ci]);
         Act whole = view[cname];
-        Act a{whole.p + it->second.second, shp[i][0], shp[i][1], shp[i][2], shp[i][3], whole.cs};
+        Act a{whole.p + it->second.second, sh[0], sh[1], sh[2], sh[3], whole.cs};
         return a;
     };
+    auto out_view = [&](size_t i) -> Act { return view_for(steps[i].output, shp[i]); };
     auto release = [&](size_t i) {
         // Buffers whose last reader was step i go back to the pool (stream order keeps the reuse
         // safe). A value inside a Concat's buffer is freed with that buffer, whose last use was
@@ -364,6 +425,17 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
                 ConvArgs ca;
                 ca.x = a;
                 ca.y = y;
+                if (s.pool_only) {
+                    // y is the pooled value; the full-size output is never written.
+                    ca.ypool = y;
+                    ca.y = Act{nullptr, y.n, (a.h + s.pt + s.pb - s.kh) + 1, (a.w + s.pl + s.pr - s.kw) + 1, y.c, y.c};
+                    ca.keep_full = false;
+                } else if (!s.pool_output.empty()) {
+                    ca.ypool = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
+                    view[s.pool_output] = ca.ypool;
+                }
+                ca.ph = s.ph;
+                ca.pw = s.pw;
                 ca.wt_hi = s.whi;
                 ca.wt_lo = s.wlo;
                 ca.bias = s.b;
@@ -383,7 +455,29 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
             break;
         case OpKind::ConvT:
             y = out_view(i);
-            conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
+            if (s.phases.empty()) {
+                conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
+                break;
+            }
+            for (const Step::TPhase &ph : s.phases) {
+                const int st2 = s.sh;
+                const int ohp = (y.h - ph.py + st2 - 1) / st2, owp = (y.w - ph.px + st2 - 1) / st2;
+                if (ohp < 1 || owp < 1) continue;
+                ConvArgs ca;
+                ca.x = a;
+                ca.y = Act{y.p + (size_t(ph.py) * y.w + ph.px) * y.cs, y.n, ohp, owp, y.c, y.cs};
+                ca.y_px = st2;
+                ca.y_row = long(st2) * y.w;
+                ca.y_img = long(y.h) * y.w;
+                ca.wt_hi = ph.whi;
+                ca.wt_lo = ph.wlo;
+                ca.bias = s.b;
+                ca.pt = ph.ty - 1;
+                ca.pl = ph.tx - 1;
+                ca.act = s.act;
+                ca.pk = ph.pk;
+                conv_mfma(ca, st);
+            }
             break;
         case OpKind::MaxPool:
             y = out_view(i);

@@ -24,7 +24,20 @@ struct Step {
     ConvPack pk;
     const uint16_t *whi = nullptr, *wlo = nullptr;
     const float *w = nullptr, *b = nullptr;  // float32 weights (direct, transpose, generic) and bias
-    int ph = 1, pw = 1;                       // Direct's fused MaxPool, or MaxPool's kernel
+    int ph = 1, pw = 1;                       // a fused MaxPool's kernel, or MaxPool's kernel
+    // A MaxPool fused into a dense conv: pool_only when it was the conv's only reader (output is
+    // then the pooled value); otherwise pool_output names the pooled value next to the full one.
+    bool pool_only = false;
+    std::string pool_output;
+    // ConvTranspose with stride s as s x s sub-pixel phases: phase (py, px) is a stride-1
+    // ty x tx conv of the input written to output pixels (s * i + py, s * j + px), on the matrix
+    // cores. Empty when the kernel is smaller than the stride or a phase would exceed 3 x 3.
+    struct TPhase {
+        int py = 0, px = 0, ty = 0, tx = 0;
+        ConvPack pk;
+        const uint16_t *whi = nullptr, *wlo = nullptr;
+    };
+    std::vector<TPhase> phases;
     std::vector<int64_t> starts, ends, axes;  // Slice
 };
 

@@ -41,6 +41,14 @@ struct ConvArgs {
     // channels, (max value, index as float bits) of acc + bias, first index on ties, at
     // amax_part[pixel * nblocks + block] (float2 pairs).
     float *amax_part = nullptr;
+    // MaxPool (ph, pw) fused (kernel = stride, floor; NHWC, 3 x 3 only): the pooled output goes
+    // to ypool; the full-size output to y as well when keep_full (its other readers need it).
+    Act ypool;
+    int ph = 1, pw = 1;
+    bool keep_full = true;
+    // NHWC output pixel strides (0: dense): column, row and image steps in pixels, so a conv can
+    // write one phase of a strided output (ConvTranspose's sub-pixel phases).
+    long y_px = 0, y_row = 0, y_img = 0;
     ConvPack pk;
 };
 // True when the MFMA path takes this shape (stride 1, kernel at most 3 x 3).

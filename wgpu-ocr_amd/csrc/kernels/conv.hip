@@ -41,6 +41,9 @@ struct ConvParams {
     const half8 *wt_hi, *wt_lo;
     const float *bias, *res, *affine, *in_scale;
     float2 *amax;  // arg-max partials [pixels][nblocks] instead of y, or null
+    float *yp;     // MaxPool (ph, pw) of the activated output (NHWC), or null
+    size_t yn, yy, yx;  // NHWC output pixel strides: image, row, column
+    int poh, pow_, ypcs, ph, pw;
     int rcs;
     int kh, kw, pt, pl, act, chunks, tiles_x, tiles_y, vec, nchw;
 };
@@ -203,6 +206,47 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
             }
         return;
     }
+    if constexpr (KS == 3) if (p.yp) {
+        // MaxPool fused: the activated tile goes to LDS (the weight buffer, free after the last
+        // barrier), then each thread takes one channel of successive pooled pixels, so pooled
+        // (and full-size) NHWC stores are contiguous along the channels. The tile's TH x TW
+        // pixels hold whole pooling windows (the host picks TH, TW divisible by ph, pw).
+        constexpr int SROW = BN + 1;
+        float *s_out = reinterpret_cast<float *>(&s_w[0][0][0]);
+        static_assert(128 * SROW * 4 <= int(sizeof(s_w)), "pooled tile does not fit the weight buffer");
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const int co = co0 + t * 16 + r;
+                const float bv = (co < p.cout && p.bias) ? p.bias[co] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    s_out[(wave * 32 + m * 16 + 4 * g + i) * SROW + t * 16 + r] = activate_dev(acc[m][t][i] + bv, p.act);
+            }
+        __syncthreads();
+        if (p.y) {
+            for (int idx = tid; idx < 128 * BN; idx += 256) {
+                const int c = idx % BN, pix = idx / BN;
+                const int oy = oy0 + pix / TW, ox = ox0 + pix % TW;
+                if (oy < p.oh && ox < p.ow && co0 + c < p.cout)
+                    p.y[((size_t(img) * p.oh + oy) * p.ow + ox) * p.ycs + co0 + c] = s_out[pix * SROW + c];
+            }
+        }
+        const int pth = TH / p.ph, ptw = TW / p.pw;
+        for (int idx = tid; idx < pth * ptw * BN; idx += 256) {
+            const int c = idx % BN, pp = idx / BN;
+            const int py = pp / ptw, px = pp - py * ptw;
+            const int poy = oy0 / p.ph + py, pox = ox0 / p.pw + px;
+            if (poy >= p.poh || pox >= p.pow_ || co0 + c >= p.cout) continue;
+            float v = -INFINITY;
+            for (int qy = 0; qy < p.ph; qy++)
+                for (int qx = 0; qx < p.pw; qx++)
+                    v = fmaxf(v, s_out[((py * p.ph + qy) * TW + px * p.pw + qx) * SROW + c]);
+            p.yp[((size_t(img) * p.poh + poy) * p.pow_ + pox) * p.ypcs + co0 + c] = v;
+        }
+        return;
+    }
 #pragma unroll
     for (int m = 0; m < 2; m++) {
 #pragma unroll
@@ -224,7 +268,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
                     if (p.res) v += p.res[o];
                     p.y[o] = v;
                 } else {
-                    const size_t o = (size_t(img) * p.oh + oy) * p.ow + ox;
+                    const size_t o = size_t(img) * p.yn + size_t(oy) * p.yy + size_t(ox) * p.yx;
                     if (p.res) v += p.res[o * p.rcs + co];
                     p.y[o * p.ycs + co] = v;
                 }
@@ -321,16 +365,37 @@ void conv_mfma(const ConvArgs &a, hipStream_t s) {
     if (a.y.n != a.x.n) fail("conv_mfma: batch mismatch");
     const bool lo = !pk.exact;
     const int ks = (pk.kh == 1 && pk.kw == 1) ? 1 : 3;
+    const bool pooled = a.ypool.p != nullptr;
+    if (pooled) {
+        if (ks != 3 || a.nchw || a.res || a.affine || a.amax_part) fail("conv_mfma: MaxPool fused only into a 3 x 3 NHWC conv");
+        if (a.ph < 1 || a.pw < 1 || a.ph > 8 || a.pw > 16) fail("conv_mfma: pool size");
+        if (a.ypool.h != a.y.h / a.ph || a.ypool.w != a.y.w / a.pw || a.ypool.c != a.y.c || a.ypool.n != a.y.n)
+            fail("conv_mfma: pooled output shape");
+    }
+    p.y = pooled && !a.keep_full ? nullptr : a.y.p;
+    p.yx = a.y_px ? size_t(a.y_px) : 1;
+    p.yy = a.y_row ? size_t(a.y_row) : size_t(p.ow) * p.yx;
+    p.yn = a.y_img ? size_t(a.y_img) : size_t(p.oh) * p.yy;
+    if ((a.y_px || a.y_row || a.y_img) && (a.nchw || pooled || a.amax_part)) fail("conv_mfma: output strides only for plain NHWC");
+    p.yp = a.ypool.p;
+    p.poh = a.ypool.h;
+    p.pow_ = a.ypool.w;
+    p.ypcs = a.ypool.cs;
+    p.ph = pooled ? a.ph : 1;
+    p.pw = pooled ? a.pw : 1;
     int tw = 128;
     if (ks == 3) {
-        // The tile shape that wastes the fewest pixels (padding and halo) for this output size.
+        // The tile shape that wastes the fewest pixels (padding and halo) for this output size
+        // (whole pooling windows per tile when a MaxPool is fused).
         double best = 1e300;
         for (int cand : {16, 32, 64}) {
             const int th = 128 / cand;
+            if (pooled && (th % a.ph != 0 || cand % a.pw != 0)) continue;
             const double cost = double((p.oh + th - 1) / th * th) * ((p.ow + cand - 1) / cand * cand) *
                                 double((th + 2) * (cand + 2)) / (th * cand);
             if (cost < best) { best = cost; tw = cand; }
         }
+        if (best == 1e300) fail("conv_mfma: no tile holds whole pooling windows");
     }
     const int th = 128 / tw;
     p.tiles_x = (p.ow + tw - 1) / tw;

@@ -1,6 +1,7 @@
 #include "pipeline.h"
 
 #include <algorithm>
+#include <map>
 #include <chrono>
 #include <condition_variable>
 #include <deque>
@@ -156,34 +157,41 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             if (!error.empty()) break;
         }
         RecPass &R = passes[size_t(r)];
-        std::vector<Recognizer::Batch> batches;
-        std::vector<DBuf> batch_bufs;
-        int max_wb = 0;
+        // A line's recognition depends on its batch's width (the padding), not on which lines
+        // share the batch, so every page's batches of one width run as one trunk batch: the
+        // same results with fewer, fuller launches. Widths ascending, pages and batches in order.
+        std::map<int, std::vector<std::pair<int, int>>> by_width;  // width -> (page, line)
         for (int p = p0; p < p1; p++) {
             const PageLayout &L = layouts[size_t(p)];
             pages_[size_t(p)].words = L.words;
             pages_[size_t(p)].lines.assign(L.lines.size(), std::string());
             for (size_t b = 0; b < L.plan.lines.size(); b++) {
-                const int wb = L.plan.width[b], n = int(L.plan.lines[b].size());
-                batch_bufs.emplace_back(&ctx, size_t(n) * LINE_H * wb * sizeof(float));
-                float *base = batch_bufs.back().as<float>();
-                batches.push_back({base, n, wb});
-                max_wb = std::max(max_wb, wb);
-                for (int k = 0; k < n; k++) {
-                    const int li = L.plan.lines[b][size_t(k)];
-                    const LineGeom &g = L.lines[size_t(li)];
-                    CropLine c{d_rgb[p], w[p], h[p], g.left, g.top, g.bw, g.bh, g.out_w,
-                               int(R.row_off.size()), base + size_t(k) * LINE_H * wb, wb};
-                    const int sbase = int(R.spans.size());
-                    for (int32_t o : g.row_off) R.row_off.push_back(o + sbase);
-                    R.spans.insert(R.spans.end(), g.spans.begin(), g.spans.end());
-                    R.crops.push_back(c);
-                    R.rows.push_back({p, li});
-                    R.widths.push_back(g.out_w);
-                }
+                stats_.batches++;
+                for (int li : L.plan.lines[b]) by_width[L.plan.width[b]].push_back({p, li});
             }
         }
-        stats_.batches += int(batches.size());
+        std::vector<Recognizer::Batch> batches;
+        std::vector<DBuf> batch_bufs;
+        int max_wb = 0;
+        for (const auto &kv : by_width) {
+            const int wb = kv.first, n = int(kv.second.size());
+            batch_bufs.emplace_back(&ctx, size_t(n) * LINE_H * wb * sizeof(float));
+            float *base = batch_bufs.back().as<float>();
+            batches.push_back({base, n, wb});
+            max_wb = std::max(max_wb, wb);
+            for (int k = 0; k < n; k++) {
+                const int p = kv.second[size_t(k)].first, li = kv.second[size_t(k)].second;
+                const LineGeom &g = layouts[size_t(p)].lines[size_t(li)];
+                CropLine c{d_rgb[p], w[p], h[p], g.left, g.top, g.bw, g.bh, g.out_w,
+                           int(R.row_off.size()), base + size_t(k) * LINE_H * wb, wb};
+                const int sbase = int(R.spans.size());
+                for (int32_t o : g.row_off) R.row_off.push_back(o + sbase);
+                R.spans.insert(R.spans.end(), g.spans.begin(), g.spans.end());
+                R.crops.push_back(c);
+                R.rows.push_back({p, li});
+                R.widths.push_back(g.out_w);
+            }
+        }
         if (batches.empty()) continue;
         DBuf dcrops(&ctx, R.crops.size() * sizeof(CropLine)), droff(&ctx, R.row_off.size() * 4),
             dspans(&ctx, std::max<size_t>(R.spans.size(), 1) * 4);
