@@ -39,23 +39,44 @@ struct Pt {
 
 float cross(const Pt &o, const Pt &a, const Pt &b) { return (a.x - o.x) * (b.y - o.y) - (a.y - o.y) * (b.x - o.x); }
 
-// Andrew's monotone chain; returns the hull counter-clockwise without repeating the first point.
-std::vector<Pt> hull(std::vector<Pt> p) {
-    std::sort(p.begin(), p.end(), [](const Pt &a, const Pt &b) { return a.x < b.x || (a.x == b.x && a.y < b.y); });
-    p.erase(std::unique(p.begin(), p.end(), [](const Pt &a, const Pt &b) { return a.x == b.x && a.y == b.y; }),
-            p.end());
-    if (p.size() < 3) return p;
+// Convex hull of a component given as row extents (rows ascending; per row the leftmost and
+// rightmost pixel), counter-clockwise in the sense cross > 0, starting at the vertex with the
+// smallest (x, y), collinear points dropped, without repeating the first point. Only a row's two
+// extremes can be hull vertices, and listing them row by row already sorts the points by (y, x):
+// Andrew's monotone chain runs on the transposed points (x, y) -> (y, x) with no sort, and the
+// transposed chain's turn test is the original one negated, so reversing its output restores the
+// orientation. The vertex list is the one the chain over (x, y)-sorted points would give.
+std::vector<Pt> hull_rows(const std::vector<Pt> &p) {
+    // p: (x, y) in (y, x) order, unique.
+    auto tcross = [](const Pt &o, const Pt &a, const Pt &b) {  // cross product of the transposed points
+        return (a.y - o.y) * (b.x - o.x) - (a.x - o.x) * (b.y - o.y);
+    };
+    auto before = [](const Pt &a, const Pt &b) { return a.x < b.x || (a.x == b.x && a.y < b.y); };
+    if (p.size() < 3) {
+        std::vector<Pt> q = p;
+        if (q.size() == 2 && before(q[1], q[0])) std::swap(q[0], q[1]);
+        return q;
+    }
     std::vector<Pt> h(2 * p.size());
     size_t k = 0;
     for (size_t i = 0; i < p.size(); i++) {
-        while (k >= 2 && cross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
+        while (k >= 2 && tcross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
         h[k++] = p[i];
     }
     for (size_t i = p.size() - 1, t = k + 1; i-- > 0;) {
-        while (k >= t && cross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
+        while (k >= t && tcross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
         h[k++] = p[i];
     }
     h.resize(k - 1);
+    if (h.size() == 2) {  // all points collinear: the two ends, smallest (x, y) first
+        if (before(h[1], h[0])) std::swap(h[0], h[1]);
+        return h;
+    }
+    std::reverse(h.begin(), h.end());
+    size_t first = 0;
+    for (size_t i = 1; i < h.size(); i++)
+        if (before(h[i], h[first])) first = i;
+    std::rotate(h.begin(), h.begin() + long(first), h.end());
     return h;
 }
 
@@ -111,8 +132,8 @@ int find(std::vector<int> &parent, int a) {
 
 }  // namespace
 
-// Pixel coordinates of every 8-connected component of a bit mask (h rows of ceil(w / 32) words),
-// reduced to the ends of its row runs (enough for the convex hull).
+// Every 8-connected component of a bit mask (h rows of ceil(w / 32) words) as its rows'
+// leftmost and rightmost pixels, rows ascending (all the convex hull needs; see hull_rows).
 static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w, int h) {
     const int words = (w + 31) / 32;
     std::vector<Run> runs;
@@ -156,7 +177,9 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
             else j++;
         }
     }
-    // Both ends of each run, per component (components in order of their first run).
+    // Row extremes per component (components in order of their first run). Runs are listed row
+    // by row and left to right, so a component's later run in the same row only moves its right
+    // end.
     std::vector<int> comp(runs.size(), -1);
     std::vector<std::vector<Pt>> pts;
     for (size_t r = 0; r < runs.size(); r++) {
@@ -166,8 +189,16 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
             pts.emplace_back();
         }
         auto &v = pts[size_t(comp[size_t(root)])];
-        v.push_back({float(runs[r].x0), float(runs[r].y)});
-        if (runs[r].x1 != runs[r].x0) v.push_back({float(runs[r].x1), float(runs[r].y)});
+        const float y = float(runs[r].y), x0 = float(runs[r].x0), x1 = float(runs[r].x1);
+        const bool same_row = !v.empty() && v.back().y == y;
+        if (same_row) {
+            // the row holds (left) or (left, right): the new right end replaces the old one
+            if (v.size() >= 2 && v[v.size() - 2].y == y) v.back().x = x1;
+            else if (x1 != v.back().x) v.push_back({x1, y});
+        } else {
+            v.push_back({x0, y});
+            if (x1 != x0) v.push_back({x1, y});
+        }
     }
     return pts;
 }
@@ -175,7 +206,7 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
 std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area) {
     std::vector<RRect> out;
     for (auto &v : component_points(bits, w, h)) {
-        RRect r = min_area_rect(hull(std::move(v)));
+        RRect r = min_area_rect(hull_rows(v));
         r.resize(r.w + 2 * expand, r.h + 2 * expand);
         if (r.area() >= min_area) out.push_back(r);
     }
@@ -208,7 +239,7 @@ std::vector<RRect> db_boxes(const uint32_t *bits, const float *prob, int w, int 
                             const DbParams &db) {
     std::vector<RRect> out;
     for (auto &v : component_points(bits, w, h)) {
-        const RRect r = min_area_rect(hull(std::move(v)));
+        const RRect r = min_area_rect(hull_rows(v));
         if (std::min(r.w, r.h) < db.min_size || db_score(prob, w, h, r) < db.box_thresh) continue;
         // Unclip: grown by area * ratio / perimeter on every side (ppdet.rs:104-109).
         const float d = r.w * r.h * db.unclip_ratio / std::max(2.f * (r.w + r.h), 1e-6f);

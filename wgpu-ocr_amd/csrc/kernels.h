@@ -49,6 +49,9 @@ struct ConvArgs {
     // NHWC output pixel strides (0: dense): column, row and image steps in pixels, so a conv can
     // write one phase of a strided output (ConvTranspose's sub-pixel phases).
     long y_px = 0, y_row = 0, y_img = 0;
+    // 1 x 1 GEMM over x = [1][1][M] pixels: GEMM row i reads x's row rows[i] and writes y's row
+    // rows[i] (M = x.w entries), so only the listed rows are computed; or null (dense).
+    const int *rows = nullptr;
     ConvPack pk;
 };
 // True when the MFMA path takes this shape (stride 1, kernel at most 3 x 3).
@@ -78,8 +81,9 @@ void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, 
 // AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c] at
 // line offset noff (gpu.rs:595-614).
 void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s);
-// Per row of [rows][classes]: the arg-max, the last index on ties (ocr-bench.rs:67).
-void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s);
+// Per row of [rows][classes]: the arg-max, the last index on ties (ocr-bench.rs:67). With a row
+// map, row i is physical row map[i] of x and of best.
+void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s, const int *map = nullptr);
 
 // ---- GRU recurrence (kernels/gru.hip) -------------------------------------------------------
 // One layer, both directions, every line with its own length (gpu.rs:680-819). G [t][n][1536]

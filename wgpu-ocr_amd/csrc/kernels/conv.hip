@@ -41,6 +41,7 @@ struct ConvParams {
     const half8 *wt_hi, *wt_lo;
     const float *bias, *res, *affine, *in_scale;
     float2 *amax;  // arg-max partials [pixels][nblocks] instead of y, or null
+    const int *rows;  // 1 x 1 GEMM: row i of x and of y is physical row rows[i] (gather/scatter), or null
     float *yp;     // MaxPool (ph, pw) of the activated output (NHWC), or null
     size_t yn, yy, yx;  // NHWC output pixel strides: image, row, column
     int poh, pow_, ypcs, ph, pw;
@@ -111,7 +112,9 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
                 const int iy = iy0 + hy, ix = ix0 + hx, ci = ci0 + 4 * q;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w && ci < p.cin) {
-                    const float *src = xim + (size_t(iy) * p.w + ix) * p.xcs + ci;
+                    size_t px = size_t(iy) * p.w + ix;
+                    if constexpr (KS == 1) if (p.rows) px = size_t(p.rows[ix]);
+                    const float *src = xim + px * p.xcs + ci;
                     if (p.vec) {
                         v = *reinterpret_cast<const float4 *>(src);
                     } else {
@@ -268,7 +271,8 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
                     if (p.res) v += p.res[o];
                     p.y[o] = v;
                 } else {
-                    const size_t o = size_t(img) * p.yn + size_t(oy) * p.yy + size_t(ox) * p.yx;
+                    size_t o = size_t(img) * p.yn + size_t(oy) * p.yy + size_t(ox) * p.yx;
+                    if constexpr (KS == 1) if (p.rows) o = size_t(p.rows[ox]);
                     if (p.res) v += p.res[o * p.rcs + co];
                     p.y[o * p.ycs + co] = v;
                 }
@@ -351,6 +355,10 @@ void conv_mfma(const ConvArgs &a, hipStream_t s) {
     p.affine = a.affine;
     p.in_scale = a.in_scale;
     p.amax = reinterpret_cast<float2 *>(a.amax_part);
+    p.rows = a.rows;
+    if (a.rows && (pk.kh != 1 || pk.kw != 1 || a.nchw || a.x.n != 1 || a.x.h != 1 || a.amax_part || a.res ||
+                   a.y_px || a.y_row || a.y_img))
+        fail("conv_mfma: a row map needs a plain 1 x 1 NHWC GEMM over one row of pixels");
     p.nchw = a.nchw ? 1 : 0;
     p.rcs = a.res_cs;
     p.kh = pk.kh;

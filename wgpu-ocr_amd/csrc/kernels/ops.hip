@@ -235,10 +235,11 @@ __global__ void avgpool_t_kernel(const float *x, int n, int h, int kh, int T, in
 }
 
 // ---- argmax: one wavefront per row, the last index on ties ---------------------------------
-__global__ void argmax_kernel(const float *x, int rows, int classes, uint32_t *best) {
+__global__ void argmax_kernel(const float *x, int rows, int classes, uint32_t *best, const int *map) {
     int row = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
     int lane = threadIdx.x & 63;
     if (row >= rows) return;
+    if (map) row = map[row];
     const float *r = x + size_t(row) * classes;
     float bv = -INFINITY;
     int bi = -1;
@@ -348,10 +349,11 @@ void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s
     OCR_HIP(hipGetLastError());
 }
 
-void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s) {
+void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s, const int *map) {
     if (rows <= 0) return;
     ProbeScope probe("argmax", s, 0, 4.0 * double(rows) * (classes + 1));
-    hipLaunchKernelGGL(argmax_kernel, dim3(blocks_for(size_t(rows), 4)), dim3(256), 0, s, x, rows, classes, best);
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks_for(size_t(rows), 4)), dim3(256), 0, s, x, rows, classes, best,
+                       map);
     OCR_HIP(hipGetLastError());
 }
 

@@ -177,9 +177,11 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         if ((t.h - pool_kh_) / pool_kh_ + 1 != 1)
             fail("trunk height " + std::to_string(t.h) + " does not pool to one row");
     }
-    const int tmax = d.tmax, ntot = d.ntot, M = tmax * ntot;
+    const int tmax = d.tmax, ntot = d.ntot;
+    if (double(tmax) * ntot >= 2147483647.0) fail("recognition pass too large");
+    const int M = tmax * ntot;
+    // X [t][ntot][256] time-major (gpu.rs:1538-1555); rows t >= a line's length are never read.
     DBuf X(&ctx_, size_t(M) * 256 * sizeof(float));
-    fill(X.as<float>(), size_t(M) * 256, 0.f, st);
     int noff = 0;
     for (int b = 0; b < count; b++) {
         const Act &t = trunks[b].act;
@@ -188,8 +190,18 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         noff += t.n;
     }
     trunks.clear();
-    long long steps = 0;
-    for (int i = 0; i < ntot; i++) steps += lens[i];
+    // The rows that carry a step of some line, t-major: (t, line) with t < lens[line]. The
+    // projections and the output layer run on these rows only (the reference computes all
+    // tmax x ntot rows and ignores the padding ones); G, Y and the logits keep the [t][ntot]
+    // layout, so the recurrence and the caller see the reference's layout.
+    std::vector<int32_t> rows;
+    for (int t = 0; t < tmax; t++)
+        for (int i = 0; i < ntot; i++)
+            if (uint32_t(t) < lens[i]) rows.push_back(t * ntot + i);
+    const int P = int(rows.size());
+    const long long steps = P;
+    DBuf rowsd(&ctx_, rows.size() * sizeof(int32_t));
+    ctx_.h2d(rowsd.get(), rows.data(), rows.size() * sizeof(int32_t));
     DBuf lensd(&ctx_, size_t(ntot) * sizeof(uint32_t));
     ctx_.h2d(lensd.get(), lens, size_t(ntot) * sizeof(uint32_t));
     DBuf G(&ctx_, size_t(M) * 1536 * sizeof(float));
@@ -200,27 +212,28 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         const Layer &L = layers_[l];
         if (in_c != L.input) fail("GRU layer input size");
         ConvArgs ca;
-        ca.x = Act{const_cast<float *>(in), 1, 1, M, in_c, in_c};
-        ca.y = Act{G.as<float>(), 1, 1, M, 1536, 1536};
+        ca.x = Act{const_cast<float *>(in), 1, 1, P, in_c, in_c};
+        ca.y = Act{G.as<float>(), 1, 1, P, 1536, 1536};
+        ca.rows = rowsd.as<int32_t>();
         ca.wt_hi = L.w_hi;
         ca.wt_lo = L.w_lo;
         ca.bias = L.wb;
         ca.pk = L.pk;
         conv_mfma(ca, st);
-        fill(Y[l].as<float>(), size_t(M) * 512, 0.f, st);
         gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd.as<uint32_t>(), ntot, tmax, steps, st);
         in = Y[l].as<float>();
         in_c = 512;
     }
     ConvArgs ca;
-    ca.x = Act{const_cast<float *>(in), 1, 1, M, 512, 512};
-    ca.y = Act{logits, 1, 1, M, classes_, classes_};
+    ca.x = Act{const_cast<float *>(in), 1, 1, P, 512, 512};
+    ca.y = Act{logits, 1, 1, P, classes_, classes_};
+    ca.rows = rowsd.as<int32_t>();
     ca.wt_hi = lin_hi_;
     ca.wt_lo = lin_lo_;
     ca.bias = lin_b_;
     ca.pk = lin_pk_;
     conv_mfma(ca, st);
-    if (best) argmax_rows(logits, M, classes_, best, st);
+    if (best) argmax_rows(logits, P, classes_, best, st, rowsd.as<int32_t>());
 }
 
 }  // namespace ocr

@@ -1,6 +1,7 @@
 #include "runtime.h"
 
 #include <cstdio>
+#include <cstring>
 
 namespace ocr {
 
@@ -179,6 +180,9 @@ Ctx::Ctx(int device, uint32_t lines, size_t pool_mb) : device_(device), lines_(l
 Ctx::~Ctx() {
     (void)hipSetDevice(device_);
     if (stream_) (void)hipStreamSynchronize(stream_);
+    for (const Staged &st : staged_) (void)hipEventDestroy(st.done);
+    for (hipEvent_t e : spare_events_) (void)hipEventDestroy(e);
+    if (ring_) (void)hipHostFree(ring_);
     pool_.trim();
     for (void *p : weights_) (void)hipFree(p);
     if (stream_) (void)hipStreamDestroy(stream_);
@@ -196,8 +200,50 @@ const void *Ctx::upload_raw(const void *data, size_t bytes) {
     return p;
 }
 
+namespace {
+constexpr size_t RING_BYTES = size_t(32) << 20;
+}
+
 void Ctx::h2d(void *dst, const void *src, size_t bytes) {
-    if (bytes) OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_));
+    if (!bytes) return;
+    if (bytes > RING_BYTES / 4) {
+        // Large uploads (whole pages, inputs) go straight from the caller's memory.
+        OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_));
+        return;
+    }
+    std::lock_guard<std::mutex> lk(ring_mu_);
+    if (!ring_) OCR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ring_), RING_BYTES, hipHostMallocDefault));
+    const size_t need = (bytes + 255) & ~size_t(255);
+    if (ring_head_ + need > RING_BYTES) ring_head_ = 0;
+    const size_t b = ring_head_, e = b + need;
+    // Copies that have finished give their regions back; a region still being read by a copy
+    // on the stream is waited for (oldest first) before it is written again.
+    while (!staged_.empty() && hipEventQuery(staged_.front().done) == hipSuccess) {
+        spare_events_.push_back(staged_.front().done);
+        staged_.pop_front();
+    }
+    auto overlaps = [&] {
+        for (const Staged &st : staged_)
+            if (st.begin < e && b < st.end) return true;
+        return false;
+    };
+    while (overlaps()) {
+        OCR_HIP(hipEventSynchronize(staged_.front().done));
+        spare_events_.push_back(staged_.front().done);
+        staged_.pop_front();
+    }
+    std::memcpy(ring_ + b, src, bytes);
+    OCR_HIP(hipMemcpyAsync(dst, ring_ + b, bytes, hipMemcpyHostToDevice, stream_));
+    hipEvent_t ev = nullptr;
+    if (!spare_events_.empty()) {
+        ev = spare_events_.back();
+        spare_events_.pop_back();
+    } else {
+        OCR_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    }
+    OCR_HIP(hipEventRecord(ev, stream_));
+    staged_.push_back({b, e, ev});
+    ring_head_ = e;
 }
 
 void Ctx::d2h(void *dst, const void *src, size_t bytes) {

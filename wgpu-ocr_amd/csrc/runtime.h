@@ -5,6 +5,7 @@
 
 #include <atomic>
 #include <cstddef>
+#include <deque>
 #include <cstdint>
 #include <map>
 #include <mutex>
@@ -128,7 +129,9 @@ class Ctx {
     template <class T> const T *upload_weights(const T *data, size_t count) {
         return static_cast<const T *>(upload_raw(data, count * sizeof(T)));
     }
-    void h2d(void *dst, const void *src, size_t bytes);  // async on the stream (pageable src is staged)
+    // Async on the stream: src is copied into a pinned staging ring first, so the call returns
+    // at once and src may be reused (a copy from pageable memory would wait for the stream).
+    void h2d(void *dst, const void *src, size_t bytes);
     void d2h(void *dst, const void *src, size_t bytes);  // synchronous: waits for the stream
 
   private:
@@ -138,6 +141,16 @@ class Ctx {
     hipStream_t stream_ = nullptr;
     Pool pool_;
     std::vector<void *> weights_;
+    // Pinned staging ring of h2d: regions still read by a copy on the stream, oldest first.
+    struct Staged {
+        size_t begin, end;
+        hipEvent_t done;
+    };
+    char *ring_ = nullptr;
+    size_t ring_head_ = 0;
+    std::deque<Staged> staged_;
+    std::vector<hipEvent_t> spare_events_;
+    std::mutex ring_mu_;
 };
 
 }  // namespace ocr
