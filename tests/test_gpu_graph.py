@@ -167,3 +167,30 @@ def test_shape_errors(ctx, tmp_path):
     gr = ocrhip.Graph(ctx, p)
     with pytest.raises(ocrhip.OcrError):
         gr.run(np.zeros((1, 3, 5, 5), np.float32))  # wrong channel count
+
+
+@pytest.mark.parametrize("cin,cout,h,w,pool,two", [(32, 64, 17, 45, (2, 2), False), (64, 128, 16, 37, (2, 1), False),
+                                                   (128, 256, 4, 53, (2, 1), False), (16, 97, 9, 23, (2, 1), True),
+                                                   (256, 128, 13, 19, (2, 2), True), (20, 48, 31, 70, (2, 2), False)])
+def test_conv_pool_fusion_shapes(ctx, tmp_path, cin, cout, h, w, pool, two):
+    """MaxPool fused into the conv epilogue over odd sizes, several channel blocks (cout not a
+    multiple of the block), several input slices and partial slices; `two`: the full output is
+    read as well (by a Concat), so both are written."""
+    h2, w2 = h // pool[0] * pool[0], w // pool[1] * pool[1]
+
+    def crop(g, y, name):
+        return g.add("Slice", [y, g.init(f"{name}0", np.array([0, 0], np.int64)),
+                               g.init(f"{name}1", np.array([h2, w2], np.int64)),
+                               g.init(f"{name}2", np.array([2, 3], np.int64))])
+
+    def net(g, x):
+        a = conv(g, x, cin, cout, act="Relu")
+        pa = g.add("MaxPool", [a], kernel_shape=list(pool), strides=list(pool))
+        if not two:
+            return pa
+        wu = f16x(RNG.standard_normal((cout, 8, 2, 2)).astype(np.float32) * 0.1)
+        up = g.add("ConvTranspose", [pa, g.init("wu", wu)], kernel_shape=[2, 2], strides=[2, 2])
+        return g.add("Concat", [crop(g, up, "cu"), crop(g, a, "ca")], axis=1)
+
+    p = build(tmp_path, "pfs", net, (2, cin, h, w))
+    check(ctx, p, RNG.standard_normal((2, cin, h, w)).astype(np.float32))

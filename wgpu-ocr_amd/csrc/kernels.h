@@ -56,7 +56,13 @@ struct ConvArgs {
 };
 // True when the MFMA path takes this shape (stride 1, kernel at most 3 x 3).
 bool conv_mfma_supported(int kh, int kw, int sh, int sw);
+// Runs the convolution on the matrix cores: conv_igemm when it takes the shape, else the general
+// kernel (NCHW, SE input scale, BatchNormalization affine, residual, arg-max partials, any pool).
 void conv_mfma(const ConvArgs &a, hipStream_t s);
+// The NHWC hot path (kernels/igemm.hip): kernel up to 3 x 3, float16-exact weights, bias +
+// activation, optional 2 x 2 / 2 x 1 MaxPool, output pixel strides or a GEMM row map. Returns
+// false (and launches nothing) for anything else.
+bool conv_igemm(const ConvArgs &a, hipStream_t s);
 
 // ---- Everything else (kernels/ops.hip) ----------------------------------------------------
 // Any conv (grouped, strided) in float32, one thread per output: the fallback path.

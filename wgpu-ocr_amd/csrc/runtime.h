@@ -45,7 +45,7 @@ class Ctx;
 // Kernel timing with HIP events, for measurement (the role of the reference's OPPROFILE,
 // src/gpu.rs:1247-1368, without its waits): while a kernel family is being probed, each launch
 // of it is bracketed by two events recorded on the launch's own stream, and its algorithmic
-// FLOPs and bytes are added up. Process-wide; families are "conv_mfma", "gru", "conv_transpose",
+// FLOPs and bytes are added up. Process-wide; families are "conv_igemm", "conv_mfma", "gru", "conv_transpose",
 // "conv_direct", "maxpool", "mask_up", "grey_resize", "line_crop", "avgpool_t", "argmax", "copy".
 class Probe {
   public:
