@@ -144,6 +144,9 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     s.pk.exact = exact;
                     s.whi = ctx.upload_weights(hi.data(), hi.size());
                     if (!exact) s.wlo = ctx.upload_weights(lo.data(), lo.size());
+                    std::vector<uint16_t> frag(s.pk.halves());
+                    pack_conv_frags(s.pk, hi.data(), frag.data());
+                    s.wfrag = ctx.upload_weights(frag.data(), frag.size());
                 } else {
                     s.w = ctx.upload_weights(w.data.data(), w.data.size());
                 }
@@ -207,6 +210,9 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     ph.pk.exact = exact;
                     ph.whi = ctx.upload_weights(hi.data(), hi.size());
                     if (!exact) ph.wlo = ctx.upload_weights(lo.data(), lo.size());
+                    std::vector<uint16_t> frag(ph.pk.halves());
+                    pack_conv_frags(ph.pk, hi.data(), frag.data());
+                    ph.wfrag = ctx.upload_weights(frag.data(), frag.size());
                     s.phases.push_back(std::move(ph));
                 }
             if (!ok) s.phases.clear();
@@ -438,6 +444,7 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
                 ca.pw = s.pw;
                 ca.wt_hi = s.whi;
                 ca.wt_lo = s.wlo;
+                ca.wt_frag = s.wfrag;
                 ca.bias = s.b;
                 ca.pt = s.pt;
                 ca.pl = s.pl;
@@ -471,6 +478,7 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
                 ca.y_img = long(y.h) * y.w;
                 ca.wt_hi = ph.whi;
                 ca.wt_lo = ph.wlo;
+                ca.wt_frag = ph.wfrag;
                 ca.bias = s.b;
                 ca.pt = ph.ty - 1;
                 ca.pl = ph.tx - 1;

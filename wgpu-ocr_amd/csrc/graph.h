@@ -22,7 +22,7 @@ struct Step {
     int act = ACT_NONE;
     bool mfma = false;        // dense conv on the matrix cores (else conv_generic)
     ConvPack pk;
-    const uint16_t *whi = nullptr, *wlo = nullptr;
+    const uint16_t *whi = nullptr, *wlo = nullptr, *wfrag = nullptr;  // wfrag: conv_igemm's packing
     const float *w = nullptr, *b = nullptr;  // float32 weights (direct, transpose, generic) and bias
     int ph = 1, pw = 1;                       // a fused MaxPool's kernel, or MaxPool's kernel
     // A MaxPool fused into a dense conv: pool_only when it was the conv's only reader (output is
@@ -35,7 +35,7 @@ struct Step {
     struct TPhase {
         int py = 0, px = 0, ty = 0, tx = 0;
         ConvPack pk;
-        const uint16_t *whi = nullptr, *wlo = nullptr;
+        const uint16_t *whi = nullptr, *wlo = nullptr, *wfrag = nullptr;
     };
     std::vector<TPhase> phases;
     std::vector<int64_t> starts, ends, axes;  // Slice

@@ -25,10 +25,14 @@ struct ConvPack {
 // w is ONNX's [cout][cin][kh][kw]. Returns the pack description; hi/lo (host) are filled.
 ConvPack plan_conv_pack(int cin, int cout, int kh, int kw);
 void pack_conv_weights(const ConvPack &pk, const float *w, uint16_t *hi, uint16_t *lo, bool *exact);
+// The same float16 weights as MFMA B fragments for conv_igemm: [16-channel tile][slice][tap]
+// [lane][8], lane 16 g + r holding inputs 8g..8g+7 of channel 16 * tile + r (pk.halves() halves).
+void pack_conv_frags(const ConvPack &pk, const uint16_t *hi, uint16_t *frag);
 
 struct ConvArgs {
     Act x, y;                       // input and output views (NHWC, or NCHW with nchw set)
     const uint16_t *wt_hi = nullptr, *wt_lo = nullptr;
+    const uint16_t *wt_frag = nullptr;  // pack_conv_frags of wt_hi (conv_igemm), or null
     const float *bias = nullptr;    // [cout] or null
     const float *res = nullptr;     // residual added after the activation (gpu.rs:65), or null
     int res_cs = 0;
@@ -63,6 +67,10 @@ void conv_mfma(const ConvArgs &a, hipStream_t s);
 // activation, optional 2 x 2 / 2 x 1 MaxPool, output pixel strides or a GEMM row map. Returns
 // false (and launches nothing) for anything else.
 bool conv_igemm(const ConvArgs &a, hipStream_t s);
+// 3 x 3, pad 1, NHWC, more than 32 output channels, float16-exact weights with wt_frag, bias +
+// ReLU / Sigmoid, optional 2 x 2 / 2 x 1 MaxPool (kernels/conv3.hip): operands fed by LDS DMA.
+// Returns false (and launches nothing) for anything else.
+bool conv3x3_dma(const ConvArgs &a, hipStream_t s);
 
 // ---- Everything else (kernels/ops.hip) ----------------------------------------------------
 // Any conv (grouped, strided) in float32, one thread per output: the fallback path.

@@ -336,7 +336,8 @@ void pack_conv_weights(const ConvPack &pk, const float *w, uint16_t *hi, uint16_
 bool conv_mfma_supported(int kh, int kw, int sh, int sw) { return sh == 1 && sw == 1 && kh <= 3 && kw <= 3; }
 
 void conv_mfma(const ConvArgs &a, hipStream_t s) {
-    static const bool no_igemm = std::getenv("NOIGEMM") != nullptr;
+    static const bool no_igemm = std::getenv("NOIGEMM") != nullptr, no_dma = std::getenv("NOCONVDMA") != nullptr;
+    if (!no_igemm && !no_dma && conv3x3_dma(a, s)) return;
     if (!no_igemm && conv_igemm(a, s)) return;
     const ConvPack &pk = a.pk;
     ConvParams p{};

@@ -1,0 +1,458 @@
+// 3 x 3 stride-1 convolution (NHWC float32 activations, float16-exact weights, more than 32
+// output channels) on the gfx950 matrix cores with the operands fed by the LDS DMA path: the hot
+// path of the recogniser trunk and the detector's deeper layers. Semantics of the reference's
+// conv / conv_fast / conv128 programs (src/gpu.rs:37-350): y = act(sum x * w + b[c]), then an
+// optional 2 x 2 or 2 x 1 MaxPool of the activated output (gpu.rs:462-482).
+//
+// Precision: each float32 activation is split into float16 hi and the float16 remainder lo
+// (x = hi + lo to about 2^-22) and both go through v_mfma_f32_16x16x32_f16 against the exact
+// float16 weights with float32 accumulation.
+//
+// Data movement: nothing is staged through registers. global_load_lds_dwordx4 writes 16 bytes a
+// lane straight into LDS (lane l at base + 16 l), so
+// - weights: one stage is one kernel row (3 taps) of one 32-channel input slice for the block's
+//   output channels; its MFMA B fragments (1 KiB each, lane-ordered in HBM) are copied as they
+//   are into one of two stage buffers;
+// - input: the tile's halo for the next slice lands float32 in a staging buffer (HF) while the
+//   current slice is being computed, a pixel's eight 16-byte parts XOR-swizzled by half the
+//   pixel index; at the slice boundary all threads split it once into the hi / lo buffer (HS, 144
+//   bytes a pixel: 4 hi parts, 4 lo parts, 16 bytes of padding; a halo row's stride is 8 mod 16
+//   units). LDS serves a 16-byte read 16 lanes at a time over 64 banks: the 16 pixels (2 rows x 8
+//   columns) of one fragment read then fall on 16 distinct 16-byte bank groups, and every
+//   fragment address stays a fixed offset from the lane's base.
+// While the matrix cores work on stage k, the weights of stage k+1 and (for two stages) the next
+// slice's halo are in flight, their DMA instructions interleaved with the MFMAs; each stage ends
+// with an explicit vmcnt wait and a barrier. The buffers are separate LDS objects used with
+// compile-time parity, so the compiler adds no waits of its own between a DMA into one buffer and
+// the reads of another. Tile bookkeeping is incremental and uniform, addresses are 32-bit
+// offsets from per-tile bases: the VALU work per MFMA stays small.
+//
+// Work split: a persistent workgroup of 8 wavefronts (2 per SIMD) per CU walks a contiguous run
+// of TH x TW output tiles (runs of neighbouring tiles on one XCD) for one block of BN output
+// channels; wavefront (wm, wn) computes 64 pixels (four 2 x 8 row tiles, each four 2 x 2
+// squares, so a fused MaxPool reduces a lane's own accumulators) x 16 * NT channels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+#include "../kernels.h"
+#include "../runtime.h"
+
+namespace ocr {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int MT = 4;                // row tiles (of 16 pixels) per wavefront
+constexpr int HMAX = 51;             // halo staging size in 1 KiB blocks (8 pixels of 32 channels)
+constexpr int HPX = HMAX * 8;        // halo pixels at most
+constexpr int NHI = (HMAX + 7) / 8;  // halo DMA instructions per wavefront and slice
+constexpr int PXU = 9;               // HS units (16 bytes) per pixel
+constexpr int HSU = HPX * PXU;       // HS size in units
+constexpr int NSI = 4;               // split items (pixel, 8 channels) per thread and slice
+static_assert((HPX + 15) / 16 * 64 <= NSI * 512, "split items fit");
+
+struct C3Params {
+    const float *x;
+    int n, h, w, cin, xcs;
+    float *y;
+    int oh, ow, ycs;
+    float *yp;
+    int poh, pow_, ypcs, pool;
+    const half8 *wt;  // fragments [n-tile][slice][tap][64 lanes] of 8 halves
+    int ntiles, cout, chunks;
+    const float *bias;
+    int th, tw, mx, hw, hh, rs, npx, hblocks;
+    int tiles_x, tiles_y, tiles, nblocks, runs;
+    const float4 *zero;  // 16 zero bytes (the DMA source for padding)
+};
+
+__device__ inline float act3(float v, int act) {
+    if (act == ACT_RELU) return fmaxf(v, 0.f);
+    if (act == ACT_SIGMOID) return 1.f / (1.f + expf(-v));
+    return v;
+}
+
+__device__ inline int xcd_index3(int b, int G) {
+    const int q = G >> 3, rem = G & 7, x = b & 7;
+    return x * q + min(x, rem) + (b >> 3);
+}
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// A (tile, slice) position of the workgroup's walk, all values uniform.
+struct Seq {
+    int t, c, tx, ty, img;
+};
+
+template <int WM, int WN, int NT, int ACT>
+__global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
+    constexpr int NTW = NT * WN, WBLK = 3 * NTW, NWI = (WBLK + 7) / 8;
+    static_assert(WM * WN == 8, "8 wavefronts");
+    static_assert(NWI + NHI <= 3 * MT, "a stage's DMA instructions fit its steps");
+    __shared__ __align__(16) half8 W0[WBLK * 64];
+    __shared__ __align__(16) half8 W1[WBLK * 64];
+    __shared__ __align__(16) float4 HF[HMAX * 64];  // float32 staging of the next slice
+    __shared__ __align__(16) half8 HS[HSU];         // hi / lo of the current slice
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wn = wave / WM;
+    const int g = lane >> 4, r = lane & 15;
+    const int v = xcd_index3(blockIdx.x, gridDim.x);
+    const int nb = v % p.nblocks, run = v / p.nblocks;
+    if (run >= p.runs) return;
+    const int t_begin = int((long(run) * p.tiles) / p.runs), t_end = int((long(run + 1) * p.tiles) / p.runs);
+    if (t_begin >= t_end) return;
+    const int nt0 = nb * NTW, co_w = (nt0 + wn * NT) * 16;
+
+    // This lane's pixel in each row tile: its HS unit for tap (0, 0) and its square's corner.
+    int abase[MT], pyb[MT], pxb[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int mi = wm * MT + mt, mxi = mi % p.mx, myi = mi / p.mx, q = r & 3;
+        pyb[mt] = 2 * myi, pxb[mt] = 8 * mxi;
+        abase[mt] = (pyb[mt] + (q >> 1)) * p.rs + (pxb[mt] + 2 * (r >> 2) + (q & 1)) * PXU + g;
+    }
+    // This lane's halo slot (row, column, channel part) for each halo DMA instruction; row -1
+    // for padding slots. Unit U = 8 P + (u ^ ((P >> 1) & 7)) of HF holds channels 4u..4u+3 of
+    // slot P = row * hw + column.
+    int dhy[NHI], dhx[NHI], dch[NHI];
+#pragma unroll
+    for (int i = 0; i < NHI; i++) {
+        const int b = min(i * 8 + wave, p.hblocks - 1), U = b * 64 + lane, P = U >> 3;
+        const int hy = P / p.hw, hx = P - hy * p.hw;
+        dhy[i] = P < p.npx ? hy : -1;
+        dhx[i] = hx;
+        dch[i] = 4 * ((U & 7) ^ ((P >> 1) & 7));
+    }
+    // This thread's split items: item i = tid + 512 k is pixel (i & 15) + 16 (i >> 6), channels
+    // 8q..8q+7 with q = (i >> 4) & 3, so 16 neighbouring lanes take 16 pixels (distinct banks
+    // for the reads of HF and the writes of HS). sf: its HF unit, ss: its HS hi unit (-1: none).
+    int sf[NSI], ss[NSI];
+#pragma unroll
+    for (int k = 0; k < NSI; k++) {
+        const int i = tid + 512 * k, P = (i & 15) + 16 * (i >> 6), q = (i >> 4) & 3;
+        const int hy = P / p.hw, hx = P - hy * p.hw;
+        sf[k] = 8 * P + ((2 * q) ^ ((P >> 1) & 7));
+        ss[k] = P < p.npx ? hy * p.rs + hx * PXU + q : -1;
+    }
+    // Bias of this lane's output channel in each n-tile.
+    const int co_l = co_w + r;
+    float bv[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) bv[j] = (p.bias && co_l + 16 * j < p.cout) ? p.bias[co_l + 16 * j] : 0.f;
+
+    auto advance = [&](Seq s) __attribute__((always_inline)) {
+        if (++s.c == p.chunks) {
+            s.c = 0, s.t++;
+            if (++s.tx == p.tiles_x) {
+                s.tx = 0;
+                if (++s.ty == p.tiles_y) s.ty = 0, s.img++;
+            }
+        }
+        return s;
+    };
+    Seq cur;
+    cur.t = t_begin, cur.c = 0, cur.tx = t_begin % p.tiles_x;
+    cur.ty = (t_begin / p.tiles_x) % p.tiles_y, cur.img = t_begin / (p.tiles_x * p.tiles_y);
+
+    // Weights of slice c, kernel row ky: block b = kx * NTW + j (n-tile nt0 + j); instruction i.
+    auto dma_w = [&](half8 *dst, int c, int ky, int i) __attribute__((always_inline)) {
+        const int b = min(i * 8 + wave, WBLK - 1), kx = b / NTW, j = b - kx * NTW, nt = nt0 + j;
+        const half8 *src = reinterpret_cast<const half8 *>(p.zero);
+        if (nt < p.ntiles) src = p.wt + ((size_t(nt) * p.chunks + c) * 9 + ky * 3 + kx) * 64 + lane;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)(dst + b * 64), 16, 0, 0);
+    };
+    // Halo of position s into HF, instruction i.
+    auto dma_h = [&](const Seq &s, int i) __attribute__((always_inline)) {
+        const float *base = p.x + size_t(s.img) * p.h * p.w * p.xcs + s.c * 32;
+        const int b = min(i * 8 + wave, p.hblocks - 1);
+        const int iy = s.ty * p.th - 1 + dhy[i], ix = s.tx * p.tw - 1 + dhx[i];
+        const void *src = p.zero;
+        if (dhy[i] >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(p.w) && s.c * 32 + dch[i] < p.cin)
+            src = base + unsigned((iy * p.w + ix) * p.xcs + dch[i]);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)(HF + b * 64), 16, 0, 0);
+    };
+    // HF -> HS, once a slice: hi part q (channels 8q..8q+7) of a pixel at its unit + q, lo at
+    // + 4 + q; lo = x - hi rounded to float16 (x = hi + lo to about 2^-22).
+    auto split = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < NSI; k++) {
+            if (ss[k] < 0) continue;
+            const float4 a = HF[sf[k]], b = HF[sf[k] ^ 1];
+            const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            half8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                hi[e] = (_Float16)xs[e];
+                lo[e] = (_Float16)__builtin_fmaf(-1.f, (float)hi[e], xs[e]);
+            }
+            HS[ss[k]] = hi;
+            HS[ss[k] + 4] = lo;
+        }
+    };
+
+    floatx4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int j = 0; j < NT; j++) acc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // One kernel row of one slice: 3 taps x MT row tiles x NT n-tiles x (hi, lo), as 12 steps
+    // (tap, row tile). Each step's A fragments (and at a new tap its B fragments) are read one
+    // step ahead into a second register set; `issue(step)` puts this step's share of the next
+    // stage's DMA between the MFMAs.
+    auto compute = [&](const half8 *Wb, int ky, auto &&issue) __attribute__((always_inline)) {
+        int base[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            base[mt] = abase[mt] + ky * p.rs;
+            asm volatile("" : "+v"(base[mt]));  // per stage, not hoisted out of the stage loop
+        }
+        half8 ah[2], al[2], bb[2][NT];
+        auto read_a = [&](int kx, int mt, half8 &hi, half8 &lo) __attribute__((always_inline)) {
+            hi = HS[base[mt] + kx * PXU];
+            lo = HS[base[mt] + kx * PXU + 4];
+        };
+        auto read_b = [&](int kx, half8 (&b)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < NT; j++) b[j] = Wb[(kx * NTW + wn * NT + j) * 64 + lane];
+        };
+        read_b(0, bb[0]);
+        read_a(0, 0, ah[0], al[0]);
+#pragma unroll
+        for (int st = 0; st < 3 * MT; st++) {
+            const int kx = st / MT, mt = st % MT, ca = st & 1, cb = kx & 1;
+            issue(st);
+            if (st + 1 < 3 * MT) {
+                const int kx1 = (st + 1) / MT, mt1 = (st + 1) % MT;
+                if (mt1 == 0) read_b(kx1, bb[cb ^ 1]);
+                read_a(kx1, mt1, ah[ca ^ 1], al[ca ^ 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < NT; j++) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ca], bb[cb][j], acc[mt][j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < NT; j++) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ca], bb[cb][j], acc[mt][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // The tile's outputs: bias, activation, then the full output (when p.y is set) and the
+    // pooled output (POOL 1: 2 x 2, 2: 2 x 1). Offsets are 32-bit from the tile's corner; CHECK
+    // bounds-checks every store (tiles on the image's or the channels' edge).
+    auto epi = [&](const Seq &s, auto POOLc, auto CHECKc) __attribute__((always_inline)) {
+        constexpr int POOL = decltype(POOLc)::value;
+        constexpr bool CHECK = decltype(CHECKc)::value;
+        const int oy0 = s.ty * p.th, ox0 = s.tx * p.tw;
+        float *yt = p.y ? p.y + (size_t(s.img) * p.oh * p.ow + size_t(oy0) * p.ow + ox0) * p.ycs : nullptr;
+        float *pt = nullptr;
+        if (POOL == 1) pt = p.yp + (size_t(s.img) * p.poh * p.pow_ + size_t(oy0 / 2) * p.pow_ + ox0 / 2) * p.ypcs;
+        if (POOL == 2) pt = p.yp + (size_t(s.img) * p.poh * p.pow_ + size_t(oy0 / 2) * p.pow_ + ox0) * p.ypcs;
+        // The lane's parts of the offsets, computed here (not kept live across the tile loop).
+        int lf = 2 * g * p.ycs + co_l, lp = (POOL == 1 ? g : 2 * g) * p.ypcs + co_l;
+        asm volatile("" : "+v"(lf), "+v"(lp));
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int dy = pyb[mt], dx = pxb[mt] + 2 * g;
+            const unsigned fo = unsigned((dy * p.ow + pxb[mt]) * p.ycs + lf);
+            const unsigned po = POOL == 1 ? unsigned(((dy >> 1) * p.pow_ + (pxb[mt] >> 1)) * p.ypcs + lp)
+                                          : unsigned(((dy >> 1) * p.pow_ + pxb[mt]) * p.ypcs + lp);
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = act3(acc[mt][j][i] + bv[j], ACT);
+                acc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                const bool cok = !CHECK || co_l + 16 * j < p.cout;
+                if (yt) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const bool in = !CHECK || (cok && oy0 + dy + (i >> 1) < p.oh && ox0 + dx + (i & 1) < p.ow);
+                        if (in) yt[fo + unsigned(((i >> 1) * p.ow + (i & 1)) * p.ycs + 16 * j)] = v[i];
+                    }
+                }
+                if (POOL == 1) {
+                    const bool in = !CHECK || (cok && (oy0 + dy) / 2 < p.poh && (ox0 + dx) / 2 < p.pow_);
+                    if (in) pt[po + 16 * j] = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+                }
+                if (POOL == 2) {
+                    const bool iny = !CHECK || (cok && (oy0 + dy) / 2 < p.poh);
+                    if (iny && (!CHECK || ox0 + dx < p.pow_)) pt[po + 16 * j] = fmaxf(v[0], v[2]);
+                    if (iny && (!CHECK || ox0 + dx + 1 < p.pow_)) pt[po + unsigned(p.ypcs) + 16 * j] = fmaxf(v[1], v[3]);
+                }
+            }
+        }
+    };
+    auto epilogue = [&](const Seq &s) __attribute__((always_inline)) {
+        const int oy0 = s.ty * p.th, ox0 = s.tx * p.tw;
+        const bool cin_ = co_w + 16 * NT <= p.cout && (!p.y || (oy0 + p.th <= p.oh && ox0 + p.tw <= p.ow));
+        auto run = [&](auto POOLc, bool inside) __attribute__((always_inline)) {
+            if (inside) epi(s, POOLc, std::false_type{});
+            else epi(s, POOLc, std::true_type{});
+        };
+        if (p.pool == 1)
+            run(std::integral_constant<int, 1>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && (ox0 + p.tw) / 2 <= p.pow_);
+        else if (p.pool == 2)
+            run(std::integral_constant<int, 2>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && ox0 + p.tw <= p.pow_);
+        else
+            run(std::integral_constant<int, 0>{}, cin_);
+    };
+
+    // Stage (position cur, kernel row KY); weight buffer (KY + HP) & 1 with HP the parity of the
+    // slice sequence (three stages a slice). Returns false after the last stage.
+    Seq nxt = advance(cur);
+    auto stage = [&](auto KYc, auto HPc) __attribute__((always_inline)) -> bool {
+        constexpr int KY = decltype(KYc)::value, HP = decltype(HPc)::value;
+        constexpr int WP = (KY + HP) & 1;
+        half8 *Wc = WP ? W1 : W0, *Wn = WP ? W0 : W1;
+        const bool more = nxt.t < t_end;
+        // The next stage's weights (steps 0..NWI-1), then at a slice's first row the next slice's
+        // halo (steps NWI..NWI+NHI-1), one DMA instruction per step between the MFMAs.
+        const bool wnext = KY < 2 || more, hnext = KY == 0 && more;
+        const int wc = KY < 2 ? cur.c : nxt.c, wky = KY < 2 ? KY + 1 : 0;
+        compute(Wc, KY, [&](int st) __attribute__((always_inline)) {
+            if (st < NWI) {
+                if (wnext) dma_w(Wn, wc, wky, st);
+            } else if (st < NWI + NHI) {
+                if (hnext) dma_h(nxt, st - NWI);
+            }
+        });
+        if (KY == 2 && cur.c == p.chunks - 1) epilogue(cur);
+        if (hnext) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NHI) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (KY == 2) {
+            if (!more) return false;
+            split();  // the next slice's halo, landed in HF, becomes its hi / lo
+            __syncthreads();
+            cur = nxt;
+            nxt = advance(nxt);
+        }
+        return true;
+    };
+
+#pragma unroll
+    for (int i = 0; i < NWI; i++) dma_w(W0, 0, 0, i);
+#pragma unroll
+    for (int i = 0; i < NHI; i++) dma_h(cur, i);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    split();
+    __syncthreads();
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    for (;;) {
+        if (!stage(I0{}, I0{}) || !stage(I1{}, I0{}) || !stage(I2{}, I0{})) break;
+        if (!stage(I0{}, I1{}) || !stage(I1{}, I1{}) || !stage(I2{}, I1{})) break;
+    }
+}
+
+int cu_count3() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0;
+        OCR_HIP(hipGetDevice(&dev));
+        OCR_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        if (n <= 0) n = 256;
+    }
+    return n;
+}
+
+const float4 *zero_block() {
+    static float4 *z = nullptr;
+    if (!z) {
+        OCR_HIP(hipMalloc(&z, 64));
+        OCR_HIP(hipMemset(z, 0, 64));
+    }
+    return z;
+}
+
+}  // namespace
+
+bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
+    const ConvPack &pk = a.pk;
+    if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res || a.rows || !pk.exact) return false;
+    if (pk.kh != 3 || pk.kw != 3 || a.pt != 1 || a.pl != 1 || pk.cin != a.x.c || pk.cout != a.y.c) return false;
+    if (a.y.n != a.x.n || a.y.h != a.x.h || a.y.w != a.x.w || a.y_px || a.y_row || a.y_img) return false;
+    if (a.x.c % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15) || a.y.c <= 32) return false;
+    if (a.act != ACT_NONE && a.act != ACT_RELU && a.act != ACT_SIGMOID) return false;
+    // 32-bit offsets within one image of the input, the output and the pooled output.
+    if (double(a.x.h) * a.x.w * a.x.cs >= 2147483647.0 || double(a.y.h) * a.y.w * a.y.cs >= 2147483647.0) return false;
+    const bool pooled = a.ypool.p != nullptr;
+    int pool = 0;
+    if (pooled) {
+        if (a.ph == 2 && a.pw == 2) pool = 1;
+        else if (a.ph == 2 && a.pw == 1) pool = 2;
+        else return false;
+        if (a.ypool.h != a.y.h / a.ph || a.ypool.w != a.y.w / a.pw || a.ypool.c != a.y.c || a.ypool.n != a.y.n)
+            fail("conv3x3_dma: pooled output shape");
+    }
+    const int cout = a.y.c, nt = cout > 64 ? 4 : 2, bn = 32 * nt;
+    C3Params p{};
+    p.x = a.x.p;
+    p.n = a.x.n;
+    p.h = a.x.h;
+    p.w = a.x.w;
+    p.cin = a.x.c;
+    p.xcs = a.x.cs;
+    p.y = pooled && !a.keep_full ? nullptr : a.y.p;
+    p.oh = a.y.h;
+    p.ow = a.y.w;
+    p.ycs = a.y.cs;
+    p.yp = a.ypool.p;
+    p.poh = a.ypool.h;
+    p.pow_ = a.ypool.w;
+    p.ypcs = a.ypool.cs;
+    p.pool = pool;
+    p.wt = reinterpret_cast<const half8 *>(a.wt_frag);
+    p.ntiles = pk.nblocks * pk.bn / 16;
+    p.cout = cout;
+    p.chunks = pk.chunks;
+    p.bias = a.bias;
+    // Tile: 16 blocks of 2 x 8 pixels; the shape wasting the fewest pixels whose halo fits.
+    double best = 1e300;
+    for (int mxc : {1, 2, 4, 8}) {
+        const int tw = 8 * mxc, th = 2 * (16 / mxc), hw = tw + 2, hh = th + 2;
+        const int rs = 9 * hw + (24 - 9 * hw % 16) % 16;  // 8 mod 16 units
+        if (hh * hw > HPX || hh * rs > HSU) continue;
+        const double cost = double((p.oh + th - 1) / th * th) * ((p.ow + tw - 1) / tw * tw) * double(hh * hw) / (th * tw);
+        if (cost < best) best = cost, p.tw = tw, p.th = th, p.mx = mxc, p.rs = rs;
+    }
+    if (best == 1e300) return false;
+    p.hw = p.tw + 2;
+    p.hh = p.th + 2;
+    p.npx = p.hh * p.hw;
+    p.hblocks = (p.npx + 7) / 8;
+    p.tiles_x = (p.ow + p.tw - 1) / p.tw;
+    p.tiles_y = (p.oh + p.th - 1) / p.th;
+    const double tiles = double(p.tiles_x) * p.tiles_y * p.n;
+    if (tiles > 0x7fffffff) return false;
+    p.tiles = int(tiles);
+    p.nblocks = (cout + bn - 1) / bn;
+    p.runs = std::max(1, std::min(p.tiles, cu_count3() / p.nblocks));
+    p.zero = zero_block();
+    const int grid = p.runs * p.nblocks;
+    const double flops = 2.0 * p.n * p.oh * p.ow * cout * p.cin * 9;
+    const double bytes = 4.0 * (double(p.n) * p.h * p.w * p.cin + double(p.n) * p.oh * p.ow * cout) +
+                         2.0 * double(pk.halves());
+    ProbeScope probe("conv3x3_dma", s, flops, bytes);
+    auto launch = [&](auto ACTc) {
+        constexpr int A = decltype(ACTc)::value;
+        if (nt == 4) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 4, A>), dim3(unsigned(grid)), dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 2, A>), dim3(unsigned(grid)), dim3(512), 0, s, p);
+    };
+    if (a.act == ACT_RELU) launch(std::integral_constant<int, ACT_RELU>{});
+    else if (a.act == ACT_SIGMOID) launch(std::integral_constant<int, ACT_SIGMOID>{});
+    else launch(std::integral_constant<int, ACT_NONE>{});
+    OCR_HIP(hipGetLastError());
+    return true;
+}
+
+}  // namespace ocr

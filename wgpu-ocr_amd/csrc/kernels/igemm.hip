@@ -29,6 +29,7 @@
 #include <cmath>
 #include <map>
 #include <mutex>
+#include <cstring>
 
 #include "../kernels.h"
 #include "../runtime.h"
@@ -254,6 +255,22 @@ void launch_si(const IgParams &p, dim3 grid, size_t lds, hipStream_t s) {
 }
 
 }  // namespace
+
+void pack_conv_frags(const ConvPack &pk, const uint16_t *hi, uint16_t *frag) {
+    // hi: [nblock][chunk][tap][bn][32]; frag: [n-tile][chunk][tap][lane = 16 g + r][8], lane
+    // (g, r) holding inputs 8g..8g+7 of channel 16 * tile + r.
+    const int taps = pk.kh * pk.kw, ntiles = pk.nblocks * pk.bn / 16;
+    size_t o = 0;
+    for (int nt = 0; nt < ntiles; nt++)
+        for (int c = 0; c < pk.chunks; c++)
+            for (int tap = 0; tap < taps; tap++)
+                for (int l = 0; l < 64; l++, o += 8) {
+                    const int g = l >> 4, r = l & 15, co = nt * 16 + r;
+                    const int nb = co / pk.bn, off = co - nb * pk.bn;
+                    const size_t src = (((size_t(nb) * pk.chunks + c) * taps + tap) * pk.bn + off) * 32 + 8 * g;
+                    std::memcpy(frag + o, hi + src, 8 * sizeof(uint16_t));
+                }
+}
 
 bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     const ConvPack &pk = a.pk;

@@ -64,7 +64,7 @@ std::vector<float> Detector::detect(const float *input, int h, int w) {
 namespace {
 
 void pack_linear(Ctx &ctx, const std::vector<float> &w_rows, int rows, int cols, ConvPack &pk, const uint16_t *&hi,
-                 const uint16_t *&lo) {
+                 const uint16_t *&lo, const uint16_t *&frag) {
     // w_rows is [rows = outputs][cols = inputs]: a 1 x 1 convolution's [cout][cin][1][1].
     pk = plan_conv_pack(cols, rows, 1, 1);
     std::vector<uint16_t> h(pk.halves()), l(pk.halves());
@@ -73,6 +73,9 @@ void pack_linear(Ctx &ctx, const std::vector<float> &w_rows, int rows, int cols,
     pk.exact = exact;
     hi = ctx.upload_weights(h.data(), h.size());
     lo = exact ? nullptr : ctx.upload_weights(l.data(), l.size());
+    std::vector<uint16_t> f(pk.halves());
+    pack_conv_frags(pk, h.data(), f.data());
+    frag = ctx.upload_weights(f.data(), f.size());
 }
 
 }  // namespace
@@ -103,7 +106,7 @@ Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), 
         Layer &L = layers_[nl++];
         L.input = int(w.dims[2]);
         // W [2][768][in] is already the projection's [1536 outputs][in] (gpu.rs:1466-1472).
-        pack_linear(ctx, w.data, 1536, L.input, L.pk, L.w_hi, L.w_lo);
+        pack_linear(ctx, w.data, 1536, L.input, L.pk, L.w_hi, L.w_lo, L.w_frag);
         std::vector<float> wb, rb;
         for (int d = 0; d < 2; d++) {
             wb.insert(wb.end(), b.data.begin() + d * 1536, b.data.begin() + d * 1536 + 768);
@@ -146,7 +149,7 @@ Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), 
     std::vector<float> t(size_t(classes_) * 512);
     for (int i = 0; i < 512; i++)
         for (int c = 0; c < classes_; c++) t[size_t(c) * 512 + i] = lin.data[size_t(i) * classes_ + c];
-    pack_linear(ctx, t, classes_, 512, lin_pk_, lin_hi_, lin_lo_);
+    pack_linear(ctx, t, classes_, 512, lin_pk_, lin_hi_, lin_lo_, lin_frag_);
     lin_b_ = ctx.upload_weights(bias->data.data(), bias->data.size());
 }
 
@@ -217,6 +220,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         ca.rows = rowsd.as<int32_t>();
         ca.wt_hi = L.w_hi;
         ca.wt_lo = L.w_lo;
+        ca.wt_frag = L.w_frag;
         ca.bias = L.wb;
         ca.pk = L.pk;
         conv_mfma(ca, st);
@@ -230,6 +234,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     ca.rows = rowsd.as<int32_t>();
     ca.wt_hi = lin_hi_;
     ca.wt_lo = lin_lo_;
+    ca.wt_frag = lin_frag_;
     ca.bias = lin_b_;
     ca.pk = lin_pk_;
     conv_mfma(ca, st);

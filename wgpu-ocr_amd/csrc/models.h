@@ -51,7 +51,7 @@ class Recognizer {
   private:
     struct Layer {
         ConvPack pk;  // the input projection as a 1 x 1 convolution: [1536][input]
-        const uint16_t *w_hi = nullptr, *w_lo = nullptr;
+        const uint16_t *w_hi = nullptr, *w_lo = nullptr, *w_frag = nullptr;
         const float *wb = nullptr;  // [2][768]
         const uint16_t *r = nullptr;  // [2][768][256] float16
         const float *rb = nullptr;    // [2][768]
@@ -62,7 +62,7 @@ class Recognizer {
     int pool_kh_ = 0;
     Layer layers_[2];
     ConvPack lin_pk_;
-    const uint16_t *lin_hi_ = nullptr, *lin_lo_ = nullptr;
+    const uint16_t *lin_hi_ = nullptr, *lin_lo_ = nullptr, *lin_frag_ = nullptr;
     const float *lin_b_ = nullptr;
     int classes_ = 0;
     uint32_t lines_ = 8;
