@@ -53,6 +53,14 @@ def test_conv3x3_mfma(ctx, tmp_path, cin, cout, h, w):
     check(ctx, p, RNG.standard_normal((2, cin, h, w)).astype(np.float32))
 
 
+@pytest.mark.parametrize("cin,cout,h,w,act", [(256, 1536, 1, 700, None), (512, 97, 3, 301, None), (160, 70, 5, 61, "Relu"),
+                                              (512, 256, 2, 1031, "Sigmoid"), (132, 40, 1, 300, None)])
+def test_conv1x1_gemm(ctx, tmp_path, cin, cout, h, w, act):
+    # The GEMM path: row tails (M % 256), column tails (N % 16, N % 4), K % 32 != 0.
+    p = build(tmp_path, "g", lambda g, x: conv(g, x, cin, cout, k=(1, 1), pads=(0, 0, 0, 0), act=act), (1, cin, h, w))
+    check(ctx, p, RNG.standard_normal((1, cin, h, w)).astype(np.float32))
+
+
 def test_conv1x1_and_sigmoid(ctx, tmp_path):
     p = build(tmp_path, "c1", lambda g, x: conv(g, x, 16, 3, k=(1, 1), pads=(0, 0, 0, 0), act="Sigmoid"), (1, 16, 7, 130))
     check(ctx, p, RNG.standard_normal((1, 16, 7, 130)).astype(np.float32))

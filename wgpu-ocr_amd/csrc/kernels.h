@@ -67,6 +67,10 @@ void conv_mfma(const ConvArgs &a, hipStream_t s);
 // activation, optional 2 x 2 / 2 x 1 MaxPool, output pixel strides or a GEMM row map. Returns
 // false (and launches nothing) for anything else.
 bool conv_igemm(const ConvArgs &a, hipStream_t s);
+// 1 x 1 convolution / GEMM (kernels/gemm.hip): NHWC pixels or GEMM rows with a row map, at
+// least four 32-wide input chunks, float16-exact weights with wt_frag, bias + ReLU / Sigmoid.
+// Returns false (and launches nothing) for anything else.
+bool gemm_dma(const ConvArgs &a, hipStream_t s);
 // 3 x 3, pad 1, NHWC, more than 32 output channels, float16-exact weights with wt_frag, bias +
 // ReLU / Sigmoid, optional 2 x 2 / 2 x 1 MaxPool (kernels/conv3.hip): operands fed by LDS DMA.
 // Returns false (and launches nothing) for anything else.

@@ -338,6 +338,7 @@ bool conv_mfma_supported(int kh, int kw, int sh, int sw) { return sh == 1 && sw 
 void conv_mfma(const ConvArgs &a, hipStream_t s) {
     static const bool no_igemm = std::getenv("NOIGEMM") != nullptr, no_dma = std::getenv("NOCONVDMA") != nullptr;
     if (!no_igemm && !no_dma && conv3x3_dma(a, s)) return;
+    if (!no_igemm && !no_dma && gemm_dma(a, s)) return;
     if (!no_igemm && conv_igemm(a, s)) return;
     const ConvPack &pk = a.pk;
     ConvParams p{};

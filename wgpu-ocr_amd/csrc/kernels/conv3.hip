@@ -39,6 +39,7 @@
 
 #include "../kernels.h"
 #include "../runtime.h"
+#include "lds_dma.h"
 
 namespace ocr {
 
@@ -82,7 +83,7 @@ __device__ inline int xcd_index3(int b, int G) {
     return x * q + min(x, rem) + (b >> 3);
 }
 
-typedef __attribute__((address_space(3))) void *lds_ptr;
+
 
 // A (tile, slice) position of the workgroup's walk, all values uniform.
 struct Seq {
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
         const int b = min(i * 8 + wave, WBLK - 1), kx = b / NTW, j = b - kx * NTW, nt = nt0 + j;
         const half8 *src = reinterpret_cast<const half8 *>(p.zero);
         if (nt < p.ntiles) src = p.wt + ((size_t(nt) * p.chunks + c) * 9 + ky * 3 + kx) * 64 + lane;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)(dst + b * 64), 16, 0, 0);
+        dma16(src, dst + b * 64);
     };
     // Halo of position s into HF, instruction i.
     auto dma_h = [&](const Seq &s, int i) __attribute__((always_inline)) {
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
         const void *src = p.zero;
         if (dhy[i] >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(p.w) && s.c * 32 + dch[i] < p.cin)
             src = base + unsigned((iy * p.w + ix) * p.xcs + dch[i]);
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)(HF + b * 64), 16, 0, 0);
+        dma16(src, HF + b * 64);
     };
     // HF -> HS, once a slice: hi part q (channels 8q..8q+7) of a pixel at its unit + q, lo at
     // + 4 + q; lo = x - hi rounded to float16 (x = hi + lo to about 2^-22).
@@ -326,11 +327,11 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
         if (KY == 2 && cur.c == p.chunks - 1) epilogue(cur);
         if (hnext) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NHI) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        lds_barrier();
         if (KY == 2) {
             if (!more) return false;
             split();  // the next slice's halo, landed in HF, becomes its hi / lo
-            __syncthreads();
+            lds_barrier();
             cur = nxt;
             nxt = advance(nxt);
         }
@@ -342,9 +343,9 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
 #pragma unroll
     for (int i = 0; i < NHI; i++) dma_h(cur, i);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    lds_barrier();
     split();
-    __syncthreads();
+    lds_barrier();
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;

@@ -1,0 +1,28 @@
+// LDS DMA and an LDS-only barrier for the pipelined matrix-core kernels (conv3.hip, gemm.hip).
+//
+// global_load_lds_dwordx4 copies 16 bytes a lane from global memory straight into LDS (lane l at
+// M0 + 16 l). Issued through the compiler's builtin, the copy makes the compiler wait for every
+// copy in flight (vmcnt(0)) before any later LDS access it cannot prove disjoint, and
+// __syncthreads waits for all memory operations: both would expose the latency the pipelines
+// hide. Issued here, the copies are invisible to the compiler, so each kernel waits for them
+// itself with explicit vmcnt counts before the barrier that publishes their data.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace ocr {
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// 16 bytes from src (per lane) to LDS at dst + 16 * lane; dst must be the same for the whole
+// wavefront. Completion: vmcnt.
+__device__ inline void dma16(const void *src, void *dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(unsigned(reinterpret_cast<size_t>((lds_ptr)dst)));
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+// Workgroup barrier for LDS: this wavefront's LDS operations are complete and no memory operation
+// moves across it; global loads, stores and LDS DMA stay in flight.
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+}  // namespace ocr
