@@ -11,11 +11,12 @@
 // Roles: the weights are the MFMA's A operand and the activations its B operand, so a lane's four
 // accumulators are four neighbouring output channels of one row and leave as one 16-byte store.
 //
-// Pipeline (one 32-wide K chunk a stage, three LDS stages): during stage s the weights of chunk
-// s + 2 arrive by LDS DMA (lane-ordered fragments copied as they are), the float32 activations of
-// chunk s + 3 are loaded into registers, and those of chunk s + 2 (loaded during stage s - 1) are
-// split into hi / lo and written to LDS; at the end of the stage the fragments of chunk s + 1 are
-// read into registers before the barrier, so the next stage starts on the matrix cores at once.
+// Pipeline (one 32-wide K chunk a stage, three LDS stages): between the MFMAs of stage s the
+// weights of chunk s + 2 arrive by LDS DMA (lane-ordered fragments copied as they are), the
+// float32 activations of chunk s + 2 (loaded during stage s - 1) are split into hi / lo and
+// written to LDS, those of chunk s + 3 are loaded into registers, and in the last step the
+// fragments of chunk s + 1 are read into registers, so the next stage starts on the matrix cores
+// right after the barrier.
 // A workgroup (8 wavefronts, 256 rows x 32 NT columns) is persistent: it keeps one block of
 // output channels (its bias and the row map of its tiles sit in LDS) and walks a contiguous run of
 // row tiles with the pipeline running on across tile boundaries.
@@ -126,21 +127,19 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GParams p) {
                 R[2 * h + e] = *src;
             }
     };
-    auto convert = [&](const float4(&R)[4], half8 *as) __attribute__((always_inline)) {
+    // Row lr + 128 h of the loaded chunk, split into hi / lo, into an LDS stage.
+    auto convert = [&](const float4(&R)[4], half8 *as, int h) __attribute__((always_inline)) {
+        const float xs[8] = {R[2 * h].x, R[2 * h].y, R[2 * h].z, R[2 * h].w,
+                             R[2 * h + 1].x, R[2 * h + 1].y, R[2 * h + 1].z, R[2 * h + 1].w};
+        half8 hi, lo;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const float xs[8] = {R[2 * h].x, R[2 * h].y, R[2 * h].z, R[2 * h].w,
-                                 R[2 * h + 1].x, R[2 * h + 1].y, R[2 * h + 1].z, R[2 * h + 1].w};
-            half8 hi, lo;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                hi[e] = (_Float16)xs[e];
-                lo[e] = (_Float16)(xs[e] - (float)hi[e]);
-            }
-            const int u = (lr + 128 * h) * RSU + lq;
-            as[u] = hi;
-            as[u + 4] = lo;
+        for (int e = 0; e < 8; e++) {
+            hi[e] = (_Float16)xs[e];
+            lo[e] = (_Float16)(xs[e] - (float)hi[e]);
         }
+        const int u = (lr + 128 * h) * RSU + lq;
+        as[u] = hi;
+        as[u + 4] = lo;
     };
     // Weights of chunk c: fragment b = n-tile nt0 + b, instruction i.
     auto dma_w = [&](half8 *dst, int c, int i) __attribute__((always_inline)) {
@@ -168,8 +167,10 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GParams p) {
 #pragma unroll
     for (int i = 0; i < NWI; i++) dma_w(WB1, 1, i);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    convert(R0, AS0);
-    convert(R1, AS1);
+    convert(R0, AS0, 0);
+    convert(R0, AS0, 1);
+    convert(R1, AS1, 0);
+    convert(R1, AS1, 1);
     // The loader's position: chunk la_c of tile la_t (stage s + 3 of the run).
     int la_t = tb, la_c = 2;
     load_a(R0, la_c, 2 < S);
@@ -182,16 +183,13 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GParams p) {
 #pragma unroll
         for (int j = 0; j < NT; j++) acc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     half8 wf[NT], ah[2], al[2];
-    auto read_w = [&](const half8 *wb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < NT; j++) wf[j] = wb[(wn * NT + j) * 64 + lane];
-    };
     auto read_a = [&](const half8 *as, int mt, int set) __attribute__((always_inline)) {
         const int u = (wm * 64 + mt * 16 + r) * RSU + g;
         ah[set] = as[u];
         al[set] = as[u + 4];
     };
-    read_w(WB0);
+#pragma unroll
+    for (int j = 0; j < NT; j++) wf[j] = WB0[(wn * NT + j) * 64 + lane];
     read_a(AS0, 0, 0);
 
     // Output of the tile that ended with the previous stage; orow: its rows for this lane (read
@@ -239,26 +237,25 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GParams p) {
         half8 *WB2n = S3 == 0 ? WB2 : S3 == 1 ? WB0 : WB1;
         float4(&Rc)[4] = S2 == 0 ? R0 : R1;  // chunk s + 2, loaded during stage s - 1
         float4(&Rn)[4] = S2 == 0 ? R1 : R0;  // chunk s + 3, loaded now
+        // The activations of chunk s + 2 are the previous stage's last loads.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (pend) {
             epilogue();
             pend = false;
         }
-        // Rows of the tile after the next one, when the loader moves on at the end of this stage
-        // (gathered before this stage's activation loads: those must be its last loads).
+        // Rows of the tile after the next one, when the loader moves on in this stage (gathered
+        // before this stage's activation loads: those must be its last loads).
         const bool entering = s + 3 < S && la_c == p.chunks - 1;
         int nx2[2] = {-1, -1};
         if (entering) {
 #pragma unroll
             for (int h = 0; h < 2; h++) nx2[h] = row_of(la_t + 2, h);
         }
-        if (s + 2 < S) {
-#pragma unroll
-            for (int i = 0; i < NWI; i++) dma_w(WB2n, wc, i);
-        }
-        if (++wc == p.chunks) wc = 0;
         // Chunk s: MT row tiles x NT n-tiles x (hi, lo); the next row tile's fragments are read
-        // one step ahead, and in the last step the next stage's weights and first row tile.
-        const bool more = s + 1 < S;
+        // one step ahead. Between the MFMAs: the weights of chunk s + 2 (DMA), the hi / lo split
+        // of chunk s + 2, the loads of chunk s + 3, and in the last step the next stage's
+        // weights (each fragment after its last use) and first row tile.
+        const bool more = s + 1 < S, conv = s + 2 < S;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const int ca = mt & 1;
@@ -266,26 +263,42 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GParams p) {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < NT; j++) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], ah[ca], acc[mt][j], 0, 0, 0);
-#pragma unroll
-            for (int j = 0; j < NT; j++) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], al[ca], acc[mt][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
+            if (mt == 0 && conv) {
+#pragma unroll
+                for (int i = 0; i < NWI; i++) dma_w(WB2n, wc, i);
+            }
+            if (mt < 2 && conv) convert(Rc, AS2n, mt);
+            __builtin_amdgcn_sched_barrier(0);
+            if (mt + 1 < MT) {
+#pragma unroll
+                for (int j = 0; j < NT; j++) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], al[ca], acc[mt][j], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < NT; j++) {
+                    acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], al[ca], acc[mt][j], 0, 0, 0);
+                    if (more) wf[j] = WBn[(wn * NT + j) * 64 + lane];
+                }
+                if (more) read_a(ASn, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (mt == 0) {
+                // Chunk s + 3 into registers (zeros past the run), always four loads: the end of
+                // the stage leaves exactly these outstanding.
+                load_a(Rn, la_c, s + 3 < S);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        if (more) {
-            read_w(WBn);
-            read_a(ASn, 0, 0);
-        }
+        if (++wc == p.chunks) wc = 0;
         if (++cc == p.chunks) {
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) orow[mt] = ROWS[ct & 1][wm * 64 + mt * 16 + r];
             pend = true;
             cc = 0, ct++;
         }
-        // Chunk s + 3 into registers (zeros past the run), always four loads: the wait below
-        // leaves exactly these outstanding.
-        load_a(Rn, la_c, s + 3 < S);
         if (s + 3 < S && ++la_c == p.chunks) la_c = 0, enter_tile(++la_t, nx2);
+        // The weights of chunk s + 2 have landed (the loads of chunk s + 3 may be in flight).
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-        if (s + 2 < S) convert(Rc, AS2n);
         lds_barrier();
         return ++s < S;
     };
