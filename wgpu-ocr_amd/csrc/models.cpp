@@ -81,6 +81,11 @@ void pack_linear(Ctx &ctx, const std::vector<float> &w_rows, int rows, int cols,
 }  // namespace
 
 Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), lines_(lines) {
+    for (int i = 0; i < TRUNK_STREAMS; i++) {
+        aux_.emplace_back(new Ctx(ctx.device(), ctx.lines(), 2048));
+        OCR_HIP(hipEventCreateWithFlags(&join_[i], hipEventDisableTiming));
+    }
+    OCR_HIP(hipEventCreateWithFlags(&fork_, hipEventDisableTiming));
     Node pool;
     bool found = false;
     trunk_ = Graph::build(ctx, onnx, "AveragePool", &pool, &found);
@@ -153,6 +158,14 @@ Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), 
     lin_b_ = ctx.upload_weights(bias->data.data(), bias->data.size());
 }
 
+Recognizer::~Recognizer() {
+    (void)hipSetDevice(ctx_.device());
+    for (auto &a : aux_) a->sync();
+    for (hipEvent_t e : join_)
+        if (e) (void)hipEventDestroy(e);
+    if (fork_) (void)hipEventDestroy(fork_);
+}
+
 Recognizer::Dims Recognizer::dims(const Batch *batches, int count) const {
     Dims d{0, 0, classes_};
     for (int b = 0; b < count; b++) {
@@ -168,30 +181,37 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     const hipStream_t st = ctx_.stream();
     const Dims d = dims(batches, count);
     if (d.ntot == 0) return;
-    // The trunks first (gpu.rs:1516-1526), all on the stream.
+    const int M = d.tmax * d.ntot;
+    if (double(d.tmax) * d.ntot >= 2147483647.0) fail("recognition pass too large");
+    // X [t][ntot][256] time-major (gpu.rs:1538-1555); rows t >= a line's length are never read.
+    DBuf X(&ctx_, size_t(M) * 256 * sizeof(float));
+    // The trunks first (gpu.rs:1516-1526). With several width batches they run side by side on
+    // the trunk streams, after everything already on the stream (the line images); the stream
+    // waits for all of them before the projections.
+    const int ns = count > 1 ? TRUNK_STREAMS : 0;
+    if (ns) OCR_HIP(hipEventRecord(fork_, st));
+    for (int i = 0; i < ns; i++) OCR_HIP(hipStreamWaitEvent(aux_[size_t(i)]->stream(), fork_, 0));
     std::vector<Graph::Out> trunks;
     trunks.reserve(size_t(count));
+    int noff = 0;
     for (int b = 0; b < count; b++) {
+        Ctx &c = ns ? *aux_[size_t(b % ns)] : ctx_;
         Act x{const_cast<float *>(batches[b].data), batches[b].n, 64, batches[b].w, 1, 1};
-        trunks.push_back(trunk_.run(ctx_, x));
+        trunks.push_back(trunk_.run(c, x));
         const Act &t = trunks.back().act;
         if (t.c != layers_[0].input)
             fail("trunk gives " + std::to_string(t.c) + " features, GRU takes " + std::to_string(layers_[0].input));
         if ((t.h - pool_kh_) / pool_kh_ + 1 != 1)
             fail("trunk height " + std::to_string(t.h) + " does not pool to one row");
-    }
-    const int tmax = d.tmax, ntot = d.ntot;
-    if (double(tmax) * ntot >= 2147483647.0) fail("recognition pass too large");
-    const int M = tmax * ntot;
-    // X [t][ntot][256] time-major (gpu.rs:1538-1555); rows t >= a line's length are never read.
-    DBuf X(&ctx_, size_t(M) * 256 * sizeof(float));
-    int noff = 0;
-    for (int b = 0; b < count; b++) {
-        const Act &t = trunks[b].act;
-        avgpool_t(t, pool_kh_, X.as<float>(), ntot, noff, st);
+        avgpool_t(t, pool_kh_, X.as<float>(), d.ntot, noff, c.stream());
         for (int i = 0; i < t.n; i++) lens[noff + i] = uint32_t(t.w);
         noff += t.n;
     }
+    for (int i = 0; i < ns; i++) {
+        OCR_HIP(hipEventRecord(join_[i], aux_[size_t(i)]->stream()));
+        OCR_HIP(hipStreamWaitEvent(st, join_[i], 0));
+    }
+    const int tmax = d.tmax, ntot = d.ntot;
     trunks.clear();
     // The rows that carry a step of some line, t-major: (t, line) with t < lens[line]. The
     // projections and the output layer run on these rows only (the reference computes all

@@ -1,6 +1,7 @@
 // The ocrs detection and recognition models on the GPU (src/gpu.rs:1380-1603).
 #pragma once
 
+#include <memory>
 #include <vector>
 
 #include "graph.h"
@@ -30,6 +31,7 @@ class Detector {
 class Recognizer {
   public:
     Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines);  // Recognizer::new (gpu.rs:1452-1506)
+    ~Recognizer();
 
     struct Batch {
         const float *data;  // [n][64][w] line images (host or device memory, see below)
@@ -59,6 +61,11 @@ class Recognizer {
     };
     Ctx &ctx_;
     Graph trunk_;
+    // The trunks of one pass's width batches run side by side on these streams (their own pools),
+    // so the small per-width launches fill the GPU together; events order them with ctx_'s stream.
+    static constexpr int TRUNK_STREAMS = 3;
+    std::vector<std::unique_ptr<Ctx>> aux_;
+    hipEvent_t fork_ = nullptr, join_[TRUNK_STREAMS] = {};
     int pool_kh_ = 0;
     Layer layers_[2];
     ConvPack lin_pk_;

@@ -76,10 +76,20 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         cv.notify_all();
     };
 
-    // 1. Detection of every page, det_batch pages a pass; the bit masks come back asynchronously.
-    const int ngroups = (npages + I.opts.det_batch - 1) / I.opts.det_batch;
-    std::vector<hipEvent_t> det_ev(size_t(ngroups), nullptr);
+    // 1. Detection of every page, at most det_batch pages a pass and never across a recognition
+    // pass's pages: the first pass's layouts then start while the later pages are still being
+    // detected. The bit masks come back asynchronously.
     const int nrec = (npages + I.opts.merge - 1) / I.opts.merge;
+    std::vector<int> group_of(static_cast<size_t>(npages)), group_p0;
+    for (int r = 0; r < nrec; r++) {
+        const int r0 = r * I.opts.merge, r1 = std::min(npages, r0 + I.opts.merge);
+        for (int p = r0; p < r1; p++) {
+            if ((p - r0) % I.opts.det_batch == 0) group_p0.push_back(p);
+            group_of[size_t(p)] = int(group_p0.size()) - 1;
+        }
+    }
+    const int ngroups = int(group_p0.size());
+    std::vector<hipEvent_t> det_ev(size_t(ngroups), nullptr);
     std::vector<hipEvent_t> rec_ev(size_t(nrec), nullptr);
     struct RecPass {
         std::vector<std::pair<int, int>> rows;  // (page, line in page) of every recogniser line
@@ -99,7 +109,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         I.bits_host[size_t(p)].ensure(words_of[size_t(p)] * 4);
     }
     for (int g = 0; g < ngroups; g++) {
-        const int p0 = g * I.opts.det_batch, p1 = std::min(npages, p0 + I.opts.det_batch);
+        const int p0 = group_p0[size_t(g)], p1 = g + 1 < ngroups ? group_p0[size_t(g) + 1] : npages;
         std::vector<DBuf> bits;
         std::vector<uint32_t *> bp;
         for (int p = p0; p < p1; p++) {
@@ -120,7 +130,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             std::lock_guard<std::mutex> lk(mu);
             pending_tasks++;
         }
-        hipEvent_t ev = det_ev[size_t(p / I.opts.det_batch)];
+        hipEvent_t ev = det_ev[size_t(group_of[size_t(p)])];
         const uint32_t *bits = static_cast<const uint32_t *>(I.bits_host[size_t(p)].p);
         const int pw = w[p], ph = h[p];
         I.workers.submit([&, p, ev, bits, pw, ph, dev] {
