@@ -102,6 +102,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--pages", type=int, default=12)
     ap.add_argument("--merge", type=int, default=6)
+    ap.add_argument("--det-batch", type=int, default=6, help="pages per detection pass")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-pp", action="store_true", help="skip the PP-OCR pipeline measurement")
     args = ap.parse_args()
@@ -118,7 +119,7 @@ def main():
     ctx = ocrhip.Context()
     det = ocrhip.Detector(ctx, det_path)
     rec = ocrhip.Recognizer(ctx, rec_path)
-    pipe = ocrhip.Pipeline(det, rec, merge=args.merge)
+    pipe = ocrhip.Pipeline(det, rec, merge=args.merge, det_batch=args.det_batch)
     h, w = pages[0].shape[:2]
     d_pages = []
     for p in pages:
@@ -168,7 +169,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"ocrs whole-page pipeline, {len(pages)} synthetic 300-dpi US Letter RGB pages "
-                               f"(2550x3300) per step: det U-Net 16-256 + CNN/2xBiGRU(256) rec, merge {args.merge}",
+                               f"(2550x3300) per step: det U-Net 16-256 + CNN/2xBiGRU(256) rec, merge {args.merge}, "
+                               f"det batch {args.det_batch}",
                    "pages_per_step": len(pages), "page": [h, w], "models": "random-init ocrs architecture"},
         "ms_per_page": 1e3 * secs / n_pages,
         "rec_lines_per_sec": lines / secs,

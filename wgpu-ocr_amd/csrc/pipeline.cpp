@@ -7,6 +7,8 @@
 #include <deque>
 #include <functional>
 #include <mutex>
+#include <cstdio>
+#include <cstdlib>
 #include <thread>
 
 #include "crop.h"
@@ -63,6 +65,14 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
 
     std::mutex mu;
     std::condition_variable cv;
+    // OCR_PIPE_TRACE=1: host timestamps of the pipeline's steps, printed to stderr at the end.
+    static const bool tracing = std::getenv("OCR_PIPE_TRACE") != nullptr;
+    std::vector<std::pair<double, std::string>> trace;
+    auto mark = [&](const std::string &what) {
+        if (!tracing) return;
+        std::lock_guard<std::mutex> lk(mu);
+        trace.push_back({ms_since(t0), what});
+    };
     std::vector<int> layout_ready(size_t(npages), 0);
     std::vector<PageLayout> layouts(static_cast<size_t>(npages));
     std::string error;
@@ -122,6 +132,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
                                    hipMemcpyDeviceToHost, st));
         OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming));
         OCR_HIP(hipEventRecord(det_ev[size_t(g)], st));
+        mark("det group " + std::to_string(g) + " enqueued");
     }
     // 2. Host layout of each page as soon as its mask is on the host.
     const int dev = ctx.device();
@@ -139,9 +150,11 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             try {
                 (void)hipSetDevice(dev);
                 OCR_HIP(hipEventSynchronize(ev));
+                mark("layout " + std::to_string(p) + " start");
                 const auto tc = Clock::now();
                 PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend);
                 busy = ms_since(tc);
+                mark("layout " + std::to_string(p) + " done");
                 std::lock_guard<std::mutex> lk(mu);
                 layouts[size_t(p)] = std::move(L);
                 layout_ready[size_t(p)] = 1;
@@ -166,6 +179,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             });
             if (!error.empty()) break;
         }
+        mark("rec " + std::to_string(r) + " layouts ready");
         RecPass &R = passes[size_t(r)];
         // A line's recognition depends on its batch's width (the padding), not on which lines
         // share the batch, so every page's batches of one width run as one trunk batch: the
@@ -208,6 +222,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         ctx.h2d(dcrops.get(), R.crops.data(), R.crops.size() * sizeof(CropLine));
         ctx.h2d(droff.get(), R.row_off.data(), R.row_off.size() * 4);
         if (!R.spans.empty()) ctx.h2d(dspans.get(), R.spans.data(), R.spans.size() * 4);
+        mark("rec " + std::to_string(r) + " crops built");
         line_crop(dcrops.as<CropLine>(), int(R.crops.size()), droff.as<int>(), dspans.as<int>(), max_wb, st);
         const Recognizer::Dims d = I.rec.dims(batches.data(), int(batches.size()));
         R.tmax = d.tmax;
@@ -217,6 +232,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         DBuf best(&ctx, size_t(d.tmax) * d.ntot * sizeof(uint32_t));
         I.rec.recognize_device(batches.data(), int(batches.size()), logits.as<float>(), best.as<uint32_t>(),
                                R.lens.data());
+        mark("rec " + std::to_string(r) + " enqueued");
         I.best_host[size_t(r)].ensure(size_t(d.tmax) * d.ntot * sizeof(uint32_t));
         OCR_HIP(hipMemcpyAsync(I.best_host[size_t(r)].p, best.get(), size_t(d.tmax) * d.ntot * sizeof(uint32_t),
                                hipMemcpyDeviceToHost, st));
@@ -264,6 +280,11 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
     if (!error.empty()) fail("pipeline: " + error);
     ctx.sync();
     stats_.ms = ms_since(t0);
+    if (tracing) {
+        mark("end");
+        std::sort(trace.begin(), trace.end());
+        for (const auto &e : trace) std::fprintf(stderr, "[pipe] %8.3f ms  %s\n", e.first, e.second.c_str());
+    }
     stats_.cpu_busy_ms = cpu_busy;
     for (const PageText &pt : pages_) {
         stats_.lines += int(pt.lines.size());
