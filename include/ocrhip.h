@@ -267,6 +267,14 @@ int ocr_db_boxes(const uint32_t *bits, const float *prob, uint32_t w, uint32_t h
 /* One box as a PP-OCR line image (ocr-bench.rs:538-555, ppocr.rs:42-53): out = {left, top,
  * width, height, resized width at height 48} on a page_w x page_h page. */
 int ocr_pp_line_box(const ocr_rrect *box, float relv, uint32_t page_w, uint32_t page_h, int32_t *out);
+/* ocrs' line images (prepare_recognition_input, called at src/bin/ocr-bench.rs:378, and the batch
+ * assembly of ocr-bench.rs:388-404) on the GPU: count lines of an RGB page (host), lines = count x
+ * {left, top, width, height, resized width, first row offset} with every line's (height + 1) span
+ * offsets in row_off (indices into spans, pairs [x0, x1) of crop columns), into out
+ * [count][64][wb] (host), black (-0.5) outside the polygon and past each line's width. */
+int ocr_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t page_h, const int32_t *lines,
+                    uint32_t count, const int32_t *row_off, uint32_t n_row_off, const int32_t *spans, uint32_t n_spans,
+                    uint32_t wb, float *out);
 /* ppocr::line_input + ppocr::batch (src/ppocr.rs:42-78) on the GPU: count line images of an RGB
  * page (host), lines = count x {left, top, width, height, resized width}, into out
  * [count][3][48][wb] (host), zero past each line's width. */

@@ -41,6 +41,34 @@ def test_pipeline_text_matches_cpu(pipeline, detector, det_oracle, rec_oracle):
     assert sum(len(t) for t in texts) > 0
 
 
+def test_line_images_match_oracle(detector, ctx):
+    # Every line of a page's layout: the GPU line image (one launch for all lines, batch width
+    # 800) equals the oracle's line crop bit for bit, black past each line's width.
+    page = synth.page(5)
+    bits = detector.detect_page(page, 0.5)
+    lay = layout_of(bits, page.shape[1])
+    lines = [lay.line(i) for i in range(lay.nlines)]
+    assert len(lines) > 20
+    print(f"line images: {len(lines)} lines", flush=True)
+    got = ocrhip.line_images(ctx, page, lines, 800)
+    for k, (box, row_off, spans) in enumerate(lines):
+        want = og.line_crop(page, box, row_off, spans, 800)
+        np.testing.assert_array_equal(got[k], want, err_msg=f"line {k} box {list(box)}")
+
+
+def test_detect_mask_words_at_odd_widths(detector, det_oracle):
+    # Page widths that end inside a 64-pixel group and inside a 32-bit word.
+    for w in (2549, 97):
+        page = np.ascontiguousarray(synth.page(2)[:1100, :w])
+        print(f"mask width {w}", flush=True)
+        bits = detector.detect_page(page, 0.5)
+        want_bits, prob, _ = og.detect_page(det_oracle, page, 0.5)
+        diff = np.unpackbits((bits ^ want_bits).view(np.uint8), bitorder="little").reshape(bits.shape[0], -1)
+        assert not diff[:, w:].any(), "bits past the page width"
+        diff = diff[:, :w].astype(bool)
+        assert np.all(np.abs(prob[diff] - 0.5) < 1e-4)
+
+
 def test_pipeline_merge_and_device_entry(detector, recognizer, ctx):
     pages = [synth.page(s) for s in (4, 5, 6)]
     a = ocrhip.Pipeline(detector, recognizer, merge=1, det_batch=1)

@@ -839,6 +839,44 @@ int ocr_pp_line_box(const ocr_rrect *box, float relv, uint32_t page_w, uint32_t 
 }
 
 
+int ocr_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t page_h, const int32_t *lines,
+                    uint32_t count, const int32_t *row_off, uint32_t n_row_off, const int32_t *spans, uint32_t n_spans,
+                    uint32_t wb, float *out) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(rgb, "rgb");
+        need(lines, "lines");
+        need(row_off, "row_off");
+        need(out, "out");
+        if (count == 0) return;
+        if (wb == 0 || page_w == 0 || page_h == 0) fail("empty page or batch width");
+        if (n_spans && !spans) fail("spans is null");
+        for (uint32_t i = 0; i < n_row_off; i++)
+            if (row_off[i] < 0 || uint32_t(row_off[i]) > n_spans || (i && row_off[i] < row_off[i - 1]))
+                fail("row offsets out of range");
+        Ctx &c = *ctx->ctx;
+        c.bind();
+        const size_t slot = size_t(LINE_H) * wb;
+        DBuf drgb(&c, size_t(page_w) * page_h * 3), dout(&c, size_t(count) * slot * sizeof(float));
+        DBuf droff(&c, size_t(n_row_off) * 4), dspans(&c, std::max<size_t>(n_spans, 1) * 4);
+        c.h2d(drgb.get(), rgb, size_t(page_w) * page_h * 3);
+        c.h2d(droff.get(), row_off, size_t(n_row_off) * 4);
+        if (n_spans) c.h2d(dspans.get(), spans, size_t(n_spans) * 4);
+        std::vector<CropLine> crops;
+        for (uint32_t i = 0; i < count; i++) {
+            const int32_t *l = lines + size_t(i) * 6;
+            if (l[2] < 1 || l[3] < 1 || l[4] < 1 || uint32_t(l[4]) > wb) fail("line box or width out of range");
+            if (l[5] < 0 || size_t(l[5]) + size_t(l[3]) + 1 > n_row_off) fail("line row offsets out of range");
+            crops.push_back({drgb.as<uint8_t>(), int(page_w), int(page_h), l[0], l[1], l[2], l[3], l[4], l[5],
+                             dout.as<float>() + size_t(i) * slot, int(wb)});
+        }
+        DBuf dc(&c, crops.size() * sizeof(CropLine));
+        c.h2d(dc.get(), crops.data(), crops.size() * sizeof(CropLine));
+        line_crop(dc.as<CropLine>(), int(count), droff.as<int>(), dspans.as<int>(), int(wb), c.stream());
+        c.d2h(out, dout.get(), size_t(count) * slot * sizeof(float));
+    });
+}
+
 int ocr_pp_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t page_h, const int32_t *lines,
                        uint32_t count, uint32_t wb, float *out) {
     return guard([&] {

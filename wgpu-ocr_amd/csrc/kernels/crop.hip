@@ -29,33 +29,34 @@ __device__ inline float grey_px(const uint8_t *rgb, int w, int h, int x, int y) 
     return g + float(q[2]) * (0.114f / 255.f);
 }
 
-__device__ inline float crop_px(const CropLine &L, const int *row_off, const int *spans, int cx, int cy) {
-    const int s0 = row_off[L.row_base + cy], s1 = row_off[L.row_base + cy + 1];
-    for (int s = s0; s < s1; s += 2)
-        if (cx >= spans[s] && cx < spans[s + 1]) return grey_px(L.rgb, L.pw, L.ph, L.left + cx, L.top + cy);
-    return -0.5f;
-}
-
-__global__ void line_crop_kernel(const CropLine *lines, const int *row_off, const int *spans) {
+// One thread per output pixel, a workgroup per 256 columns of one output row: the row's source
+// rows, their polygon spans and the vertical weight are the same for the whole workgroup.
+__global__ __launch_bounds__(256) void line_crop_kernel(const CropLine *lines, const int *row_off, const int *spans) {
 #pragma clang fp contract(off)
-    const CropLine L = lines[blockIdx.y];
-    const int total = LINE_H * L.wb;
-    const float sy = float(L.bh) / float(LINE_H), sx = float(L.bw) / float(L.out_w);
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
-        const int ox = i % L.wb, oy = i / L.wb;
-        float v = -0.5f;
-        if (ox < L.out_w) {
-            const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(L.bh) - 1.f);
-            const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(L.bw) - 1.f);
-            const int y1 = int(iy), x1 = int(ix);
-            const int y2 = min(y1 + 1, L.bh - 1), x2 = min(x1 + 1, L.bw - 1);
-            const float fy = iy - float(y1), fx = ix - float(x1);
-            const float top = mixf(crop_px(L, row_off, spans, x1, y1), crop_px(L, row_off, spans, x2, y1), fx);
-            const float bot = mixf(crop_px(L, row_off, spans, x1, y2), crop_px(L, row_off, spans, x2, y2), fx);
-            v = mixf(top, bot, fy);
-        }
-        L.dst[size_t(oy) * L.wb + ox] = v;
+    const CropLine L = lines[blockIdx.z];
+    const int oy = blockIdx.y, ox = blockIdx.x * 256 + threadIdx.x;
+    if (ox >= L.wb) return;
+    float v = -0.5f;
+    if (ox < L.out_w) {
+        const float sy = float(L.bh) / float(LINE_H), sx = float(L.bw) / float(L.out_w);
+        const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(L.bh) - 1.f);
+        const int y1 = int(iy), y2 = min(y1 + 1, L.bh - 1);
+        const float fy = iy - float(y1);
+        // Crop pixel (cx, cy): the page's grey inside the row's spans, black elsewhere.
+        auto px = [&](int cx, int cy) -> float {
+            const int s0 = row_off[L.row_base + cy], s1 = row_off[L.row_base + cy + 1];
+            for (int s = s0; s < s1; s += 2)
+                if (cx >= spans[s] && cx < spans[s + 1]) return grey_px(L.rgb, L.pw, L.ph, L.left + cx, L.top + cy);
+            return -0.5f;
+        };
+        const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(L.bw) - 1.f);
+        const int x1 = int(ix), x2 = min(x1 + 1, L.bw - 1);
+        const float fx = ix - float(x1);
+        const float top = mixf(px(x1, y1), px(x2, y1), fx);
+        const float bot = mixf(px(x1, y2), px(x2, y2), fx);
+        v = mixf(top, bot, fy);
     }
+    L.dst[size_t(oy) * L.wb + ox] = v;
 }
 
 // PP-OCR line images: the crop resized to 48 rows x out_w columns bilinearly (half-pixel,
@@ -106,8 +107,8 @@ void pp_line_crop(const PpCropLine *d_lines, int nlines, int max_wb, hipStream_t
 void line_crop(const CropLine *d_lines, int nlines, const int *d_row_off, const int *d_spans, int max_wb,
                hipStream_t s) {
     if (nlines <= 0) return;
-    const int per_line = (LINE_H * max_wb + 255) / 256;
-    dim3 grid(unsigned(per_line < 64 ? per_line : 64), unsigned(nlines));
+    if (nlines > 65535) fail("line_crop: more than 65535 lines");
+    dim3 grid(unsigned((max_wb + 255) / 256), LINE_H, unsigned(nlines));
     ProbeScope probe("line_crop", s, 0, 4.0 * double(nlines) * LINE_H * max_wb);
     hipLaunchKernelGGL(line_crop_kernel, grid, dim3(256), 0, s, d_lines, d_row_off, d_spans);
     OCR_HIP(hipGetLastError());

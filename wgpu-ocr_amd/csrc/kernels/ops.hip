@@ -198,28 +198,33 @@ __global__ void grey_resize_kernel(const uint8_t *rgb, int w, int h, int pw, int
     y[i] = mixf(top, bot, wy);
 }
 
-// ---- mask_up (gpu.rs:563-593): one thread per 32-pixel word ----------------------------------
+// ---- mask_up (gpu.rs:563-593): one thread per page pixel, a wavefront per 64 pixels of a row --
+// (two bit words, assembled with a ballot).
 __global__ void mask_up_kernel(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, int words,
                                float sx, float sy, float thr) {
 #pragma clang fp contract(off)
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= words * h) return;
-    int wx = i % words, oy = i / words;
-    float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(mh) - 1.f);
-    int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
-    float fy = iy - float(y1);
-    uint32_t out = 0;
-    for (int b = 0; b < 32; b++) {
-        int ox = wx * 32 + b;
-        if (ox >= w) break;
-        float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(mw) - 1.f);
-        int x1 = int(ix), x2 = min(x1 + 1, mw - 1);
-        float fx = ix - float(x1);
-        float top = mixf(m[size_t(y1) * stride + x1], m[size_t(y1) * stride + x2], fx);
-        float bot = mixf(m[size_t(y2) * stride + x1], m[size_t(y2) * stride + x2], fx);
-        if (mixf(top, bot, fy) > thr) out |= 1u << b;
+    const int lane = threadIdx.x & 63;
+    const long wv = (long(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+    const int pairs = (words + 1) / 2;
+    if (wv >= long(pairs) * h) return;  // the whole wavefront
+    const int oy = int(wv / pairs), wp = int(wv - long(oy) * pairs);
+    const int ox = wp * 64 + lane;
+    bool on = false;
+    if (ox < w) {
+        const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(mh) - 1.f);
+        const int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
+        const float fy = iy - float(y1);
+        const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(mw) - 1.f);
+        const int x1 = int(ix), x2 = min(x1 + 1, mw - 1);
+        const float fx = ix - float(x1);
+        const float top = mixf(m[size_t(y1) * stride + x1], m[size_t(y1) * stride + x2], fx);
+        const float bot = mixf(m[size_t(y2) * stride + x1], m[size_t(y2) * stride + x2], fx);
+        on = mixf(top, bot, fy) > thr;
     }
-    bits[i] = out;
+    const unsigned long long b = __ballot(on);
+    uint32_t *row = bits + size_t(oy) * words;
+    if (lane == 0) row[2 * wp] = uint32_t(b);
+    if (lane == 1 && 2 * wp + 1 < words) row[2 * wp + 1] = uint32_t(b >> 32);
 }
 
 // ---- avgpool_t (gpu.rs:595-614): [n][kh][T][c] -> X[t][ntot][c] at line offset noff ----------
@@ -336,8 +341,8 @@ void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, 
              hipStream_t s) {
     int words = (w + 31) / 32;
     ProbeScope probe("mask_up", s, 0, 4.0 * double(mw) * mh + 4.0 * double(words) * h);
-    hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t(words) * h)), dim3(256), 0, s, m, stride, mw, mh, bits,
-                       w, h, words, sx, sy, thr);
+    hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t((words + 1) / 2) * h * 64)), dim3(256), 0, s, m, stride,
+                       mw, mh, bits, w, h, words, sx, sy, thr);
     OCR_HIP(hipGetLastError());
 }
 

@@ -93,6 +93,7 @@ SIGNATURES = {
     "ocr_db_boxes": (ctypes.c_int, [P, P, U32, U32, F32, F32, F32, F32, F32, P, U32, PU32]),
     "ocr_pp_line_box": (ctypes.c_int, [P, F32, U32, U32, P]),
     "ocr_pp_line_images": (ctypes.c_int, [P, P, U32, U32, P, U32, U32, P]),
+    "ocr_line_images": (ctypes.c_int, [P, P, U32, U32, P, U32, P, U32, P, U32, U32, P]),
 }
 
 
@@ -584,6 +585,25 @@ def pp_line_box(box, relv: float, page_w: int, page_h: int):
     out = np.zeros(5, np.int32)
     _check(lib().ocr_pp_line_box(_ptr(b), relv, page_w, page_h, _ptr(out)))
     return tuple(int(v) for v in out)
+
+
+def line_images(ctx: Context, rgb: np.ndarray, lines, wb: int) -> np.ndarray:
+    """ocrs line images on the GPU: lines = [(box, row_off, spans)] with box = (left, top, width,
+    height, resized width) as Layout.line gives them; returns [n][64][wb] float32."""
+    rgb = np.ascontiguousarray(rgb, np.uint8)
+    desc, ro, sp = [], [], []
+    for box, row_off, spans in lines:
+        base = len(sp)
+        desc.append(list(box[:5]) + [len(ro)])
+        ro.extend(int(o) + base for o in row_off)
+        sp.extend(int(v) for v in np.asarray(spans).reshape(-1))
+    d = np.ascontiguousarray(desc, np.int32).reshape(-1, 6)
+    r = np.ascontiguousarray(ro, np.int32)
+    s = np.ascontiguousarray(sp if sp else [0], np.int32)
+    out = np.empty((len(lines), 64, wb), np.float32)
+    _check(lib().ocr_line_images(ctx.handle, _ptr(rgb), rgb.shape[1], rgb.shape[0], _ptr(d), len(lines), _ptr(r),
+                                 len(r), _ptr(s), len(sp), wb, _ptr(out)))
+    return out
 
 
 def pp_line_images(ctx: Context, rgb: np.ndarray, lines, wb: int) -> np.ndarray:
