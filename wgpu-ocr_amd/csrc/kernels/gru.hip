@@ -17,14 +17,16 @@
 // hi and lo columns of a line are summed with one DPP rotation by 8, arranged so that lane r < 8
 // ends with units 4g, 4g+1 of line r and lane r + 8 with units 4g+2, 4g+3 of the same line:
 // every lane does gate arithmetic for two units. The step's G values are loaded at the end of
-// the previous step, so the HBM latency hides behind the barrier and the MFMA phase. The new state
-// goes to a double-buffered LDS copy of the B operand: one barrier per step.
+// the previous step, so the HBM latency hides behind the barrier (an LDS-only one: the loads and
+// the Y stores stay in flight) and the MFMA phase. The new state goes to a double-buffered LDS
+// copy of the B operand: one barrier per step.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 
 #include "../kernels.h"
 #include "../runtime.h"
+#include "lds_dma.h"
 
 namespace ocr {
 
@@ -105,70 +107,89 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
     float2 gcur[3][RT];
     load_g(0, gcur);
 
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     for (int s = 0; s < maxlen; s++) {
         const int cur = s & 1;
+        const bool on = s < len;
         floatx4 acc[3][RT];
 #pragma unroll
         for (int q = 0; q < 3; q++)
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
                 acc[q][rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // R h for row tile rt of the three gates (8 k-slices).
+        auto mfmas = [&](int rt) __attribute__((always_inline)) {
 #pragma unroll
-        for (int kt = 0; kt < 8; kt++) {
-            const half8 b = *reinterpret_cast<const half8 *>(&hbuf[cur][r][kt * 32 + 8 * g]);
+            for (int kt = 0; kt < 8; kt++) {
+                const half8 b = *reinterpret_cast<const half8 *>(&hbuf[cur][r][kt * 32 + 8 * g]);
 #pragma unroll
-            for (int q = 0; q < 3; q++)
-#pragma unroll
-                for (int rt = 0; rt < RT; rt++) {
+                for (int q = 0; q < 3; q++) {
                     const half8 a = (q == 2 && kt >= 8 - KL) ? s_rf[wave][rt * KL + kt - (8 - KL)][lane] : rf[q][rt][kt];
                     acc[q][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[q][rt], 0, 0, 0);
                 }
-        }
-        // hi + lo: lane r < 8 keeps rows 0, 1 and sends rows 2, 3 to lane r + 8 (and the reverse).
-        float rh[3][RT][2];
+            }
+        };
+        // The gates of row tile rt, branch-free (a line past its end keeps its state), and the
+        // next step's B operand: units u0 and u0 + 1 as one 32-bit word of hi parts and one of
+        // lo parts. hi + lo of R h: lane r < 8 keeps rows 0, 1 and sends rows 2, 3 to lane r + 8
+        // (and the reverse).
+        float hn[RT][2];
+        auto gates = [&](int rt) __attribute__((always_inline)) {
+            float rh[3][2];
 #pragma unroll
-        for (int q = 0; q < 3; q++)
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
+            for (int q = 0; q < 3; q++) {
                 const float send0 = upper ? acc[q][rt][0] : acc[q][rt][2];
                 const float send1 = upper ? acc[q][rt][1] : acc[q][rt][3];
                 const float keep0 = upper ? acc[q][rt][2] : acc[q][rt][0];
                 const float keep1 = upper ? acc[q][rt][3] : acc[q][rt][1];
-                rh[q][rt][0] = keep0 + ror8(send0);
-                rh[q][rt][1] = keep1 + ror8(send1);
+                rh[q][0] = keep0 + ror8(send0);
+                rh[q][1] = keep1 + ror8(send1);
             }
-        const bool on = s < len;
-        const int t = dir == 0 ? s : len - 1 - s;
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) {
             const int u0 = wave * UPW + rt * 16 + 4 * g + usub;
-            if (on) {
-                float hn[2];
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const float gz = i ? gcur[0][rt].y : gcur[0][rt].x;
-                    const float gr = i ? gcur[1][rt].y : gcur[1][rt].x;
-                    const float gh = i ? gcur[2][rt].y : gcur[2][rt].x;
-                    const float z = sigm(gz + (rh[0][rt][i] + s_rb[u0 + i]));
-                    const float rr = sigm(gr + (rh[1][rt][i] + s_rb[256 + u0 + i]));
-                    const float c = tanh_f(gh + rr * (rh[2][rt][i] + s_rb[512 + u0 + i]));
-                    hn[i] = (1.f - z) * c + z * h[rt][i];
-                    h[rt][i] = hn[i];
-                }
-                *reinterpret_cast<float2 *>(Y + (size_t(t) * ntot + line) * 512 + dir * 256 + u0) =
-                    make_float2(hn[0], hn[1]);
-            }
-            // The next step's B operand (the unchanged state when this line has ended).
+            half2_t hi2, lo2;
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                const _Float16 hi = (_Float16)h[rt][i];
-                hbuf[cur ^ 1][lr][u0 + i] = hi;
-                hbuf[cur ^ 1][lr + LINES][u0 + i] = (_Float16)(h[rt][i] - (float)hi);
+                const float gz = i ? gcur[0][rt].y : gcur[0][rt].x;
+                const float gr = i ? gcur[1][rt].y : gcur[1][rt].x;
+                const float gh = i ? gcur[2][rt].y : gcur[2][rt].x;
+                const float z = sigm(gz + (rh[0][i] + s_rb[u0 + i]));
+                const float rr = sigm(gr + (rh[1][i] + s_rb[256 + u0 + i]));
+                const float c = tanh_f(gh + rr * (rh[2][i] + s_rb[512 + u0 + i]));
+                hn[rt][i] = (1.f - z) * c + z * h[rt][i];
+                h[rt][i] = on ? hn[rt][i] : h[rt][i];
+                hi2[i] = (_Float16)h[rt][i];
+                lo2[i] = (_Float16)(h[rt][i] - (float)hi2[i]);
+            }
+            *reinterpret_cast<half2_t *>(&hbuf[cur ^ 1][lr][u0]) = hi2;
+            *reinterpret_cast<half2_t *>(&hbuf[cur ^ 1][lr + LINES][u0]) = lo2;
+        };
+        // Row tile 0's MFMAs; then row tile 1's MFMAs with row tile 0's gate arithmetic between
+        // them (the vector ALU works while the matrix core does); then row tile 1's gates.
+        static_assert(RT == 2, "two row tiles a wavefront");
+        mfmas(0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(1);
+        gates(0);
+#pragma unroll
+        for (int i = 0; i < 24; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        gates(1);
+        if (on) {
+            const int t = dir == 0 ? s : len - 1 - s;
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                const int u0 = wave * UPW + rt * 16 + 4 * g + usub;
+                *reinterpret_cast<float2 *>(Y + (size_t(t) * ntot + line) * 512 + dir * 256 + u0) =
+                    make_float2(hn[rt][0], hn[rt][1]);
             }
         }
-        // The next step's G, in flight across the barrier and the next MFMA phase.
+        // The next step's G, in flight across the barrier (which waits for LDS only) and the
+        // next MFMA phase.
         load_g(s + 1, gcur);
-        __syncthreads();
+        lds_barrier();
     }
 }
 
