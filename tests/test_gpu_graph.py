@@ -96,6 +96,16 @@ def test_direct_conv_fused_pool(ctx, tmp_path, pool):
     check(ctx, p, RNG.uniform(-0.5, 0.5, (3, 1, 64, 37)).astype(np.float32))
 
 
+@pytest.mark.parametrize("cout,act,pool", [(48, "Sigmoid", None), (64, "Relu", (2, 2)), (16, None, (2, 2))])
+def test_direct_conv_matrix_cores(ctx, tmp_path, cout, act, pool):
+    # The one-channel 3 x 3 conv on the matrix cores: tile edges (50 x 131), 1-4 channel tiles.
+    def net(g, x):
+        y = conv(g, x, 1, cout, act=act)
+        return g.add("MaxPool", [y], kernel_shape=list(pool), strides=list(pool)) if pool else y
+    p = build(tmp_path, "d1", net, (2, 1, 50, 131))
+    check(ctx, p, RNG.uniform(-0.5, 0.5, (2, 1, 50, 131)).astype(np.float32))
+
+
 def test_direct_conv_two_readers_and_concat(ctx, tmp_path):
     # e0 is read by a MaxPool and a Concat (no fusion); the Concat takes the ConvTranspose output
     # and the skip in its channel range, plus the graph input (a copy, not an alias).

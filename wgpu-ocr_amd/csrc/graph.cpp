@@ -111,6 +111,14 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     }
                 }
                 s.w = ctx.upload_weights(w.data.data(), w.data.size());
+                bool exact = kh == 3 && kw == 3 && cout % 16 == 0 && cout <= 64;
+                for (size_t k = 0; exact && k < w.data.size(); k++)
+                    exact = float(_Float16(w.data[k])) == w.data[k];
+                if (exact) {
+                    std::vector<uint16_t> frag(size_t(cout) / 16 * 64 * 8);
+                    pack_conv1_frags(w.data.data(), cout, frag.data());
+                    s.w1frag = ctx.upload_weights(frag.data(), frag.size());
+                }
             } else if (group == 1) {
                 s.kind = OpKind::Conv;
                 s.cin = cin_g;
@@ -458,7 +466,7 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
         }
         case OpKind::Direct:
             y = out_view(i);
-            conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st);
+            conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st, s.w1frag);
             break;
         case OpKind::ConvT:
             y = out_view(i);

@@ -24,6 +24,7 @@ struct Step {
     ConvPack pk;
     const uint16_t *whi = nullptr, *wlo = nullptr, *wfrag = nullptr;  // wfrag: conv_igemm's packing
     const float *w = nullptr, *b = nullptr;  // float32 weights (direct, transpose, generic) and bias
+    const uint16_t *w1frag = nullptr;        // direct 3 x 3 with float16-exact weights: conv1_mfma's
     int ph = 1, pw = 1;                       // a fused MaxPool's kernel, or MaxPool's kernel
     // A MaxPool fused into a dense conv: pool_only when it was the conv's only reader (output is
     // then the pooled value); otherwise pool_output names the pooled value next to the full one.

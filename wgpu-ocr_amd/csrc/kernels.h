@@ -82,7 +82,14 @@ void conv_generic(const Act &x, const Act &y, const float *w, const float *b, in
                   int pt, int pl, int group, int act, hipStream_t s);
 // One input channel, stride 1, act, and a fused MaxPool (ph, pw) (gpu.rs:385-422).
 void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int pad, int act,
-                 int ph, int pw, hipStream_t s);
+                 int ph, int pw, hipStream_t s,
+                 const uint16_t *frag = nullptr);
+// The matrix-core path of conv_direct (kernels/conv1.hip): 3 x 3, pad 1, 16 to 64 output channels
+// (a multiple of 16), float16-exact weights packed by pack_conv1_frags ([cout][9] float32 in,
+// cout / 16 KiB of fragments out), no pool or a 2 x 2 one. Returns false for anything else.
+void pack_conv1_frags(const float *w, int cout, uint16_t *frag);
+bool conv1_mfma(const Act &x, const Act &y, const uint16_t *frag, const float *b, int act, int ph, int pw,
+                hipStream_t s);
 // ConvTranspose gather form (gpu.rs:424-460); w re-laid out as [ky][kx][cin][cout].
 void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride,
                     int act, hipStream_t s);

@@ -273,7 +273,8 @@ void conv_generic(const Act &x, const Act &y, const float *w, const float *b, in
 }
 
 void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int pad, int act, int ph,
-                 int pw, hipStream_t s) {
+                 int pw, hipStream_t s, const uint16_t *frag) {
+    if (frag && kh == 3 && kw == 3 && pad == 1 && conv1_mfma(x, y, frag, b, act, ph, pw, s)) return;
     if (kh > DMAXK || kw > DMAXK || ph > DMAXP || pw > DMAXP || y.c > DMAXC)
         fail("conv_direct: kernel above 7 x 7, pool above 4 x 4 or more than 64 channels");
     if (x.c != 1) fail("conv_direct: one input channel");
