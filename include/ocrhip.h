@@ -131,6 +131,10 @@ typedef struct ocr_rrect {
  * words): 8-connected components, minimum-area rectangles grown by 3 px, area >= 100. Writes
  * at most cap rectangles; *count receives the number found. */
 int ocr_word_rects(const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out, uint32_t cap, uint32_t *count);
+/* The same on `threads` host threads (the page cut into row bands labelled side by side, joined
+ * across the cuts): the same rectangles in the same order. The page pipeline's layout runs so. */
+int ocr_word_rects_mt(const uint32_t *bits, uint32_t w, uint32_t h, uint32_t threads, ocr_rrect *out, uint32_t cap,
+                      uint32_t *count);
 
 /* The page layout before recognition (src/bin/ocr-bench.rs:503-559): words, text lines in
  * reading order, line padding (relv, relend), every line's crop box, polygon spans and resized

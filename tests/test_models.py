@@ -87,3 +87,30 @@ def test_library_exports_every_declared_symbol():
 def test_binding_covers_the_header():
     import ocrhip
     assert sorted(ocrhip.SIGNATURES) == _header_functions()
+
+
+def test_word_rects_threads_identical():
+    # The page cut into row bands on several threads: the same rectangles, in the same order, as
+    # one thread (components that cross a cut in U shapes, combs and diagonals included).
+    import ocrhip
+    rng = np.random.Generator(np.random.PCG64(11))
+    for trial in range(12):
+        h, w = int(rng.integers(64, 900)), int(rng.integers(40, 700))
+        yy, xx = np.mgrid[0:h, 0:w]
+        kind = trial % 4
+        if kind == 0:
+            m = rng.random((h, w)) < 0.35
+        elif kind == 1:
+            m = ((xx // 7) % 3 == 0) | (yy % 97 < 2)
+        elif kind == 2:
+            m = ((xx + yy) % 23 < 3) | ((xx - yy + 10000) % 31 < 2)
+        else:
+            m = ((xx % 50 < 20) & (yy % 60 < 40)) | (rng.random((h, w)) < 0.003)
+        words = (w + 31) // 32
+        padded = np.zeros((h, words * 32), bool)
+        padded[:, :w] = m
+        bits = np.packbits(padded, axis=1, bitorder="little").view(np.uint32).reshape(h, words)
+        want = ocrhip.word_rects(bits, w)
+        for t in (2, 3, 5):
+            got = ocrhip.word_rects(bits, w, threads=t)
+            np.testing.assert_array_equal(got, want, err_msg=f"trial {trial} threads {t}")

@@ -359,6 +359,18 @@ int ocr_word_rects(const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out,
     });
 }
 
+int ocr_word_rects_mt(const uint32_t *bits, uint32_t w, uint32_t h, uint32_t threads, ocr_rrect *out, uint32_t cap,
+                      uint32_t *count) {
+    return guard([&] {
+        need(bits, "bits");
+        need(count, "count");
+        if (threads < 1 || threads > 256) fail("threads must be 1..256");
+        std::vector<RRect> r = word_rects(bits, int(w), int(h), 3.f, 100.f, int(threads));
+        *count = uint32_t(r.size());
+        for (size_t i = 0; i < r.size() && i < cap; i++) out[i] = {r[i].cx, r[i].cy, r[i].ux, r[i].uy, r[i].w, r[i].h};
+    });
+}
+
 ocr_layout *ocr_layout_page(const uint32_t *bits, uint32_t w, uint32_t h, float relv, float relend) {
     return guard_ptr<ocr_layout>([&] {
         need(bits, "bits");

@@ -5,6 +5,7 @@
 #include <cstring>
 #include <numeric>
 #include <string>
+#include <thread>
 
 namespace ocr {
 
@@ -132,14 +133,24 @@ int find(std::vector<int> &parent, int a) {
 
 }  // namespace
 
-// Every 8-connected component of a bit mask (h rows of ceil(w / 32) words) as its rows'
-// leftmost and rightmost pixels, rows ascending (all the convex hull needs; see hull_rows).
-static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w, int h) {
-    const int words = (w + 31) / 32;
+namespace {
+
+// The 8-connected components of rows [y0, y1) of a bit mask (ceil(w / 32) words a row), each as
+// its rows' leftmost and rightmost pixels, rows ascending (all the convex hull needs; see
+// hull_rows), in order of their first run; and the runs of the first and last rows with their
+// components, for joining neighbouring bands.
+struct BandComps {
+    std::vector<std::vector<Pt>> pts;
+    std::vector<Run> first, last;
+    std::vector<int> first_c, last_c;
+};
+
+BandComps band_components(const uint32_t *bits, int w, int y0, int y1) {
+    const int words = (w + 31) / 32, h = y1 - y0;
     std::vector<Run> runs;
     std::vector<int> row_start(size_t(h) + 1, 0);
-    for (int y = 0; y < h; y++) {
-        row_start[y] = int(runs.size());
+    for (int y = y0; y < y1; y++) {
+        row_start[size_t(y - y0)] = int(runs.size());
         const uint32_t *row = bits + size_t(y) * words;
         int x = 0;
         while (x < w) {
@@ -160,13 +171,13 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
             x = end;
         }
     }
-    row_start[h] = int(runs.size());
+    row_start[size_t(h)] = int(runs.size());
     // Union the runs of neighbouring rows that touch with 8-connectivity.
     std::vector<int> parent(runs.size());
     std::iota(parent.begin(), parent.end(), 0);
     for (int y = 1; y < h; y++) {
-        int i = row_start[y - 1], j = row_start[y];
-        const int ie = row_start[y], je = row_start[y + 1];
+        int i = row_start[size_t(y) - 1], j = row_start[size_t(y)];
+        const int ie = row_start[size_t(y)], je = row_start[size_t(y) + 1];
         while (i < ie && j < je) {
             const Run &a = runs[size_t(i)], &b = runs[size_t(j)];
             if (a.x1 + 1 >= b.x0 && b.x1 + 1 >= a.x0) {
@@ -180,15 +191,16 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
     // Row extremes per component (components in order of their first run). Runs are listed row
     // by row and left to right, so a component's later run in the same row only moves its right
     // end.
-    std::vector<int> comp(runs.size(), -1);
-    std::vector<std::vector<Pt>> pts;
+    BandComps out;
+    std::vector<int> comp(runs.size(), -1), run_comp(runs.size());
     for (size_t r = 0; r < runs.size(); r++) {
         const int root = find(parent, int(r));
         if (comp[size_t(root)] < 0) {
-            comp[size_t(root)] = int(pts.size());
-            pts.emplace_back();
+            comp[size_t(root)] = int(out.pts.size());
+            out.pts.emplace_back();
         }
-        auto &v = pts[size_t(comp[size_t(root)])];
+        run_comp[r] = comp[size_t(root)];
+        auto &v = out.pts[size_t(comp[size_t(root)])];
         const float y = float(runs[r].y), x0 = float(runs[r].x0), x1 = float(runs[r].x1);
         const bool same_row = !v.empty() && v.back().y == y;
         if (same_row) {
@@ -200,16 +212,113 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
             if (x1 != x0) v.push_back({x1, y});
         }
     }
-    return pts;
+    if (h > 0) {
+        for (int r = row_start[0]; r < row_start[1]; r++) out.first.push_back(runs[size_t(r)]), out.first_c.push_back(run_comp[size_t(r)]);
+        for (int r = row_start[size_t(h) - 1]; r < row_start[size_t(h)]; r++)
+            out.last.push_back(runs[size_t(r)]), out.last_c.push_back(run_comp[size_t(r)]);
+    }
+    return out;
 }
 
-std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area) {
-    std::vector<RRect> out;
-    for (auto &v : component_points(bits, w, h)) {
-        RRect r = min_area_rect(hull_rows(v));
-        r.resize(r.w + 2 * expand, r.h + 2 * expand);
-        if (r.area() >= min_area) out.push_back(r);
+// Row extremes of one component made of several band components: per row the leftmost and the
+// rightmost pixel of all of them (the right one only when it differs), rows ascending.
+std::vector<Pt> merge_rows(std::vector<Pt> all) {
+    std::stable_sort(all.begin(), all.end(), [](const Pt &a, const Pt &b) { return a.y < b.y; });
+    std::vector<Pt> out;
+    for (size_t i = 0; i < all.size();) {
+        size_t j = i;
+        float lo = all[i].x, hi = all[i].x;
+        for (; j < all.size() && all[j].y == all[i].y; j++) lo = std::min(lo, all[j].x), hi = std::max(hi, all[j].x);
+        out.push_back({lo, all[i].y});
+        if (hi != lo) out.push_back({hi, all[i].y});
+        i = j;
     }
+    return out;
+}
+
+// fn(i) for i in [0, n) on `threads` threads (the caller's included), contiguous chunks.
+template <class F> void parallel_for(int n, int threads, F fn) {
+    threads = std::max(1, std::min(threads, n));
+    if (threads == 1) {
+        for (int i = 0; i < n; i++) fn(i);
+        return;
+    }
+    std::vector<std::thread> th;
+    auto chunk = [&](int t) {
+        for (int i = int(long(n) * t / threads); i < int(long(n) * (t + 1) / threads); i++) fn(i);
+    };
+    for (int t = 1; t < threads; t++) th.emplace_back(chunk, t);
+    chunk(0);
+    for (auto &t : th) t.join();
+}
+
+}  // namespace
+
+// Every 8-connected component of a bit mask (h rows of ceil(w / 32) words) as its rows'
+// leftmost and rightmost pixels, rows ascending, in order of its first run (row-major). With
+// several threads the rows are cut into bands labelled on their own, then the components that
+// meet across a cut are joined (the same components, in the same order).
+static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w, int h, int threads = 1) {
+    const int bands = std::max(1, std::min(threads, h / 64));
+    if (bands == 1) return band_components(bits, w, 0, h).pts;
+    std::vector<BandComps> B(static_cast<size_t>(bands));
+    parallel_for(bands, bands, [&](int b) {
+        B[size_t(b)] = band_components(bits, w, int(long(h) * b / bands), int(long(h) * (b + 1) / bands));
+    });
+    std::vector<int> off(static_cast<size_t>(bands) + 1, 0);
+    for (int b = 0; b < bands; b++) off[size_t(b) + 1] = off[size_t(b)] + int(B[size_t(b)].pts.size());
+    std::vector<int> parent(static_cast<size_t>(off[size_t(bands)]));
+    std::iota(parent.begin(), parent.end(), 0);
+    for (int b = 0; b + 1 < bands; b++) {
+        const BandComps &A = B[size_t(b)], &C = B[size_t(b) + 1];
+        size_t i = 0, j = 0;
+        while (i < A.last.size() && j < C.first.size()) {
+            const Run &a = A.last[i], &c = C.first[j];
+            if (a.x1 + 1 >= c.x0 && c.x1 + 1 >= a.x0) {
+                int ra = find(parent, off[size_t(b)] + A.last_c[i]), rc = find(parent, off[size_t(b) + 1] + C.first_c[j]);
+                if (ra != rc) parent[size_t(std::max(ra, rc))] = std::min(ra, rc);
+            }
+            if (a.x1 < c.x1) i++;
+            else j++;
+        }
+    }
+    std::vector<int> gid(parent.size(), -1);
+    std::vector<std::vector<int>> members;
+    for (int k = 0; k < int(parent.size()); k++) {
+        const int root = find(parent, k);
+        if (gid[size_t(root)] < 0) {
+            gid[size_t(root)] = int(members.size());
+            members.emplace_back();
+        }
+        members[size_t(gid[size_t(root)])].push_back(k);
+    }
+    std::vector<std::vector<Pt>> out(members.size());
+    auto local = [&](int k) -> std::vector<Pt> & {
+        const int b = int(std::upper_bound(off.begin(), off.end(), k) - off.begin()) - 1;
+        return B[size_t(b)].pts[size_t(k - off[size_t(b)])];
+    };
+    for (size_t m = 0; m < members.size(); m++) {
+        if (members[m].size() == 1) {
+            out[m] = std::move(local(members[m][0]));
+            continue;
+        }
+        std::vector<Pt> all;
+        for (int k : members[m]) all.insert(all.end(), local(k).begin(), local(k).end());
+        out[m] = merge_rows(std::move(all));
+    }
+    return out;
+}
+
+std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area, int threads) {
+    const auto comps = component_points(bits, w, h, threads);
+    std::vector<RRect> rects(comps.size());
+    parallel_for(int(comps.size()), threads, [&](int i) {
+        rects[size_t(i)] = min_area_rect(hull_rows(comps[size_t(i)]));
+        rects[size_t(i)].resize(rects[size_t(i)].w + 2 * expand, rects[size_t(i)].h + 2 * expand);
+    });
+    std::vector<RRect> out;
+    for (const RRect &r : rects)
+        if (r.area() >= min_area) out.push_back(r);
     return out;
 }
 

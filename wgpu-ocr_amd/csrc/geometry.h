@@ -25,8 +25,9 @@ struct RRect {
 
 // word_rects (ocr-bench.rs:40-60): 8-connected components of the mask (h rows of ceil(w/32)
 // words), each component's minimum-area rectangle over its pixels, grown by `expand` on every
-// side, kept when its area is at least min_area.
-std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand = 3.f, float min_area = 100.f);
+// side, kept when its area is at least min_area; on `threads` threads (the same result).
+std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand = 3.f, float min_area = 100.f,
+                              int threads = 1);
 
 // Text lines from words, left to right within a line, lines top to bottom (the role of ocrs'
 // find_text_lines, ocr-bench.rs:516).

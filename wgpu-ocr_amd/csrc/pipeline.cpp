@@ -16,18 +16,26 @@
 
 namespace ocr {
 
-PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend) {
+PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads) {
     PageLayout L;
-    std::vector<RRect> words = word_rects(bits, w, h);
+    std::vector<RRect> words = word_rects(bits, w, h, 3.f, 100.f, threads);
     L.words = int(words.size());
     auto lines = find_text_lines(words);
     pad_lines(lines, relv, relend);
+    lines.erase(std::remove_if(lines.begin(), lines.end(), [](const std::vector<RRect> &l) { return l.empty(); }),
+                lines.end());
+    L.lines.resize(lines.size());
+    const int nt = std::max(1, std::min(threads, int(lines.size())));
+    std::vector<std::thread> th;
+    auto chunk = [&](int t) {
+        for (size_t i = lines.size() * size_t(t) / size_t(nt); i < lines.size() * size_t(t + 1) / size_t(nt); i++)
+            L.lines[i] = line_geometry(lines[i]);
+    };
+    for (int t = 1; t < nt; t++) th.emplace_back(chunk, t);
+    chunk(0);
+    for (auto &t : th) t.join();
     std::vector<int> out_w;
-    for (const auto &line : lines) {
-        if (line.empty()) continue;
-        L.lines.push_back(line_geometry(line));
-        out_w.push_back(L.lines.back().out_w);
-    }
+    for (const LineGeom &g : L.lines) out_w.push_back(g.out_w);
     L.plan = plan_batches(out_w);
     return L;
 }
@@ -40,8 +48,12 @@ struct Pipeline::Impl {
     PipelineOpts opts;
     Workers workers;
     std::vector<Pinned> bits_host, best_host;
+    // Threads one page's layout uses (its word boxes in row bands, its lines side by side): the
+    // host cores shared by the pages of a detection pass.
+    int layout_threads;
     explicit Impl(Ctx &c, Detector &d, Recognizer &r, const PipelineOpts &o, int nthreads)
-        : ctx(c), det(d), rec(r), opts(o), workers(nthreads) {}
+        : ctx(c), det(d), rec(r), opts(o), workers(nthreads),
+          layout_threads(std::max(1, std::min(4, (int(std::thread::hardware_concurrency()) + o.det_batch - 1) / std::max(1, o.det_batch)))) {}
 };
 
 Pipeline::Pipeline(Ctx &ctx, Detector &det, Recognizer &rec, const PipelineOpts &opts)
@@ -152,7 +164,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
                 OCR_HIP(hipEventSynchronize(ev));
                 mark("layout " + std::to_string(p) + " start");
                 const auto tc = Clock::now();
-                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend);
+                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, I.layout_threads);
                 busy = ms_since(tc);
                 mark("layout " + std::to_string(p) + " done");
                 std::lock_guard<std::mutex> lk(mu);

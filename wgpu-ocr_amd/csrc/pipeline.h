@@ -38,7 +38,7 @@ struct PageLayout {
     std::vector<LineGeom> lines;
     BatchPlan plan;
 };
-PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend);
+PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads = 1);
 
 class Pipeline {
   public:

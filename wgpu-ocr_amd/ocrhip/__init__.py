@@ -59,6 +59,7 @@ SIGNATURES = {
     "ocr_probe_start": (ctypes.c_int, [ctypes.c_char_p]),
     "ocr_probe_stop": (ctypes.c_int, [ctypes.c_char_p, PU32, P, P, P]),
     "ocr_word_rects": (ctypes.c_int, [P, U32, U32, P, U32, PU32]),
+    "ocr_word_rects_mt": (ctypes.c_int, [P, U32, U32, U32, P, U32, PU32]),
     "ocr_layout_page": (P, [P, U32, U32, F32, F32]),
     "ocr_layout_free": (None, [P]),
     "ocr_layout_counts": (ctypes.c_int, [P, PU32, PU32, PU32]),
@@ -405,14 +406,15 @@ def probe_stop(family: str) -> dict:
 
 
 # ---- host geometry (no GPU) -----------------------------------------------------------------
-def word_rects(bits: np.ndarray, w: int):
-    """Words of a page mask (ocr-bench.rs:40-60) as an [n, 6] array (cx, cy, ux, uy, w, h)."""
+def word_rects(bits: np.ndarray, w: int, threads: int = 1):
+    """Words of a page mask (ocr-bench.rs:40-60) as an [n, 6] array (cx, cy, ux, uy, w, h),
+    computed on `threads` host threads."""
     bits = np.ascontiguousarray(bits, np.uint32)
     h = bits.shape[0]
     count = ctypes.c_uint32()
-    _check(lib().ocr_word_rects(_ptr(bits), w, h, None, 0, ctypes.byref(count)))
+    _check(lib().ocr_word_rects_mt(_ptr(bits), w, h, threads, None, 0, ctypes.byref(count)))
     out = np.zeros((count.value, 6), np.float32)
-    _check(lib().ocr_word_rects(_ptr(bits), w, h, _ptr(out), count.value, ctypes.byref(count)))
+    _check(lib().ocr_word_rects_mt(_ptr(bits), w, h, threads, _ptr(out), count.value, ctypes.byref(count)))
     return out
 
 
