@@ -98,8 +98,8 @@ def pp_pipeline(ctx, d_pages, ws, hs, merge, steps=2):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--pages", type=int, default=12)
     ap.add_argument("--merge", type=int, default=6)
     ap.add_argument("--det-batch", type=int, default=6, help="pages per detection pass")

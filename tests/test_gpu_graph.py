@@ -106,6 +106,23 @@ def test_direct_conv_matrix_cores(ctx, tmp_path, cout, act, pool):
     check(ctx, p, RNG.uniform(-0.5, 0.5, (2, 1, 50, 131)).astype(np.float32))
 
 
+def test_direct_conv_full_and_pooled_outputs(ctx, tmp_path):
+    # e0 read by a 2 x 2 MaxPool and a Concat (16-aligned channel slice): one pass writes the
+    # full output into the Concat and the pooled one (the detector's first level).
+    def net(g, x):
+        e0 = conv(g, x, 1, 16, act="Relu")
+        p0 = g.add("MaxPool", [e0], kernel_shape=[2, 2], strides=[2, 2])
+        e1 = conv(g, p0, 16, 16, act="Relu")
+        wt = f16x(RNG.standard_normal((16, 16, 2, 2)).astype(np.float32) * 0.25)
+        u = g.add("ConvTranspose", [e1, g.init("ut", wt), g.init("ub", np.zeros(16, np.float32) + 0.05)],
+                  kernel_shape=[2, 2], strides=[2, 2])
+        u = g.add("Relu", [u])
+        c = g.add("Concat", [u, e0], axis=1)
+        return conv(g, c, 32, 8, act="Relu")
+    p = build(tmp_path, "fp", net, (2, 1, 40, 52))
+    check(ctx, p, RNG.uniform(-0.5, 0.5, (2, 1, 40, 52)).astype(np.float32))
+
+
 def test_direct_conv_two_readers_and_concat(ctx, tmp_path):
     # e0 is read by a MaxPool and a Concat (no fusion); the Concat takes the ConvTranspose output
     # and the skip in its channel range, plus the graph input (a copy, not an alias).

@@ -101,12 +101,17 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     const Node &nx = nodes[i + 1];
                     auto k = nx.ints("kernel_shape");
                     auto ks = nx.ints("strides");
-                    if (nx.op == "MaxPool" && nx.inputs.at(0) == s.output && onnx.readers(s.output) == 1 && k &&
+                    const int rd = onnx.readers(s.output);
+                    if (nx.op == "MaxPool" && nx.inputs.at(0) == s.output && (rd == 1 || rd == 2) && k &&
                         k->size() == 2 && (!ks || *ks == *k) && symmetric(nx, "pads", 0) == 0 &&
-                        nx.int_("ceil_mode").value_or(0) == 0) {
+                        nx.int_("ceil_mode").value_or(0) == 0 && (rd == 1 || ((*k)[0] == 2 && (*k)[1] == 2)) &&
+                        s.output != onnx.output) {
                         s.ph = int((*k)[0]);
                         s.pw = int((*k)[1]);
-                        s.output = nx.outputs.at(0);
+                        // The only reader: the pooled value replaces the output. Two readers (a 2 x 2
+                        // pool): both are written, the pooled one as pool_output.
+                        if (rd == 1) s.output = nx.outputs.at(0);
+                        else s.pool_output = nx.outputs.at(0);
                         i++;
                     }
                 }
@@ -310,7 +315,13 @@ std::vector<Shape> Graph::shapes(const Shape &in) const {
             if (c != 1) fail("direct conv takes one channel");
             const int ch = h + 2 * s.pt - s.kh + 1, cw = w + 2 * s.pt - s.kw + 1;
             if (ch < 1 || cw < 1) fail("Conv input smaller than its kernel");
-            o = {n, ch / s.ph, cw / s.pw, s.cout};
+            if (s.pool_output.empty()) {
+                o = {n, ch / s.ph, cw / s.pw, s.cout};
+            } else {
+                o = {n, ch, cw, s.cout};
+                if (ch / s.ph < 1 || cw / s.pw < 1) fail("empty output shape");
+                sh[s.pool_output] = Shape{n, ch / s.ph, cw / s.pw, s.cout};
+            }
             break;
         }
         case OpKind::ConvT:
@@ -466,7 +477,19 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
         }
         case OpKind::Direct:
             y = out_view(i);
-            conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st, s.w1frag);
+            if (s.pool_output.empty()) {
+                conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st, s.w1frag);
+            } else {
+                // Full output and its 2 x 2 pool: in one pass on the matrix cores, else the conv
+                // and then the pool.
+                const Act yp = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
+                view[s.pool_output] = yp;
+                if (!(s.w1frag && s.kh == 3 && s.kw == 3 && s.pt == 1 &&
+                      conv1_mfma(a, y, s.w1frag, s.b, s.act, s.ph, s.pw, st, &yp))) {
+                    conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, 1, 1, st, s.w1frag);
+                    maxpool(y, yp, s.ph, s.pw, st);
+                }
+            }
             break;
         case OpKind::ConvT:
             y = out_view(i);

@@ -88,8 +88,9 @@ void conv_direct(const Act &x, const Act &y, const float *w, const float *b, int
 // (a multiple of 16), float16-exact weights packed by pack_conv1_frags ([cout][9] float32 in,
 // cout / 16 KiB of fragments out), no pool or a 2 x 2 one. Returns false for anything else.
 void pack_conv1_frags(const float *w, int cout, uint16_t *frag);
+// With ypool (2 x 2 pool, full-size y) both outputs are written.
 bool conv1_mfma(const Act &x, const Act &y, const uint16_t *frag, const float *b, int act, int ph, int pw,
-                hipStream_t s);
+                hipStream_t s, const Act *ypool = nullptr);
 // ConvTranspose gather form (gpu.rs:424-460); w re-laid out as [ky][kx][cin][cout].
 void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride,
                     int act, hipStream_t s);

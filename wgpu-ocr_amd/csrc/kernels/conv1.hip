@@ -44,9 +44,12 @@ __device__ inline float act1(float v, int act) {
 __device__ inline float xor1(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false)); }
 __device__ inline float xor2(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false)); }
 
+// POOL 0: the output y only; 1: the 2 x 2 pooled output only (in y); 2: both, the full output in
+// y and the pooled one in yp.
 template <int NT, int POOL>
 __global__ __launch_bounds__(256) void conv1_kernel(const float *__restrict__ x, int h, int w, int xcs,
                                                     float *__restrict__ y, int oh, int ow, int ycs,
+                                                    float *__restrict__ yp, int poh, int pow_, int ypcs,
                                                     const half8 *__restrict__ wf, const float *__restrict__ bias,
                                                     int act, int tiles_x) {
     __shared__ _Float16 s_in[2 * PLANE];  // hi plane, then lo plane
@@ -96,6 +99,9 @@ __global__ __launch_bounds__(256) void conv1_kernel(const float *__restrict__ x,
             const floatx4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             float v[4] = {act1(acc[0] + b4[j].x, act), act1(acc[1] + b4[j].y, act), act1(acc[2] + b4[j].z, act),
                           act1(acc[3] + b4[j].w, act)};
+            if (POOL != 1 && oy < oh && ox < ow)
+                *reinterpret_cast<float4 *>(y + ((size_t(img) * oh + oy) * ow + ox) * ycs + j * 16 + 4 * g) =
+                    make_float4(v[0], v[1], v[2], v[3]);
             if (POOL) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -103,12 +109,9 @@ __global__ __launch_bounds__(256) void conv1_kernel(const float *__restrict__ x,
                     v[e] = fmaxf(v[e], xor2(v[e]));
                 }
                 const int qy = oy >> 1, qx = ox >> 1;
-                if (q == 0 && qy < oh && qx < ow)
-                    *reinterpret_cast<float4 *>(y + ((size_t(img) * oh + qy) * ow + qx) * ycs + j * 16 + 4 * g) =
+                if (q == 0 && qy < poh && qx < pow_)
+                    *reinterpret_cast<float4 *>(yp + ((size_t(img) * poh + qy) * pow_ + qx) * ypcs + j * 16 + 4 * g) =
                         make_float4(v[0], v[1], v[2], v[3]);
-            } else if (oy < oh && ox < ow) {
-                *reinterpret_cast<float4 *>(y + ((size_t(img) * oh + oy) * ow + ox) * ycs + j * 16 + 4 * g) =
-                    make_float4(v[0], v[1], v[2], v[3]);
             }
         }
     }
@@ -130,33 +133,46 @@ void pack_conv1_frags(const float *w, int cout, uint16_t *frag) {
 }
 
 bool conv1_mfma(const Act &x, const Act &y, const uint16_t *frag, const float *b, int act, int ph, int pw,
-                hipStream_t s) {
+                hipStream_t s, const Act *ypool) {
     if (!frag || x.c != 1 || y.c % 16 || y.c > 64 || y.c < 16 || y.n != x.n) return false;
     if (act != ACT_NONE && act != ACT_RELU && act != ACT_SIGMOID) return false;
-    const int pool = (ph == 2 && pw == 2) ? 1 : (ph == 1 && pw == 1) ? 0 : -1;
-    if (pool < 0) return false;
-    if (y.h != x.h / ph || y.w != x.w / pw) return false;
-    if (y.cs % 4 || (reinterpret_cast<uintptr_t>(y.p) & 15) || (b && (reinterpret_cast<uintptr_t>(b) & 15))) return false;
+    auto aligned = [](const Act &a) { return a.cs % 4 == 0 && (reinterpret_cast<uintptr_t>(a.p) & 15) == 0; };
+    int pool;
+    if (ypool) {
+        if (ph != 2 || pw != 2 || y.h != x.h || y.w != x.w || ypool->h != x.h / 2 || ypool->w != x.w / 2 ||
+            ypool->c != y.c || ypool->n != y.n || !aligned(*ypool))
+            return false;
+        pool = 2;
+    } else {
+        pool = (ph == 2 && pw == 2) ? 1 : (ph == 1 && pw == 1) ? 0 : -1;
+        if (pool < 0 || y.h != x.h / ph || y.w != x.w / pw) return false;
+    }
+    if (!aligned(y) || (b && (reinterpret_cast<uintptr_t>(b) & 15))) return false;
     const int tiles_x = (x.w + TX - 1) / TX, tiles_y = (x.h + TY - 1) / TY;
     if (double(tiles_x) * tiles_y > 2147483647.0 || y.n > 65535) return false;
     dim3 grid(unsigned(tiles_x * tiles_y), unsigned(y.n));
-    ProbeScope probe("conv_direct", s, 2.0 * double(x.pixels()) * y.c * 9, 4.0 * double(x.pixels() + y.count()));
+    ProbeScope probe("conv_direct", s, 2.0 * double(x.pixels()) * y.c * 9,
+                     4.0 * double(x.pixels() + y.count() + (ypool ? ypool->count() : 0)));
     const half8 *wf = reinterpret_cast<const half8 *>(frag);
+    // POOL 1 writes the pooled output through (yp, poh, pow_, ypcs) = y.
+    const Act &yp = ypool ? *ypool : y;
 #define C1_LAUNCH(NT, P)                                                                                              \
-    hipLaunchKernelGGL((conv1_kernel<NT, P>), grid, dim3(256), 0, s, x.p, x.h, x.w, x.cs, y.p, y.h, y.w, y.cs, wf, b, \
-                       act, tiles_x)
+    hipLaunchKernelGGL((conv1_kernel<NT, P>), grid, dim3(256), 0, s, x.p, x.h, x.w, x.cs, y.p, y.h, y.w, y.cs, yp.p,  \
+                       yp.h, yp.w, yp.cs, wf, b, act, tiles_x)
+#define C1_NT(P)                  \
+    if (nt == 1) C1_LAUNCH(1, P);  \
+    else if (nt == 2) C1_LAUNCH(2, P); \
+    else if (nt == 3) C1_LAUNCH(3, P); \
+    else C1_LAUNCH(4, P)
     const int nt = y.c / 16;
-    if (pool) {
-        if (nt == 1) C1_LAUNCH(1, 1);
-        else if (nt == 2) C1_LAUNCH(2, 1);
-        else if (nt == 3) C1_LAUNCH(3, 1);
-        else C1_LAUNCH(4, 1);
+    if (pool == 2) {
+        C1_NT(2);
+    } else if (pool == 1) {
+        C1_NT(1);
     } else {
-        if (nt == 1) C1_LAUNCH(1, 0);
-        else if (nt == 2) C1_LAUNCH(2, 0);
-        else if (nt == 3) C1_LAUNCH(3, 0);
-        else C1_LAUNCH(4, 0);
+        C1_NT(0);
     }
+#undef C1_NT
 #undef C1_LAUNCH
     OCR_HIP(hipGetLastError());
     return true;

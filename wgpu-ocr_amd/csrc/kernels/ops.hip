@@ -198,33 +198,41 @@ __global__ void grey_resize_kernel(const uint8_t *rgb, int w, int h, int pw, int
     y[i] = mixf(top, bot, wy);
 }
 
-// ---- mask_up (gpu.rs:563-593): one thread per page pixel, a wavefront per 64 pixels of a row --
-// (two bit words, assembled with a ballot).
+// ---- mask_up (gpu.rs:563-593): a wavefront per 64 columns of MR rows (two bit words a row,
+// assembled with a ballot); a thread walks its column down the rows, so a wavefront's loads of
+// neighbouring rows (which share source rows) are in flight together.
+constexpr int MR = 8;
 __global__ void mask_up_kernel(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, int words,
                                float sx, float sy, float thr) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const long wv = (long(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-    const int pairs = (words + 1) / 2;
-    if (wv >= long(pairs) * h) return;  // the whole wavefront
-    const int oy = int(wv / pairs), wp = int(wv - long(oy) * pairs);
+    const int pairs = (words + 1) / 2, groups = (h + MR - 1) / MR;
+    if (wv >= long(pairs) * groups) return;  // the whole wavefront
+    const int rg = int(wv / pairs), wp = int(wv - long(rg) * pairs);
     const int ox = wp * 64 + lane;
-    bool on = false;
-    if (ox < w) {
-        const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(mh) - 1.f);
-        const int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
-        const float fy = iy - float(y1);
-        const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(mw) - 1.f);
-        const int x1 = int(ix), x2 = min(x1 + 1, mw - 1);
-        const float fx = ix - float(x1);
-        const float top = mixf(m[size_t(y1) * stride + x1], m[size_t(y1) * stride + x2], fx);
-        const float bot = mixf(m[size_t(y2) * stride + x1], m[size_t(y2) * stride + x2], fx);
-        on = mixf(top, bot, fy) > thr;
+    const bool col = ox < w;
+    const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(mw) - 1.f);
+    const int x1 = int(ix), x2 = min(x1 + 1, mw - 1);
+    const float fx = ix - float(x1);
+#pragma unroll
+    for (int k = 0; k < MR; k++) {
+        const int oy = rg * MR + k;
+        if (oy >= h) break;
+        bool on = false;
+        if (col) {
+            const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(mh) - 1.f);
+            const int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
+            const float fy = iy - float(y1);
+            const float top = mixf(m[size_t(y1) * stride + x1], m[size_t(y1) * stride + x2], fx);
+            const float bot = mixf(m[size_t(y2) * stride + x1], m[size_t(y2) * stride + x2], fx);
+            on = mixf(top, bot, fy) > thr;
+        }
+        const unsigned long long b = __ballot(on);
+        uint32_t *row = bits + size_t(oy) * words;
+        if (lane == 0) row[2 * wp] = uint32_t(b);
+        if (lane == 1 && 2 * wp + 1 < words) row[2 * wp + 1] = uint32_t(b >> 32);
     }
-    const unsigned long long b = __ballot(on);
-    uint32_t *row = bits + size_t(oy) * words;
-    if (lane == 0) row[2 * wp] = uint32_t(b);
-    if (lane == 1 && 2 * wp + 1 < words) row[2 * wp + 1] = uint32_t(b >> 32);
 }
 
 // ---- avgpool_t (gpu.rs:595-614): [n][kh][T][c] -> X[t][ntot][c] at line offset noff ----------
@@ -342,8 +350,8 @@ void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, 
              hipStream_t s) {
     int words = (w + 31) / 32;
     ProbeScope probe("mask_up", s, 0, 4.0 * double(mw) * mh + 4.0 * double(words) * h);
-    hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t((words + 1) / 2) * h * 64)), dim3(256), 0, s, m, stride,
-                       mw, mh, bits, w, h, words, sx, sy, thr);
+    hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t((words + 1) / 2) * ((h + MR - 1) / MR) * 64)), dim3(256),
+                       0, s, m, stride, mw, mh, bits, w, h, words, sx, sy, thr);
     OCR_HIP(hipGetLastError());
 }
 
