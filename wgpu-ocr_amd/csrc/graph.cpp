@@ -160,6 +160,11 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     std::vector<uint16_t> frag(s.pk.halves());
                     pack_conv_frags(s.pk, hi.data(), frag.data());
                     s.wfrag = ctx.upload_weights(frag.data(), frag.size());
+                    // A 1 x 1 conv to a few channels (a head) also keeps float32 weights for the
+                    // bandwidth-bound kernel.
+                    if (kh == 1 && kw == 1 && cout <= 4 && cin_g % 4 == 0 && s.pt == 0 && s.pl == 0 && s.pb == 0 &&
+                        s.pr == 0 && s.sh == 1 && s.sw == 1)
+                        s.w = ctx.upload_weights(w.data.data(), w.data.size());
                 } else {
                     s.w = ctx.upload_weights(w.data.data(), w.data.size());
                 }
@@ -446,7 +451,10 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
         switch (s.kind) {
         case OpKind::Conv: {
             y = out_view(i);
-            if (s.mfma) {
+            if (s.mfma && s.w && !s.pool_only && s.pool_output.empty() && a.cs % 4 == 0 &&
+                (reinterpret_cast<uintptr_t>(a.p) & 15) == 0) {
+                conv1x1_narrow(a, y, s.w, s.b, s.act, st);
+            } else if (s.mfma) {
                 ConvArgs ca;
                 ca.x = a;
                 ca.y = y;

@@ -71,10 +71,13 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s);
 // least four 32-wide input chunks, float16-exact weights with wt_frag, bias + ReLU / Sigmoid.
 // Returns false (and launches nothing) for anything else.
 bool gemm_dma(const ConvArgs &a, hipStream_t s);
-// 3 x 3, pad 1, NHWC, more than 32 output channels, float16-exact weights with wt_frag, bias +
+// 3 x 3, pad 1, NHWC, float16-exact weights with wt_frag, bias +
 // ReLU / Sigmoid, optional 2 x 2 / 2 x 1 MaxPool (kernels/conv3.hip): operands fed by LDS DMA.
 // Returns false (and launches nothing) for anything else.
 bool conv3x3_dma(const ConvArgs &a, hipStream_t s);
+// 1 x 1 convolution to at most 4 output channels (a detector head) in float32 on the vector ALU:
+// bandwidth-bound, one thread a pixel (kernels/ops.hip). w [cout][cin] float32.
+void conv1x1_narrow(const Act &x, const Act &y, const float *w, const float *b, int act, hipStream_t s);
 
 // ---- Everything else (kernels/ops.hip) ----------------------------------------------------
 // Any conv (grouped, strided) in float32, one thread per output: the fallback path.

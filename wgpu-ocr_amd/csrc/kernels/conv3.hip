@@ -1,5 +1,5 @@
-// 3 x 3 stride-1 convolution (NHWC float32 activations, float16-exact weights, more than 32
-// output channels) on the gfx950 matrix cores with the operands fed by the LDS DMA path: the hot
+// 3 x 3 stride-1 convolution (NHWC float32 activations, float16-exact weights) on the gfx950
+// matrix cores with the operands fed by the LDS DMA path: the hot
 // path of the recogniser trunk and the detector's deeper layers. Semantics of the reference's
 // conv / conv_fast / conv128 programs (src/gpu.rs:37-350): y = act(sum x * w + b[c]), then an
 // optional 2 x 2 or 2 x 1 MaxPool of the activated output (gpu.rs:462-482).
@@ -382,7 +382,7 @@ bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
     if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res || a.rows || !pk.exact) return false;
     if (pk.kh != 3 || pk.kw != 3 || a.pt != 1 || a.pl != 1 || pk.cin != a.x.c || pk.cout != a.y.c) return false;
     if (a.y.n != a.x.n || a.y.h != a.x.h || a.y.w != a.x.w || a.y_px || a.y_row || a.y_img) return false;
-    if (a.x.c % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15) || a.y.c <= 32) return false;
+    if (a.x.c % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15)) return false;
     if (a.act != ACT_NONE && a.act != ACT_RELU && a.act != ACT_SIGMOID) return false;
     // 32-bit offsets within one image of the input, the output and the pooled output.
     if (double(a.x.h) * a.x.w * a.x.cs >= 2147483647.0 || double(a.y.h) * a.y.w * a.y.cs >= 2147483647.0) return false;
@@ -395,7 +395,7 @@ bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
         if (a.ypool.h != a.y.h / a.ph || a.ypool.w != a.y.w / a.pw || a.ypool.c != a.y.c || a.ypool.n != a.y.n)
             fail("conv3x3_dma: pooled output shape");
     }
-    const int cout = a.y.c, nt = cout > 64 ? 4 : 2, bn = 32 * nt;
+    const int cout = a.y.c, nt = cout > 64 ? 4 : cout > 32 ? 2 : 1, bn = 32 * nt;
     C3Params p{};
     p.x = a.x.p;
     p.n = a.x.n;
@@ -447,7 +447,8 @@ bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
     auto launch = [&](auto ACTc) {
         constexpr int A = decltype(ACTc)::value;
         if (nt == 4) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 4, A>), dim3(unsigned(grid)), dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 2, A>), dim3(unsigned(grid)), dim3(512), 0, s, p);
+        else if (nt == 2) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 2, A>), dim3(unsigned(grid)), dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 1, A>), dim3(unsigned(grid)), dim3(512), 0, s, p);
     };
     if (a.act == ACT_RELU) launch(std::integral_constant<int, ACT_RELU>{});
     else if (a.act == ACT_SIGMOID) launch(std::integral_constant<int, ACT_SIGMOID>{});

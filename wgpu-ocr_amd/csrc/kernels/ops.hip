@@ -235,6 +235,32 @@ __global__ void mask_up_kernel(const float *m, int stride, int mw, int mh, uint3
     }
 }
 
+// ---- 1 x 1 convolution to CO <= 4 channels (gpu.rs:37-350 for this shape): one thread a pixel,
+// the input channels in float4 loads, float32 products summed in channel order.
+template <int CO>
+__global__ void conv1x1_narrow_kernel(const float *__restrict__ x, long pixels, int cin, int xcs, float *__restrict__ y,
+                                      int ycs, const float *__restrict__ w, const float *__restrict__ b, int act) {
+    const long p = long(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= pixels) return;
+    const float4 *xp = reinterpret_cast<const float4 *>(x + size_t(p) * xcs);
+    float acc[CO];
+#pragma unroll
+    for (int c = 0; c < CO; c++) acc[c] = 0.f;
+    for (int k = 0; k < cin / 4; k++) {
+        const float4 v = xp[k];
+#pragma unroll
+        for (int c = 0; c < CO; c++) {
+            const float *wc = w + c * cin + 4 * k;
+            acc[c] = fmaf(v.x, wc[0], acc[c]);
+            acc[c] = fmaf(v.y, wc[1], acc[c]);
+            acc[c] = fmaf(v.z, wc[2], acc[c]);
+            acc[c] = fmaf(v.w, wc[3], acc[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CO; c++) y[size_t(p) * ycs + c] = act_f(acc[c] + (b ? b[c] : 0.f), act);
+}
+
 // ---- avgpool_t (gpu.rs:595-614): [n][kh][T][c] -> X[t][ntot][c] at line offset noff ----------
 __global__ void avgpool_t_kernel(const float *x, int n, int h, int kh, int T, int c, int xcs, float *X, int ntot,
                                  int noff) {
@@ -352,6 +378,20 @@ void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, 
     ProbeScope probe("mask_up", s, 0, 4.0 * double(mw) * mh + 4.0 * double(words) * h);
     hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t((words + 1) / 2) * ((h + MR - 1) / MR) * 64)), dim3(256),
                        0, s, m, stride, mw, mh, bits, w, h, words, sx, sy, thr);
+    OCR_HIP(hipGetLastError());
+}
+
+void conv1x1_narrow(const Act &x, const Act &y, const float *w, const float *b, int act, hipStream_t s) {
+    if (y.c < 1 || y.c > 4 || x.c % 4 || x.cs % 4 || (reinterpret_cast<uintptr_t>(x.p) & 15) || x.n != y.n ||
+        x.h != y.h || x.w != y.w)
+        fail("conv1x1_narrow: shape");
+    const long pixels = long(x.n) * x.h * x.w;
+    ProbeScope probe("conv_narrow", s, 2.0 * double(pixels) * x.c * y.c, 4.0 * double(pixels) * (x.c + y.c));
+    const dim3 grid(blocks_for(size_t(pixels))), blk(256);
+    if (y.c == 1) hipLaunchKernelGGL((conv1x1_narrow_kernel<1>), grid, blk, 0, s, x.p, pixels, x.c, x.cs, y.p, y.cs, w, b, act);
+    else if (y.c == 2) hipLaunchKernelGGL((conv1x1_narrow_kernel<2>), grid, blk, 0, s, x.p, pixels, x.c, x.cs, y.p, y.cs, w, b, act);
+    else if (y.c == 3) hipLaunchKernelGGL((conv1x1_narrow_kernel<3>), grid, blk, 0, s, x.p, pixels, x.c, x.cs, y.p, y.cs, w, b, act);
+    else hipLaunchKernelGGL((conv1x1_narrow_kernel<4>), grid, blk, 0, s, x.p, pixels, x.c, x.cs, y.p, y.cs, w, b, act);
     OCR_HIP(hipGetLastError());
 }
 

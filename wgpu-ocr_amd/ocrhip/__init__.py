@@ -386,9 +386,9 @@ class Recognizer:
             pass
 
 
-FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_igemm", "conv_mfma", "gru", "conv_transpose", "conv_direct", "conv_generic", "maxpool", "mask_up",
+FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_narrow", "conv_igemm", "conv_mfma", "gru", "conv_transpose", "conv_direct", "conv_generic", "maxpool", "mask_up",
             "grey_resize", "line_crop", "avgpool_t", "argmax", "copy")
-ND_FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_igemm", "conv_mfma", "nd_bgemm", "nd_conv_generic", "nd_conv_transpose", "nd_elementwise", "nd_copy",
+ND_FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_narrow", "conv_igemm", "conv_mfma", "nd_bgemm", "nd_conv_generic", "nd_conv_transpose", "nd_elementwise", "nd_copy",
                "nd_reduce", "nd_layer_norm", "nd_softmax", "nd_argmax", "nd_pool", "nd_resize", "nd_det_prep",
                "nd_threshold")
 
