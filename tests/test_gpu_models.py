@@ -61,6 +61,28 @@ def test_recognition_edge_shapes(recognizer, rec_oracle):
     check_recognition(recognizer, rec_oracle, batches, [8, 37, 37, 37] + [203] * 9)
 
 
+def test_recognition_batches_together_match_separate(recognizer):
+    # The trunk layers of a pass run once over all width batches (more batches than one launch
+    # takes, widths from 8 to 301, one to three lines each): every line's logits are the same
+    # bits as when its batch is recognised alone.
+    rng = np.random.Generator(np.random.PCG64(21))
+    batches = []
+    for i in range(35):
+        w = int(rng.integers(8, 302))
+        n = 1 + i % 3
+        batches.append((rng.uniform(-0.5, 0.5, (n, 64, w)).astype(np.float32), n, w))
+    print(f"recognize {len(batches)} batches together", flush=True)
+    logits, lens, best = recognizer.recognize(batches)
+    k0 = 0
+    for d, n, w in batches:
+        one, lens1, best1 = recognizer.recognize([(d, n, w)])
+        T = int(lens1[0])
+        assert np.all(lens[k0: k0 + n] == T)
+        assert np.array_equal(logits[:T, k0: k0 + n], one[:T]), (n, w)
+        assert np.array_equal(best[:T, k0: k0 + n], best1[:T])
+        k0 += n
+
+
 def test_recognition_empty_batch_is_an_error(recognizer):
     import ocrhip
     with pytest.raises(ocrhip.OcrError):

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <map>
+#include <memory>
 #include <set>
 
 namespace ocr {
@@ -380,199 +381,230 @@ Shape Graph::infer(const Shape &in) const {
     fail("graph output " + output + " not computed");
 }
 
-Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
-    const std::vector<Shape> shp = shapes({x.n, x.h, x.w, x.c});
-    const hipStream_t st = ctx.stream();
-    // Last reader of every value, and the Concat each value is written into (if any).
-    std::map<std::string, size_t> last;
+// One input's walk through the steps: shapes, liveness, views and buffers.
+struct Graph::Exec {
+    const Graph &g;
+    Ctx &ctx;
+    hipStream_t st;
+    Act x;
+    std::vector<Shape> shp;
+    std::map<std::string, size_t> last;                  // last reader of every value
     std::map<std::string, std::pair<size_t, int>> into;  // value -> (concat step, channel offset)
-    std::set<std::string> produced;
-    for (size_t i = 0; i < steps.size(); i++) {
-        for (const std::string &nm : steps[i].inputs) last[nm] = i;
-        if (steps[i].kind != OpKind::Identity) produced.insert(steps[i].output);
-        if (!steps[i].pool_output.empty()) produced.insert(steps[i].pool_output);
-    }
-    for (size_t i = 0; i < steps.size(); i++) {
-        const Step &s = steps[i];
-        if (s.kind != OpKind::Concat) continue;
-        int off = 0;
-        for (const std::string &nm : s.inputs) {
-            const int c = [&] {
-                for (size_t j = 0; j < i; j++)
-                    if (steps[j].output == nm || steps[j].pool_output == nm) return shp[j][3];
-                return x.c;
-            }();
-            if (produced.count(nm) && !into.count(nm) && nm != output && nm != input) into[nm] = {i, off};
-            off += c;
-        }
-    }
-    // A value written into a Concat's buffer keeps that buffer alive until its own last reader.
-    for (const auto &kv : into) {
-        auto lv = last.find(kv.first);
-        if (lv == last.end()) continue;
-        size_t &lc = last[steps[kv.second.first].output];
-        lc = std::max(lc, lv->second);
-    }
     std::map<std::string, Act> view;
     std::map<std::string, DBuf> owned;  // buffers by the value that owns them
-    view[input] = x;
-    auto alloc = [&](const std::string &name, const Shape &sh) -> Act {
+
+    Exec(const Graph &graph, Ctx &c, const Act &in) : g(graph), ctx(c), st(c.stream()), x(in) {
+        shp = g.shapes({x.n, x.h, x.w, x.c});
+        std::set<std::string> produced;
+        for (size_t i = 0; i < g.steps.size(); i++) {
+            for (const std::string &nm : g.steps[i].inputs) last[nm] = i;
+            if (g.steps[i].kind != OpKind::Identity) produced.insert(g.steps[i].output);
+            if (!g.steps[i].pool_output.empty()) produced.insert(g.steps[i].pool_output);
+        }
+        for (size_t i = 0; i < g.steps.size(); i++) {
+            const Step &s = g.steps[i];
+            if (s.kind != OpKind::Concat) continue;
+            int off = 0;
+            for (const std::string &nm : s.inputs) {
+                const int c2 = [&] {
+                    for (size_t j = 0; j < i; j++)
+                        if (g.steps[j].output == nm || g.steps[j].pool_output == nm) return shp[j][3];
+                    return x.c;
+                }();
+                if (produced.count(nm) && !into.count(nm) && nm != g.output && nm != g.input) into[nm] = {i, off};
+                off += c2;
+            }
+        }
+        // A value written into a Concat's buffer keeps that buffer alive until its own last reader.
+        for (const auto &kv : into) {
+            auto lv = last.find(kv.first);
+            if (lv == last.end()) continue;
+            size_t &lc = last[g.steps[kv.second.first].output];
+            lc = std::max(lc, lv->second);
+        }
+        view[g.input] = x;
+    }
+    Act alloc(const std::string &name, const Shape &sh) {
         Act a{nullptr, sh[0], sh[1], sh[2], sh[3], sh[3]};
         DBuf b(&ctx, a.count() * sizeof(float));
         a.p = b.as<float>();
         owned[name] = std::move(b);
         return a;
-    };
+    }
     // Where a value of shape sh is written: its own buffer, or its channel range of a Concat's.
-    auto view_for = [&](const std::string &name, const Shape &sh) -> Act {
+    Act view_for(const std::string &name, const Shape &sh) {
         auto it = into.find(name);
         if (it == into.end()) return alloc(name, sh);
         const size_t ci = it->second.first;
-        const std::string &cname = steps[ci].output;
+        const std::string &cname = g.steps[ci].output;
         if (!view.count(cname)) view[cname] = alloc(cname, shp[ci]);
         Act whole = view[cname];
         Act a{whole.p + it->second.second, sh[0], sh[1], sh[2], sh[3], whole.cs};
         return a;
-    };
-    auto out_view = [&](size_t i) -> Act { return view_for(steps[i].output, shp[i]); };
-    auto release = [&](size_t i) {
-        // Buffers whose last reader was step i go back to the pool (stream order keeps the reuse
-        // safe). A value inside a Concat's buffer is freed with that buffer, whose last use was
-        // extended above to cover it.
+    }
+    Act out_view(size_t i) { return view_for(g.steps[i].output, shp[i]); }
+    // Buffers whose last reader was step i go back to the pool (stream order keeps the reuse
+    // safe). A value inside a Concat's buffer is freed with that buffer, whose last use was
+    // extended above to cover it.
+    void release(size_t i) {
         for (const auto &kv : last) {
-            if (kv.second != i || kv.first == output || into.count(kv.first)) continue;
+            if (kv.second != i || kv.first == g.output || into.count(kv.first)) continue;
             owned.erase(kv.first);
         }
-    };
-    for (size_t i = 0; i < steps.size(); i++) {
-        const Step &s = steps[i];
-        const Act a = view.at(s.inputs[0]);
-        Act y;
-        switch (s.kind) {
-        case OpKind::Conv: {
-            y = out_view(i);
-            if (s.mfma && s.w && !s.pool_only && s.pool_output.empty() && a.cs % 4 == 0 &&
-                (reinterpret_cast<uintptr_t>(a.p) & 15) == 0) {
-                conv1x1_narrow(a, y, s.w, s.b, s.act, st);
-            } else if (s.mfma) {
-                ConvArgs ca;
-                ca.x = a;
-                ca.y = y;
-                if (s.pool_only) {
-                    // y is the pooled value; the full-size output is never written.
-                    ca.ypool = y;
-                    ca.y = Act{nullptr, y.n, (a.h + s.pt + s.pb - s.kh) + 1, (a.w + s.pl + s.pr - s.kw) + 1, y.c, y.c};
-                    ca.keep_full = false;
-                } else if (!s.pool_output.empty()) {
-                    ca.ypool = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
-                    view[s.pool_output] = ca.ypool;
-                }
-                ca.ph = s.ph;
-                ca.pw = s.pw;
-                ca.wt_hi = s.whi;
-                ca.wt_lo = s.wlo;
-                ca.wt_frag = s.wfrag;
-                ca.bias = s.b;
-                ca.pt = s.pt;
-                ca.pl = s.pl;
-                ca.act = s.act;
-                ca.pk = s.pk;
-                conv_mfma(ca, st);
-            } else {
-                conv_generic(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.sw, s.pt, s.pl, s.group, s.act, st);
-            }
-            break;
-        }
-        case OpKind::Direct:
-            y = out_view(i);
-            if (s.pool_output.empty()) {
-                conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st, s.w1frag);
-            } else {
-                // Full output and its 2 x 2 pool: in one pass on the matrix cores, else the conv
-                // and then the pool.
-                const Act yp = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
-                view[s.pool_output] = yp;
-                if (!(s.w1frag && s.kh == 3 && s.kw == 3 && s.pt == 1 &&
-                      conv1_mfma(a, y, s.w1frag, s.b, s.act, s.ph, s.pw, st, &yp))) {
-                    conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, 1, 1, st, s.w1frag);
-                    maxpool(y, yp, s.ph, s.pw, st);
-                }
-            }
-            break;
-        case OpKind::ConvT:
-            y = out_view(i);
-            if (s.phases.empty()) {
-                conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
-                break;
-            }
-            for (const Step::TPhase &ph : s.phases) {
-                const int st2 = s.sh;
-                const int ohp = (y.h - ph.py + st2 - 1) / st2, owp = (y.w - ph.px + st2 - 1) / st2;
-                if (ohp < 1 || owp < 1) continue;
-                ConvArgs ca;
-                ca.x = a;
-                ca.y = Act{y.p + (size_t(ph.py) * y.w + ph.px) * y.cs, y.n, ohp, owp, y.c, y.cs};
-                ca.y_px = st2;
-                ca.y_row = long(st2) * y.w;
-                ca.y_img = long(y.h) * y.w;
-                ca.wt_hi = ph.whi;
-                ca.wt_lo = ph.wlo;
-                ca.wt_frag = ph.wfrag;
-                ca.bias = s.b;
-                ca.pt = ph.ty - 1;
-                ca.pl = ph.tx - 1;
-                ca.act = s.act;
-                ca.pk = ph.pk;
-                conv_mfma(ca, st);
-            }
-            break;
-        case OpKind::MaxPool:
-            y = out_view(i);
-            maxpool(a, y, s.ph, s.pw, st);
-            break;
-        case OpKind::Slice: {
-            y = out_view(i);
-            int y0 = 0, x0 = 0;
-            for (size_t k = 0; k < s.starts.size() && k < s.axes.size(); k++) {
-                int64_t ax = s.axes[k] < 0 ? s.axes[k] + 4 : s.axes[k];
-                int64_t dim = ax == 2 ? a.h : a.w;
-                int64_t v = s.starts[k] < 0 ? s.starts[k] + dim : s.starts[k];
-                v = std::clamp<int64_t>(v, 0, dim);
-                if (ax == 2) y0 = int(v);
-                if (ax == 3) x0 = int(v);
-            }
-            copy_act(a, y, y0, x0, st);
-            break;
-        }
-        case OpKind::Concat: {
-            if (!view.count(s.output)) view[s.output] = alloc(s.output, shp[i]);
-            y = view[s.output];
-            int off = 0;
-            for (const std::string &nm : s.inputs) {
-                const Act part = view.at(nm);
-                auto it = into.find(nm);
-                if (it == into.end() || it->second.first != i) {
-                    Act dst{y.p + off, part.n, part.h, part.w, part.c, y.cs};
-                    copy_act(part, dst, 0, 0, st);
-                }
-                off += part.c;
-            }
-            break;
-        }
-        case OpKind::Act:
-            y = out_view(i);
-            activate(a, y, s.act, st);
-            break;
-        case OpKind::Identity: y = a; break;
-        }
-        view[s.output] = y;
+    }
+    void done(size_t i, const Act &y) {
+        view[g.steps[i].output] = y;
         release(i);
     }
+    // Step i is a dense conv on the matrix cores (not the narrow 1 x 1 one).
+    bool mfma_conv(size_t i) const {
+        const Step &s = g.steps[i];
+        if (s.kind != OpKind::Conv || !s.mfma) return false;
+        const Act &a = view.at(s.inputs[0]);
+        return !(s.w && !s.pool_only && s.pool_output.empty() && a.cs % 4 == 0 &&
+                 (reinterpret_cast<uintptr_t>(a.p) & 15) == 0);
+    }
+    // The arguments of such a step (its outputs get their views); y: the step's value.
+    ConvArgs conv_args(size_t i, Act &y) {
+        const Step &s = g.steps[i];
+        const Act a = view.at(s.inputs[0]);
+        y = out_view(i);
+        ConvArgs ca;
+        ca.x = a;
+        ca.y = y;
+        if (s.pool_only) {
+            // y is the pooled value; the full-size output is never written.
+            ca.ypool = y;
+            ca.y = Act{nullptr, y.n, (a.h + s.pt + s.pb - s.kh) + 1, (a.w + s.pl + s.pr - s.kw) + 1, y.c, y.c};
+            ca.keep_full = false;
+        } else if (!s.pool_output.empty()) {
+            ca.ypool = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
+            view[s.pool_output] = ca.ypool;
+        }
+        ca.ph = s.ph;
+        ca.pw = s.pw;
+        ca.wt_hi = s.whi;
+        ca.wt_lo = s.wlo;
+        ca.wt_frag = s.wfrag;
+        ca.bias = s.b;
+        ca.pt = s.pt;
+        ca.pl = s.pl;
+        ca.act = s.act;
+        ca.pk = s.pk;
+        return ca;
+    }
+    void step(size_t i);
+    Out result();
+};
+
+void Graph::Exec::step(size_t i) {
+    const Step &s = g.steps[i];
+    const Act a = view.at(s.inputs[0]);
+    Act y;
+    switch (s.kind) {
+    case OpKind::Conv: {
+        if (mfma_conv(i)) {
+            conv_mfma(conv_args(i, y), st);
+        } else if (s.mfma) {
+            y = out_view(i);
+            conv1x1_narrow(a, y, s.w, s.b, s.act, st);
+        } else {
+            y = out_view(i);
+            conv_generic(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.sw, s.pt, s.pl, s.group, s.act, st);
+        }
+        break;
+    }
+    case OpKind::Direct:
+        y = out_view(i);
+        if (s.pool_output.empty()) {
+            conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st, s.w1frag);
+        } else {
+            // Full output and its 2 x 2 pool: in one pass on the matrix cores, else the conv
+            // and then the pool.
+            const Act yp = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
+            view[s.pool_output] = yp;
+            if (!(s.w1frag && s.kh == 3 && s.kw == 3 && s.pt == 1 &&
+                  conv1_mfma(a, y, s.w1frag, s.b, s.act, s.ph, s.pw, st, &yp))) {
+                conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, 1, 1, st, s.w1frag);
+                maxpool(y, yp, s.ph, s.pw, st);
+            }
+        }
+        break;
+    case OpKind::ConvT:
+        y = out_view(i);
+        if (s.phases.empty()) {
+            conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
+            break;
+        }
+        for (const Step::TPhase &ph : s.phases) {
+            const int st2 = s.sh;
+            const int ohp = (y.h - ph.py + st2 - 1) / st2, owp = (y.w - ph.px + st2 - 1) / st2;
+            if (ohp < 1 || owp < 1) continue;
+            ConvArgs ca;
+            ca.x = a;
+            ca.y = Act{y.p + (size_t(ph.py) * y.w + ph.px) * y.cs, y.n, ohp, owp, y.c, y.cs};
+            ca.y_px = st2;
+            ca.y_row = long(st2) * y.w;
+            ca.y_img = long(y.h) * y.w;
+            ca.wt_hi = ph.whi;
+            ca.wt_lo = ph.wlo;
+            ca.wt_frag = ph.wfrag;
+            ca.bias = s.b;
+            ca.pt = ph.ty - 1;
+            ca.pl = ph.tx - 1;
+            ca.act = s.act;
+            ca.pk = ph.pk;
+            conv_mfma(ca, st);
+        }
+        break;
+    case OpKind::MaxPool:
+        y = out_view(i);
+        maxpool(a, y, s.ph, s.pw, st);
+        break;
+    case OpKind::Slice: {
+        y = out_view(i);
+        int y0 = 0, x0 = 0;
+        for (size_t k = 0; k < s.starts.size() && k < s.axes.size(); k++) {
+            int64_t ax = s.axes[k] < 0 ? s.axes[k] + 4 : s.axes[k];
+            int64_t dim = ax == 2 ? a.h : a.w;
+            int64_t v = s.starts[k] < 0 ? s.starts[k] + dim : s.starts[k];
+            v = std::clamp<int64_t>(v, 0, dim);
+            if (ax == 2) y0 = int(v);
+            if (ax == 3) x0 = int(v);
+        }
+        copy_act(a, y, y0, x0, st);
+        break;
+    }
+    case OpKind::Concat: {
+        if (!view.count(s.output)) view[s.output] = alloc(s.output, shp[i]);
+        y = view[s.output];
+        int off = 0;
+        for (const std::string &nm : s.inputs) {
+            const Act part = view.at(nm);
+            auto it = into.find(nm);
+            if (it == into.end() || it->second.first != i) {
+                Act dst{y.p + off, part.n, part.h, part.w, part.c, y.cs};
+                copy_act(part, dst, 0, 0, st);
+            }
+            off += part.c;
+        }
+        break;
+    }
+    case OpKind::Act:
+        y = out_view(i);
+        activate(a, y, s.act, st);
+        break;
+    case OpKind::Identity: y = a; break;
+    }
+    done(i, y);
+}
+
+Graph::Out Graph::Exec::result() {
     Out out;
-    auto vit = view.find(output);
-    if (vit == view.end()) fail("graph output " + output + " not computed");
+    auto vit = view.find(g.output);
+    if (vit == view.end()) fail("graph output " + g.output + " not computed");
     out.act = vit->second;
-    auto oit = owned.find(output);
+    auto oit = owned.find(g.output);
     if (oit != owned.end() && out.act.cs == out.act.c) {
         out.buf = std::move(oit->second);
     } else {
@@ -583,6 +615,37 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
         copy_act(out.act, dst, 0, 0, st);
         out.act = dst;
     }
+    return out;
+}
+
+Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
+    Exec e(*this, ctx, x);
+    for (size_t i = 0; i < steps.size(); i++) e.step(i);
+    return e.result();
+}
+
+std::vector<Graph::Out> Graph::run_multi(Ctx &ctx, const std::vector<Act> &xs) const {
+    std::vector<std::unique_ptr<Exec>> es;
+    for (const Act &x : xs) es.emplace_back(new Exec(*this, ctx, x));
+    std::vector<ConvArgs> cas;
+    std::vector<Act> ys;
+    for (size_t i = 0; i < steps.size(); i++) {
+        bool all = !es.empty();
+        for (auto &e : es) all = all && e->mfma_conv(i);
+        if (all && es.size() > 1) {
+            // One launch for every input's conv when the kernel takes them together.
+            cas.clear();
+            ys.assign(es.size(), Act{});
+            for (size_t k = 0; k < es.size(); k++) cas.push_back(es[k]->conv_args(i, ys[k]));
+            if (!conv3x3_dma_multi(cas.data(), int(cas.size()), ctx.stream()))
+                for (const ConvArgs &ca : cas) conv_mfma(ca, ctx.stream());
+            for (size_t k = 0; k < es.size(); k++) es[k]->done(i, ys[k]);
+        } else {
+            for (auto &e : es) e->step(i);
+        }
+    }
+    std::vector<Out> out;
+    for (auto &e : es) out.push_back(e->result());
     return out;
 }
 

@@ -60,11 +60,15 @@ class Graph {
     };
     // Record the graph on `x` on the context's stream; returns the output (gpu.rs:1243-1377).
     Out run(Ctx &ctx, const Act &x) const;
+    // The same on several inputs of one height and channel count (any widths and image counts):
+    // each step for all of them before the next, a dense 3 x 3 conv as one launch over all.
+    std::vector<Out> run_multi(Ctx &ctx, const std::vector<Act> &xs) const;
 
     std::string input, output;
     std::vector<Step> steps;
 
   private:
+    struct Exec;
     std::vector<Shape> shapes(const Shape &in) const;  // output shape of every step
 };
 

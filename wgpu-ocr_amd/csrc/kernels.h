@@ -75,6 +75,10 @@ bool gemm_dma(const ConvArgs &a, hipStream_t s);
 // ReLU / Sigmoid, optional 2 x 2 / 2 x 1 MaxPool (kernels/conv3.hip): operands fed by LDS DMA.
 // Returns false (and launches nothing) for anything else.
 bool conv3x3_dma(const ConvArgs &a, hipStream_t s);
+// The same conv over several tensors in one launch (the width batches of a recogniser pass): same
+// weights, bias, activation, pool, height and channel layout, any widths and image counts.
+// Returns false (and launches nothing) unless every one is taken and they are alike.
+bool conv3x3_dma_multi(const ConvArgs *args, int count, hipStream_t s);
 // 1 x 1 convolution to at most 4 output channels (a detector head) in float32 on the vector ALU:
 // bandwidth-bound, one thread a pixel (kernels/ops.hip). w [cout][cin] float32.
 void conv1x1_narrow(const Act &x, const Act &y, const float *w, const float *b, int act, hipStream_t s);

@@ -57,19 +57,26 @@ constexpr int HSU = HPX * PXU;       // HS size in units
 constexpr int NSI = 4;               // split items (pixel, 8 channels) per thread and slice
 static_assert((HPX + 15) / 16 * 64 <= NSI * 512, "split items fit");
 
-struct C3Params {
+// One segment: a tensor of n images of width w (output width ow, pooled pow_); every segment of
+// a launch has the same height, channels and weights (the width batches of one recogniser pass).
+struct C3Seg {
     const float *x;
-    int n, h, w, cin, xcs;
-    float *y;
-    int oh, ow, ycs;
-    float *yp;
-    int poh, pow_, ypcs, pool;
+    float *y, *yp;
+    int n, w, ow, pow_, tiles_x, t0;  // t0: the segment's first tile in the launch
+};
+constexpr int C3MAXSEG = 32;
+
+struct C3Params {
+    int h, cin, xcs;
+    int oh, ycs;
+    int poh, ypcs, pool;
     const half8 *wt;  // fragments [n-tile][slice][tap][64 lanes] of 8 halves
     int ntiles, cout, chunks;
     const float *bias;
     int th, tw, mx, hw, hh, rs, npx, hblocks;
-    int tiles_x, tiles_y, tiles, nblocks, runs;
+    int tiles_y, tiles, nblocks, runs, nseg;
     const float4 *zero;  // 16 zero bytes (the DMA source for padding)
+    C3Seg seg[C3MAXSEG];
 };
 
 __device__ inline float act3(float v, int act) {
@@ -87,7 +94,7 @@ __device__ inline int xcd_index3(int b, int G) {
 
 // A (tile, slice) position of the workgroup's walk, all values uniform.
 struct Seq {
-    int t, c, tx, ty, img;
+    int t, c, tx, ty, img, sg;
 };
 
 template <int WM, int WN, int NT, int ACT>
@@ -151,16 +158,24 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     auto advance = [&](Seq s) __attribute__((always_inline)) {
         if (++s.c == p.chunks) {
             s.c = 0, s.t++;
-            if (++s.tx == p.tiles_x) {
+            if (++s.tx == p.seg[s.sg].tiles_x) {
                 s.tx = 0;
-                if (++s.ty == p.tiles_y) s.ty = 0, s.img++;
+                if (++s.ty == p.tiles_y) {
+                    s.ty = 0;
+                    if (++s.img == p.seg[s.sg].n) s.img = 0, s.sg = min(s.sg + 1, C3MAXSEG - 1);
+                }
             }
         }
         return s;
     };
     Seq cur;
-    cur.t = t_begin, cur.c = 0, cur.tx = t_begin % p.tiles_x;
-    cur.ty = (t_begin / p.tiles_x) % p.tiles_y, cur.img = t_begin / (p.tiles_x * p.tiles_y);
+    cur.sg = 0;
+    while (cur.sg + 1 < p.nseg && t_begin >= p.seg[cur.sg + 1].t0) cur.sg++;
+    {
+        const int l = t_begin - p.seg[cur.sg].t0, tx_n = p.seg[cur.sg].tiles_x;
+        cur.t = t_begin, cur.c = 0, cur.tx = l % tx_n;
+        cur.ty = (l / tx_n) % p.tiles_y, cur.img = l / (tx_n * p.tiles_y);
+    }
 
     // Weights of slice c, kernel row ky: block b = kx * NTW + j (n-tile nt0 + j); instruction i.
     auto dma_w = [&](half8 *dst, int c, int ky, int i) __attribute__((always_inline)) {
@@ -171,12 +186,13 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     };
     // Halo of position s into HF, instruction i.
     auto dma_h = [&](const Seq &s, int i) __attribute__((always_inline)) {
-        const float *base = p.x + size_t(s.img) * p.h * p.w * p.xcs + s.c * 32;
+        const C3Seg &sd = p.seg[s.sg];
+        const float *base = sd.x + size_t(s.img) * p.h * sd.w * p.xcs + s.c * 32;
         const int b = min(i * 8 + wave, p.hblocks - 1);
         const int iy = s.ty * p.th - 1 + dhy[i], ix = s.tx * p.tw - 1 + dhx[i];
         const void *src = p.zero;
-        if (dhy[i] >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(p.w) && s.c * 32 + dch[i] < p.cin)
-            src = base + unsigned((iy * p.w + ix) * p.xcs + dch[i]);
+        if (dhy[i] >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(sd.w) && s.c * 32 + dch[i] < p.cin)
+            src = base + unsigned((iy * sd.w + ix) * p.xcs + dch[i]);
         dma16(src, HF + b * 64);
     };
     // HF -> HS, once a slice: hi part q (channels 8q..8q+7) of a pixel at its unit + q, lo at
@@ -251,19 +267,21 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
         constexpr int POOL = decltype(POOLc)::value;
         constexpr bool CHECK = decltype(CHECKc)::value;
         const int oy0 = s.ty * p.th, ox0 = s.tx * p.tw;
-        float *yt = p.y ? p.y + (size_t(s.img) * p.oh * p.ow + size_t(oy0) * p.ow + ox0) * p.ycs : nullptr;
+        const C3Seg &sd = p.seg[s.sg];
+        const int ow = sd.ow, pow_ = sd.pow_;
+        float *yt = sd.y ? sd.y + (size_t(s.img) * p.oh * ow + size_t(oy0) * ow + ox0) * p.ycs : nullptr;
         float *pt = nullptr;
-        if (POOL == 1) pt = p.yp + (size_t(s.img) * p.poh * p.pow_ + size_t(oy0 / 2) * p.pow_ + ox0 / 2) * p.ypcs;
-        if (POOL == 2) pt = p.yp + (size_t(s.img) * p.poh * p.pow_ + size_t(oy0 / 2) * p.pow_ + ox0) * p.ypcs;
+        if (POOL == 1) pt = sd.yp + (size_t(s.img) * p.poh * pow_ + size_t(oy0 / 2) * pow_ + ox0 / 2) * p.ypcs;
+        if (POOL == 2) pt = sd.yp + (size_t(s.img) * p.poh * pow_ + size_t(oy0 / 2) * pow_ + ox0) * p.ypcs;
         // The lane's parts of the offsets, computed here (not kept live across the tile loop).
         int lf = 2 * g * p.ycs + co_l, lp = (POOL == 1 ? g : 2 * g) * p.ypcs + co_l;
         asm volatile("" : "+v"(lf), "+v"(lp));
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const int dy = pyb[mt], dx = pxb[mt] + 2 * g;
-            const unsigned fo = unsigned((dy * p.ow + pxb[mt]) * p.ycs + lf);
-            const unsigned po = POOL == 1 ? unsigned(((dy >> 1) * p.pow_ + (pxb[mt] >> 1)) * p.ypcs + lp)
-                                          : unsigned(((dy >> 1) * p.pow_ + pxb[mt]) * p.ypcs + lp);
+            const unsigned fo = unsigned((dy * ow + pxb[mt]) * p.ycs + lf);
+            const unsigned po = POOL == 1 ? unsigned(((dy >> 1) * pow_ + (pxb[mt] >> 1)) * p.ypcs + lp)
+                                          : unsigned(((dy >> 1) * pow_ + pxb[mt]) * p.ypcs + lp);
 #pragma unroll
             for (int j = 0; j < NT; j++) {
                 float v[4];
@@ -274,33 +292,34 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
                 if (yt) {
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const bool in = !CHECK || (cok && oy0 + dy + (i >> 1) < p.oh && ox0 + dx + (i & 1) < p.ow);
-                        if (in) yt[fo + unsigned(((i >> 1) * p.ow + (i & 1)) * p.ycs + 16 * j)] = v[i];
+                        const bool in = !CHECK || (cok && oy0 + dy + (i >> 1) < p.oh && ox0 + dx + (i & 1) < ow);
+                        if (in) yt[fo + unsigned(((i >> 1) * ow + (i & 1)) * p.ycs + 16 * j)] = v[i];
                     }
                 }
                 if (POOL == 1) {
-                    const bool in = !CHECK || (cok && (oy0 + dy) / 2 < p.poh && (ox0 + dx) / 2 < p.pow_);
+                    const bool in = !CHECK || (cok && (oy0 + dy) / 2 < p.poh && (ox0 + dx) / 2 < pow_);
                     if (in) pt[po + 16 * j] = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
                 }
                 if (POOL == 2) {
                     const bool iny = !CHECK || (cok && (oy0 + dy) / 2 < p.poh);
-                    if (iny && (!CHECK || ox0 + dx < p.pow_)) pt[po + 16 * j] = fmaxf(v[0], v[2]);
-                    if (iny && (!CHECK || ox0 + dx + 1 < p.pow_)) pt[po + unsigned(p.ypcs) + 16 * j] = fmaxf(v[1], v[3]);
+                    if (iny && (!CHECK || ox0 + dx < pow_)) pt[po + 16 * j] = fmaxf(v[0], v[2]);
+                    if (iny && (!CHECK || ox0 + dx + 1 < pow_)) pt[po + unsigned(p.ypcs) + 16 * j] = fmaxf(v[1], v[3]);
                 }
             }
         }
     };
     auto epilogue = [&](const Seq &s) __attribute__((always_inline)) {
         const int oy0 = s.ty * p.th, ox0 = s.tx * p.tw;
-        const bool cin_ = co_w + 16 * NT <= p.cout && (!p.y || (oy0 + p.th <= p.oh && ox0 + p.tw <= p.ow));
+        const C3Seg &sd = p.seg[s.sg];
+        const bool cin_ = co_w + 16 * NT <= p.cout && (!sd.y || (oy0 + p.th <= p.oh && ox0 + p.tw <= sd.ow));
         auto run = [&](auto POOLc, bool inside) __attribute__((always_inline)) {
             if (inside) epi(s, POOLc, std::false_type{});
             else epi(s, POOLc, std::true_type{});
         };
         if (p.pool == 1)
-            run(std::integral_constant<int, 1>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && (ox0 + p.tw) / 2 <= p.pow_);
+            run(std::integral_constant<int, 1>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && (ox0 + p.tw) / 2 <= sd.pow_);
         else if (p.pool == 2)
-            run(std::integral_constant<int, 2>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && ox0 + p.tw <= p.pow_);
+            run(std::integral_constant<int, 2>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && ox0 + p.tw <= sd.pow_);
         else
             run(std::integral_constant<int, 0>{}, cin_);
     };
@@ -377,39 +396,40 @@ const float4 *zero_block() {
 
 }  // namespace
 
-bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
+namespace {
+
+// The checks of one segment; pool mode out (0 none, 1 = 2 x 2, 2 = 2 x 1), -1 when not taken.
+int c3_accepts(const ConvArgs &a) {
     const ConvPack &pk = a.pk;
-    if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res || a.rows || !pk.exact) return false;
-    if (pk.kh != 3 || pk.kw != 3 || a.pt != 1 || a.pl != 1 || pk.cin != a.x.c || pk.cout != a.y.c) return false;
-    if (a.y.n != a.x.n || a.y.h != a.x.h || a.y.w != a.x.w || a.y_px || a.y_row || a.y_img) return false;
-    if (a.x.c % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15)) return false;
-    if (a.act != ACT_NONE && a.act != ACT_RELU && a.act != ACT_SIGMOID) return false;
+    if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res || a.rows || !pk.exact) return -1;
+    if (pk.kh != 3 || pk.kw != 3 || a.pt != 1 || a.pl != 1 || pk.cin != a.x.c || pk.cout != a.y.c) return -1;
+    if (a.y.n != a.x.n || a.y.h != a.x.h || a.y.w != a.x.w || a.y_px || a.y_row || a.y_img) return -1;
+    if (a.x.c % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15)) return -1;
+    if (a.act != ACT_NONE && a.act != ACT_RELU && a.act != ACT_SIGMOID) return -1;
     // 32-bit offsets within one image of the input, the output and the pooled output.
-    if (double(a.x.h) * a.x.w * a.x.cs >= 2147483647.0 || double(a.y.h) * a.y.w * a.y.cs >= 2147483647.0) return false;
-    const bool pooled = a.ypool.p != nullptr;
-    int pool = 0;
-    if (pooled) {
-        if (a.ph == 2 && a.pw == 2) pool = 1;
-        else if (a.ph == 2 && a.pw == 1) pool = 2;
-        else return false;
-        if (a.ypool.h != a.y.h / a.ph || a.ypool.w != a.y.w / a.pw || a.ypool.c != a.y.c || a.ypool.n != a.y.n)
-            fail("conv3x3_dma: pooled output shape");
-    }
+    if (double(a.x.h) * a.x.w * a.x.cs >= 2147483647.0 || double(a.y.h) * a.y.w * a.y.cs >= 2147483647.0) return -1;
+    if (!a.ypool.p) return 0;
+    int pool;
+    if (a.ph == 2 && a.pw == 2) pool = 1;
+    else if (a.ph == 2 && a.pw == 1) pool = 2;
+    else return -1;
+    if (a.ypool.h != a.y.h / a.ph || a.ypool.w != a.y.w / a.pw || a.ypool.c != a.y.c || a.ypool.n != a.y.n)
+        fail("conv3x3_dma: pooled output shape");
+    return pool;
+}
+
+// Segments [0, count) of one launch (count <= C3MAXSEG), all accepted and alike.
+void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
+    const ConvArgs &a = args[0];
+    const ConvPack &pk = a.pk;
     const int cout = a.y.c, nt = cout > 64 ? 4 : cout > 32 ? 2 : 1, bn = 32 * nt;
     C3Params p{};
-    p.x = a.x.p;
-    p.n = a.x.n;
     p.h = a.x.h;
-    p.w = a.x.w;
     p.cin = a.x.c;
     p.xcs = a.x.cs;
-    p.y = pooled && !a.keep_full ? nullptr : a.y.p;
     p.oh = a.y.h;
-    p.ow = a.y.w;
     p.ycs = a.y.cs;
-    p.yp = a.ypool.p;
     p.poh = a.ypool.h;
-    p.pow_ = a.ypool.w;
     p.ypcs = a.ypool.cs;
     p.pool = pool;
     p.wt = reinterpret_cast<const half8 *>(a.wt_frag);
@@ -417,32 +437,50 @@ bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
     p.cout = cout;
     p.chunks = pk.chunks;
     p.bias = a.bias;
-    // Tile: 16 blocks of 2 x 8 pixels; the shape wasting the fewest pixels whose halo fits.
+    // Tile: 16 blocks of 2 x 8 pixels; the shape wasting the fewest pixels (over all segments)
+    // whose halo fits.
     double best = 1e300;
     for (int mxc : {1, 2, 4, 8}) {
         const int tw = 8 * mxc, th = 2 * (16 / mxc), hw = tw + 2, hh = th + 2;
         const int rs = 9 * hw + (24 - 9 * hw % 16) % 16;  // 8 mod 16 units
         if (hh * hw > HPX || hh * rs > HSU) continue;
-        const double cost = double((p.oh + th - 1) / th * th) * ((p.ow + tw - 1) / tw * tw) * double(hh * hw) / (th * tw);
+        double cost = 0;
+        for (int k = 0; k < count; k++)
+            cost += double(args[k].y.n) * ((p.oh + th - 1) / th * th) * ((args[k].y.w + tw - 1) / tw * tw) *
+                    double(hh * hw) / (th * tw);
         if (cost < best) best = cost, p.tw = tw, p.th = th, p.mx = mxc, p.rs = rs;
     }
-    if (best == 1e300) return false;
+    if (best == 1e300) fail("conv3x3_dma: no tile fits");
     p.hw = p.tw + 2;
     p.hh = p.th + 2;
     p.npx = p.hh * p.hw;
     p.hblocks = (p.npx + 7) / 8;
-    p.tiles_x = (p.ow + p.tw - 1) / p.tw;
     p.tiles_y = (p.oh + p.th - 1) / p.th;
-    const double tiles = double(p.tiles_x) * p.tiles_y * p.n;
-    if (tiles > 0x7fffffff) return false;
+    double tiles = 0, flops = 0, bytes = 2.0 * double(pk.halves());
+    for (int k = 0; k < count; k++) {
+        const ConvArgs &b = args[k];
+        C3Seg &sg = p.seg[k];
+        sg.x = b.x.p;
+        sg.y = b.ypool.p && !b.keep_full ? nullptr : b.y.p;
+        sg.yp = b.ypool.p;
+        sg.n = b.x.n;
+        sg.w = b.x.w;
+        sg.ow = b.y.w;
+        sg.pow_ = b.ypool.w;
+        sg.tiles_x = (sg.ow + p.tw - 1) / p.tw;
+        sg.t0 = int(tiles);
+        tiles += double(sg.tiles_x) * p.tiles_y * sg.n;
+        flops += 2.0 * b.y.n * b.y.h * b.y.w * cout * p.cin * 9;
+        bytes += 4.0 * (double(b.x.n) * b.x.h * b.x.w * p.cin + double(b.y.n) * b.y.h * b.y.w * cout);
+        if (tiles > 0x7fffffff) fail("conv3x3_dma: too many tiles");
+    }
+    p.nseg = count;
     p.tiles = int(tiles);
+    if (p.tiles == 0) return;
     p.nblocks = (cout + bn - 1) / bn;
     p.runs = std::max(1, std::min(p.tiles, cu_count3() / p.nblocks));
     p.zero = zero_block();
     const int grid = p.runs * p.nblocks;
-    const double flops = 2.0 * p.n * p.oh * p.ow * cout * p.cin * 9;
-    const double bytes = 4.0 * (double(p.n) * p.h * p.w * p.cin + double(p.n) * p.oh * p.ow * cout) +
-                         2.0 * double(pk.halves());
     ProbeScope probe("conv3x3_dma", s, flops, bytes);
     auto launch = [&](auto ACTc) {
         constexpr int A = decltype(ACTc)::value;
@@ -454,6 +492,31 @@ bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
     else if (a.act == ACT_SIGMOID) launch(std::integral_constant<int, ACT_SIGMOID>{});
     else launch(std::integral_constant<int, ACT_NONE>{});
     OCR_HIP(hipGetLastError());
+}
+
+}  // namespace
+
+bool conv3x3_dma(const ConvArgs &a, hipStream_t s) {
+    const int pool = c3_accepts(a);
+    if (pool < 0) return false;
+    c3_launch(&a, 1, pool, s);
+    return true;
+}
+
+bool conv3x3_dma_multi(const ConvArgs *args, int count, hipStream_t s) {
+    if (count < 1) return true;
+    const ConvArgs &a = args[0];
+    const int pool = c3_accepts(a);
+    if (pool < 0) return false;
+    for (int k = 1; k < count; k++) {
+        const ConvArgs &b = args[k];
+        if (c3_accepts(b) != pool || b.wt_frag != a.wt_frag || b.bias != a.bias || b.act != a.act ||
+            b.x.h != a.x.h || b.x.c != a.x.c || b.x.cs != a.x.cs || b.y.c != a.y.c || b.y.cs != a.y.cs ||
+            b.ypool.cs != a.ypool.cs || (b.ypool.p && !b.keep_full) != (a.ypool.p && !a.keep_full) ||
+            b.pk.chunks != a.pk.chunks)
+            return false;
+    }
+    for (int k = 0; k < count; k += C3MAXSEG) c3_launch(args + k, std::min(C3MAXSEG, count - k), pool, s);
     return true;
 }
 

@@ -81,11 +81,6 @@ void pack_linear(Ctx &ctx, const std::vector<float> &w_rows, int rows, int cols,
 }  // namespace
 
 Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), lines_(lines) {
-    for (int i = 0; i < TRUNK_STREAMS; i++) {
-        aux_.emplace_back(new Ctx(ctx.device(), ctx.lines(), 2048));
-        OCR_HIP(hipEventCreateWithFlags(&join_[i], hipEventDisableTiming));
-    }
-    OCR_HIP(hipEventCreateWithFlags(&fork_, hipEventDisableTiming));
     Node pool;
     bool found = false;
     trunk_ = Graph::build(ctx, onnx, "AveragePool", &pool, &found);
@@ -158,13 +153,7 @@ Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), 
     lin_b_ = ctx.upload_weights(bias->data.data(), bias->data.size());
 }
 
-Recognizer::~Recognizer() {
-    (void)hipSetDevice(ctx_.device());
-    for (auto &a : aux_) a->sync();
-    for (hipEvent_t e : join_)
-        if (e) (void)hipEventDestroy(e);
-    if (fork_) (void)hipEventDestroy(fork_);
-}
+Recognizer::~Recognizer() = default;
 
 Recognizer::Dims Recognizer::dims(const Batch *batches, int count) const {
     Dims d{0, 0, classes_};
@@ -185,31 +174,23 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     if (double(d.tmax) * d.ntot >= 2147483647.0) fail("recognition pass too large");
     // X [t][ntot][256] time-major (gpu.rs:1538-1555); rows t >= a line's length are never read.
     DBuf X(&ctx_, size_t(M) * 256 * sizeof(float));
-    // The trunks first (gpu.rs:1516-1526). With several width batches they run side by side on
-    // the trunk streams, after everything already on the stream (the line images); the stream
-    // waits for all of them before the projections.
-    const int ns = count > 1 ? TRUNK_STREAMS : 0;
-    if (ns) OCR_HIP(hipEventRecord(fork_, st));
-    for (int i = 0; i < ns; i++) OCR_HIP(hipStreamWaitEvent(aux_[size_t(i)]->stream(), fork_, 0));
-    std::vector<Graph::Out> trunks;
-    trunks.reserve(size_t(count));
+    // The trunks first (gpu.rs:1516-1526). The width batches share the 64-row height, so each
+    // trunk layer runs once over all of them: one launch a dense conv layer fills the GPU where
+    // a launch per width batch would not.
+    std::vector<Act> xs;
+    for (int b = 0; b < count; b++)
+        xs.push_back(Act{const_cast<float *>(batches[b].data), batches[b].n, 64, batches[b].w, 1, 1});
+    std::vector<Graph::Out> trunks = trunk_.run_multi(ctx_, xs);
     int noff = 0;
     for (int b = 0; b < count; b++) {
-        Ctx &c = ns ? *aux_[size_t(b % ns)] : ctx_;
-        Act x{const_cast<float *>(batches[b].data), batches[b].n, 64, batches[b].w, 1, 1};
-        trunks.push_back(trunk_.run(c, x));
-        const Act &t = trunks.back().act;
+        const Act &t = trunks[size_t(b)].act;
         if (t.c != layers_[0].input)
             fail("trunk gives " + std::to_string(t.c) + " features, GRU takes " + std::to_string(layers_[0].input));
         if ((t.h - pool_kh_) / pool_kh_ + 1 != 1)
             fail("trunk height " + std::to_string(t.h) + " does not pool to one row");
-        avgpool_t(t, pool_kh_, X.as<float>(), d.ntot, noff, c.stream());
+        avgpool_t(t, pool_kh_, X.as<float>(), d.ntot, noff, st);
         for (int i = 0; i < t.n; i++) lens[noff + i] = uint32_t(t.w);
         noff += t.n;
-    }
-    for (int i = 0; i < ns; i++) {
-        OCR_HIP(hipEventRecord(join_[i], aux_[size_t(i)]->stream()));
-        OCR_HIP(hipStreamWaitEvent(st, join_[i], 0));
     }
     const int tmax = d.tmax, ntot = d.ntot;
     trunks.clear();

@@ -61,11 +61,6 @@ class Recognizer {
     };
     Ctx &ctx_;
     Graph trunk_;
-    // The trunks of one pass's width batches run side by side on these streams (their own pools),
-    // so the small per-width launches fill the GPU together; events order them with ctx_'s stream.
-    static constexpr int TRUNK_STREAMS = 3;
-    std::vector<std::unique_ptr<Ctx>> aux_;
-    hipEvent_t fork_ = nullptr, join_[TRUNK_STREAMS] = {};
     int pool_kh_ = 0;
     Layer layers_[2];
     ConvPack lin_pk_;
