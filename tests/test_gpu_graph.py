@@ -96,7 +96,8 @@ def test_direct_conv_fused_pool(ctx, tmp_path, pool):
     check(ctx, p, RNG.uniform(-0.5, 0.5, (3, 1, 64, 37)).astype(np.float32))
 
 
-@pytest.mark.parametrize("cout,act,pool", [(48, "Sigmoid", None), (64, "Relu", (2, 2)), (16, None, (2, 2))])
+@pytest.mark.parametrize("cout,act,pool", [(48, "Sigmoid", None), (64, "Relu", (2, 2)), (16, None, (2, 2)),
+                                          (32, "Sigmoid", (2, 2))])
 def test_direct_conv_matrix_cores(ctx, tmp_path, cout, act, pool):
     # The one-channel 3 x 3 conv on the matrix cores: tile edges (50 x 131), 1-4 channel tiles.
     def net(g, x):

@@ -56,6 +56,39 @@ def test_line_images_match_oracle(detector, ctx):
         np.testing.assert_array_equal(got[k], want, err_msg=f"line {k} box {list(box)}")
 
 
+def test_line_images_edge_boxes(ctx):
+    # Boxes that leave the page, tall crops shrunk many times (the kernel narrows its tiles to
+    # keep the source window in LDS), a wide crop squeezed to 800 columns, rows with two spans or
+    # none, a 1 x 1 crop: bit for bit the oracle's line crop.
+    rng = np.random.Generator(np.random.PCG64(17))
+    page = rng.integers(0, 256, (700, 2600, 3), dtype=np.uint8)
+    ph, pw = page.shape[:2]
+
+    def full(bw, bh):
+        return list(range(0, 2 * bh + 1, 2)), [v for _ in range(bh) for v in (0, bw)]
+
+    def two_spans(bw, bh):
+        row_off, spans = [0], []
+        for r in range(bh):
+            if r % 3 != 2:
+                spans += [r % 7, bw // 3, bw // 2 + r % 5, bw - r % 4]
+            row_off.append(len(spans))
+        return row_off, spans
+
+    boxes = [((-30, -10, 300, 40, 480), full), ((100, 20, 120, 680, 12), full), ((50, 300, 2400, 50, 800), full),
+             ((400, 100, 200, 60, 213), two_spans), ((pw - 50, ph - 20, 100, 40, 160), full),
+             ((7, 9, 1, 1, 1), full), ((900, 200, 700, 130, 345), two_spans), ((1300, 5, 37, 300, 8), full)]
+    lines = []
+    for box, spans_of in boxes:
+        row_off, spans = spans_of(box[2], box[3])
+        lines.append((box, row_off, spans))
+    print(f"line images: {len(lines)} edge boxes", flush=True)
+    got = ocrhip.line_images(ctx, page, lines, 800)
+    for k, (box, row_off, spans) in enumerate(lines):
+        want = og.line_crop(page, box, row_off, spans, 800)
+        np.testing.assert_array_equal(got[k], want, err_msg=f"box {box}")
+
+
 def test_detect_mask_words_at_odd_widths(detector, det_oracle):
     # Page widths that end inside a 64-pixel group and inside a 32-bit word.
     for w in (2549, 97):

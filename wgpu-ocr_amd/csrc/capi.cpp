@@ -882,9 +882,7 @@ int ocr_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t 
             crops.push_back({drgb.as<uint8_t>(), int(page_w), int(page_h), l[0], l[1], l[2], l[3], l[4], l[5],
                              dout.as<float>() + size_t(i) * slot, int(wb)});
         }
-        DBuf dc(&c, crops.size() * sizeof(CropLine));
-        c.h2d(dc.get(), crops.data(), crops.size() * sizeof(CropLine));
-        line_crop(dc.as<CropLine>(), int(count), droff.as<int>(), dspans.as<int>(), int(wb), c.stream());
+        line_crop(c, crops, droff.as<int>(), dspans.as<int>(), c.stream());
         c.d2h(out, dout.get(), size_t(count) * slot * sizeof(float));
     });
 }

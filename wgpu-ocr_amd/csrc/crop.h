@@ -4,9 +4,11 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <vector>
 
 #include "common.h"
 #include "geometry.h"
+#include "runtime.h"
 
 namespace ocr {
 
@@ -17,12 +19,15 @@ struct CropLine {
     int row_base;        // index of this line's first row offset in the row_off array
     float *dst;          // the line's slot in its batch: [64][wb] floats (device)
     int wb;              // batch width
+    // Set by line_crop: output tiles of tr rows x tc columns, ntx across the slot, the line's
+    // first block.
+    int tr = 0, tc = 0, ntx = 0, blk0 = 0;
 };
 
 // All lines in one launch; row_off holds every line's (bh + 1) span offsets (already rebased
-// into the shared spans array).
-void line_crop(const CropLine *d_lines, int nlines, const int *d_row_off, const int *d_spans, int max_wb,
-               hipStream_t s);
+// into the shared spans array). The descriptors and a block-to-line map are uploaded through
+// the context's staging ring.
+void line_crop(Ctx &ctx, std::vector<CropLine> &lines, const int *d_row_off, const int *d_spans, hipStream_t s);
 
 // One PP-OCR line image (ppocr::line_input, src/ppocr.rs:42-62, and ppocr::batch, ppocr.rs:64-78).
 struct PpCropLine {

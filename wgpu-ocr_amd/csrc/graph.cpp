@@ -493,6 +493,31 @@ struct Graph::Exec {
         ca.pk = s.pk;
         return ca;
     }
+    // Step i is a one-channel conv the matrix-core kernel takes (3 x 3, pad 1, packed weights).
+    bool direct_mfma(size_t i) const {
+        const Step &s = g.steps[i];
+        return s.kind == OpKind::Direct && s.w1frag && s.kh == 3 && s.kw == 3 && s.pt == 1;
+    }
+    // The output views of a one-channel conv: y, and with a fused pool its pooled output yp.
+    void direct_views(size_t i, Act &y, Act &yp) {
+        const Step &s = g.steps[i];
+        y = out_view(i);
+        yp = Act{};
+        if (!s.pool_output.empty()) {
+            yp = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
+            view[s.pool_output] = yp;
+        }
+    }
+    // The same step without the matrix-core kernel: the conv and then the pool.
+    void direct_fallback(size_t i, const Act &a, const Act &y, const Act &yp) {
+        const Step &s = g.steps[i];
+        if (s.pool_output.empty()) {
+            conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st, s.w1frag);
+        } else {
+            conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, 1, 1, st, s.w1frag);
+            maxpool(y, yp, s.ph, s.pw, st);
+        }
+    }
     void step(size_t i);
     Out result();
 };
@@ -514,22 +539,16 @@ void Graph::Exec::step(size_t i) {
         }
         break;
     }
-    case OpKind::Direct:
-        y = out_view(i);
+    case OpKind::Direct: {
+        Act yp;
+        direct_views(i, y, yp);
         if (s.pool_output.empty()) {
             conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, s.ph, s.pw, st, s.w1frag);
-        } else {
-            // Full output and its 2 x 2 pool: in one pass on the matrix cores, else the conv
-            // and then the pool.
-            const Act yp = view_for(s.pool_output, {y.n, y.h / s.ph, y.w / s.pw, y.c});
-            view[s.pool_output] = yp;
-            if (!(s.w1frag && s.kh == 3 && s.kw == 3 && s.pt == 1 &&
-                  conv1_mfma(a, y, s.w1frag, s.b, s.act, s.ph, s.pw, st, &yp))) {
-                conv_direct(a, y, s.w, s.b, s.kh, s.kw, s.pt, s.act, 1, 1, st, s.w1frag);
-                maxpool(y, yp, s.ph, s.pw, st);
-            }
+        } else if (!(direct_mfma(i) && conv1_mfma(a, y, s.w1frag, s.b, s.act, s.ph, s.pw, st, &yp))) {
+            direct_fallback(i, a, y, yp);
         }
         break;
+    }
     case OpKind::ConvT:
         y = out_view(i);
         if (s.phases.empty()) {
@@ -628,11 +647,26 @@ std::vector<Graph::Out> Graph::run_multi(Ctx &ctx, const std::vector<Act> &xs) c
     std::vector<std::unique_ptr<Exec>> es;
     for (const Act &x : xs) es.emplace_back(new Exec(*this, ctx, x));
     std::vector<ConvArgs> cas;
-    std::vector<Act> ys;
+    std::vector<Act> as, ys, yps;
     for (size_t i = 0; i < steps.size(); i++) {
-        bool all = !es.empty();
-        for (auto &e : es) all = all && e->mfma_conv(i);
-        if (all && es.size() > 1) {
+        bool all = !es.empty(), all1 = !es.empty();
+        for (auto &e : es) all = all && e->mfma_conv(i), all1 = all1 && e->direct_mfma(i);
+        if (all1 && es.size() > 1) {
+            // The one-channel first layer of every input in one launch.
+            const Step &s = steps[i];
+            as.clear();
+            ys.assign(es.size(), Act{});
+            yps.assign(es.size(), Act{});
+            for (size_t k = 0; k < es.size(); k++) {
+                as.push_back(es[k]->view.at(s.inputs[0]));
+                es[k]->direct_views(i, ys[k], yps[k]);
+            }
+            const bool pooled = !s.pool_output.empty();
+            if (!conv1_mfma_multi(as.data(), ys.data(), pooled ? yps.data() : nullptr, int(es.size()), s.w1frag, s.b,
+                                  s.act, s.ph, s.pw, ctx.stream()))
+                for (size_t k = 0; k < es.size(); k++) es[k]->direct_fallback(i, as[k], ys[k], yps[k]);
+            for (size_t k = 0; k < es.size(); k++) es[k]->done(i, ys[k]);
+        } else if (all && es.size() > 1) {
             // One launch for every input's conv when the kernel takes them together.
             cas.clear();
             ys.assign(es.size(), Act{});

@@ -98,6 +98,10 @@ void pack_conv1_frags(const float *w, int cout, uint16_t *frag);
 // With ypool (2 x 2 pool, full-size y) both outputs are written.
 bool conv1_mfma(const Act &x, const Act &y, const uint16_t *frag, const float *b, int act, int ph, int pw,
                 hipStream_t s, const Act *ypool = nullptr);
+// The same over count inputs of one height (any widths and image counts), one launch for up to
+// 32 of them; ypool is null or an array of count pooled outputs.
+bool conv1_mfma_multi(const Act *x, const Act *y, const Act *ypool, int count, const uint16_t *frag, const float *b,
+                      int act, int ph, int pw, hipStream_t s);
 // ConvTranspose gather form (gpu.rs:424-460); w re-laid out as [ky][kx][cin][cout].
 void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride,
                     int act, hipStream_t s);
@@ -111,9 +115,9 @@ void grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int
 // Model output (row stride `stride`, valid mw x mh) -> page size bits (gpu.rs:563-593).
 void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, float sx, float sy,
              float thr, hipStream_t s);
-// AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c] at
-// line offset noff (gpu.rs:595-614).
-void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s);
+// AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c]
+// (gpu.rs:595-614): the count inputs (same channel count) at line offsets 0, n0, n0 + n1, ...
+void avgpool_t(const Act *xs, int count, int kh, float *X, int ntot, hipStream_t s);
 // Per row of [rows][classes]: the arg-max, the last index on ties (ocr-bench.rs:67). With a row
 // map, row i is physical row map[i] of x and of best.
 void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s, const int *map = nullptr);

@@ -7,6 +7,8 @@
 // and written into the line's slot of its batch, padded with black to the batch width.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+
 #include "../crop.h"
 #include "../runtime.h"
 
@@ -29,34 +31,112 @@ __device__ inline float grey_px(const uint8_t *rgb, int w, int h, int x, int y) 
     return g + float(q[2]) * (0.114f / 255.f);
 }
 
-// One thread per output pixel, a workgroup per 256 columns of one output row: the row's source
-// rows, their polygon spans and the vertical weight are the same for the whole workgroup.
-__global__ __launch_bounds__(256) void line_crop_kernel(const CropLine *lines, const int *row_off, const int *spans) {
+constexpr int CROP_WIN = 6144;   // grey values of a block's source window in LDS
+constexpr int CROP_SPANS = 512;  // polygon span bounds of the window's rows in LDS
+constexpr int CROP_ROWS = 256;   // window rows
+
+// Source coordinate of output coordinate o (half-pixel centres, clamped): the lower tap, the
+// upper tap and the weight of the upper one.
+struct Tap {
+    int a, b;
+    float f;
+};
+__device__ inline Tap tap(float scale, int o, int n) {
 #pragma clang fp contract(off)
-    const CropLine L = lines[blockIdx.z];
-    const int oy = blockIdx.y, ox = blockIdx.x * 256 + threadIdx.x;
-    if (ox >= L.wb) return;
-    float v = -0.5f;
-    if (ox < L.out_w) {
-        const float sy = float(L.bh) / float(LINE_H), sx = float(L.bw) / float(L.out_w);
-        const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(L.bh) - 1.f);
-        const int y1 = int(iy), y2 = min(y1 + 1, L.bh - 1);
-        const float fy = iy - float(y1);
-        // Crop pixel (cx, cy): the page's grey inside the row's spans, black elsewhere.
-        auto px = [&](int cx, int cy) -> float {
-            const int s0 = row_off[L.row_base + cy], s1 = row_off[L.row_base + cy + 1];
-            for (int s = s0; s < s1; s += 2)
-                if (cx >= spans[s] && cx < spans[s + 1]) return grey_px(L.rgb, L.pw, L.ph, L.left + cx, L.top + cy);
-            return -0.5f;
-        };
-        const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(L.bw) - 1.f);
-        const int x1 = int(ix), x2 = min(x1 + 1, L.bw - 1);
-        const float fx = ix - float(x1);
-        const float top = mixf(px(x1, y1), px(x2, y1), fx);
-        const float bot = mixf(px(x1, y2), px(x2, y2), fx);
-        v = mixf(top, bot, fy);
+    const float i = fminf(fmaxf(scale * (float(o) + 0.5f) - 0.5f, 0.f), float(n) - 1.f);
+    const int a = int(i);
+    return {a, min(a + 1, n - 1), i - float(a)};
+}
+
+// A workgroup per output tile (tr rows x tc columns) of one line. The tile's source window (the
+// crop rows and columns its taps touch) is first made grey in LDS, each source pixel once:
+// inside the row's polygon spans the page's grey, else black; then every output pixel reads its
+// four taps from LDS. A window too large for LDS (only possible for a tile shape the host did not
+// size) is read straight from the page instead, with the same arithmetic.
+__global__ __launch_bounds__(256) void line_crop_kernel(const CropLine *lines, const int *map, const int *row_off,
+                                                        const int *spans) {
+#pragma clang fp contract(off)
+    __shared__ float s_grey[CROP_WIN];
+    __shared__ int s_span[CROP_SPANS];
+    __shared__ int s_roff[CROP_ROWS + 1];
+    const CropLine L = lines[map[blockIdx.x]];
+    const int t = int(blockIdx.x) - L.blk0;
+    const int band = t / L.ntx, chunk = t - band * L.ntx;
+    const int oy0 = band * L.tr, ox0 = chunk * L.tc;
+    const int nr = min(L.tr, LINE_H - oy0), nc = min(L.tc, L.wb - ox0);
+    const int ncw = min(nc, L.out_w - ox0);  // columns of the tile inside the resized crop
+    const float sy = float(L.bh) / float(LINE_H), sx = float(L.bw) / float(L.out_w);
+    const int tid = threadIdx.x;
+    // The window: crop rows wy0 .. wy1, columns wx0 .. wx1.
+    int wy0 = 0, wx0 = 0, wr = 0, wc = 0;
+    if (ncw > 0) {
+        wy0 = tap(sy, oy0, L.bh).a;
+        wx0 = tap(sx, ox0, L.bw).a;
+        wr = tap(sy, oy0 + nr - 1, L.bh).b - wy0 + 1;
+        wc = tap(sx, ox0 + ncw - 1, L.bw).b - wx0 + 1;
     }
-    L.dst[size_t(oy) * L.wb + ox] = v;
+    const int sp0 = ncw > 0 ? row_off[L.row_base + wy0] : 0;
+    const int nsp = ncw > 0 ? row_off[L.row_base + wy0 + wr] - sp0 : 0;
+    const bool staged = ncw > 0 && wr * wc <= CROP_WIN && wr <= CROP_ROWS && nsp <= CROP_SPANS;
+    if (staged) {
+        for (int i = tid; i <= wr; i += 256) s_roff[i] = row_off[L.row_base + wy0 + i] - sp0;
+        for (int i = tid; i < nsp; i += 256) s_span[i] = spans[sp0 + i];
+        __syncthreads();
+        // Grey of the window, four pixels a thread at a time with all their loads issued first.
+        const int n = wr * wc;
+        for (int i0 = tid; i0 < n; i0 += 4 * 256) {
+            float g[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int i = i0 + k * 256;
+                const int r = i / wc, c = i - r * wc;
+                g[k] = i < n ? grey_px(L.rgb, L.pw, L.ph, L.left + wx0 + c, L.top + wy0 + r) : -0.5f;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int i = i0 + k * 256;
+                if (i >= n) break;
+                const int r = i / wc, cx = wx0 + i - r * wc;
+                bool in = false;
+                for (int q = s_roff[r]; q < s_roff[r + 1]; q += 2) in = in || (cx >= s_span[q] && cx < s_span[q + 1]);
+                s_grey[i] = in ? g[k] : -0.5f;
+            }
+        }
+        __syncthreads();
+    }
+    // Crop pixel (cx, cy) read straight from the page: the page's grey inside the row's spans,
+    // black elsewhere.
+    auto px = [&](int cx, int cy) -> float {
+        const int s0 = row_off[L.row_base + cy], s1 = row_off[L.row_base + cy + 1];
+        for (int q = s0; q < s1; q += 2)
+            if (cx >= spans[q] && cx < spans[q + 1]) return grey_px(L.rgb, L.pw, L.ph, L.left + cx, L.top + cy);
+        return -0.5f;
+    };
+    for (int i = tid; i < nr * nc; i += 256) {
+        const int r = i / nc, c = i - r * nc;
+        const int oy = oy0 + r, ox = ox0 + c;
+        float v = -0.5f;
+        if (ox < L.out_w) {
+            const Tap ty = tap(sy, oy, L.bh), tx = tap(sx, ox, L.bw);
+            float p11, p21, p12, p22;
+            if (staged) {
+                const int r1 = (ty.a - wy0) * wc, r2 = (ty.b - wy0) * wc, c1 = tx.a - wx0, c2 = tx.b - wx0;
+                p11 = s_grey[r1 + c1];
+                p21 = s_grey[r1 + c2];
+                p12 = s_grey[r2 + c1];
+                p22 = s_grey[r2 + c2];
+            } else {
+                p11 = px(tx.a, ty.a);
+                p21 = px(tx.b, ty.a);
+                p12 = px(tx.a, ty.b);
+                p22 = px(tx.b, ty.b);
+            }
+            const float top = mixf(p11, p21, tx.f);
+            const float bot = mixf(p12, p22, tx.f);
+            v = mixf(top, bot, ty.f);
+        }
+        L.dst[size_t(oy) * L.wb + ox] = v;
+    }
 }
 
 // PP-OCR line images: the crop resized to 48 rows x out_w columns bilinearly (half-pixel,
@@ -104,13 +184,36 @@ void pp_line_crop(const PpCropLine *d_lines, int nlines, int max_wb, hipStream_t
     OCR_HIP(hipGetLastError());
 }
 
-void line_crop(const CropLine *d_lines, int nlines, const int *d_row_off, const int *d_spans, int max_wb,
-               hipStream_t s) {
-    if (nlines <= 0) return;
-    if (nlines > 65535) fail("line_crop: more than 65535 lines");
-    dim3 grid(unsigned((max_wb + 255) / 256), LINE_H, unsigned(nlines));
-    ProbeScope probe("line_crop", s, 0, 4.0 * double(nlines) * LINE_H * max_wb);
-    hipLaunchKernelGGL(line_crop_kernel, grid, dim3(256), 0, s, d_lines, d_row_off, d_spans);
+void line_crop(Ctx &ctx, std::vector<CropLine> &lines, const int *d_row_off, const int *d_spans, hipStream_t s) {
+    if (lines.empty()) return;
+    // Tile shape per line: 16 rows x 256 columns, narrowed until the source window (at most
+    // (tr - 1) sy + 3 rows by (tc - 1) sx + 3 columns) fits in LDS.
+    std::vector<int> map;
+    double bytes = 0;
+    for (size_t i = 0; i < lines.size(); i++) {
+        CropLine &L = lines[i];
+        if (L.wb < 1 || L.out_w < 1 || L.out_w > L.wb || L.bw < 1 || L.bh < 1) fail("line_crop: line box or width");
+        const double sy = double(L.bh) / LINE_H, sx = double(L.bw) / L.out_w;
+        auto win = [&](int tr, int tc) { return (std::floor((tr - 1) * sy) + 3) * (std::floor((tc - 1) * sx) + 3); };
+        int tr = 16, tc = 256;
+        while (win(tr, tc) > CROP_WIN && tc > 64) tc /= 2;
+        while (win(tr, tc) > CROP_WIN && tr > 1) tr /= 2;
+        while (win(tr, tc) > CROP_WIN && tc > 1) tc /= 2;
+        L.tr = tr;
+        L.tc = tc;
+        L.ntx = (L.wb + tc - 1) / tc;
+        L.blk0 = int(map.size());
+        const long long nb = (long long)((LINE_H + tr - 1) / tr) * L.ntx;
+        if (double(map.size()) + double(nb) > 2147483647.0) fail("line_crop: grid too large");
+        map.insert(map.end(), size_t(nb), int(i));
+        bytes += 4.0 * LINE_H * L.wb + 3.0 * double(L.bw) * L.bh;
+    }
+    DBuf dl(&ctx, lines.size() * sizeof(CropLine)), dm(&ctx, map.size() * sizeof(int));
+    ctx.h2d(dl.get(), lines.data(), lines.size() * sizeof(CropLine));
+    ctx.h2d(dm.get(), map.data(), map.size() * sizeof(int));
+    ProbeScope probe("line_crop", s, 0, bytes);
+    hipLaunchKernelGGL(line_crop_kernel, dim3(unsigned(map.size())), dim3(256), 0, s, dl.as<CropLine>(), dm.as<int>(),
+                       d_row_off, d_spans);
     OCR_HIP(hipGetLastError());
 }
 

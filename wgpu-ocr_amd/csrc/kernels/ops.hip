@@ -262,15 +262,31 @@ __global__ void conv1x1_narrow_kernel(const float *__restrict__ x, long pixels, 
 }
 
 // ---- avgpool_t (gpu.rs:595-614): [n][kh][T][c] -> X[t][ntot][c] at line offset noff ----------
-__global__ void avgpool_t_kernel(const float *x, int n, int h, int kh, int T, int c, int xcs, float *X, int ntot,
-                                 int noff) {
-    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(n) * T * c) return;
-    int ch = int(i % c);
-    int t = int((i / c) % T), img = int(i / (size_t(c) * T));
+// Up to APMAXSEG inputs a launch; segment s owns the blocks from blk0 (its elements padded to
+// whole blocks, so a block lies in one segment).
+struct ApSeg {
+    const float *x;
+    int n, h, T, xcs, noff, blk0;
+};
+constexpr int APMAXSEG = 32;
+struct ApParams {
+    int nseg, kh, c, ntot;
+    float *X;
+    ApSeg seg[APMAXSEG];
+};
+
+__global__ __launch_bounds__(256) void avgpool_t_kernel(const ApParams p) {
+    int sg = 0;
+    while (sg + 1 < p.nseg && int(blockIdx.x) >= p.seg[sg + 1].blk0) sg++;
+    const ApSeg &S = p.seg[sg];
+    const size_t i = size_t(int(blockIdx.x) - S.blk0) * 256 + threadIdx.x;
+    const int c = p.c;
+    if (i >= size_t(S.n) * S.T * c) return;
+    const int ch = int(i % c);
+    const int t = int((i / c) % S.T), img = int(i / (size_t(c) * S.T));
     float s = 0.f;
-    for (int r = 0; r < kh; r++) s += x[((size_t(img) * h + r) * T + t) * xcs + ch];
-    X[(size_t(t) * ntot + noff + img) * c + ch] = s / float(kh);
+    for (int r = 0; r < p.kh; r++) s += S.x[((size_t(img) * S.h + r) * S.T + t) * S.xcs + ch];
+    p.X[(size_t(t) * p.ntot + S.noff + img) * c + ch] = s / float(p.kh);
 }
 
 // ---- argmax: one wavefront per row, the last index on ties ---------------------------------
@@ -395,12 +411,37 @@ void conv1x1_narrow(const Act &x, const Act &y, const float *w, const float *b, 
     OCR_HIP(hipGetLastError());
 }
 
-void avgpool_t(const Act &x, int kh, float *X, int ntot, int noff, hipStream_t s) {
-    if (kh < 1 || kh > x.h) fail("avgpool_t: pool height");
-    ProbeScope probe("avgpool_t", s, 0, 4.0 * double(x.n) * x.w * x.c * (kh + 1));
-    hipLaunchKernelGGL(avgpool_t_kernel, dim3(blocks_for(size_t(x.n) * x.w * x.c)), dim3(256), 0, s, x.p, x.n, x.h,
-                       kh, x.w, x.c, x.cs, X, ntot, noff);
-    OCR_HIP(hipGetLastError());
+void avgpool_t(const Act *xs, int count, int kh, float *X, int ntot, hipStream_t s) {
+    if (count < 1) return;
+    const int c = xs[0].c;
+    double bytes = 0;
+    int noff = 0;
+    for (int k0 = 0; k0 < count; k0 += APMAXSEG) {
+        const int cnt = std::min(APMAXSEG, count - k0);
+        ApParams p{};
+        p.nseg = cnt;
+        p.kh = kh;
+        p.c = c;
+        p.ntot = ntot;
+        p.X = X;
+        long long blocks = 0;
+        for (int k = 0; k < cnt; k++) {
+            const Act &x = xs[k0 + k];
+            if (kh < 1 || kh > x.h) fail("avgpool_t: pool height");
+            if (x.c != c) fail("avgpool_t: channel counts differ");
+            p.seg[k] = ApSeg{x.p, x.n, x.h, x.w, x.cs, noff, int(blocks)};
+            blocks += (long long)((size_t(x.n) * x.w * c + 255) / 256);
+            if (blocks > 2147483647LL) fail("avgpool_t: grid too large");
+            noff += x.n;
+            bytes += 4.0 * double(x.n) * x.w * c * (kh + 1);
+        }
+        if (noff > ntot) fail("avgpool_t: more lines than the output holds");
+        if (blocks == 0) continue;
+        ProbeScope probe("avgpool_t", s, 0, bytes);
+        bytes = 0;
+        hipLaunchKernelGGL(avgpool_t_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, p);
+        OCR_HIP(hipGetLastError());
+    }
 }
 
 void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStream_t s, const int *map) {

@@ -181,6 +181,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     for (int b = 0; b < count; b++)
         xs.push_back(Act{const_cast<float *>(batches[b].data), batches[b].n, 64, batches[b].w, 1, 1});
     std::vector<Graph::Out> trunks = trunk_.run_multi(ctx_, xs);
+    std::vector<Act> feats;
     int noff = 0;
     for (int b = 0; b < count; b++) {
         const Act &t = trunks[size_t(b)].act;
@@ -188,10 +189,11 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
             fail("trunk gives " + std::to_string(t.c) + " features, GRU takes " + std::to_string(layers_[0].input));
         if ((t.h - pool_kh_) / pool_kh_ + 1 != 1)
             fail("trunk height " + std::to_string(t.h) + " does not pool to one row");
-        avgpool_t(t, pool_kh_, X.as<float>(), d.ntot, noff, st);
+        feats.push_back(t);
         for (int i = 0; i < t.n; i++) lens[noff + i] = uint32_t(t.w);
         noff += t.n;
     }
+    avgpool_t(feats.data(), count, pool_kh_, X.as<float>(), d.ntot, st);
     const int tmax = d.tmax, ntot = d.ntot;
     trunks.clear();
     // The rows that carry a step of some line, t-major: (t, line) with t < lens[line]. The

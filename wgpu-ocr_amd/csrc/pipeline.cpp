@@ -100,13 +100,17 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
 
     // 1. Detection of every page, at most det_batch pages a pass and never across a recognition
     // pass's pages: the first pass's layouts then start while the later pages are still being
-    // detected. The bit masks come back asynchronously.
+    // detected. The first group is a third of det_batch (at least one page), so the host starts
+    // on layouts while the GPU detects the rest of the first pass. The bit masks come back
+    // asynchronously.
     const int nrec = (npages + I.opts.merge - 1) / I.opts.merge;
     std::vector<int> group_of(static_cast<size_t>(npages)), group_p0;
     for (int r = 0; r < nrec; r++) {
         const int r0 = r * I.opts.merge, r1 = std::min(npages, r0 + I.opts.merge);
+        const int first = r == 0 ? std::max(1, I.opts.det_batch / 3) : I.opts.det_batch;
         for (int p = r0; p < r1; p++) {
-            if ((p - r0) % I.opts.det_batch == 0) group_p0.push_back(p);
+            const int k = p - r0;
+            if (k == 0 || (k >= first && (k - first) % I.opts.det_batch == 0)) group_p0.push_back(p);
             group_of[size_t(p)] = int(group_p0.size()) - 1;
         }
     }
@@ -208,13 +212,11 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         }
         std::vector<Recognizer::Batch> batches;
         std::vector<DBuf> batch_bufs;
-        int max_wb = 0;
         for (const auto &kv : by_width) {
             const int wb = kv.first, n = int(kv.second.size());
             batch_bufs.emplace_back(&ctx, size_t(n) * LINE_H * wb * sizeof(float));
             float *base = batch_bufs.back().as<float>();
             batches.push_back({base, n, wb});
-            max_wb = std::max(max_wb, wb);
             for (int k = 0; k < n; k++) {
                 const int p = kv.second[size_t(k)].first, li = kv.second[size_t(k)].second;
                 const LineGeom &g = layouts[size_t(p)].lines[size_t(li)];
@@ -229,13 +231,11 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             }
         }
         if (batches.empty()) continue;
-        DBuf dcrops(&ctx, R.crops.size() * sizeof(CropLine)), droff(&ctx, R.row_off.size() * 4),
-            dspans(&ctx, std::max<size_t>(R.spans.size(), 1) * 4);
-        ctx.h2d(dcrops.get(), R.crops.data(), R.crops.size() * sizeof(CropLine));
+        DBuf droff(&ctx, R.row_off.size() * 4), dspans(&ctx, std::max<size_t>(R.spans.size(), 1) * 4);
         ctx.h2d(droff.get(), R.row_off.data(), R.row_off.size() * 4);
         if (!R.spans.empty()) ctx.h2d(dspans.get(), R.spans.data(), R.spans.size() * 4);
         mark("rec " + std::to_string(r) + " crops built");
-        line_crop(dcrops.as<CropLine>(), int(R.crops.size()), droff.as<int>(), dspans.as<int>(), max_wb, st);
+        line_crop(ctx, R.crops, droff.as<int>(), dspans.as<int>(), st);
         const Recognizer::Dims d = I.rec.dims(batches.data(), int(batches.size()));
         R.tmax = d.tmax;
         R.ntot = d.ntot;
