@@ -151,18 +151,27 @@ def test_conv_transpose_2x3(ctx, tmp_path):
     check(ctx, p, RNG.standard_normal((2, 20, 5, 7)).astype(np.float32))
 
 
-@pytest.mark.parametrize("k,stride,cin,cout", [((3, 3), 1, 8, 5), ((2, 2), 2, 40, 16), ((3, 3), 2, 12, 7),
-                                               ((1, 1), 2, 6, 4)])
-def test_conv_transpose_phases(ctx, tmp_path, k, stride, cin, cout):
-    """Sub-pixel phases on the matrix cores (any kernel at least the stride), and the scalar
-    kernel when a phase has no taps (1 x 1 with stride 2)."""
+@pytest.mark.parametrize("k,stride,cin,cout,hw,exact", [((3, 3), 1, 8, 5, (6, 9), False),
+                                                        ((2, 2), 2, 40, 16, (6, 9), False),
+                                                        ((3, 3), 2, 12, 7, (6, 9), False),
+                                                        ((1, 1), 2, 6, 4, (6, 9), False),
+                                                        ((2, 2), 2, 40, 16, (6, 9), True),
+                                                        ((2, 2), 2, 64, 32, (13, 37), True),
+                                                        ((2, 2), 2, 32, 48, (1, 1), True),
+                                                        ((3, 3), 3, 16, 16, (5, 4), True)])
+def test_conv_transpose_phases(ctx, tmp_path, k, stride, cin, cout, hw, exact):
+    """Sub-pixel phases on the matrix cores (any kernel at least the stride; kernel = stride with
+    float16-exact weights as one GEMM over the input pixels), and the scalar kernel when a phase
+    has no taps (1 x 1 with stride 2)."""
     def net(g, x):
         wt = RNG.standard_normal((cin, cout, *k)).astype(np.float32) * 0.3
+        if exact:
+            wt = f16x(wt)
         y = g.add("ConvTranspose", [x, g.init("w", wt), g.init("b", RNG.standard_normal(cout).astype(np.float32))],
                   kernel_shape=list(k), strides=[stride, stride])
         return g.add("Relu", [y])
-    p = build(tmp_path, "tp", net, (2, cin, 6, 9))
-    check(ctx, p, RNG.standard_normal((2, cin, 6, 9)).astype(np.float32))
+    p = build(tmp_path, "tp", net, (2, cin, *hw))
+    check(ctx, p, RNG.standard_normal((2, cin, *hw)).astype(np.float32))
 
 
 def test_conv_pool_fusion_single_and_dual(ctx, tmp_path):

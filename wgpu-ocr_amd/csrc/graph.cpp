@@ -235,6 +235,29 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     s.phases.push_back(std::move(ph));
                 }
             if (!ok) s.phases.clear();
+            if (ok && s.kh == st2 && s.kw == st2 && s.cout % 16 == 0) {
+                // [k * cout + co][ci] = w[ci][co][k / s][k % s]
+                const int nph = st2 * st2;
+                std::vector<float> cw(size_t(nph) * s.cout * s.cin);
+                for (int k = 0; k < nph; k++)
+                    for (int co = 0; co < s.cout; co++)
+                        for (int ci = 0; ci < s.cin; ci++)
+                            cw[(size_t(k) * s.cout + co) * s.cin + ci] =
+                                w.data[((size_t(ci) * s.cout + co) * s.kh + k / st2) * s.kw + k % st2];
+                Step::TPhase &ap = s.allph;
+                ap.ty = ap.tx = 1;
+                ap.pk = plan_conv_pack(s.cin, nph * s.cout, 1, 1);
+                std::vector<uint16_t> hi(ap.pk.halves()), lo(ap.pk.halves());
+                bool exact = true;
+                pack_conv_weights(ap.pk, cw.data(), hi.data(), lo.data(), &exact);
+                ap.pk.exact = exact;
+                if (exact) {
+                    ap.whi = ctx.upload_weights(hi.data(), hi.size());
+                    std::vector<uint16_t> frag(ap.pk.halves());
+                    pack_conv_frags(ap.pk, hi.data(), frag.data());
+                    ap.wfrag = ctx.upload_weights(frag.data(), frag.size());
+                }
+            }
         } else if (n.op == "MaxPool") {
             auto k = n.ints("kernel_shape");
             if (!k || k->size() != 2) fail("MaxPool without kernel_shape");
@@ -554,6 +577,20 @@ void Graph::Exec::step(size_t i) {
         if (s.phases.empty()) {
             conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
             break;
+        }
+        if (s.allph.whi) {
+            // All phases as one GEMM over the input pixels.
+            ConvArgs ca;
+            ca.x = a;
+            ca.y = y;
+            ca.wt_hi = s.allph.whi;
+            ca.wt_frag = s.allph.wfrag;
+            ca.bias = s.b;
+            ca.act = s.act;
+            ca.pk = s.allph.pk;
+            ca.ph_cout = s.cout;
+            ca.ph_s = s.sh;
+            if (conv_igemm(ca, st)) break;
         }
         for (const Step::TPhase &ph : s.phases) {
             const int st2 = s.sh;

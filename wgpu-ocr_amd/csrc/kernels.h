@@ -56,6 +56,10 @@ struct ConvArgs {
     // 1 x 1 GEMM over x = [1][1][M] pixels: GEMM row i reads x's row rows[i] and writes y's row
     // rows[i] (M = x.w entries), so only the listed rows are computed; or null (dense).
     const int *rows = nullptr;
+    // ConvTranspose with kernel = stride s as one 1 x 1 GEMM over the input pixels: output
+    // channel k * ph_cout + c of input pixel (i, j) is channel c of y's pixel
+    // (s i + k / s, s j + k % s) (conv_igemm only; 0: off).
+    int ph_cout = 0, ph_s = 0;
     ConvPack pk;
 };
 // True when the MFMA path takes this shape (stride 1, kernel at most 3 x 3).

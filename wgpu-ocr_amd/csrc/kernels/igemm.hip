@@ -58,6 +58,7 @@ struct IgParams {
     int cout;
     const float *bias;
     const int *rows;  // GEMM row map (gather x rows, scatter y rows), or null
+    int phc, phs, phw;  // ConvTranspose phases: channels a phase, stride, y's row length (0: off)
     int kw, pt, pl, act, chunks, taps;
     int th, tw, mx;   // tile rows and columns; row tiles per tile row of blocks
     int hw, hwp, halo_px;  // halo columns, padded row length, halo pixels
@@ -189,8 +190,15 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
     // Epilogue: lane (g, r) holds rows 4g..4g+3 of channel co_w + 16 j + r in each row tile.
 #pragma unroll
     for (int j = 0; j < NT; j++) {
-        const int co = co_w + 16 * j + r;
+        int co = co_w + 16 * j + r;
         if (co >= p.cout) continue;
+        // ConvTranspose phase k of channel co: its pixel offset in y and its own channel.
+        size_t phoff = 0;
+        if (p.phc) {
+            const int k = co / p.phc;
+            co -= k * p.phc;
+            phoff = size_t(k / p.phs) * p.phw + size_t(k % p.phs);
+        }
         const float bv = p.bias ? p.bias[co] : 0.f;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
@@ -218,7 +226,7 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
                 for (int i = 0; i < 4; i++) {
                     const int yy = oy + (i >> 1), xx = ox + (i & 1);
                     if (yy < p.oh && xx < p.ow)
-                        p.y[(size_t(img) * p.yn + size_t(yy) * p.yy + size_t(xx) * p.yx) * p.ycs + co] = v[i];
+                        p.y[(size_t(img) * p.yn + size_t(yy) * p.yy + size_t(xx) * p.yx + phoff) * p.ycs + co] = v[i];
                 }
             }
             if (p.pool == 1) {
@@ -275,7 +283,18 @@ void pack_conv_frags(const ConvPack &pk, const uint16_t *hi, uint16_t *frag) {
 bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     const ConvPack &pk = a.pk;
     if (a.nchw || a.in_scale || a.affine || a.amax_part || a.res || !pk.exact) return false;
-    if (pk.kh > 3 || pk.kw > 3 || pk.cin != a.x.c || pk.cout != a.y.c || a.y.n != a.x.n) return false;
+    const bool phm = a.ph_cout > 0;
+    if (phm) {
+        // All s x s phases of a ConvTranspose with kernel = stride: one 1 x 1 GEMM over x.
+        const int st = a.ph_s;
+        if (st < 1 || pk.kh != 1 || pk.kw != 1 || pk.cout != st * st * a.ph_cout || a.y.c != a.ph_cout ||
+            a.y.h != st * a.x.h || a.y.w != st * a.x.w || a.ypool.p || a.rows || a.y_px || a.y_row || a.y_img ||
+            a.pt || a.pl)
+            return false;
+    } else if (pk.cout != a.y.c) {
+        return false;
+    }
+    if (pk.kh > 3 || pk.kw > 3 || pk.cin != a.x.c || a.y.n != a.x.n) return false;
     if (a.x.c % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15)) return false;
     const bool pooled = a.ypool.p != nullptr;
     int pool = 0;
@@ -288,7 +307,7 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
             fail("conv_igemm: pooled output shape");
     }
     if (a.rows && (pk.kh != 1 || pk.kw != 1 || a.x.n != 1 || a.x.h != 1 || pooled)) return false;
-    const int cout = a.y.c;
+    const int cout = pk.cout;
     // Wavefront grid and channels per wavefront for this output width.
     int WM, WN, NT;
     if (cout <= 16) WM = 4, WN = 1, NT = 1;
@@ -310,6 +329,17 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     p.yx = a.y_px ? a.y_px : 1;
     p.yy = a.y_row ? a.y_row : long(p.ow) * p.yx;
     p.yn = a.y_img ? a.y_img : long(p.oh) * p.yy;
+    if (phm) {
+        // The GEMM's pixels are x's; y's pixel (s i + py, s j + px) is phase (py, px) of (i, j).
+        p.oh = a.x.h;
+        p.ow = a.x.w;
+        p.yx = a.ph_s;
+        p.yy = long(a.ph_s) * a.y.w;
+        p.yn = long(a.y.h) * a.y.w;
+        p.phc = a.ph_cout;
+        p.phs = a.ph_s;
+        p.phw = a.y.w;
+    }
     p.y = pooled && !a.keep_full ? nullptr : a.y.p;
     p.yp = a.ypool.p;
     p.poh = a.ypool.h;
@@ -331,7 +361,7 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
 
     // Tile shape: one row of bm pixels for a one-row input (GEMM rows); otherwise 2 x 8 blocks,
     // the column count that wastes the fewest pixels (padding and halo) for this output.
-    if (p.oh == 1 && p.h == 1 && pk.kh == 1 && !pooled) {
+    if (p.oh == 1 && p.h == 1 && pk.kh == 1 && !pooled && !phm) {
         p.lin = 1;
         p.th = 1;
         p.tw = bm;
