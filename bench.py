@@ -42,8 +42,36 @@ def roofline(kernels):
         out = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                "frac": achieved / HBM_PEAK_GBS}
     out.update({"kernel": fam, "calls": k["calls"], "avg_us": 1e3 * k["ms"] / max(k["calls"], 1),
-                "traffic": None})
+                "traffic": measured_traffic(fam)})
     return out
+
+
+def measured_traffic(fam):
+    """HBM bytes per launch of kernel family `fam` in this workload, as measured by rocprofv3
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters on a copy of known size)
+    and recorded in profiles/traffic_<family>.md as a `bytes_per_launch:` line; None if absent."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{fam}.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration():
+    """A device-to-device copy of 1 GiB, three times: the reference point for the HBM traffic
+    counters (run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+    n = 1 << 28
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": 4 * n, "copies": 3}))
 
 
 def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
@@ -105,7 +133,12 @@ def main():
     ap.add_argument("--det-batch", type=int, default=6, help="pages per detection pass")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-pp", action="store_true", help="skip the PP-OCR pipeline measurement")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 1 GiB device to device (the reference for traffic counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the pipeline shards by page with no exchange, so N GPUs run N "
               "independent copies with no collective; run it with --gpus 1.", file=sys.stderr)
