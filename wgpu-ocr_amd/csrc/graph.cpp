@@ -681,11 +681,62 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
 }
 
 std::vector<Graph::Out> Graph::run_multi(Ctx &ctx, const std::vector<Act> &xs) const {
+    std::vector<Out> outs;
+    run_multi_tm(ctx, xs, 0, nullptr, 0, outs);
+    return outs;
+}
+
+bool Graph::run_multi_time_major(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot,
+                                 std::vector<Out> &outs) const {
+    if (!X || kh != 2) fail("run_multi_time_major: X and an average pool over 2 rows");
+    return run_multi_tm(ctx, xs, kh, X, ntot, outs);
+}
+
+bool Graph::run_multi_tm(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot,
+                         std::vector<Out> &outs) const {
     std::vector<std::unique_ptr<Exec>> es;
     for (const Act &x : xs) es.emplace_back(new Exec(*this, ctx, x));
     std::vector<ConvArgs> cas;
     std::vector<Act> as, ys, yps;
+    outs.clear();
     for (size_t i = 0; i < steps.size(); i++) {
+        if (X && i + 1 == steps.size() && !es.empty()) {
+            // The last layer: conv + ReLU + MaxPool (2, 1) of four rows, then the average pool
+            // to one row, time-major, in the conv's epilogue.
+            const Step &s = steps[i];
+            bool all = s.pool_only && s.ph == 2 && s.pw == 1 && s.output == output;
+            for (auto &e : es) all = all && e->mfma_conv(i) && e->shp[i][1] * 2 == 4;
+            if (all) {
+                cas.clear();
+                int noff = 0;
+                for (auto &e : es) {
+                    const Act a = e->view.at(s.inputs[0]);
+                    ConvArgs ca;
+                    ca.x = a;
+                    ca.y = Act{nullptr, a.n, a.h + s.pt + s.pb - s.kh + 1, a.w + s.pl + s.pr - s.kw + 1, s.cout, s.cout};
+                    ca.ph = 2;
+                    ca.pw = 1;
+                    ca.keep_full = false;
+                    ca.wt_hi = s.whi;
+                    ca.wt_lo = s.wlo;
+                    ca.wt_frag = s.wfrag;
+                    ca.bias = s.b;
+                    ca.pt = s.pt;
+                    ca.pl = s.pl;
+                    ca.act = s.act;
+                    ca.pk = s.pk;
+                    ca.tm = X;
+                    ca.tm_ntot = ntot;
+                    ca.tm_noff = noff;
+                    noff += a.n;
+                    cas.push_back(ca);
+                }
+                if (noff <= ntot && conv3x3_dma_multi(cas.data(), int(cas.size()), ctx.stream())) {
+                    outs.resize(es.size());
+                    return true;
+                }
+            }
+        }
         bool all = !es.empty(), all1 = !es.empty();
         for (auto &e : es) all = all && e->mfma_conv(i), all1 = all1 && e->direct_mfma(i);
         if (all1 && es.size() > 1) {
@@ -715,9 +766,8 @@ std::vector<Graph::Out> Graph::run_multi(Ctx &ctx, const std::vector<Act> &xs) c
             for (auto &e : es) e->step(i);
         }
     }
-    std::vector<Out> out;
-    for (auto &e : es) out.push_back(e->result());
-    return out;
+    for (auto &e : es) outs.push_back(e->result());
+    return false;
 }
 
 }  // namespace ocr

@@ -66,12 +66,19 @@ class Graph {
     // The same on several inputs of one height and channel count (any widths and image counts):
     // each step for all of them before the next, a dense 3 x 3 conv as one launch over all.
     std::vector<Out> run_multi(Ctx &ctx, const std::vector<Act> &xs) const;
+    // The same, where the graph's output (a 2 x 1 MaxPool of a conv with 4 output rows) is
+    // followed by an AveragePool (kh, 1) to one row written time-major into X[t][ntot][c] at line
+    // offsets 0, n0, n0 + n1, ...: when the last layer can do that in its own epilogue it does,
+    // returns true and the outputs are left empty; otherwise returns false with the outputs.
+    bool run_multi_time_major(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot,
+                              std::vector<Out> &outs) const;
 
     std::string input, output;
     std::vector<Step> steps;
 
   private:
     struct Exec;
+    bool run_multi_tm(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot, std::vector<Out> &outs) const;
     std::vector<Shape> shapes(const Shape &in) const;  // output shape of every step
 };
 

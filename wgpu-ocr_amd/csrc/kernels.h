@@ -60,6 +60,11 @@ struct ConvArgs {
     // channel k * ph_cout + c of input pixel (i, j) is channel c of y's pixel
     // (s i + k / s, s j + k % s) (conv_igemm only; 0: off).
     int ph_cout = 0, ph_s = 0;
+    // conv3x3_dma only: with a 2 x 1 MaxPool of a 4-row output, the two pooled rows averaged into
+    // one (AveragePool (2, 1)) and written time-major: column t of image i to
+    // tm[(t * tm_ntot + tm_noff + i) * cout + c]; nothing else is written (0: off).
+    float *tm = nullptr;
+    int tm_ntot = 0, tm_noff = 0;
     ConvPack pk;
 };
 // True when the MFMA path takes this shape (stride 1, kernel at most 3 x 3).

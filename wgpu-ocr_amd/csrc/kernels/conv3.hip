@@ -63,13 +63,16 @@ struct C3Seg {
     const float *x;
     float *y, *yp;
     int n, w, ow, pow_, tiles_x, t0;  // t0: the segment's first tile in the launch
+    int noff;                         // pool mode 3: the segment's first line in tm
 };
 constexpr int C3MAXSEG = 32;
 
 struct C3Params {
     int h, cin, xcs;
     int oh, ycs;
-    int poh, ypcs, pool;
+    int poh, ypcs, pool;  // pool: 0 none, 1 = 2 x 2, 2 = 2 x 1, 3 = 2 x 1 then mean of 2 rows into tm
+    float *tm;
+    int tm_ntot;
     const half8 *wt;  // fragments [n-tile][slice][tap][64 lanes] of 8 halves
     int ntiles, cout, chunks;
     const float *bias;
@@ -122,7 +125,10 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     int abase[MT], pyb[MT], pxb[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-        const int mi = wm * MT + mt, mxi = mi % p.mx, myi = mi / p.mx, q = r & 3;
+        // Row tiles run along rows; in pool mode 3 (four output rows) down columns instead, so
+        // a lane's row tiles mt and mt + 1 are the same columns' rows 0-1 and 2-3.
+        const int mi = wm * MT + mt, q = r & 3;
+        const int mxi = p.pool == 3 ? mi >> 1 : mi % p.mx, myi = p.pool == 3 ? mi & 1 : mi / p.mx;
         pyb[mt] = 2 * myi, pxb[mt] = 8 * mxi;
         abase[mt] = (pyb[mt] + (q >> 1)) * p.rs + (pxb[mt] + 2 * (r >> 2) + (q & 1)) * PXU + g;
     }
@@ -273,6 +279,34 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
         float *pt = nullptr;
         if (POOL == 1) pt = sd.yp + (size_t(s.img) * p.poh * pow_ + size_t(oy0 / 2) * pow_ + ox0 / 2) * p.ypcs;
         if (POOL == 2) pt = sd.yp + (size_t(s.img) * p.poh * pow_ + size_t(oy0 / 2) * pow_ + ox0) * p.ypcs;
+        if (POOL == 3) {
+            // Row tiles mt (rows 0-1) and mt + 1 (rows 2-3) of the same columns: max over each
+            // pair of rows, then the mean of the two maxima, summed in row order as the
+            // average pool does.
+            const size_t line = size_t(sd.noff + s.img);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt += 2) {
+                const int t = ox0 + pxb[mt] + 2 * g;
+#pragma unroll
+                for (int j = 0; j < NT; j++) {
+                    float v[4], u[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        v[i] = act3(acc[mt][j][i] + bv[j], ACT);
+                        u[i] = act3(acc[mt + 1][j][i] + bv[j], ACT);
+                    }
+                    acc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    acc[mt + 1][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    const int co = co_l + 16 * j;
+                    if (CHECK && co >= p.cout) continue;
+                    float *dst = p.tm + (size_t(t) * p.tm_ntot + line) * p.cout + co;
+                    if (!CHECK || t < ow) dst[0] = (fmaxf(v[0], v[2]) + fmaxf(u[0], u[2])) / 2.f;
+                    if (!CHECK || t + 1 < ow)
+                        dst[size_t(p.tm_ntot) * p.cout] = (fmaxf(v[1], v[3]) + fmaxf(u[1], u[3])) / 2.f;
+                }
+            }
+            return;
+        }
         // The lane's parts of the offsets, computed here (not kept live across the tile loop).
         int lf = 2 * g * p.ycs + co_l, lp = (POOL == 1 ? g : 2 * g) * p.ypcs + co_l;
         asm volatile("" : "+v"(lf), "+v"(lp));
@@ -316,7 +350,9 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
             if (inside) epi(s, POOLc, std::false_type{});
             else epi(s, POOLc, std::true_type{});
         };
-        if (p.pool == 1)
+        if (p.pool == 3)
+            run(std::integral_constant<int, 3>{}, cin_ && ox0 + p.tw <= sd.ow);
+        else if (p.pool == 1)
             run(std::integral_constant<int, 1>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && (ox0 + p.tw) / 2 <= sd.pow_);
         else if (p.pool == 2)
             run(std::integral_constant<int, 2>{}, cin_ && (oy0 + p.th) / 2 <= p.poh && ox0 + p.tw <= sd.pow_);
@@ -408,6 +444,13 @@ int c3_accepts(const ConvArgs &a) {
     if (a.act != ACT_NONE && a.act != ACT_RELU && a.act != ACT_SIGMOID) return -1;
     // 32-bit offsets within one image of the input, the output and the pooled output.
     if (double(a.x.h) * a.x.w * a.x.cs >= 2147483647.0 || double(a.y.h) * a.y.w * a.y.cs >= 2147483647.0) return -1;
+    if (a.tm) {
+        // Max pool (2, 1) and the mean of the two pooled rows, time-major; nothing else written.
+        if (a.ph != 2 || a.pw != 1 || a.y.h != 4 || a.ypool.p || a.keep_full || a.tm_ntot < 1 || a.tm_noff < 0 ||
+            a.tm_noff + a.y.n > a.tm_ntot)
+            return -1;
+        return 3;
+    }
     if (!a.ypool.p) return 0;
     int pool;
     if (a.ph == 2 && a.pw == 2) pool = 1;
@@ -439,8 +482,11 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     p.bias = a.bias;
     // Tile: 16 blocks of 2 x 8 pixels; the shape wasting the fewest pixels (over all segments)
     // whose halo fits.
+    p.tm = a.tm;
+    p.tm_ntot = a.tm_ntot;
     double best = 1e300;
     for (int mxc : {1, 2, 4, 8}) {
+        if (pool == 3 && mxc != 8) continue;  // four rows: the whole output height in one tile
         const int tw = 8 * mxc, th = 2 * (16 / mxc), hw = tw + 2, hh = th + 2;
         const int rs = 9 * hw + (24 - 9 * hw % 16) % 16;  // 8 mod 16 units
         if (hh * hw > HPX || hh * rs > HSU) continue;
@@ -461,8 +507,9 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
         const ConvArgs &b = args[k];
         C3Seg &sg = p.seg[k];
         sg.x = b.x.p;
-        sg.y = b.ypool.p && !b.keep_full ? nullptr : b.y.p;
+        sg.y = (b.ypool.p && !b.keep_full) || pool == 3 ? nullptr : b.y.p;
         sg.yp = b.ypool.p;
+        sg.noff = b.tm_noff;
         sg.n = b.x.n;
         sg.w = b.x.w;
         sg.ow = b.y.w;
@@ -471,7 +518,12 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
         sg.t0 = int(tiles);
         tiles += double(sg.tiles_x) * p.tiles_y * sg.n;
         flops += 2.0 * b.y.n * b.y.h * b.y.w * cout * p.cin * 9;
-        bytes += 4.0 * (double(b.x.n) * b.x.h * b.x.w * p.cin + double(b.y.n) * b.y.h * b.y.w * cout);
+        // Algorithmic bytes: the input once and every output actually stored.
+        double out = 0;
+        if (sg.y) out += double(b.y.n) * b.y.h * b.y.w;
+        if (sg.yp) out += double(b.ypool.n) * b.ypool.h * b.ypool.w;
+        if (pool == 3) out += double(b.y.n) * b.y.w;
+        bytes += 4.0 * (double(b.x.n) * b.x.h * b.x.w * p.cin + out * cout);
         if (tiles > 0x7fffffff) fail("conv3x3_dma: too many tiles");
     }
     p.nseg = count;
@@ -510,7 +562,8 @@ bool conv3x3_dma_multi(const ConvArgs *args, int count, hipStream_t s) {
     if (pool < 0) return false;
     for (int k = 1; k < count; k++) {
         const ConvArgs &b = args[k];
-        if (c3_accepts(b) != pool || b.wt_frag != a.wt_frag || b.bias != a.bias || b.act != a.act ||
+        if (c3_accepts(b) != pool || b.tm != a.tm || b.tm_ntot != a.tm_ntot || b.wt_frag != a.wt_frag ||
+            b.bias != a.bias || b.act != a.act ||
             b.x.h != a.x.h || b.x.c != a.x.c || b.x.cs != a.x.cs || b.y.c != a.y.c || b.y.cs != a.y.cs ||
             b.ypool.cs != a.ypool.cs || (b.ypool.p && !b.keep_full) != (a.ypool.p && !a.keep_full) ||
             b.pk.chunks != a.pk.chunks)

@@ -177,23 +177,28 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     // The trunks first (gpu.rs:1516-1526). The width batches share the 64-row height, so each
     // trunk layer runs once over all of them: one launch a dense conv layer fills the GPU where
     // a launch per width batch would not.
+    // The average pool (gpu.rs:595-614) runs in the last trunk layer's epilogue when that layer
+    // takes it, else as its own kernel over all width batches.
     std::vector<Act> xs;
-    for (int b = 0; b < count; b++)
-        xs.push_back(Act{const_cast<float *>(batches[b].data), batches[b].n, 64, batches[b].w, 1, 1});
-    std::vector<Graph::Out> trunks = trunk_.run_multi(ctx_, xs);
-    std::vector<Act> feats;
     int noff = 0;
     for (int b = 0; b < count; b++) {
-        const Act &t = trunks[size_t(b)].act;
-        if (t.c != layers_[0].input)
-            fail("trunk gives " + std::to_string(t.c) + " features, GRU takes " + std::to_string(layers_[0].input));
-        if ((t.h - pool_kh_) / pool_kh_ + 1 != 1)
-            fail("trunk height " + std::to_string(t.h) + " does not pool to one row");
-        feats.push_back(t);
-        for (int i = 0; i < t.n; i++) lens[noff + i] = uint32_t(t.w);
-        noff += t.n;
+        xs.push_back(Act{const_cast<float *>(batches[b].data), batches[b].n, 64, batches[b].w, 1, 1});
+        const Shape t = trunk_.infer({batches[b].n, 64, batches[b].w, 1});
+        if (t[3] != layers_[0].input)
+            fail("trunk gives " + std::to_string(t[3]) + " features, GRU takes " + std::to_string(layers_[0].input));
+        if ((t[1] - pool_kh_) / pool_kh_ + 1 != 1)
+            fail("trunk height " + std::to_string(t[1]) + " does not pool to one row");
+        for (int i = 0; i < t[0]; i++) lens[noff + i] = uint32_t(t[2]);
+        noff += t[0];
     }
-    avgpool_t(feats.data(), count, pool_kh_, X.as<float>(), d.ntot, st);
+    std::vector<Graph::Out> trunks;
+    const bool fused = pool_kh_ == 2 && trunk_.run_multi_time_major(ctx_, xs, pool_kh_, X.as<float>(), d.ntot, trunks);
+    if (!fused) {
+        if (pool_kh_ != 2) trunks = trunk_.run_multi(ctx_, xs);
+        std::vector<Act> feats;
+        for (const Graph::Out &t : trunks) feats.push_back(t.act);
+        avgpool_t(feats.data(), count, pool_kh_, X.as<float>(), d.ntot, st);
+    }
     const int tmax = d.tmax, ntot = d.ntot;
     trunks.clear();
     // The rows that carry a step of some line, t-major: (t, line) with t < lens[line]. The
