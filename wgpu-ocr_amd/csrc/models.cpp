@@ -205,10 +205,25 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     // projections and the output layer run on these rows only (the reference computes all
     // tmax x ntot rows and ignores the padding ones); G, Y and the logits keep the [t][ntot]
     // layout, so the recurrence and the caller see the reference's layout.
+    // Lines come in batches of one length each: per step, the runs of lines still going.
     std::vector<int32_t> rows;
-    for (int t = 0; t < tmax; t++)
-        for (int i = 0; i < ntot; i++)
-            if (uint32_t(t) < lens[i]) rows.push_back(t * ntot + i);
+    {
+        std::vector<std::pair<int, int>> runs;  // (first line, length) of each batch
+        size_t total = 0;
+        for (int i = 0; i < ntot;) {
+            int j = i + 1;
+            while (j < ntot && lens[j] == lens[i]) j++;
+            runs.push_back({i, j});
+            total += size_t(j - i) * lens[i];
+            i = j;
+        }
+        rows.resize(total);
+        size_t k = 0;
+        for (int t = 0; t < tmax; t++)
+            for (const auto &rn : runs)
+                if (uint32_t(t) < lens[rn.first])
+                    for (int i = rn.first; i < rn.second; i++) rows[k++] = t * ntot + i;
+    }
     const int P = int(rows.size());
     const long long steps = P;
     DBuf rowsd(&ctx_, rows.size() * sizeof(int32_t));

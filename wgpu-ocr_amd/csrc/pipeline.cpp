@@ -37,6 +37,12 @@ PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float rel
     std::vector<int> out_w;
     for (const LineGeom &g : L.lines) out_w.push_back(g.out_w);
     L.plan = plan_batches(out_w);
+    for (const LineGeom &g : L.lines) {
+        L.line_row0.push_back(int32_t(L.row_off.size()));
+        const int32_t sbase = int32_t(L.spans.size());
+        for (int32_t o : g.row_off) L.row_off.push_back(o + sbase);
+        L.spans.insert(L.spans.end(), g.spans.begin(), g.spans.end());
+    }
     return L;
 }
 
@@ -48,12 +54,12 @@ struct Pipeline::Impl {
     PipelineOpts opts;
     Workers workers;
     std::vector<Pinned> bits_host, best_host;
-    // Threads one page's layout uses (its word boxes in row bands, its lines side by side): the
-    // host cores shared by the pages of a detection pass.
-    int layout_threads;
+    // Host threads the layouts of one recognition pass share (a page's word boxes in row bands,
+    // its lines side by side).
+    int host_threads;
     explicit Impl(Ctx &c, Detector &d, Recognizer &r, const PipelineOpts &o, int nthreads)
         : ctx(c), det(d), rec(r), opts(o), workers(nthreads),
-          layout_threads(std::max(1, std::min(4, (int(std::thread::hardware_concurrency()) + o.det_batch - 1) / std::max(1, o.det_batch)))) {}
+          host_threads(std::max(1, int(std::thread::hardware_concurrency()))) {}
 };
 
 Pipeline::Pipeline(Ctx &ctx, Detector &det, Recognizer &rec, const PipelineOpts &opts)
@@ -98,20 +104,30 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         cv.notify_all();
     };
 
-    // 1. Detection of every page, at most det_batch pages a pass and never across a recognition
-    // pass's pages: the first pass's layouts then start while the later pages are still being
-    // detected. The first group is a third of det_batch (at least one page), so the host starts
-    // on layouts while the GPU detects the rest of the first pass. The bit masks come back
-    // asynchronously.
-    const int nrec = (npages + I.opts.merge - 1) / I.opts.merge;
+    // Recognition passes of `merge` pages, in page order.
+    std::vector<int> pass_p0;
+    for (int p = 0; p < npages; p += I.opts.merge) pass_p0.push_back(p);
+    pass_p0.push_back(npages);
+    const int nrec = int(pass_p0.size()) - 1;
+    // 1. Detection of every page in groups of at most det_batch pages (near-equal sizes) that
+    // never straddle a recognition pass: the first pass's layouts then start while the later
+    // pages are still being detected. The first group is a third of det_batch (at least one
+    // page), so the host starts on layouts early. The bit masks come back asynchronously.
     std::vector<int> group_of(static_cast<size_t>(npages)), group_p0;
     for (int r = 0; r < nrec; r++) {
-        const int r0 = r * I.opts.merge, r1 = std::min(npages, r0 + I.opts.merge);
-        const int first = r == 0 ? std::max(1, I.opts.det_batch / 3) : I.opts.det_batch;
-        for (int p = r0; p < r1; p++) {
-            const int k = p - r0;
-            if (k == 0 || (k >= first && (k - first) % I.opts.det_batch == 0)) group_p0.push_back(p);
-            group_of[size_t(p)] = int(group_p0.size()) - 1;
+        int q0 = pass_p0[size_t(r)];
+        const int r1 = pass_p0[size_t(r) + 1];
+        if (r == 0 && r1 - q0 > 1) {
+            const int first = std::min(r1 - q0, std::max(1, I.opts.det_batch / 3));
+            group_p0.push_back(q0);
+            for (int p = q0; p < q0 + first; p++) group_of[size_t(p)] = int(group_p0.size()) - 1;
+            q0 += first;
+        }
+        const int ng = (r1 - q0 + I.opts.det_batch - 1) / I.opts.det_batch;
+        for (int k = 0; k < ng; k++) {
+            const int g0 = q0 + int(long(r1 - q0) * k / ng), g1 = q0 + int(long(r1 - q0) * (k + 1) / ng);
+            group_p0.push_back(g0);
+            for (int p = g0; p < g1; p++) group_of[size_t(p)] = int(group_p0.size()) - 1;
         }
     }
     const int ngroups = int(group_p0.size());
@@ -150,7 +166,9 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         OCR_HIP(hipEventRecord(det_ev[size_t(g)], st));
         mark("det group " + std::to_string(g) + " enqueued");
     }
-    // 2. Host layout of each page as soon as its mask is on the host.
+    // 2. Host layout of each page once its mask is on the host and every page of the earlier
+    // recognition passes is laid out (the pass needed first gets the host cores first), with
+    // the host's threads shared among the pages of its pass.
     const int dev = ctx.device();
     for (int p = 0; p < npages; p++) {
         {
@@ -160,15 +178,27 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         hipEvent_t ev = det_ev[size_t(group_of[size_t(p)])];
         const uint32_t *bits = static_cast<const uint32_t *>(I.bits_host[size_t(p)].p);
         const int pw = w[p], ph = h[p];
-        I.workers.submit([&, p, ev, bits, pw, ph, dev] {
+        int pr = 0;
+        while (pass_p0[size_t(pr) + 1] <= p) pr++;
+        const int before = pass_p0[size_t(pr)];
+        const int threads = std::max(1, std::min(8, I.host_threads / (pass_p0[size_t(pr) + 1] - before)));
+        I.workers.submit([&, p, ev, bits, pw, ph, dev, before, threads] {
             std::string err;
             double busy = 0;
             try {
                 (void)hipSetDevice(dev);
                 OCR_HIP(hipEventSynchronize(ev));
+                {
+                    std::unique_lock<std::mutex> lk(mu);
+                    cv.wait(lk, [&] {
+                        for (int q = 0; q < before; q++)
+                            if (!layout_ready[size_t(q)]) return false;
+                        return true;
+                    });
+                }
                 mark("layout " + std::to_string(p) + " start");
                 const auto tc = Clock::now();
-                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, I.layout_threads);
+                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads);
                 busy = ms_since(tc);
                 mark("layout " + std::to_string(p) + " done");
                 std::lock_guard<std::mutex> lk(mu);
@@ -182,10 +212,10 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             task_done(busy, err);
         });
     }
-    // 3. Recognition, `merge` pages a pass, in page order.
+    // 3. Recognition, pass by pass in page order.
     if (I.best_host.size() < size_t(nrec)) I.best_host.resize(size_t(nrec));
     for (int r = 0; r < nrec; r++) {
-        const int p0 = r * I.opts.merge, p1 = std::min(npages, p0 + I.opts.merge);
+        const int p0 = pass_p0[size_t(r)], p1 = pass_p0[size_t(r) + 1];
         {
             std::unique_lock<std::mutex> lk(mu);
             cv.wait(lk, [&] {
@@ -201,6 +231,17 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         // share the batch, so every page's batches of one width run as one trunk batch: the
         // same results with fewer, fuller launches. Widths ascending, pages and batches in order.
         std::map<int, std::vector<std::pair<int, int>>> by_width;  // width -> (page, line)
+        // The pages' row offsets and spans, appended page by page (offsets rebased).
+        std::vector<int> page_row0(size_t(p1 - p0));
+        for (int p = p0; p < p1; p++) {
+            const PageLayout &L = layouts[size_t(p)];
+            page_row0[size_t(p - p0)] = int(R.row_off.size());
+            const int32_t sbase = int32_t(R.spans.size());
+            const size_t r0 = R.row_off.size();
+            R.row_off.resize(r0 + L.row_off.size());
+            for (size_t k = 0; k < L.row_off.size(); k++) R.row_off[r0 + k] = L.row_off[k] + sbase;
+            R.spans.insert(R.spans.end(), L.spans.begin(), L.spans.end());
+        }
         for (int p = p0; p < p1; p++) {
             const PageLayout &L = layouts[size_t(p)];
             pages_[size_t(p)].words = L.words;
@@ -219,12 +260,10 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             batches.push_back({base, n, wb});
             for (int k = 0; k < n; k++) {
                 const int p = kv.second[size_t(k)].first, li = kv.second[size_t(k)].second;
-                const LineGeom &g = layouts[size_t(p)].lines[size_t(li)];
+                const PageLayout &L = layouts[size_t(p)];
+                const LineGeom &g = L.lines[size_t(li)];
                 CropLine c{d_rgb[p], w[p], h[p], g.left, g.top, g.bw, g.bh, g.out_w,
-                           int(R.row_off.size()), base + size_t(k) * LINE_H * wb, wb};
-                const int sbase = int(R.spans.size());
-                for (int32_t o : g.row_off) R.row_off.push_back(o + sbase);
-                R.spans.insert(R.spans.end(), g.spans.begin(), g.spans.end());
+                           page_row0[size_t(p - p0)] + L.line_row0[size_t(li)], base + size_t(k) * LINE_H * wb, wb};
                 R.crops.push_back(c);
                 R.rows.push_back({p, li});
                 R.widths.push_back(g.out_w);

@@ -37,6 +37,9 @@ struct PageLayout {
     int words = 0;
     std::vector<LineGeom> lines;
     BatchPlan plan;
+    // Every line's row offsets and spans one after another: line i's offsets start at
+    // row_off[line_row0[i]] and index this page's spans.
+    std::vector<int32_t> row_off, spans, line_row0;
 };
 PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads = 1);
 
