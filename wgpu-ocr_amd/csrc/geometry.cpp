@@ -1,5 +1,7 @@
 #include "geometry.h"
 
+#include "host_util.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -147,32 +149,42 @@ struct BandComps {
 
 BandComps band_components(const uint32_t *bits, int w, int y0, int y1) {
     const int words = (w + 31) / 32, h = y1 - y0;
+    const uint32_t last_mask = (w & 31) ? (1u << (w & 31)) - 1 : ~0u;
     std::vector<Run> runs;
+    runs.reserve(size_t(h) * 16);
     std::vector<int> row_start(size_t(h) + 1, 0);
     for (int y = y0; y < y1; y++) {
         row_start[size_t(y - y0)] = int(runs.size());
         const uint32_t *row = bits + size_t(y) * words;
-        int x = 0;
-        while (x < w) {
-            // next set bit at or after x
-            int wi = x >> 5;
-            uint32_t word = row[wi] & (~0u << (x & 31));
-            while (!word && ++wi < words) word = row[wi];
-            if (!word) break;
-            const int start = (wi << 5) + __builtin_ctz(word);
-            if (start >= w) break;
-            // next clear bit at or after start
-            int wj = start >> 5;
-            uint32_t inv = ~row[wj] & (~0u << (start & 31));
-            while (!inv && ++wj < words) inv = ~row[wj];
-            int end = inv ? (wj << 5) + __builtin_ctz(inv) : words * 32;
-            end = std::min(end, w);
-            runs.push_back({y, start, end - 1});
-            x = end;
+        uint32_t any = row[words - 1] & last_mask;
+        for (int wi = 0; wi + 1 < words; wi++) any |= row[wi];
+        if (!any) continue;
+        // Runs from the row's bit transitions: bit b of t is set where pixel b differs from
+        // pixel b - 1 (pixel -1 and pixels past w are background).
+        int start = -1;
+        uint32_t prev = 0;
+        for (int wi = 0; wi < words; wi++) {
+            const uint32_t word = wi + 1 == words ? row[wi] & last_mask : row[wi];
+            uint32_t t = word ^ ((word << 1) | prev);
+            prev = word >> 31;
+            while (t) {
+                const int b = __builtin_ctz(t);
+                t &= t - 1;
+                const int x = (wi << 5) + b;
+                if ((word >> b) & 1u) {
+                    start = x;
+                } else {
+                    runs.push_back({y, start, x - 1});
+                    start = -1;
+                }
+            }
         }
+        if (start >= 0) runs.push_back({y, start, w - 1});
     }
     row_start[size_t(h)] = int(runs.size());
-    // Union the runs of neighbouring rows that touch with 8-connectivity.
+    // Union the runs of neighbouring rows that touch with 8-connectivity. A parent always has a
+    // smaller index than its child (roots link to the smaller root; a run still alone joins
+    // the root of the run above it).
     std::vector<int> parent(runs.size());
     std::iota(parent.begin(), parent.end(), 0);
     for (int y = 1; y < h; y++) {
@@ -181,26 +193,41 @@ BandComps band_components(const uint32_t *bits, int w, int y0, int y1) {
         while (i < ie && j < je) {
             const Run &a = runs[size_t(i)], &b = runs[size_t(j)];
             if (a.x1 + 1 >= b.x0 && b.x1 + 1 >= a.x0) {
-                int ra = find(parent, i), rb = find(parent, j);
-                if (ra != rb) parent[size_t(std::max(ra, rb))] = std::min(ra, rb);
+                if (parent[size_t(j)] == j) {
+                    parent[size_t(j)] = find(parent, i);
+                } else {
+                    const int ra = find(parent, i), rb = find(parent, j);
+                    if (ra != rb) parent[size_t(std::max(ra, rb))] = std::min(ra, rb);
+                }
             }
             if (a.x1 < b.x1) i++;
             else j++;
         }
     }
+    // Every run's root in one forward pass (its parent's root is already final).
+    for (size_t r = 0; r < runs.size(); r++) parent[r] = parent[size_t(parent[r])];
     // Row extremes per component (components in order of their first run). Runs are listed row
     // by row and left to right, so a component's later run in the same row only moves its right
     // end.
     BandComps out;
     std::vector<int> comp(runs.size(), -1), run_comp(runs.size());
+    // Component ids in order of first run, and room for two points a row.
+    std::vector<int> npts, last_y;
     for (size_t r = 0; r < runs.size(); r++) {
-        const int root = find(parent, int(r));
+        const int root = parent[r];
         if (comp[size_t(root)] < 0) {
-            comp[size_t(root)] = int(out.pts.size());
-            out.pts.emplace_back();
+            comp[size_t(root)] = int(npts.size());
+            npts.push_back(0);
+            last_y.push_back(-1);
         }
-        run_comp[r] = comp[size_t(root)];
-        auto &v = out.pts[size_t(comp[size_t(root)])];
+        const int c = comp[size_t(root)];
+        run_comp[r] = c;
+        if (last_y[size_t(c)] != runs[r].y) npts[size_t(c)] += 2, last_y[size_t(c)] = runs[r].y;
+    }
+    out.pts.resize(npts.size());
+    for (size_t c = 0; c < npts.size(); c++) out.pts[c].reserve(size_t(npts[c]));
+    for (size_t r = 0; r < runs.size(); r++) {
+        auto &v = out.pts[size_t(run_comp[r])];
         const float y = float(runs[r].y), x0 = float(runs[r].x0), x1 = float(runs[r].x1);
         const bool same_row = !v.empty() && v.back().y == y;
         if (same_row) {
@@ -236,23 +263,29 @@ std::vector<Pt> merge_rows(std::vector<Pt> all) {
     return out;
 }
 
-// fn(i) for i in [0, n) on `threads` threads (the caller's included), contiguous chunks.
+thread_local int t_loop_prio = 0;
+
+// fn(i) for i in [0, n): on the calling thread alone when threads is 1, else in contiguous
+// chunks (up to 4 per thread, for balance) on the caller and the shared loop pool, at this
+// thread's loop priority.
 template <class F> void parallel_for(int n, int threads, F fn) {
     threads = std::max(1, std::min(threads, n));
     if (threads == 1) {
         for (int i = 0; i < n; i++) fn(i);
         return;
     }
-    std::vector<std::thread> th;
-    auto chunk = [&](int t) {
-        for (int i = int(long(n) * t / threads); i < int(long(n) * (t + 1) / threads); i++) fn(i);
-    };
-    for (int t = 1; t < threads; t++) th.emplace_back(chunk, t);
-    chunk(0);
-    for (auto &t : th) t.join();
+    const int chunks = std::min(n, 4 * threads);
+    LoopPool::get().run(
+        chunks,
+        [&](int t) {
+            for (int i = int(long(n) * t / chunks); i < int(long(n) * (t + 1) / chunks); i++) fn(i);
+        },
+        t_loop_prio);
 }
 
 }  // namespace
+
+void set_loop_priority(int prio) { t_loop_prio = prio; }
 
 // Every 8-connected component of a bit mask (h rows of ceil(w / 32) words) as its rows'
 // leftmost and rightmost pixels, rows ascending, in order of its first run (row-major). With

@@ -23,6 +23,10 @@ struct RRect {
     void resize(float nw, float nh) { w = nw; h = nh; }
 };
 
+// Priority of this thread's parallel loops (word boxes, line geometry) in the shared host loop
+// pool: lower runs first.
+void set_loop_priority(int prio);
+
 // word_rects (ocr-bench.rs:40-60): 8-connected components of the mask (h rows of ceil(w/32)
 // words), each component's minimum-area rectangle over its pixels, grown by `expand` on every
 // side, kept when its area is at least min_area; on `threads` threads (the same result).

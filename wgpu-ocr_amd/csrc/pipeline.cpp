@@ -16,7 +16,20 @@
 
 namespace ocr {
 
-PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads) {
+// Waits for a GPU event by polling every 20 microseconds: the worker threads waiting for
+// detection or recognition results sleep instead of spinning, so the host cores go to the
+// layouts.
+static void wait_event(hipEvent_t ev) {
+    for (;;) {
+        const hipError_t e = hipEventQuery(ev);
+        if (e == hipSuccess) return;
+        if (e != hipErrorNotReady) OCR_HIP(e);
+        std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+}
+
+PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads, int page_prio) {
+    set_loop_priority(page_prio);
     PageLayout L;
     std::vector<RRect> words = word_rects(bits, w, h, 3.f, 100.f, threads);
     L.words = int(words.size());
@@ -25,15 +38,12 @@ PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float rel
     lines.erase(std::remove_if(lines.begin(), lines.end(), [](const std::vector<RRect> &l) { return l.empty(); }),
                 lines.end());
     L.lines.resize(lines.size());
-    const int nt = std::max(1, std::min(threads, int(lines.size())));
-    std::vector<std::thread> th;
-    auto chunk = [&](int t) {
-        for (size_t i = lines.size() * size_t(t) / size_t(nt); i < lines.size() * size_t(t + 1) / size_t(nt); i++)
-            L.lines[i] = line_geometry(lines[i]);
-    };
-    for (int t = 1; t < nt; t++) th.emplace_back(chunk, t);
-    chunk(0);
-    for (auto &t : th) t.join();
+    const int n = int(lines.size());
+    if (threads <= 1) {
+        for (int i = 0; i < n; i++) L.lines[size_t(i)] = line_geometry(lines[size_t(i)]);
+    } else {
+        LoopPool::get().run(n, [&](int i) { L.lines[size_t(i)] = line_geometry(lines[size_t(i)]); }, page_prio);
+    }
     std::vector<int> out_w;
     for (const LineGeom &g : L.lines) out_w.push_back(g.out_w);
     L.plan = plan_batches(out_w);
@@ -142,6 +152,14 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         std::vector<int32_t> row_off, spans;
     };
     std::vector<RecPass> passes(static_cast<size_t>(nrec));
+    // Detection groups completed so far (set by the watcher thread below).
+    int det_done = 0;
+    struct Joiner {
+        std::thread t;
+        ~Joiner() {
+            if (t.joinable()) t.join();
+        }
+    } watcher;
     // Worker tasks refer to the locals above: whatever happens, wait for them before returning.
     try {
     if (I.bits_host.size() < size_t(npages)) I.bits_host.resize(size_t(npages));
@@ -162,43 +180,64 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         for (int p = p0; p < p1; p++)
             OCR_HIP(hipMemcpyAsync(I.bits_host[size_t(p)].p, bp[size_t(p - p0)], words_of[size_t(p)] * 4,
                                    hipMemcpyDeviceToHost, st));
-        OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming));
+        OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming | hipEventBlockingSync));
         OCR_HIP(hipEventRecord(det_ev[size_t(g)], st));
         mark("det group " + std::to_string(g) + " enqueued");
     }
-    // 2. Host layout of each page once its mask is on the host and every page of the earlier
-    // recognition passes is laid out (the pass needed first gets the host cores first), with
-    // the host's threads shared among the pages of its pass.
+    // One thread waits for the detection groups in order and wakes the layouts; the layout
+    // tasks sleep meanwhile, so the host cores go to the layouts that can run.
     const int dev = ctx.device();
+    watcher.t = std::thread([&, dev] {
+        std::string err;
+        try {
+            (void)hipSetDevice(dev);
+            for (int g = 0; g < ngroups; g++) {
+                OCR_HIP(hipEventSynchronize(det_ev[size_t(g)]));
+                std::lock_guard<std::mutex> lk(mu);
+                det_done = g + 1;
+                cv.notify_all();
+            }
+        } catch (const std::exception &e) {
+            err = e.what();
+        }
+        std::lock_guard<std::mutex> lk(mu);
+        if (!err.empty() && error.empty()) error = err;
+        det_done = ngroups;
+        cv.notify_all();
+    });
+    // 2. Host layout of each page once its mask is on the host and every page of the earlier
+    // recognition passes is laid out; its loops run on the shared host loop pool, earlier pages
+    // first.
     for (int p = 0; p < npages; p++) {
         {
             std::lock_guard<std::mutex> lk(mu);
             pending_tasks++;
         }
-        hipEvent_t ev = det_ev[size_t(group_of[size_t(p)])];
+        const int grp = group_of[size_t(p)];
         const uint32_t *bits = static_cast<const uint32_t *>(I.bits_host[size_t(p)].p);
         const int pw = w[p], ph = h[p];
         int pr = 0;
         while (pass_p0[size_t(pr) + 1] <= p) pr++;
-        const int before = pass_p0[size_t(pr)];
-        const int threads = std::max(1, std::min(8, I.host_threads / (pass_p0[size_t(pr) + 1] - before)));
-        I.workers.submit([&, p, ev, bits, pw, ph, dev, before, threads] {
+        const int before = pass_p0[size_t(pr)], threads = I.host_threads;
+        I.workers.submit([&, p, grp, bits, pw, ph, dev, before, threads] {
             std::string err;
             double busy = 0;
             try {
                 (void)hipSetDevice(dev);
-                OCR_HIP(hipEventSynchronize(ev));
                 {
                     std::unique_lock<std::mutex> lk(mu);
                     cv.wait(lk, [&] {
+                        if (!error.empty()) return true;
+                        if (det_done <= grp) return false;
                         for (int q = 0; q < before; q++)
                             if (!layout_ready[size_t(q)]) return false;
                         return true;
                     });
+                    if (!error.empty()) fail("an earlier step failed");
                 }
                 mark("layout " + std::to_string(p) + " start");
                 const auto tc = Clock::now();
-                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads);
+                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads, p);
                 busy = ms_since(tc);
                 mark("layout " + std::to_string(p) + " done");
                 std::lock_guard<std::mutex> lk(mu);
@@ -302,7 +341,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             double busy = 0;
             try {
                 (void)hipSetDevice(dev);
-                OCR_HIP(hipEventSynchronize(ev));
+                wait_event(ev);
                 const auto tc = Clock::now();
                 const RecPass &R2 = passes[size_t(r)];
                 for (size_t j = 0; j < R2.rows.size(); j++) {

@@ -41,7 +41,9 @@ struct PageLayout {
     // row_off[line_row0[i]] and index this page's spans.
     std::vector<int32_t> row_off, spans, line_row0;
 };
-PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads = 1);
+// threads > 1: its loops run on the shared host loop pool at priority page_prio (lower first).
+PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads = 1,
+                       int page_prio = 0);
 
 class Pipeline {
   public:
