@@ -158,7 +158,9 @@ def test_conv_transpose_2x3(ctx, tmp_path):
                                                         ((2, 2), 2, 40, 16, (6, 9), True),
                                                         ((2, 2), 2, 64, 32, (13, 37), True),
                                                         ((2, 2), 2, 32, 48, (1, 1), True),
-                                                        ((3, 3), 3, 16, 16, (5, 4), True)])
+                                                        ((3, 3), 3, 16, 16, (5, 4), True),
+                                                        ((3, 3), 2, 16, 16, (5, 7), True),
+                                                        ((2, 3), 2, 32, 16, (4, 5), True)])
 def test_conv_transpose_phases(ctx, tmp_path, k, stride, cin, cout, hw, exact):
     """Sub-pixel phases on the matrix cores (any kernel at least the stride; kernel = stride with
     float16-exact weights as one GEMM over the input pixels), and the scalar kernel when a phase

@@ -235,18 +235,27 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     s.phases.push_back(std::move(ph));
                 }
             if (!ok) s.phases.clear();
-            if (ok && s.kh == st2 && s.kw == st2 && s.cout % 16 == 0) {
-                // [k * cout + co][ci] = w[ci][co][k / s][k % s]
+            const int aty = (s.kh + st2 - 1) / st2, atx = (s.kw + st2 - 1) / st2;
+            if (ok && s.cout % 16 == 0 && aty <= 3 && atx <= 3) {
+                // All phases as one conv over the input: output channel k * cout + co is phase
+                // k = py * s + px; tap (a, b) of the aty x atx kernel (leading pads aty - 1,
+                // atx - 1) reads x[i - (aty - 1 - a)][j - (atx - 1 - b)], i.e. the weight of
+                // ky = py + s (aty - 1 - a), kx = px + s (atx - 1 - b) (zero past the kernel).
                 const int nph = st2 * st2;
-                std::vector<float> cw(size_t(nph) * s.cout * s.cin);
+                std::vector<float> cw(size_t(nph) * s.cout * s.cin * aty * atx, 0.f);
                 for (int k = 0; k < nph; k++)
                     for (int co = 0; co < s.cout; co++)
                         for (int ci = 0; ci < s.cin; ci++)
-                            cw[(size_t(k) * s.cout + co) * s.cin + ci] =
-                                w.data[((size_t(ci) * s.cout + co) * s.kh + k / st2) * s.kw + k % st2];
+                            for (int a2 = 0; a2 < aty; a2++)
+                                for (int b2 = 0; b2 < atx; b2++) {
+                                    const int ky = k / st2 + st2 * (aty - 1 - a2), kx = k % st2 + st2 * (atx - 1 - b2);
+                                    if (ky < s.kh && kx < s.kw)
+                                        cw[(((size_t(k) * s.cout + co) * s.cin + ci) * aty + a2) * atx + b2] =
+                                            w.data[((size_t(ci) * s.cout + co) * s.kh + ky) * s.kw + kx];
+                                }
                 Step::TPhase &ap = s.allph;
-                ap.ty = ap.tx = 1;
-                ap.pk = plan_conv_pack(s.cin, nph * s.cout, 1, 1);
+                ap.ty = aty, ap.tx = atx;
+                ap.pk = plan_conv_pack(s.cin, nph * s.cout, aty, atx);
                 std::vector<uint16_t> hi(ap.pk.halves()), lo(ap.pk.halves());
                 bool exact = true;
                 pack_conv_weights(ap.pk, cw.data(), hi.data(), lo.data(), &exact);
@@ -588,6 +597,8 @@ void Graph::Exec::step(size_t i) {
             ca.bias = s.b;
             ca.act = s.act;
             ca.pk = s.allph.pk;
+            ca.pt = s.allph.ty - 1;
+            ca.pl = s.allph.tx - 1;
             ca.ph_cout = s.cout;
             ca.ph_s = s.sh;
             if (conv_igemm(ca, st)) break;

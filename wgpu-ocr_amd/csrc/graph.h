@@ -39,8 +39,9 @@ struct Step {
         const uint16_t *whi = nullptr, *wlo = nullptr, *wfrag = nullptr;
     };
     std::vector<TPhase> phases;
-    // Kernel = stride: every phase is a 1 x 1 conv of the input, all of them one GEMM whose
-    // output channel k * cout + c is channel c of phase k (py = k / s, px = k % s); pk unset if not.
+    // All phases as one conv of the input over ceil(kh / s) x ceil(kw / s) taps (zero weights
+    // where a phase has fewer): output channel k * cout + c is channel c of phase k (py = k / s,
+    // px = k % s); whi unset when it does not apply.
     TPhase allph;
     std::vector<int64_t> starts, ends, axes;  // Slice
 };

@@ -118,12 +118,25 @@ void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s);
 void copy_act(const Act &x, const Act &y, int y0, int x0, hipStream_t s);  // Slice / Concat copies
 void activate(const Act &x, const Act &y, int act, hipStream_t s);
 void fill(float *p, size_t count, float v, hipStream_t s);
-// RGB bytes -> ocrs grey, padded with black, bilinear to ow x oh (gpu.rs:530-561).
-void grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh, float sx, float sy,
-                 hipStream_t s);
-// Model output (row stride `stride`, valid mw x mh) -> page size bits (gpu.rs:563-593).
-void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, float sx, float sy,
-             float thr, hipStream_t s);
+// RGB bytes -> ocrs grey, padded with black (to pw x ph), bilinear to ow x oh (gpu.rs:530-561):
+// every page of a detection pass in one launch.
+struct GreyPage {
+    const uint8_t *rgb;
+    int w, h, pw, ph;
+    float *y;
+    float sx, sy;
+};
+void grey_resize(const GreyPage *pages, int count, int ow, int oh, hipStream_t s);
+// Model output (row stride `stride`, valid mw x mh) -> page size bits (gpu.rs:563-593): every
+// page of a detection pass in one launch.
+struct MaskPage {
+    const float *m;
+    int mw, mh;
+    uint32_t *bits;
+    int w, h;
+    float sx, sy;
+};
+void mask_up(const MaskPage *pages, int count, int stride, float thr, hipStream_t s);
 // AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c]
 // (gpu.rs:595-614): the count inputs (same channel count) at line offsets 0, n0, n0 + n1, ...
 void avgpool_t(const Act *xs, int count, int kh, float *X, int ntot, hipStream_t s);

@@ -58,7 +58,7 @@ struct IgParams {
     int cout;
     const float *bias;
     const int *rows;  // GEMM row map (gather x rows, scatter y rows), or null
-    int phc, phs, phw;  // ConvTranspose phases: channels a phase, stride, y's row length (0: off)
+    int phc, phs, phh, phw;  // ConvTranspose phases: channels a phase, stride, y's size (0: off)
     int kw, pt, pl, act, chunks, taps;
     int th, tw, mx;   // tile rows and columns; row tiles per tile row of blocks
     int hw, hwp, halo_px;  // halo columns, padded row length, halo pixels
@@ -194,10 +194,12 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
         if (co >= p.cout) continue;
         // ConvTranspose phase k of channel co: its pixel offset in y and its own channel.
         size_t phoff = 0;
+        int ppy = 0, ppx = 0;
         if (p.phc) {
             const int k = co / p.phc;
             co -= k * p.phc;
-            phoff = size_t(k / p.phs) * p.phw + size_t(k % p.phs);
+            ppy = k / p.phs, ppx = k % p.phs;
+            phoff = size_t(ppy) * p.phw + size_t(ppx);
         }
         const float bv = p.bias ? p.bias[co] : 0.f;
 #pragma unroll
@@ -225,7 +227,8 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int yy = oy + (i >> 1), xx = ox + (i & 1);
-                    if (yy < p.oh && xx < p.ow)
+                    if (yy < p.oh && xx < p.ow &&
+                        (!p.phc || (yy * p.phs + ppy < p.phh && xx * p.phs + ppx < p.phw)))
                         p.y[(size_t(img) * p.yn + size_t(yy) * p.yy + size_t(xx) * p.yx + phoff) * p.ycs + co] = v[i];
                 }
             }
@@ -285,11 +288,11 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     if (a.nchw || a.in_scale || a.affine || a.amax_part || a.res || !pk.exact) return false;
     const bool phm = a.ph_cout > 0;
     if (phm) {
-        // All s x s phases of a ConvTranspose with kernel = stride: one 1 x 1 GEMM over x.
+        // All s x s phases of a ConvTranspose: one conv over x (taps (a, b) read x[i - a][j - b],
+        // leading pads kh - 1, kw - 1) on the grid of ceil(y.h / s) x ceil(y.w / s) positions.
         const int st = a.ph_s;
-        if (st < 1 || pk.kh != 1 || pk.kw != 1 || pk.cout != st * st * a.ph_cout || a.y.c != a.ph_cout ||
-            a.y.h != st * a.x.h || a.y.w != st * a.x.w || a.ypool.p || a.rows || a.y_px || a.y_row || a.y_img ||
-            a.pt || a.pl)
+        if (st < 1 || pk.cout != st * st * a.ph_cout || a.y.c != a.ph_cout || a.pt != pk.kh - 1 ||
+            a.pl != pk.kw - 1 || a.ypool.p || a.rows || a.y_px || a.y_row || a.y_img)
             return false;
     } else if (pk.cout != a.y.c) {
         return false;
@@ -330,14 +333,15 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     p.yy = a.y_row ? a.y_row : long(p.ow) * p.yx;
     p.yn = a.y_img ? a.y_img : long(p.oh) * p.yy;
     if (phm) {
-        // The GEMM's pixels are x's; y's pixel (s i + py, s j + px) is phase (py, px) of (i, j).
-        p.oh = a.x.h;
-        p.ow = a.x.w;
+        // Grid position (i, j), phase (py, px) is y's pixel (s i + py, s j + px) when inside y.
+        p.oh = (a.y.h + a.ph_s - 1) / a.ph_s;
+        p.ow = (a.y.w + a.ph_s - 1) / a.ph_s;
         p.yx = a.ph_s;
         p.yy = long(a.ph_s) * a.y.w;
         p.yn = long(a.y.h) * a.y.w;
         p.phc = a.ph_cout;
         p.phs = a.ph_s;
+        p.phh = a.y.h;
         p.phw = a.y.w;
     }
     p.y = pooled && !a.keep_full ? nullptr : a.y.p;

@@ -182,29 +182,45 @@ __device__ inline float grey_at(const uint8_t *rgb, int w, int h, int x, int yy)
     return g + float(q[2]) * (0.114f / 255.f);
 }
 
-__global__ void grey_resize_kernel(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh,
-                                   float sx, float sy) {
+// Up to GPMAX pages a launch (blockIdx.y): one thread per output pixel.
+constexpr int GPMAX = 16;
+struct GreyParams {
+    GreyPage pg[GPMAX];
+    int ow, oh;
+};
+__global__ void grey_resize_kernel(const GreyParams p) {
 #pragma clang fp contract(off)
+    const GreyPage &g = p.pg[blockIdx.y];
+    const int ow = p.ow, oh = p.oh;
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= ow * oh) return;
     int ox = i % ow, oy = i / ow;
-    float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(ph) - 1.f);
-    float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(pw) - 1.f);
+    float iy = fminf(fmaxf(g.sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(g.ph) - 1.f);
+    float ix = fminf(fmaxf(g.sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(g.pw) - 1.f);
     int y1 = int(iy), x1 = int(ix);
-    int y2 = min(y1 + 1, ph - 1), x2 = min(x1 + 1, pw - 1);
+    int y2 = min(y1 + 1, g.ph - 1), x2 = min(x1 + 1, g.pw - 1);
     float wy = iy - float(y1), wx = ix - float(x1);
-    float top = mixf(grey_at(rgb, w, h, x1, y1), grey_at(rgb, w, h, x2, y1), wx);
-    float bot = mixf(grey_at(rgb, w, h, x1, y2), grey_at(rgb, w, h, x2, y2), wx);
-    y[i] = mixf(top, bot, wy);
+    float top = mixf(grey_at(g.rgb, g.w, g.h, x1, y1), grey_at(g.rgb, g.w, g.h, x2, y1), wx);
+    float bot = mixf(grey_at(g.rgb, g.w, g.h, x1, y2), grey_at(g.rgb, g.w, g.h, x2, y2), wx);
+    g.y[i] = mixf(top, bot, wy);
 }
 
 // ---- mask_up (gpu.rs:563-593): a wavefront per 64 columns of MR rows (two bit words a row,
 // assembled with a ballot); a thread walks its column down the rows, so a wavefront's loads of
 // neighbouring rows (which share source rows) are in flight together.
 constexpr int MR = 8;
-__global__ void mask_up_kernel(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, int words,
-                               float sx, float sy, float thr) {
+struct MaskParams {
+    MaskPage pg[GPMAX];
+    int stride;
+    float thr;
+};
+__global__ void mask_up_kernel(const MaskParams p) {
 #pragma clang fp contract(off)
+    const MaskPage &g = p.pg[blockIdx.y];
+    const float *m = g.m;
+    const int stride = p.stride, mw = g.mw, mh = g.mh, w = g.w, h = g.h, words = (g.w + 31) / 32;
+    const float sx = g.sx, sy = g.sy, thr = p.thr;
+    uint32_t *bits = g.bits;
     const int lane = threadIdx.x & 63;
     const long wv = (long(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
     const int pairs = (words + 1) / 2, groups = (h + MR - 1) / MR;
@@ -380,21 +396,37 @@ void fill(float *p, size_t count, float v, hipStream_t s) {
     OCR_HIP(hipGetLastError());
 }
 
-void grey_resize(const uint8_t *rgb, int w, int h, int pw, int ph, float *y, int ow, int oh, float sx, float sy,
-                 hipStream_t s) {
-    ProbeScope probe("grey_resize", s, 0, 16.0 * double(ow) * oh);
-    hipLaunchKernelGGL(grey_resize_kernel, dim3(blocks_for(size_t(ow) * oh)), dim3(256), 0, s, rgb, w, h, pw, ph, y,
-                       ow, oh, sx, sy);
-    OCR_HIP(hipGetLastError());
+void grey_resize(const GreyPage *pages, int count, int ow, int oh, hipStream_t s) {
+    ProbeScope probe("grey_resize", s, 0, 16.0 * double(ow) * oh * count);
+    for (int k0 = 0; k0 < count; k0 += GPMAX) {
+        GreyParams p{};
+        const int cnt = std::min(GPMAX, count - k0);
+        for (int k = 0; k < cnt; k++) p.pg[k] = pages[k0 + k];
+        p.ow = ow;
+        p.oh = oh;
+        hipLaunchKernelGGL(grey_resize_kernel, dim3(blocks_for(size_t(ow) * oh), unsigned(cnt)), dim3(256), 0, s, p);
+        OCR_HIP(hipGetLastError());
+    }
 }
 
-void mask_up(const float *m, int stride, int mw, int mh, uint32_t *bits, int w, int h, float sx, float sy, float thr,
-             hipStream_t s) {
-    int words = (w + 31) / 32;
-    ProbeScope probe("mask_up", s, 0, 4.0 * double(mw) * mh + 4.0 * double(words) * h);
-    hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(size_t((words + 1) / 2) * ((h + MR - 1) / MR) * 64)), dim3(256),
-                       0, s, m, stride, mw, mh, bits, w, h, words, sx, sy, thr);
-    OCR_HIP(hipGetLastError());
+void mask_up(const MaskPage *pages, int count, int stride, float thr, hipStream_t s) {
+    double bytes = 0;
+    size_t waves = 0;
+    for (int k = 0; k < count; k++) {
+        const int words = (pages[k].w + 31) / 32;
+        bytes += 4.0 * double(pages[k].mw) * pages[k].mh + 4.0 * double(words) * pages[k].h;
+        waves = std::max(waves, size_t((words + 1) / 2) * ((pages[k].h + MR - 1) / MR));
+    }
+    ProbeScope probe("mask_up", s, 0, bytes);
+    for (int k0 = 0; k0 < count; k0 += GPMAX) {
+        MaskParams p{};
+        const int cnt = std::min(GPMAX, count - k0);
+        for (int k = 0; k < cnt; k++) p.pg[k] = pages[k0 + k];
+        p.stride = stride;
+        p.thr = thr;
+        hipLaunchKernelGGL(mask_up_kernel, dim3(blocks_for(waves * 64), unsigned(cnt)), dim3(256), 0, s, p);
+        OCR_HIP(hipGetLastError());
+    }
 }
 
 void conv1x1_narrow(const Act &x, const Act &y, const float *w, const float *b, int act, hipStream_t s) {

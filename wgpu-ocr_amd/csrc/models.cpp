@@ -20,22 +20,26 @@ void Detector::detect_pages_device(const uint8_t *const *rgb, const int *w, cons
     Act in{nullptr, count, DET_MH, DET_MW, 1, 1};
     DBuf inbuf(&ctx_, in.count() * sizeof(float));
     in.p = inbuf.as<float>();
+    std::vector<GreyPage> gp;
     for (int k = 0; k < count; k++) {
         if (w[k] <= 0 || h[k] <= 0) fail("empty page");
         const int ph = std::max(h[k], DET_MH), pw = std::max(w[k], DET_MW);
-        grey_resize(rgb[k], w[k], h[k], pw, ph, in.p + size_t(k) * DET_MH * DET_MW, DET_MW, DET_MH,
-                    float(pw) / float(DET_MW), float(ph) / float(DET_MH), st);
+        gp.push_back({rgb[k], w[k], h[k], pw, ph, in.p + size_t(k) * DET_MH * DET_MW, float(pw) / float(DET_MW),
+                      float(ph) / float(DET_MH)});
     }
+    grey_resize(gp.data(), count, DET_MW, DET_MH, st);
     Graph::Out out = graph_.run(ctx_, in);
     if (out.act.h != DET_MH || out.act.w != DET_MW || out.act.c != 1)
         fail("detection model output is not [n, 1, 800, 600]");
+    std::vector<MaskPage> mp;
     for (int k = 0; k < count; k++) {
         const int ph = std::max(h[k], DET_MH), pw = std::max(w[k], DET_MW);
         // The part of the mask that covers the page, not the padding (gpu.rs:1413-1414).
         const int vh = DET_MH - (ph - h[k]) * DET_MH / ph, vw = DET_MW - (pw - w[k]) * DET_MW / pw;
-        mask_up(out.act.p + size_t(k) * DET_MH * DET_MW, DET_MW, vw, vh, bits[k], w[k], h[k],
-                float(vw) / float(w[k]), float(vh) / float(h[k]), thr, st);
+        mp.push_back({out.act.p + size_t(k) * DET_MH * DET_MW, vw, vh, bits[k], w[k], h[k], float(vw) / float(w[k]),
+                      float(vh) / float(h[k])});
     }
+    mask_up(mp.data(), count, DET_MW, thr, st);
 }
 
 std::vector<float> Detector::detect(const float *input, int h, int w) {
