@@ -89,6 +89,44 @@ def test_line_images_edge_boxes(ctx):
         np.testing.assert_array_equal(got[k], want, err_msg=f"box {box}")
 
 
+def _pack_bits(mask):
+    """[h][w] bool -> [h][ceil(w / 32)] uint32, bit x % 32 of word x / 32."""
+    h, w = mask.shape
+    padded = np.zeros((h, (w + 31) // 32 * 32), np.uint8)
+    padded[:, :w] = mask
+    return np.packbits(padded, axis=1, bitorder="little").view(np.uint32).copy()
+
+
+def test_word_rects_gpu_labelling_identical(detector, ctx):
+    # Components labelled on the GPU give the host's rectangles bit for bit, in the same order:
+    # a detector mask, noise with many tiny and diagonal-only components, nested rings, full
+    # rows, an empty mask, widths inside a word.
+    rng = np.random.Generator(np.random.PCG64(23))
+    masks = []
+    page = synth.page(3)
+    masks.append((detector.detect_page(page, 0.5), page.shape[1]))
+    for h, w, p in ((300, 517, 0.45), (97, 33, 0.6), (64, 2048, 0.15)):
+        masks.append((_pack_bits(rng.random((h, w)) < p), w))
+    rings = np.zeros((200, 300), bool)
+    for r in range(5, 95, 6):
+        rings[100 - r: 100 + r + 1, 150 - r] = rings[100 - r: 100 + r + 1, 150 + r] = True
+        rings[100 - r, 150 - r: 150 + r + 1] = rings[100 + r, 150 - r: 150 + r + 1] = True
+    masks.append((_pack_bits(rings), 300))
+    full = np.zeros((50, 70), bool)
+    full[::3] = True
+    full[:, 35] = True
+    masks.append((_pack_bits(full), 70))
+    masks.append((_pack_bits(np.zeros((10, 40), bool)), 40))
+    diag = np.eye(120, 130, dtype=bool) | np.eye(120, 130, k=7, dtype=bool)[:, ::-1]
+    masks.append((_pack_bits(diag), 130))
+    for bits, w in masks:
+        print(f"word rects of a {bits.shape[0]} x {w} mask", flush=True)
+        want = ocrhip.word_rects(bits, w)
+        got = ocrhip.word_rects_gpu(ctx, bits, w)
+        assert got.shape == want.shape
+        np.testing.assert_array_equal(got, want)
+
+
 def test_detect_mask_words_at_odd_widths(detector, det_oracle):
     # Page widths that end inside a 64-pixel group and inside a 32-bit word.
     for w in (2549, 97):

@@ -371,6 +371,41 @@ int ocr_word_rects_mt(const uint32_t *bits, uint32_t w, uint32_t h, uint32_t thr
     });
 }
 
+int ocr_word_rects_gpu(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out, uint32_t cap,
+                       uint32_t *count) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(bits, "bits");
+        need(count, "count");
+        if (w == 0 || h == 0 || w > 65536) fail("mask size");
+        Ctx &c = *ctx->ctx;
+        c.bind();
+        const size_t words = size_t(w + 31) / 32 * h;
+        const int runs_cap = int(std::min<size_t>(words * 16, size_t(1) << 26));
+        DBuf db(&c, words * 4), dx0(&c, size_t(runs_cap) * 2), dx1(&c, size_t(runs_cap) * 2),
+            droot(&c, size_t(runs_cap) * 4), droff(&c, size_t(h + 1) * 4), dtot(&c, 4);
+        c.h2d(db.get(), bits, words * 4);
+        CclPage pg{db.as<uint32_t>(), int(w), int(h), dx0.as<uint16_t>(), dx1.as<uint16_t>(), droot.as<int32_t>(),
+                   droff.as<int32_t>(), runs_cap, dtot.as<int32_t>()};
+        ccl_runs(&pg, 1, c.stream());
+        int32_t total = 0;
+        c.d2h(&total, dtot.get(), 4);
+        if (total > runs_cap) fail("too many runs");
+        const size_t n = size_t(total);
+        std::vector<uint16_t> x0(n), x1(n);
+        std::vector<int32_t> root(n), row_off(size_t(h) + 1);
+        c.d2h(row_off.data(), droff.get(), row_off.size() * 4);
+        if (total) {
+            c.d2h(x0.data(), dx0.get(), x0.size() * 2);
+            c.d2h(x1.data(), dx1.get(), x1.size() * 2);
+            c.d2h(root.data(), droot.get(), root.size() * 4);
+        }
+        std::vector<RRect> r = word_rects_from_runs(x0.data(), x1.data(), root.data(), row_off.data(), int(h));
+        *count = uint32_t(r.size());
+        for (size_t i = 0; i < r.size() && i < cap; i++) out[i] = {r[i].cx, r[i].cy, r[i].ux, r[i].uy, r[i].w, r[i].h};
+    });
+}
+
 ocr_layout *ocr_layout_page(const uint32_t *bits, uint32_t w, uint32_t h, float relv, float relend) {
     return guard_ptr<ocr_layout>([&] {
         need(bits, "bits");

@@ -342,8 +342,10 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
     return out;
 }
 
-std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area, int threads) {
-    const auto comps = component_points(bits, w, h, threads);
+// Each component's minimum-area rectangle, grown by expand on every side; those of at least
+// min_area, in component order.
+static std::vector<RRect> rects_of(const std::vector<std::vector<Pt>> &comps, float expand, float min_area,
+                                   int threads) {
     std::vector<RRect> rects(comps.size());
     parallel_for(int(comps.size()), threads, [&](int i) {
         rects[size_t(i)] = min_area_rect(hull_rows(comps[size_t(i)]));
@@ -353,6 +355,47 @@ std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, 
     for (const RRect &r : rects)
         if (r.area() >= min_area) out.push_back(r);
     return out;
+}
+
+std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area, int threads) {
+    return rects_of(component_points(bits, w, h, threads), expand, min_area, threads);
+}
+
+std::vector<RRect> word_rects_from_runs(const uint16_t *x0, const uint16_t *x1, const int32_t *root,
+                                        const int32_t *row_off, int h, float expand, float min_area, int threads) {
+    const int n = h > 0 ? row_off[h] : 0;
+    // Component ids in order of first run (a root is its component's first run) and room for
+    // two points a row, then each component's row extremes as band_components builds them.
+    std::vector<int> comp(size_t(std::max(n, 0)), -1), run_comp(size_t(std::max(n, 0)));
+    std::vector<int> npts, last_y;
+    for (int y = 0; y < h; y++)
+        for (int r = row_off[y]; r < row_off[y + 1]; r++) {
+            const int rt = root[r];
+            if (rt < 0 || rt > r) fail("word_rects_from_runs: a run's root must be an earlier run");
+            if (comp[size_t(rt)] < 0) {
+                comp[size_t(rt)] = int(npts.size());
+                npts.push_back(0);
+                last_y.push_back(-1);
+            }
+            const int c = comp[size_t(rt)];
+            run_comp[size_t(r)] = c;
+            if (last_y[size_t(c)] != y) npts[size_t(c)] += 2, last_y[size_t(c)] = y;
+        }
+    std::vector<std::vector<Pt>> pts(npts.size());
+    for (size_t c = 0; c < npts.size(); c++) pts[c].reserve(size_t(npts[c]));
+    for (int y = 0; y < h; y++)
+        for (int r = row_off[y]; r < row_off[y + 1]; r++) {
+            auto &v = pts[size_t(run_comp[size_t(r)])];
+            const float fy = float(y), fx0 = float(x0[r]), fx1 = float(x1[r]);
+            if (!v.empty() && v.back().y == fy) {
+                if (v.size() >= 2 && v[v.size() - 2].y == fy) v.back().x = fx1;
+                else if (fx1 != v.back().x) v.push_back({fx1, fy});
+            } else {
+                v.push_back({fx0, fy});
+                if (fx1 != fx0) v.push_back({fx1, fy});
+            }
+        }
+    return rects_of(pts, expand, min_area, threads);
 }
 
 // ppdet.rs:65-85: the mean probability of the map's pixels whose position lies inside r (its

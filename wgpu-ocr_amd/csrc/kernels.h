@@ -137,6 +137,19 @@ struct MaskPage {
     float sx, sy;
 };
 void mask_up(const MaskPage *pages, int count, int stride, float thr, hipStream_t s);
+// Run-length labelling of detection masks (kernels/ccl.hip): for every page, its runs row by
+// row (row y's are [row_off[y], row_off[y + 1]), pixels x0[i] .. x1[i]) and root[i], the first
+// run of run i's 8-connected component. row_off has h + 1 entries; when the page has more than
+// cap runs only row_off and *total (the run count) are written.
+struct CclPage {
+    const uint32_t *bits;
+    int w, h;
+    uint16_t *x0, *x1;
+    int32_t *root, *row_off;
+    int cap;
+    int32_t *total;
+};
+void ccl_runs(const CclPage *pages, int count, hipStream_t s);
 // AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c]
 // (gpu.rs:595-614): the count inputs (same channel count) at line offsets 0, n0, n0 + n1, ...
 void avgpool_t(const Act *xs, int count, int kh, float *X, int ntot, hipStream_t s);

@@ -1,0 +1,214 @@
+// Run-length labelling of the detection masks on the GPU: the first half of word_rects
+// (ocr-bench.rs:40-60; the components the host restatement in geometry.cpp finds), so the host
+// only turns each component's row extremes into a rectangle.
+//
+// For every page of a detection pass: (1) a wavefront per mask row counts the row's runs (set
+// pixels whose left neighbour is clear); (2) a workgroup per page turns the counts into row
+// offsets; (3) a wavefront per row writes its runs, left to right, each run its own parent; (4)
+// a thread per run joins it with every run of the row above that touches it with 8-connectivity
+// (x ranges overlapping or adjacent), linking the larger root under the smaller with a
+// compare-and-swap, so every component's root is its smallest run index: its first run in
+// row-major order, the order the host lists components in; (5) a thread per run replaces its
+// parent by its root. A page with more runs than the buffers hold gets no runs (its total says
+// so) and the host labels it from the bits instead.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "../kernels.h"
+#include "../runtime.h"
+
+namespace ocr {
+
+namespace {
+
+constexpr int CCL_MAXPAGES = 16;
+struct CclParams {
+    CclPage pg[CCL_MAXPAGES];
+};
+
+// Word wi of a row, zero past the last one and past the mask width w.
+__device__ inline uint32_t mask_word(const uint32_t *row, int wi, int words, int w) {
+    if (wi < 0 || wi >= words) return 0u;
+    uint32_t v = row[wi];
+    if (wi == words - 1 && (w & 31)) v &= (1u << (w & 31)) - 1u;
+    return v;
+}
+
+// Exclusive prefix sum over the wavefront's lanes, and the wavefront total.
+__device__ inline int wave_scan(int v, int lane, int &total) {
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    total = __shfl(x, 63);
+    return x - v;
+}
+
+__global__ __launch_bounds__(256) void ccl_count_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.y];
+    const int lane = threadIdx.x & 63, y = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+    if (y >= g.h) return;
+    const int words = (g.w + 31) / 32;
+    const uint32_t *row = g.bits + size_t(y) * words;
+    int n = 0;
+    for (int c0 = 0; c0 < words; c0 += 64) {
+        const int wi = c0 + lane;
+        const uint32_t v = mask_word(row, wi, words, g.w), prev = mask_word(row, wi - 1, words, g.w);
+        n += __popc(v & ~((v << 1) | (prev >> 31)));
+    }
+    int total;
+    wave_scan(n, lane, total);
+    if (lane == 0) g.row_off[y + 1] = total;
+}
+
+// Row offsets: row_off[0] = 0, row_off[y + 1] = runs in rows 0 .. y; total = row_off[h].
+__global__ __launch_bounds__(1024) void ccl_scan_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.x];
+    __shared__ int s_wave[16];
+    __shared__ int s_carry;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_carry = 0;
+    __syncthreads();
+    for (int b = 0; b < g.h; b += 1024) {
+        const int y = b + tid;
+        const int v = y < g.h ? g.row_off[y + 1] : 0;
+        int wt;
+        const int ex = wave_scan(v, lane, wt);
+        if (lane == 0) s_wave[wave] = wt;
+        __syncthreads();
+        int before = s_carry;
+        for (int k = 0; k < wave; k++) before += s_wave[k];
+        if (y < g.h) g.row_off[y + 1] = before + ex + v;
+        __syncthreads();
+        if (tid == 1023) s_carry = before + ex + v;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        g.row_off[0] = 0;
+        *g.total = s_carry;
+    }
+}
+
+__global__ __launch_bounds__(256) void ccl_runs_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.y];
+    const int lane = threadIdx.x & 63, y = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+    if (y >= g.h || g.row_off[g.h] > g.cap) return;
+    const int words = (g.w + 31) / 32;
+    const uint32_t *row = g.bits + size_t(y) * words;
+    int ks = g.row_off[y], ke = ks;  // next start / end index of the row
+    for (int c0 = 0; c0 < words; c0 += 64) {
+        const int wi = c0 + lane;
+        const uint32_t v = mask_word(row, wi, words, g.w), prev = mask_word(row, wi - 1, words, g.w),
+                       next = mask_word(row, wi + 1, words, g.w);
+        uint32_t st = v & ~((v << 1) | (prev >> 31));  // run starts
+        uint32_t en = v & ~((v >> 1) | (next << 31));  // run ends (last pixel)
+        int ts, te;
+        int is = ks + wave_scan(__popc(st), lane, ts), ie = ke + wave_scan(__popc(en), lane, te);
+        while (st) {
+            const int b = __ffs(int(st)) - 1;
+            st &= st - 1;
+            g.x0[is] = uint16_t(wi * 32 + b);
+            g.root[is] = is;
+            is++;
+        }
+        while (en) {
+            const int b = __ffs(int(en)) - 1;
+            en &= en - 1;
+            g.x1[ie++] = uint16_t(wi * 32 + b);
+        }
+        ks += ts;
+        ke += te;
+    }
+}
+
+__device__ inline int ccl_find(const int32_t *parent, int x) {
+    for (;;) {
+        const int q = __atomic_load_n(parent + x, __ATOMIC_RELAXED);
+        if (q == x) return x;
+        x = q;
+    }
+}
+
+// The row of run j: the last y with row_off[y] <= j.
+__device__ inline int ccl_row(const int32_t *row_off, int h, int j) {
+    int lo = 0, hi = h - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (row_off[mid] <= j) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(256) void ccl_union_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.y];
+    const int n = g.row_off[g.h];
+    if (n > g.cap) return;
+    for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
+        const int y = ccl_row(g.row_off, g.h, j);
+        if (y == 0) continue;
+        const int lo = g.row_off[y - 1], hi = g.row_off[y];
+        const int a0 = g.x0[j], a1 = g.x1[j];
+        // First run above whose right end reaches a0 - 1 (right ends increase along a row).
+        int l = lo, r = hi;
+        while (l < r) {
+            const int m = (l + r) >> 1;
+            if (int(g.x1[m]) + 1 >= a0) r = m;
+            else l = m + 1;
+        }
+        for (int i = l; i < hi && int(g.x0[i]) <= a1 + 1; i++) {
+            int u = i, v = j;
+            for (;;) {
+                u = ccl_find(g.root, u);
+                v = ccl_find(g.root, v);
+                if (u == v) break;
+                if (u > v) {
+                    const int t = u;
+                    u = v;
+                    v = t;
+                }
+                // Link root v under the smaller root u, if v is still a root.
+                if (atomicCAS(g.root + v, v, u) == v) break;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void ccl_flatten_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.y];
+    const int n = g.row_off[g.h];
+    if (n > g.cap) return;
+    for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256)
+        g.root[j] = ccl_find(g.root, j);
+}
+
+}  // namespace
+
+void ccl_runs(const CclPage *pages, int count, hipStream_t s) {
+    for (int k0 = 0; k0 < count; k0 += CCL_MAXPAGES) {
+        CclParams p{};
+        const int cnt = std::min(CCL_MAXPAGES, count - k0);
+        int maxh = 0;
+        double bytes = 0;
+        for (int k = 0; k < cnt; k++) {
+            const CclPage &g = pages[k0 + k];
+            if (g.w < 1 || g.h < 1 || g.w > 65536 || g.cap < 1) fail("ccl_runs: page size or capacity");
+            p.pg[k] = g;
+            maxh = std::max(maxh, g.h);
+            bytes += 4.0 * double((g.w + 31) / 32) * g.h;
+        }
+        ProbeScope probe("ccl", s, 0, bytes);
+        const dim3 rows(unsigned((maxh + 3) / 4), unsigned(cnt));
+        hipLaunchKernelGGL(ccl_count_kernel, rows, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ccl_scan_kernel, dim3(unsigned(cnt)), dim3(1024), 0, s, p);
+        hipLaunchKernelGGL(ccl_runs_kernel, rows, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ccl_union_kernel, dim3(64, unsigned(cnt)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ccl_flatten_kernel, dim3(64, unsigned(cnt)), dim3(256), 0, s, p);
+        OCR_HIP(hipGetLastError());
+    }
+}
+
+}  // namespace ocr

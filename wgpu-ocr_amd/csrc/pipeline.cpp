@@ -28,10 +28,13 @@ static void wait_event(hipEvent_t ev) {
     }
 }
 
-PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads, int page_prio) {
+PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads, int page_prio,
+                       const MaskRuns *runs) {
     set_loop_priority(page_prio);
     PageLayout L;
-    std::vector<RRect> words = word_rects(bits, w, h, 3.f, 100.f, threads);
+    std::vector<RRect> words =
+        runs ? word_rects_from_runs(runs->x0, runs->x1, runs->root, runs->row_off, h, 3.f, 100.f, threads)
+             : word_rects(bits, w, h, 3.f, 100.f, threads);
     L.words = int(words.size());
     auto lines = find_text_lines(words);
     pad_lines(lines, relv, relend);
@@ -63,7 +66,7 @@ struct Pipeline::Impl {
     Recognizer &rec;
     PipelineOpts opts;
     Workers workers;
-    std::vector<Pinned> bits_host, best_host;
+    std::vector<Pinned> bits_host, best_host, runs_host;
     // Host threads the layouts of one recognition pass share (a page's word boxes in row bands,
     // its lines side by side).
     int host_threads;
@@ -163,10 +166,18 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
     // Worker tasks refer to the locals above: whatever happens, wait for them before returning.
     try {
     if (I.bits_host.size() < size_t(npages)) I.bits_host.resize(size_t(npages));
+    if (I.runs_host.size() < size_t(npages)) I.runs_host.resize(size_t(npages));
+    // Each page's labelled runs (ccl_runs), on the device and copied to the host as one block:
+    // the run count, row offsets (h + 1), roots, then the runs' first and last pixels (cap each).
     std::vector<size_t> words_of(static_cast<size_t>(npages));
+    std::vector<int> runs_cap(static_cast<size_t>(npages));
+    auto roff_bytes = [&](int p) { return (size_t(h[p] + 1) * 4 + 15) & ~size_t(15); };
+    auto runs_bytes = [&](int p) { return 16 + roff_bytes(p) + size_t(runs_cap[size_t(p)]) * 8; };
     for (int p = 0; p < npages; p++) {
         words_of[size_t(p)] = size_t((w[p] + 31) / 32) * h[p];
         I.bits_host[size_t(p)].ensure(words_of[size_t(p)] * 4);
+        runs_cap[size_t(p)] = int(std::min<size_t>(words_of[size_t(p)] * 16, size_t(1) << 17));
+        I.runs_host[size_t(p)].ensure(runs_bytes(p));
     }
     for (int g = 0; g < ngroups; g++) {
         const int p0 = group_p0[size_t(g)], p1 = g + 1 < ngroups ? group_p0[size_t(g) + 1] : npages;
@@ -177,9 +188,24 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             bp.push_back(bits.back().as<uint32_t>());
         }
         I.det.detect_pages_device(d_rgb + p0, w + p0, h + p0, p1 - p0, I.opts.thr, bp.data());
-        for (int p = p0; p < p1; p++)
+        std::vector<DBuf> rbuf;
+        std::vector<CclPage> cp;
+        for (int p = p0; p < p1; p++) {
+            rbuf.emplace_back(&ctx, runs_bytes(p));
+            char *b = rbuf.back().as<char>();
+            const int cap = runs_cap[size_t(p)];
+            char *root = b + 16 + roff_bytes(p);
+            cp.push_back({bp[size_t(p - p0)], w[p], h[p], reinterpret_cast<uint16_t *>(root + size_t(cap) * 4),
+                          reinterpret_cast<uint16_t *>(root + size_t(cap) * 6), reinterpret_cast<int32_t *>(root),
+                          reinterpret_cast<int32_t *>(b + 16), cap, reinterpret_cast<int32_t *>(b)});
+        }
+        ccl_runs(cp.data(), int(cp.size()), st);
+        for (int p = p0; p < p1; p++) {
             OCR_HIP(hipMemcpyAsync(I.bits_host[size_t(p)].p, bp[size_t(p - p0)], words_of[size_t(p)] * 4,
                                    hipMemcpyDeviceToHost, st));
+            OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), runs_bytes(p),
+                                   hipMemcpyDeviceToHost, st));
+        }
         OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming | hipEventBlockingSync));
         OCR_HIP(hipEventRecord(det_ev[size_t(g)], st));
         mark("det group " + std::to_string(g) + " enqueued");
@@ -215,11 +241,14 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         }
         const int grp = group_of[size_t(p)];
         const uint32_t *bits = static_cast<const uint32_t *>(I.bits_host[size_t(p)].p);
+        const char *rblk = static_cast<const char *>(I.runs_host[size_t(p)].p);
+        const int rcap = runs_cap[size_t(p)];
+        const size_t roff = roff_bytes(p);
         const int pw = w[p], ph = h[p];
         int pr = 0;
         while (pass_p0[size_t(pr) + 1] <= p) pr++;
         const int before = pass_p0[size_t(pr)], threads = I.host_threads;
-        I.workers.submit([&, p, grp, bits, pw, ph, dev, before, threads] {
+        I.workers.submit([&, p, grp, bits, rblk, rcap, roff, pw, ph, dev, before, threads] {
             std::string err;
             double busy = 0;
             try {
@@ -237,7 +266,14 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
                 }
                 mark("layout " + std::to_string(p) + " start");
                 const auto tc = Clock::now();
-                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads, p);
+                // The GPU's labelled runs unless the page had more runs than the buffers hold.
+                const int total = *reinterpret_cast<const int32_t *>(rblk);
+                const char *root = rblk + 16 + roff;
+                const MaskRuns mr{reinterpret_cast<const uint16_t *>(root + size_t(rcap) * 4),
+                                  reinterpret_cast<const uint16_t *>(root + size_t(rcap) * 6),
+                                  reinterpret_cast<const int32_t *>(root), reinterpret_cast<const int32_t *>(rblk + 16)};
+                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads, p,
+                                           total <= rcap ? &mr : nullptr);
                 busy = ms_since(tc);
                 mark("layout " + std::to_string(p) + " done");
                 std::lock_guard<std::mutex> lk(mu);

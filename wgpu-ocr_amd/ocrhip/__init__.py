@@ -60,6 +60,7 @@ SIGNATURES = {
     "ocr_probe_stop": (ctypes.c_int, [ctypes.c_char_p, PU32, P, P, P]),
     "ocr_word_rects": (ctypes.c_int, [P, U32, U32, P, U32, PU32]),
     "ocr_word_rects_mt": (ctypes.c_int, [P, U32, U32, U32, P, U32, PU32]),
+    "ocr_word_rects_gpu": (ctypes.c_int, [P, P, U32, U32, P, U32, PU32]),
     "ocr_layout_page": (P, [P, U32, U32, F32, F32]),
     "ocr_layout_free": (None, [P]),
     "ocr_layout_counts": (ctypes.c_int, [P, PU32, PU32, PU32]),
@@ -415,6 +416,17 @@ def word_rects(bits: np.ndarray, w: int, threads: int = 1):
     _check(lib().ocr_word_rects_mt(_ptr(bits), w, h, threads, None, 0, ctypes.byref(count)))
     out = np.zeros((count.value, 6), np.float32)
     _check(lib().ocr_word_rects_mt(_ptr(bits), w, h, threads, _ptr(out), count.value, ctypes.byref(count)))
+    return out
+
+
+def word_rects_gpu(ctx: "Context", bits: np.ndarray, w: int):
+    """The same words with the mask's runs labelled on the GPU (the page pipeline's path)."""
+    bits = np.ascontiguousarray(bits, np.uint32)
+    h = bits.shape[0]
+    count = ctypes.c_uint32()
+    _check(lib().ocr_word_rects_gpu(ctx.handle, _ptr(bits), w, h, None, 0, ctypes.byref(count)))
+    out = np.zeros((count.value, 6), np.float32)
+    _check(lib().ocr_word_rects_gpu(ctx.handle, _ptr(bits), w, h, _ptr(out), count.value, ctypes.byref(count)))
     return out
 
 
