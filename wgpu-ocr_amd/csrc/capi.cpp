@@ -377,16 +377,16 @@ int ocr_word_rects_gpu(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t 
         need(ctx, "ctx");
         need(bits, "bits");
         need(count, "count");
-        if (w == 0 || h == 0 || w > 65536) fail("mask size");
+        if (w == 0 || h == 0 || w > 65536 || h > 65536) fail("mask size");
         Ctx &c = *ctx->ctx;
         c.bind();
         const size_t words = size_t(w + 31) / 32 * h;
         const int runs_cap = int(std::min<size_t>(words * 16, size_t(1) << 26));
         DBuf db(&c, words * 4), dx0(&c, size_t(runs_cap) * 2), dx1(&c, size_t(runs_cap) * 2),
-            droot(&c, size_t(runs_cap) * 4), droff(&c, size_t(h + 1) * 4), dtot(&c, 4);
+            droot(&c, size_t(runs_cap) * 4), droff(&c, size_t(h + 1) * 4), dtot(&c, 4), dry(&c, size_t(runs_cap) * 2);
         c.h2d(db.get(), bits, words * 4);
         CclPage pg{db.as<uint32_t>(), int(w), int(h), dx0.as<uint16_t>(), dx1.as<uint16_t>(), droot.as<int32_t>(),
-                   droff.as<int32_t>(), runs_cap, dtot.as<int32_t>()};
+                   droff.as<int32_t>(), runs_cap, dtot.as<int32_t>(), dry.as<uint16_t>()};
         ccl_runs(&pg, 1, c.stream());
         int32_t total = 0;
         c.d2h(&total, dtot.get(), 4);

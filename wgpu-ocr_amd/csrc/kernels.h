@@ -140,7 +140,7 @@ void mask_up(const MaskPage *pages, int count, int stride, float thr, hipStream_
 // Run-length labelling of detection masks (kernels/ccl.hip): for every page, its runs row by
 // row (row y's are [row_off[y], row_off[y + 1]), pixels x0[i] .. x1[i]) and root[i], the first
 // run of run i's 8-connected component. row_off has h + 1 entries; when the page has more than
-// cap runs only row_off and *total (the run count) are written.
+// cap runs only row_off and *total (the run count) are written. Widths and heights up to 65536.
 struct CclPage {
     const uint32_t *bits;
     int w, h;
@@ -148,6 +148,7 @@ struct CclPage {
     int32_t *root, *row_off;
     int cap;
     int32_t *total;
+    uint16_t *ry;  // scratch: each run's row (cap entries)
 };
 void ccl_runs(const CclPage *pages, int count, hipStream_t s);
 // AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c]

@@ -6,7 +6,7 @@
 // pixels whose left neighbour is clear); (2) a workgroup per page turns the counts into row
 // offsets; (3) a wavefront per row writes its runs, left to right, each run its own parent; (4)
 // a thread per run joins it with every run of the row above that touches it with 8-connectivity
-// (x ranges overlapping or adjacent), linking the larger root under the smaller with a
+// (x ranges overlapping or adjacent; the runs above found by binary search), linking the larger root under the smaller with a
 // compare-and-swap, so every component's root is its smallest run index: its first run in
 // row-major order, the order the host lists components in; (5) a thread per run replaces its
 // parent by its root. A page with more runs than the buffers hold gets no runs (its total says
@@ -111,6 +111,7 @@ __global__ __launch_bounds__(256) void ccl_runs_kernel(const CclParams p) {
             const int b = __ffs(int(st)) - 1;
             st &= st - 1;
             g.x0[is] = uint16_t(wi * 32 + b);
+            g.ry[is] = uint16_t(y);
             g.root[is] = is;
             is++;
         }
@@ -132,23 +133,12 @@ __device__ inline int ccl_find(const int32_t *parent, int x) {
     }
 }
 
-// The row of run j: the last y with row_off[y] <= j.
-__device__ inline int ccl_row(const int32_t *row_off, int h, int j) {
-    int lo = 0, hi = h - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (row_off[mid] <= j) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
 __global__ __launch_bounds__(256) void ccl_union_kernel(const CclParams p) {
     const CclPage &g = p.pg[blockIdx.y];
     const int n = g.row_off[g.h];
     if (n > g.cap) return;
     for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
-        const int y = ccl_row(g.row_off, g.h, j);
+        const int y = g.ry[j];
         if (y == 0) continue;
         const int lo = g.row_off[y - 1], hi = g.row_off[y];
         const int a0 = g.x0[j], a1 = g.x1[j];
@@ -191,13 +181,14 @@ void ccl_runs(const CclPage *pages, int count, hipStream_t s) {
     for (int k0 = 0; k0 < count; k0 += CCL_MAXPAGES) {
         CclParams p{};
         const int cnt = std::min(CCL_MAXPAGES, count - k0);
-        int maxh = 0;
+        int maxh = 0, maxcap = 0;
         double bytes = 0;
         for (int k = 0; k < cnt; k++) {
             const CclPage &g = pages[k0 + k];
-            if (g.w < 1 || g.h < 1 || g.w > 65536 || g.cap < 1) fail("ccl_runs: page size or capacity");
+            if (g.w < 1 || g.h < 1 || g.w > 65536 || g.h > 65536 || g.cap < 1) fail("ccl_runs: page size or capacity");
             p.pg[k] = g;
             maxh = std::max(maxh, g.h);
+            maxcap = std::max(maxcap, g.cap);
             bytes += 4.0 * double((g.w + 31) / 32) * g.h;
         }
         ProbeScope probe("ccl", s, 0, bytes);
@@ -205,8 +196,10 @@ void ccl_runs(const CclPage *pages, int count, hipStream_t s) {
         hipLaunchKernelGGL(ccl_count_kernel, rows, dim3(256), 0, s, p);
         hipLaunchKernelGGL(ccl_scan_kernel, dim3(unsigned(cnt)), dim3(1024), 0, s, p);
         hipLaunchKernelGGL(ccl_runs_kernel, rows, dim3(256), 0, s, p);
-        hipLaunchKernelGGL(ccl_union_kernel, dim3(64, unsigned(cnt)), dim3(256), 0, s, p);
-        hipLaunchKernelGGL(ccl_flatten_kernel, dim3(64, unsigned(cnt)), dim3(256), 0, s, p);
+        // A thread per run (up to the capacity; threads past a page's run count return).
+        const dim3 runs_grid(unsigned(std::min(2048, (maxcap + 255) / 256)), unsigned(cnt));
+        hipLaunchKernelGGL(ccl_union_kernel, runs_grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ccl_flatten_kernel, runs_grid, dim3(256), 0, s, p);
         OCR_HIP(hipGetLastError());
     }
 }

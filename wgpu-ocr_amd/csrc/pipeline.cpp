@@ -67,12 +67,24 @@ struct Pipeline::Impl {
     PipelineOpts opts;
     Workers workers;
     std::vector<Pinned> bits_host, best_host, runs_host;
+    // The masks and labelled runs go to the host on a stream of their own, so the next
+    // detection pass does not wait for the copies.
+    hipStream_t copy = nullptr;
     // Host threads the layouts of one recognition pass share (a page's word boxes in row bands,
     // its lines side by side).
     int host_threads;
     explicit Impl(Ctx &c, Detector &d, Recognizer &r, const PipelineOpts &o, int nthreads)
         : ctx(c), det(d), rec(r), opts(o), workers(nthreads),
-          host_threads(std::max(1, int(std::thread::hardware_concurrency()))) {}
+          host_threads(std::max(1, int(std::thread::hardware_concurrency()))) {
+        ctx.bind();
+        OCR_HIP(hipStreamCreateWithFlags(&copy, hipStreamNonBlocking));
+    }
+    ~Impl() {
+        if (copy) {
+            (void)hipStreamSynchronize(copy);
+            (void)hipStreamDestroy(copy);
+        }
+    }
 };
 
 Pipeline::Pipeline(Ctx &ctx, Detector &det, Recognizer &rec, const PipelineOpts &opts)
@@ -144,7 +156,10 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         }
     }
     const int ngroups = int(group_p0.size());
-    std::vector<hipEvent_t> det_ev(size_t(ngroups), nullptr);
+    std::vector<hipEvent_t> det_ev(size_t(ngroups), nullptr), ccl_ev(size_t(ngroups), nullptr);
+    // Each detection pass's masks and runs on the device, kept until the run ends: the copy
+    // stream reads them while the next passes run.
+    std::vector<std::vector<DBuf>> keep_bits(static_cast<size_t>(ngroups)), keep_runs(static_cast<size_t>(ngroups));
     std::vector<hipEvent_t> rec_ev(size_t(nrec), nullptr);
     struct RecPass {
         std::vector<std::pair<int, int>> rows;  // (page, line in page) of every recogniser line
@@ -172,6 +187,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
     std::vector<size_t> words_of(static_cast<size_t>(npages));
     std::vector<int> runs_cap(static_cast<size_t>(npages));
     auto roff_bytes = [&](int p) { return (size_t(h[p] + 1) * 4 + 15) & ~size_t(15); };
+    // (The device block has each run's row after that, which stays on the device.)
     auto runs_bytes = [&](int p) { return 16 + roff_bytes(p) + size_t(runs_cap[size_t(p)]) * 8; };
     for (int p = 0; p < npages; p++) {
         words_of[size_t(p)] = size_t((w[p] + 31) / 32) * h[p];
@@ -181,33 +197,37 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
     }
     for (int g = 0; g < ngroups; g++) {
         const int p0 = group_p0[size_t(g)], p1 = g + 1 < ngroups ? group_p0[size_t(g) + 1] : npages;
-        std::vector<DBuf> bits;
+        std::vector<DBuf> &bits = keep_bits[size_t(g)];
         std::vector<uint32_t *> bp;
         for (int p = p0; p < p1; p++) {
             bits.emplace_back(&ctx, words_of[size_t(p)] * 4);
             bp.push_back(bits.back().as<uint32_t>());
         }
         I.det.detect_pages_device(d_rgb + p0, w + p0, h + p0, p1 - p0, I.opts.thr, bp.data());
-        std::vector<DBuf> rbuf;
+        std::vector<DBuf> &rbuf = keep_runs[size_t(g)];
         std::vector<CclPage> cp;
         for (int p = p0; p < p1; p++) {
-            rbuf.emplace_back(&ctx, runs_bytes(p));
+            rbuf.emplace_back(&ctx, runs_bytes(p) + size_t(runs_cap[size_t(p)]) * 2);
             char *b = rbuf.back().as<char>();
             const int cap = runs_cap[size_t(p)];
             char *root = b + 16 + roff_bytes(p);
             cp.push_back({bp[size_t(p - p0)], w[p], h[p], reinterpret_cast<uint16_t *>(root + size_t(cap) * 4),
                           reinterpret_cast<uint16_t *>(root + size_t(cap) * 6), reinterpret_cast<int32_t *>(root),
-                          reinterpret_cast<int32_t *>(b + 16), cap, reinterpret_cast<int32_t *>(b)});
+                          reinterpret_cast<int32_t *>(b + 16), cap, reinterpret_cast<int32_t *>(b),
+                          reinterpret_cast<uint16_t *>(root + size_t(cap) * 8)});
         }
         ccl_runs(cp.data(), int(cp.size()), st);
+        OCR_HIP(hipEventCreateWithFlags(&ccl_ev[size_t(g)], hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(ccl_ev[size_t(g)], st));
+        OCR_HIP(hipStreamWaitEvent(I.copy, ccl_ev[size_t(g)], 0));
         for (int p = p0; p < p1; p++) {
             OCR_HIP(hipMemcpyAsync(I.bits_host[size_t(p)].p, bp[size_t(p - p0)], words_of[size_t(p)] * 4,
-                                   hipMemcpyDeviceToHost, st));
+                                   hipMemcpyDeviceToHost, I.copy));
             OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), runs_bytes(p),
-                                   hipMemcpyDeviceToHost, st));
+                                   hipMemcpyDeviceToHost, I.copy));
         }
         OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming | hipEventBlockingSync));
-        OCR_HIP(hipEventRecord(det_ev[size_t(g)], st));
+        OCR_HIP(hipEventRecord(det_ev[size_t(g)], I.copy));
         mark("det group " + std::to_string(g) + " enqueued");
     }
     // One thread waits for the detection groups in order and wakes the layouts; the layout
@@ -399,7 +419,10 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         std::unique_lock<std::mutex> lk(mu);
         cv.wait(lk, [&] { return pending_tasks == 0; });
     }
+    (void)hipStreamSynchronize(I.copy);
     for (hipEvent_t e : det_ev)
+        if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ccl_ev)
         if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : rec_ev)
         if (e) (void)hipEventDestroy(e);
