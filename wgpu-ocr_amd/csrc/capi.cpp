@@ -382,25 +382,30 @@ int ocr_word_rects_gpu(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t 
         c.bind();
         const size_t words = size_t(w + 31) / 32 * h;
         const int runs_cap = int(std::min<size_t>(words * 16, size_t(1) << 26));
-        DBuf db(&c, words * 4), dx0(&c, size_t(runs_cap) * 2), dx1(&c, size_t(runs_cap) * 2),
-            droot(&c, size_t(runs_cap) * 4), droff(&c, size_t(h + 1) * 4), dtot(&c, 4), dry(&c, size_t(runs_cap) * 2);
+        // Components and row slots are at most one a run.
+        const size_t rc = size_t(runs_cap);
+        DBuf db(&c, words * 4), dx0(&c, rc * 2), dx1(&c, rc * 2), droot(&c, rc * 4), droff(&c, size_t(h + 1) * 4),
+            dtot(&c, 16), dry(&c, rc * 2), dcbot(&c, rc * 4), dcomps(&c, rc * 16), dxmin(&c, rc * 4), dxmax(&c, rc * 4);
         c.h2d(db.get(), bits, words * 4);
-        CclPage pg{db.as<uint32_t>(), int(w), int(h), dx0.as<uint16_t>(), dx1.as<uint16_t>(), droot.as<int32_t>(),
-                   droff.as<int32_t>(), runs_cap, dtot.as<int32_t>(), dry.as<uint16_t>()};
+        CclPage pg{};
+        pg.bits = db.as<uint32_t>(), pg.w = int(w), pg.h = int(h);
+        pg.x0 = dx0.as<uint16_t>(), pg.x1 = dx1.as<uint16_t>(), pg.root = droot.as<int32_t>();
+        pg.row_off = droff.as<int32_t>(), pg.cap = runs_cap, pg.total = dtot.as<int32_t>();
+        pg.ry = dry.as<uint16_t>(), pg.cbot = dcbot.as<int32_t>(), pg.comps = dcomps.as<int32_t>();
+        pg.xmin = dxmin.as<uint32_t>(), pg.xmax = dxmax.as<uint32_t>(), pg.ccap = runs_cap, pg.scap = runs_cap;
         ccl_runs(&pg, 1, c.stream());
-        int32_t total = 0;
-        c.d2h(&total, dtot.get(), 4);
-        if (total > runs_cap) fail("too many runs");
-        const size_t n = size_t(total);
-        std::vector<uint16_t> x0(n), x1(n);
-        std::vector<int32_t> root(n), row_off(size_t(h) + 1);
-        c.d2h(row_off.data(), droff.get(), row_off.size() * 4);
-        if (total) {
-            c.d2h(x0.data(), dx0.get(), x0.size() * 2);
-            c.d2h(x1.data(), dx1.get(), x1.size() * 2);
-            c.d2h(root.data(), droot.get(), root.size() * 4);
+        int32_t tot[4] = {0, 0, 0, 0};
+        c.d2h(tot, dtot.get(), 16);
+        if (tot[0] > runs_cap) fail("too many runs");
+        const size_t nc = size_t(tot[1]), ns = size_t(tot[2]);
+        std::vector<int32_t> comps(nc * 4);
+        std::vector<uint32_t> xmin(ns), xmax(ns);
+        if (nc) {
+            c.d2h(comps.data(), dcomps.get(), nc * 16);
+            c.d2h(xmin.data(), dxmin.get(), ns * 4);
+            c.d2h(xmax.data(), dxmax.get(), ns * 4);
         }
-        std::vector<RRect> r = word_rects_from_runs(x0.data(), x1.data(), root.data(), row_off.data(), int(h));
+        std::vector<RRect> r = word_rects_from_rows(comps.data(), int(nc), xmin.data(), xmax.data(), int(ns));
         *count = uint32_t(r.size());
         for (size_t i = 0; i < r.size() && i < cap; i++) out[i] = {r[i].cx, r[i].cy, r[i].ux, r[i].uy, r[i].w, r[i].h};
     });

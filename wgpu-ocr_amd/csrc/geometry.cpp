@@ -361,40 +361,27 @@ std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, 
     return rects_of(component_points(bits, w, h, threads), expand, min_area, threads);
 }
 
-std::vector<RRect> word_rects_from_runs(const uint16_t *x0, const uint16_t *x1, const int32_t *root,
-                                        const int32_t *row_off, int h, float expand, float min_area, int threads) {
-    const int n = h > 0 ? row_off[h] : 0;
-    // Component ids in order of first run (a root is its component's first run) and room for
-    // two points a row, then each component's row extremes as band_components builds them.
-    std::vector<int> comp(size_t(std::max(n, 0)), -1), run_comp(size_t(std::max(n, 0)));
-    std::vector<int> npts, last_y;
-    for (int y = 0; y < h; y++)
-        for (int r = row_off[y]; r < row_off[y + 1]; r++) {
-            const int rt = root[r];
-            if (rt < 0 || rt > r) fail("word_rects_from_runs: a run's root must be an earlier run");
-            if (comp[size_t(rt)] < 0) {
-                comp[size_t(rt)] = int(npts.size());
-                npts.push_back(0);
-                last_y.push_back(-1);
-            }
-            const int c = comp[size_t(rt)];
-            run_comp[size_t(r)] = c;
-            if (last_y[size_t(c)] != y) npts[size_t(c)] += 2, last_y[size_t(c)] = y;
+std::vector<RRect> word_rects_from_rows(const int32_t *comps, int ncomps, const uint32_t *xmin, const uint32_t *xmax,
+                                        int nslots, float expand, float min_area, int threads) {
+    // Components in order of first run: the order band_components lists them in.
+    std::vector<int> order(size_t(std::max(ncomps, 0)));
+    for (int c = 0; c < ncomps; c++) order[size_t(c)] = c;
+    std::sort(order.begin(), order.end(), [&](int a, int b) { return comps[4 * a] < comps[4 * b]; });
+    std::vector<std::vector<Pt>> pts(order.size());
+    for (size_t k = 0; k < order.size(); k++) {
+        const int32_t *rec = comps + 4 * order[k];
+        const int top = rec[1], rows = rec[2], b = rec[3];
+        if (rows < 1 || b < 0 || b + rows > nslots) fail("word_rects_from_rows: a component's row slots");
+        auto &v = pts[k];
+        v.reserve(size_t(rows) * 2);
+        for (int r = 0; r < rows; r++) {
+            const uint32_t x0 = xmin[b + r], x1 = xmax[b + r];
+            if (x0 > x1) fail("word_rects_from_rows: a component row without pixels");
+            const float fy = float(top + r);
+            v.push_back({float(x0), fy});
+            if (x1 != x0) v.push_back({float(x1), fy});
         }
-    std::vector<std::vector<Pt>> pts(npts.size());
-    for (size_t c = 0; c < npts.size(); c++) pts[c].reserve(size_t(npts[c]));
-    for (int y = 0; y < h; y++)
-        for (int r = row_off[y]; r < row_off[y + 1]; r++) {
-            auto &v = pts[size_t(run_comp[size_t(r)])];
-            const float fy = float(y), fx0 = float(x0[r]), fx1 = float(x1[r]);
-            if (!v.empty() && v.back().y == fy) {
-                if (v.size() >= 2 && v[v.size() - 2].y == fy) v.back().x = fx1;
-                else if (fx1 != v.back().x) v.push_back({fx1, fy});
-            } else {
-                v.push_back({fx0, fy});
-                if (fx1 != fx0) v.push_back({fx1, fy});
-            }
-        }
+    }
     return rects_of(pts, expand, min_area, threads);
 }
 

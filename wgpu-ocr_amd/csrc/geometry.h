@@ -33,12 +33,12 @@ void set_loop_priority(int prio);
 std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand = 3.f, float min_area = 100.f,
                               int threads = 1);
 
-// The same rectangles from the mask's runs already labelled (on the GPU, kernels/ccl.hip): row
-// y's runs are [row_off[y], row_off[y + 1]), left to right, pixels x0[i] .. x1[i]; root[i] is
-// the first (smallest) run of run i's 8-connected component.
-std::vector<RRect> word_rects_from_runs(const uint16_t *x0, const uint16_t *x1, const int32_t *root,
-                                        const int32_t *row_off, int h, float expand = 3.f, float min_area = 100.f,
-                                        int threads = 1);
+// The same rectangles from the mask's components as labelled on the GPU (kernels/ccl.hip):
+// comps holds ncomps records {first run, top row, rows, first slot} in any order, and row slot
+// i (of nslots) a component's leftmost and rightmost pixel xmin[i] .. xmax[i] in one row, its
+// rows' slots consecutive from the top. Components are listed in order of first run (row-major).
+std::vector<RRect> word_rects_from_rows(const int32_t *comps, int ncomps, const uint32_t *xmin, const uint32_t *xmax,
+                                        int nslots, float expand = 3.f, float min_area = 100.f, int threads = 1);
 
 // Text lines from words, left to right within a line, lines top to bottom (the role of ocrs'
 // find_text_lines, ocr-bench.rs:516).

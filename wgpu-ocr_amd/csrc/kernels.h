@@ -147,8 +147,15 @@ struct CclPage {
     uint16_t *x0, *x1;
     int32_t *root, *row_off;
     int cap;
-    int32_t *total;
-    uint16_t *ry;  // scratch: each run's row (cap entries)
+    int32_t *total;  // [0] runs, [1] components, [2] row slots (the rest of 4 ints unused)
+    uint16_t *ry;    // scratch: each run's row (cap entries)
+    int32_t *cbot;   // scratch (cap): a root's bottom row, then its first row slot
+    // Every component as {first run, top row, rows, first slot} (unordered, ccap entries), and
+    // per row slot the component's leftmost and rightmost pixel in that row (scap entries each).
+    // Past either capacity (or cap runs) the totals say so and these hold nothing usable.
+    int32_t *comps;
+    uint32_t *xmin, *xmax;
+    int ccap, scap;
 };
 void ccl_runs(const CclPage *pages, int count, hipStream_t s);
 // AvgPool (kh, 1) over the first kh rows to one row, written time-major into X[t][ntot][c]

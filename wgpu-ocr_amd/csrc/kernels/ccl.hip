@@ -9,8 +9,13 @@
 // (x ranges overlapping or adjacent; the runs above found by binary search), linking the larger root under the smaller with a
 // compare-and-swap, so every component's root is its smallest run index: its first run in
 // row-major order, the order the host lists components in; (5) a thread per run replaces its
-// parent by its root. A page with more runs than the buffers hold gets no runs (its total says
-// so) and the host labels it from the bits instead.
+// parent by its root and raises its root's bottom row; (6) a thread per root gives its component
+// a record and a block of row slots, one a row from top to bottom (an 8-connected component has
+// pixels in every row of its span); (7) a thread per run folds its first and last pixel into its
+// row's slot with atomic min / max. The host then reads each component's leftmost and rightmost
+// pixel per row, the points its rectangle needs. A page with more runs, components or row slots
+// than the buffers hold gets none of them (its totals say so) and the host labels it from the
+// bits instead.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -88,7 +93,9 @@ __global__ __launch_bounds__(1024) void ccl_scan_kernel(const CclParams p) {
     }
     if (tid == 0) {
         g.row_off[0] = 0;
-        *g.total = s_carry;
+        g.total[0] = s_carry;
+        g.total[1] = 0;
+        g.total[2] = 0;
     }
 }
 
@@ -112,6 +119,7 @@ __global__ __launch_bounds__(256) void ccl_runs_kernel(const CclParams p) {
             st &= st - 1;
             g.x0[is] = uint16_t(wi * 32 + b);
             g.ry[is] = uint16_t(y);
+            g.cbot[is] = y;
             g.root[is] = is;
             is++;
         }
@@ -171,8 +179,44 @@ __global__ __launch_bounds__(256) void ccl_flatten_kernel(const CclParams p) {
     const CclPage &g = p.pg[blockIdx.y];
     const int n = g.row_off[g.h];
     if (n > g.cap) return;
-    for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256)
-        g.root[j] = ccl_find(g.root, j);
+    for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
+        const int r = ccl_find(g.root, j);
+        g.root[j] = r;
+        if (r != j) atomicMax(g.cbot + r, int(g.ry[j]));
+    }
+}
+
+// Component records and row slots: slot blocks are handed out in whatever order the roots come,
+// the records carry each block's start, and the host orders the records by first run.
+__global__ __launch_bounds__(256) void ccl_comps_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.y];
+    const int n = g.row_off[g.h];
+    if (n > g.cap) return;
+    for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
+        if (g.root[j] != j) continue;
+        const int top = g.ry[j], rows = g.cbot[j] - top + 1;
+        const int k = atomicAdd(g.total + 1, 1), b = atomicAdd(g.total + 2, rows);
+        g.cbot[j] = b;
+        if (k < g.ccap) {
+            int4 rec;
+            rec.x = j, rec.y = top, rec.z = rows, rec.w = b;
+            reinterpret_cast<int4 *>(g.comps)[k] = rec;
+        }
+        if (b + rows <= g.scap)
+            for (int i = b; i < b + rows; i++) g.xmin[i] = 0xffffu, g.xmax[i] = 0u;
+    }
+}
+
+__global__ __launch_bounds__(256) void ccl_extremes_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.y];
+    const int n = g.row_off[g.h];
+    if (n > g.cap || g.total[1] > g.ccap || g.total[2] > g.scap) return;
+    for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
+        const int r = g.root[j];
+        const int slot = g.cbot[r] + int(g.ry[j]) - int(g.ry[r]);
+        atomicMin(g.xmin + slot, uint32_t(g.x0[j]));
+        atomicMax(g.xmax + slot, uint32_t(g.x1[j]));
+    }
 }
 
 }  // namespace
@@ -185,7 +229,8 @@ void ccl_runs(const CclPage *pages, int count, hipStream_t s) {
         double bytes = 0;
         for (int k = 0; k < cnt; k++) {
             const CclPage &g = pages[k0 + k];
-            if (g.w < 1 || g.h < 1 || g.w > 65536 || g.h > 65536 || g.cap < 1) fail("ccl_runs: page size or capacity");
+            if (g.w < 1 || g.h < 1 || g.w > 65536 || g.h > 65536 || g.cap < 1 || g.ccap < 1 || g.scap < 1)
+                fail("ccl_runs: page size or capacity");
             p.pg[k] = g;
             maxh = std::max(maxh, g.h);
             maxcap = std::max(maxcap, g.cap);
@@ -200,6 +245,8 @@ void ccl_runs(const CclPage *pages, int count, hipStream_t s) {
         const dim3 runs_grid(unsigned(std::min(2048, (maxcap + 255) / 256)), unsigned(cnt));
         hipLaunchKernelGGL(ccl_union_kernel, runs_grid, dim3(256), 0, s, p);
         hipLaunchKernelGGL(ccl_flatten_kernel, runs_grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ccl_comps_kernel, runs_grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ccl_extremes_kernel, runs_grid, dim3(256), 0, s, p);
         OCR_HIP(hipGetLastError());
     }
 }

@@ -29,11 +29,12 @@ static void wait_event(hipEvent_t ev) {
 }
 
 PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads, int page_prio,
-                       const MaskRuns *runs) {
+                       const MaskRows *rows) {
     set_loop_priority(page_prio);
     PageLayout L;
     std::vector<RRect> words =
-        runs ? word_rects_from_runs(runs->x0, runs->x1, runs->root, runs->row_off, h, 3.f, 100.f, threads)
+        rows ? word_rects_from_rows(rows->comps, rows->ncomps, rows->xmin, rows->xmax, rows->nslots, 3.f, 100.f,
+                                    threads)
              : word_rects(bits, w, h, 3.f, 100.f, threads);
     L.words = int(words.size());
     auto lines = find_text_lines(words);
@@ -182,18 +183,22 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
     try {
     if (I.bits_host.size() < size_t(npages)) I.bits_host.resize(size_t(npages));
     if (I.runs_host.size() < size_t(npages)) I.runs_host.resize(size_t(npages));
-    // Each page's labelled runs (ccl_runs), on the device and copied to the host as one block:
-    // the run count, row offsets (h + 1), roots, then the runs' first and last pixels (cap each).
+    // Each page's labelled components (ccl_runs) in one device block, whose head goes to the
+    // host: the totals (runs, components, row slots), the component records (RCOMPS of 16
+    // bytes), each row slot's leftmost then rightmost pixel (RSLOTS of 4 bytes each). The runs
+    // themselves (row offsets, roots, first and last pixels, rows, root bottoms; runs_cap each)
+    // follow on the device only.
+    constexpr int RCOMPS = 16384, RSLOTS = 65536;
+    constexpr size_t HEAD = 16 + size_t(RCOMPS) * 16 + size_t(RSLOTS) * 8;
     std::vector<size_t> words_of(static_cast<size_t>(npages));
     std::vector<int> runs_cap(static_cast<size_t>(npages));
     auto roff_bytes = [&](int p) { return (size_t(h[p] + 1) * 4 + 15) & ~size_t(15); };
-    // (The device block has each run's row after that, which stays on the device.)
-    auto runs_bytes = [&](int p) { return 16 + roff_bytes(p) + size_t(runs_cap[size_t(p)]) * 8; };
+    auto block_bytes = [&](int p) { return HEAD + roff_bytes(p) + size_t(runs_cap[size_t(p)]) * 14; };
     for (int p = 0; p < npages; p++) {
         words_of[size_t(p)] = size_t((w[p] + 31) / 32) * h[p];
         I.bits_host[size_t(p)].ensure(words_of[size_t(p)] * 4);
         runs_cap[size_t(p)] = int(std::min<size_t>(words_of[size_t(p)] * 16, size_t(1) << 17));
-        I.runs_host[size_t(p)].ensure(runs_bytes(p));
+        I.runs_host[size_t(p)].ensure(HEAD);
     }
     for (int g = 0; g < ngroups; g++) {
         const int p0 = group_p0[size_t(g)], p1 = g + 1 < ngroups ? group_p0[size_t(g) + 1] : npages;
@@ -207,14 +212,22 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         std::vector<DBuf> &rbuf = keep_runs[size_t(g)];
         std::vector<CclPage> cp;
         for (int p = p0; p < p1; p++) {
-            rbuf.emplace_back(&ctx, runs_bytes(p) + size_t(runs_cap[size_t(p)]) * 2);
+            rbuf.emplace_back(&ctx, block_bytes(p));
             char *b = rbuf.back().as<char>();
-            const int cap = runs_cap[size_t(p)];
-            char *root = b + 16 + roff_bytes(p);
-            cp.push_back({bp[size_t(p - p0)], w[p], h[p], reinterpret_cast<uint16_t *>(root + size_t(cap) * 4),
-                          reinterpret_cast<uint16_t *>(root + size_t(cap) * 6), reinterpret_cast<int32_t *>(root),
-                          reinterpret_cast<int32_t *>(b + 16), cap, reinterpret_cast<int32_t *>(b),
-                          reinterpret_cast<uint16_t *>(root + size_t(cap) * 8)});
+            const size_t cap = size_t(runs_cap[size_t(p)]);
+            char *comps = b + 16, *xmin = comps + size_t(RCOMPS) * 16, *xmax = xmin + size_t(RSLOTS) * 4;
+            char *roff = b + HEAD, *root = roff + roff_bytes(p), *cbot = root + cap * 4;
+            char *x0 = cbot + cap * 4, *x1 = x0 + cap * 2, *ry = x1 + cap * 2;
+            CclPage pg{};
+            pg.bits = bp[size_t(p - p0)], pg.w = w[p], pg.h = h[p];
+            pg.x0 = reinterpret_cast<uint16_t *>(x0), pg.x1 = reinterpret_cast<uint16_t *>(x1);
+            pg.root = reinterpret_cast<int32_t *>(root), pg.row_off = reinterpret_cast<int32_t *>(roff);
+            pg.cap = int(cap), pg.total = reinterpret_cast<int32_t *>(b);
+            pg.ry = reinterpret_cast<uint16_t *>(ry), pg.cbot = reinterpret_cast<int32_t *>(cbot);
+            pg.comps = reinterpret_cast<int32_t *>(comps);
+            pg.xmin = reinterpret_cast<uint32_t *>(xmin), pg.xmax = reinterpret_cast<uint32_t *>(xmax);
+            pg.ccap = RCOMPS, pg.scap = RSLOTS;
+            cp.push_back(pg);
         }
         ccl_runs(cp.data(), int(cp.size()), st);
         OCR_HIP(hipEventCreateWithFlags(&ccl_ev[size_t(g)], hipEventDisableTiming));
@@ -223,7 +236,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         for (int p = p0; p < p1; p++) {
             OCR_HIP(hipMemcpyAsync(I.bits_host[size_t(p)].p, bp[size_t(p - p0)], words_of[size_t(p)] * 4,
                                    hipMemcpyDeviceToHost, I.copy));
-            OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), runs_bytes(p),
+            OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), HEAD,
                                    hipMemcpyDeviceToHost, I.copy));
         }
         OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming | hipEventBlockingSync));
@@ -263,12 +276,11 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         const uint32_t *bits = static_cast<const uint32_t *>(I.bits_host[size_t(p)].p);
         const char *rblk = static_cast<const char *>(I.runs_host[size_t(p)].p);
         const int rcap = runs_cap[size_t(p)];
-        const size_t roff = roff_bytes(p);
         const int pw = w[p], ph = h[p];
         int pr = 0;
         while (pass_p0[size_t(pr) + 1] <= p) pr++;
         const int before = pass_p0[size_t(pr)], threads = I.host_threads;
-        I.workers.submit([&, p, grp, bits, rblk, rcap, roff, pw, ph, dev, before, threads] {
+        I.workers.submit([&, p, grp, bits, rblk, rcap, pw, ph, dev, before, threads] {
             std::string err;
             double busy = 0;
             try {
@@ -286,14 +298,15 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
                 }
                 mark("layout " + std::to_string(p) + " start");
                 const auto tc = Clock::now();
-                // The GPU's labelled runs unless the page had more runs than the buffers hold.
-                const int total = *reinterpret_cast<const int32_t *>(rblk);
-                const char *root = rblk + 16 + roff;
-                const MaskRuns mr{reinterpret_cast<const uint16_t *>(root + size_t(rcap) * 4),
-                                  reinterpret_cast<const uint16_t *>(root + size_t(rcap) * 6),
-                                  reinterpret_cast<const int32_t *>(root), reinterpret_cast<const int32_t *>(rblk + 16)};
-                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads, p,
-                                           total <= rcap ? &mr : nullptr);
+                // The GPU's labelled components unless the page had more runs, components or
+                // row slots than the buffers hold.
+                const int32_t *tot = reinterpret_cast<const int32_t *>(rblk);
+                const char *comps = rblk + 16, *xmin = comps + size_t(RCOMPS) * 16;
+                const MaskRows mr{reinterpret_cast<const int32_t *>(comps), tot[1],
+                                  reinterpret_cast<const uint32_t *>(xmin),
+                                  reinterpret_cast<const uint32_t *>(xmin + size_t(RSLOTS) * 4), tot[2]};
+                const bool fits = tot[0] <= rcap && tot[1] <= RCOMPS && tot[2] <= RSLOTS;
+                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads, p, fits ? &mr : nullptr);
                 busy = ms_since(tc);
                 mark("layout " + std::to_string(p) + " done");
                 std::lock_guard<std::mutex> lk(mu);

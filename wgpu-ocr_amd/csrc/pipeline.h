@@ -41,15 +41,17 @@ struct PageLayout {
     // row_off[line_row0[i]] and index this page's spans.
     std::vector<int32_t> row_off, spans, line_row0;
 };
-// The page mask's runs as labelled on the GPU (ccl_runs): its word boxes come from them instead
-// of the bits.
-struct MaskRuns {
-    const uint16_t *x0, *x1;
-    const int32_t *root, *row_off;
+// The page mask's components as labelled on the GPU (ccl_runs): its word boxes come from their
+// row extremes (word_rects_from_rows) instead of the bits.
+struct MaskRows {
+    const int32_t *comps;
+    int ncomps;
+    const uint32_t *xmin, *xmax;
+    int nslots;
 };
 // threads > 1: its loops run on the shared host loop pool at priority page_prio (lower first).
 PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads = 1,
-                       int page_prio = 0, const MaskRuns *runs = nullptr);
+                       int page_prio = 0, const MaskRows *rows = nullptr);
 
 class Pipeline {
   public:
