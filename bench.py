@@ -27,6 +27,11 @@ HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0
 
 
+# The kernel family with the most GPU time in this workload (the per-family breakdown each run
+# reports says whether it still is).
+DOMINANT = "conv3x3_dma"
+
+
 def roofline(kernels):
     """The kernel family with the most time in the timed region, against its bound."""
     fam, k = max(kernels.items(), key=lambda kv: kv[1]["ms"])
@@ -164,8 +169,10 @@ def main():
         pipe.run_device(d_pages, ws, hs)
     ctx.synchronize()
 
-    for fam in ocrhip.FAMILIES:
-        ocrhip.probe_start(fam)
+    # The timed region probes only the dominant kernel family (two events around each of its
+    # launches, for the roofline); the per-family breakdown comes from one more step outside the
+    # timed region with every family probed, so the events do not slow the timed steps.
+    ocrhip.probe_start(DOMINANT)
     lines = 0
     rec_steps = 0
     cpu_busy = 0.0
@@ -179,8 +186,14 @@ def main():
         cpu_busy += st["cpu_busy_ms"]
     ctx.synchronize()
     secs = time.perf_counter() - t0
+    dominant = ocrhip.probe_stop(DOMINANT)
+    for fam in ocrhip.FAMILIES:
+        ocrhip.probe_start(fam)
+    pipe.run_device(d_pages, ws, hs)
+    ctx.synchronize()
     kernels = {f: ocrhip.probe_stop(f) for f in ocrhip.FAMILIES}
     kernels = {f: k for f, k in kernels.items() if k["calls"]}
+    top = max(kernels, key=lambda f: kernels[f]["ms"])
 
     # PCIe-inclusive rate: the same pages handed over from host memory (reported, not the value).
     t1 = time.perf_counter()
@@ -211,8 +224,9 @@ def main():
         "gru_steps_per_page": rec_steps / n_pages,
         "host_busy_ms_per_page": cpu_busy / n_pages,
         "pcie_inclusive_pages_per_sec": len(pages) / host_secs,
-        "roofline": roofline(kernels),
-        "kernels_ms_per_page": {f: round(k["ms"] / n_pages, 4) for f, k in
+        "roofline": roofline({DOMINANT: dominant}),
+        "dominant_in_breakdown": top,
+        "kernels_ms_per_page": {f: round(k["ms"] / len(pages), 4) for f, k in
                                 sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])},
     }
     if not args.no_pp:

@@ -910,10 +910,9 @@ int ocr_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t 
         c.bind();
         const size_t slot = size_t(LINE_H) * wb;
         DBuf drgb(&c, size_t(page_w) * page_h * 3), dout(&c, size_t(count) * slot * sizeof(float));
-        DBuf droff(&c, size_t(n_row_off) * 4), dspans(&c, std::max<size_t>(n_spans, 1) * 4);
         c.h2d(drgb.get(), rgb, size_t(page_w) * page_h * 3);
-        c.h2d(droff.get(), row_off, size_t(n_row_off) * 4);
-        if (n_spans) c.h2d(dspans.get(), spans, size_t(n_spans) * 4);
+        const std::vector<int32_t> roff(row_off, row_off + n_row_off),
+            sp(spans ? spans : row_off, spans ? spans + n_spans : row_off);
         std::vector<CropLine> crops;
         for (uint32_t i = 0; i < count; i++) {
             const int32_t *l = lines + size_t(i) * 6;
@@ -922,7 +921,7 @@ int ocr_line_images(ocr_ctx *ctx, const uint8_t *rgb, uint32_t page_w, uint32_t 
             crops.push_back({drgb.as<uint8_t>(), int(page_w), int(page_h), l[0], l[1], l[2], l[3], l[4], l[5],
                              dout.as<float>() + size_t(i) * slot, int(wb)});
         }
-        line_crop(c, crops, droff.as<int>(), dspans.as<int>(), c.stream());
+        line_crop(c, crops, roff, sp, c.stream());
         c.d2h(out, dout.get(), size_t(count) * slot * sizeof(float));
     });
 }

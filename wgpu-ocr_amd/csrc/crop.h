@@ -24,10 +24,11 @@ struct CropLine {
     int tr = 0, tc = 0, ntx = 0, blk0 = 0;
 };
 
-// All lines in one launch; row_off holds every line's (bh + 1) span offsets (already rebased
-// into the shared spans array). The descriptors and a block-to-line map are uploaded through
-// the context's staging ring.
-void line_crop(Ctx &ctx, std::vector<CropLine> &lines, const int *d_row_off, const int *d_spans, hipStream_t s);
+// All lines in one launch; row_off (host memory) holds every line's (bh + 1) span offsets
+// (already rebased into the shared spans array). The descriptors, a block-to-line map, the row
+// offsets and the spans go to the device as one upload through the context's staging ring.
+void line_crop(Ctx &ctx, std::vector<CropLine> &lines, const std::vector<int32_t> &row_off,
+               const std::vector<int32_t> &spans, hipStream_t s);
 
 // One PP-OCR line image (ppocr::line_input, src/ppocr.rs:42-62, and ppocr::batch, ppocr.rs:64-78).
 struct PpCropLine {

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstring>
 
 #include "../crop.h"
 #include "../runtime.h"
@@ -184,7 +185,8 @@ void pp_line_crop(const PpCropLine *d_lines, int nlines, int max_wb, hipStream_t
     OCR_HIP(hipGetLastError());
 }
 
-void line_crop(Ctx &ctx, std::vector<CropLine> &lines, const int *d_row_off, const int *d_spans, hipStream_t s) {
+void line_crop(Ctx &ctx, std::vector<CropLine> &lines, const std::vector<int32_t> &row_off,
+               const std::vector<int32_t> &spans, hipStream_t s) {
     if (lines.empty()) return;
     // Tile shape per line: 16 rows x 256 columns, narrowed until the source window (at most
     // (tr - 1) sy + 3 rows by (tc - 1) sx + 3 columns) fits in LDS.
@@ -208,12 +210,22 @@ void line_crop(Ctx &ctx, std::vector<CropLine> &lines, const int *d_row_off, con
         map.insert(map.end(), size_t(nb), int(i));
         bytes += 4.0 * LINE_H * L.wb + 3.0 * double(L.bw) * L.bh;
     }
-    DBuf dl(&ctx, lines.size() * sizeof(CropLine)), dm(&ctx, map.size() * sizeof(int));
-    ctx.h2d(dl.get(), lines.data(), lines.size() * sizeof(CropLine));
-    ctx.h2d(dm.get(), map.data(), map.size() * sizeof(int));
+    // One block: descriptors, map, row offsets, spans (each from a 16-byte boundary).
+    auto up16 = [](size_t b) { return (b + 15) & ~size_t(15); };
+    const size_t o_map = up16(lines.size() * sizeof(CropLine)), o_roff = o_map + up16(map.size() * 4),
+                 o_spans = o_roff + up16(row_off.size() * 4), total = o_spans + up16(std::max<size_t>(spans.size(), 1) * 4);
+    std::vector<char> blk(total, 0);
+    std::memcpy(blk.data(), lines.data(), lines.size() * sizeof(CropLine));
+    std::memcpy(blk.data() + o_map, map.data(), map.size() * 4);
+    if (!row_off.empty()) std::memcpy(blk.data() + o_roff, row_off.data(), row_off.size() * 4);
+    if (!spans.empty()) std::memcpy(blk.data() + o_spans, spans.data(), spans.size() * 4);
+    DBuf d(&ctx, total);
+    ctx.h2d(d.get(), blk.data(), total);
+    char *b = d.as<char>();
     ProbeScope probe("line_crop", s, 0, bytes);
-    hipLaunchKernelGGL(line_crop_kernel, dim3(unsigned(map.size())), dim3(256), 0, s, dl.as<CropLine>(), dm.as<int>(),
-                       d_row_off, d_spans);
+    hipLaunchKernelGGL(line_crop_kernel, dim3(unsigned(map.size())), dim3(256), 0, s, reinterpret_cast<CropLine *>(b),
+                       reinterpret_cast<int *>(b + o_map), reinterpret_cast<const int *>(b + o_roff),
+                       reinterpret_cast<const int *>(b + o_spans));
     OCR_HIP(hipGetLastError());
 }
 

@@ -195,16 +195,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         for (int i = 0; i < t[0]; i++) lens[noff + i] = uint32_t(t[2]);
         noff += t[0];
     }
-    std::vector<Graph::Out> trunks;
-    const bool fused = pool_kh_ == 2 && trunk_.run_multi_time_major(ctx_, xs, pool_kh_, X.as<float>(), d.ntot, trunks);
-    if (!fused) {
-        if (pool_kh_ != 2) trunks = trunk_.run_multi(ctx_, xs);
-        std::vector<Act> feats;
-        for (const Graph::Out &t : trunks) feats.push_back(t.act);
-        avgpool_t(feats.data(), count, pool_kh_, X.as<float>(), d.ntot, st);
-    }
     const int tmax = d.tmax, ntot = d.ntot;
-    trunks.clear();
     // The rows that carry a step of some line, t-major: (t, line) with t < lens[line]. The
     // projections and the output layer run on these rows only (the reference computes all
     // tmax x ntot rows and ignores the padding ones); G, Y and the logits keep the [t][ntot]
@@ -230,10 +221,24 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     }
     const int P = int(rows.size());
     const long long steps = P;
-    DBuf rowsd(&ctx_, rows.size() * sizeof(int32_t));
-    ctx_.h2d(rowsd.get(), rows.data(), rows.size() * sizeof(int32_t));
-    DBuf lensd(&ctx_, size_t(ntot) * sizeof(uint32_t));
-    ctx_.h2d(lensd.get(), lens, size_t(ntot) * sizeof(uint32_t));
+    // Lengths and rows in one upload, ahead of the trunk's kernels.
+    const size_t rows_at = (size_t(ntot) * 4 + 15) & ~size_t(15);
+    std::vector<char> tab(rows_at + rows.size() * 4, 0);
+    std::memcpy(tab.data(), lens, size_t(ntot) * 4);
+    std::memcpy(tab.data() + rows_at, rows.data(), rows.size() * 4);
+    DBuf tabd(&ctx_, tab.size());
+    ctx_.h2d(tabd.get(), tab.data(), tab.size());
+    const uint32_t *lensd = reinterpret_cast<const uint32_t *>(tabd.as<char>());
+    const int32_t *rowsd = reinterpret_cast<const int32_t *>(tabd.as<char>() + rows_at);
+    std::vector<Graph::Out> trunks;
+    const bool fused = pool_kh_ == 2 && trunk_.run_multi_time_major(ctx_, xs, pool_kh_, X.as<float>(), d.ntot, trunks);
+    if (!fused) {
+        if (pool_kh_ != 2) trunks = trunk_.run_multi(ctx_, xs);
+        std::vector<Act> feats;
+        for (const Graph::Out &t : trunks) feats.push_back(t.act);
+        avgpool_t(feats.data(), count, pool_kh_, X.as<float>(), d.ntot, st);
+    }
+    trunks.clear();
     DBuf G(&ctx_, size_t(M) * 1536 * sizeof(float));
     DBuf Y[2] = {DBuf(&ctx_, size_t(M) * 512 * sizeof(float)), DBuf(&ctx_, size_t(M) * 512 * sizeof(float))};
     const float *in = X.as<float>();
@@ -244,28 +249,28 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         ConvArgs ca;
         ca.x = Act{const_cast<float *>(in), 1, 1, P, in_c, in_c};
         ca.y = Act{G.as<float>(), 1, 1, P, 1536, 1536};
-        ca.rows = rowsd.as<int32_t>();
+        ca.rows = rowsd;
         ca.wt_hi = L.w_hi;
         ca.wt_lo = L.w_lo;
         ca.wt_frag = L.w_frag;
         ca.bias = L.wb;
         ca.pk = L.pk;
         conv_mfma(ca, st);
-        gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd.as<uint32_t>(), ntot, tmax, steps, st);
+        gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd, ntot, tmax, steps, st);
         in = Y[l].as<float>();
         in_c = 512;
     }
     ConvArgs ca;
     ca.x = Act{const_cast<float *>(in), 1, 1, P, 512, 512};
     ca.y = Act{logits, 1, 1, P, classes_, classes_};
-    ca.rows = rowsd.as<int32_t>();
+    ca.rows = rowsd;
     ca.wt_hi = lin_hi_;
     ca.wt_lo = lin_lo_;
     ca.wt_frag = lin_frag_;
     ca.bias = lin_b_;
     ca.pk = lin_pk_;
     conv_mfma(ca, st);
-    if (best) argmax_rows(logits, P, classes_, best, st, rowsd.as<int32_t>());
+    if (best) argmax_rows(logits, P, classes_, best, st, rowsd);
 }
 
 }  // namespace ocr

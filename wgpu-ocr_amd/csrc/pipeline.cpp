@@ -18,13 +18,15 @@ namespace ocr {
 
 // Waits for a GPU event by polling every 20 microseconds: the worker threads waiting for
 // detection or recognition results sleep instead of spinning, so the host cores go to the
-// layouts.
-static void wait_event(hipEvent_t ev) {
+// layouts; spin: yield between polls instead (the last pass, when no layout is left to run and
+// a sleep's wake-up latency would add to the run).
+static void wait_event(hipEvent_t ev, bool spin = false) {
     for (;;) {
         const hipError_t e = hipEventQuery(ev);
         if (e == hipSuccess) return;
         if (e != hipErrorNotReady) OCR_HIP(e);
-        std::this_thread::sleep_for(std::chrono::microseconds(20));
+        if (spin) std::this_thread::yield();
+        else std::this_thread::sleep_for(std::chrono::microseconds(20));
     }
 }
 
@@ -161,7 +163,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
     // Each detection pass's masks and runs on the device, kept until the run ends: the copy
     // stream reads them while the next passes run.
     std::vector<std::vector<DBuf>> keep_bits(static_cast<size_t>(ngroups)), keep_runs(static_cast<size_t>(ngroups));
-    std::vector<hipEvent_t> rec_ev(size_t(nrec), nullptr);
+    std::vector<hipEvent_t> rec_ev(size_t(nrec), nullptr), am_ev(size_t(nrec), nullptr);
     struct RecPass {
         std::vector<std::pair<int, int>> rows;  // (page, line in page) of every recogniser line
         std::vector<uint32_t> lens;
@@ -169,6 +171,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         int tmax = 0, ntot = 0;
         std::vector<CropLine> crops;
         std::vector<int32_t> row_off, spans;
+        DBuf best;  // the arg-max classes, read by the copy to the host after the pass's kernels
     };
     std::vector<RecPass> passes(static_cast<size_t>(nrec));
     // Detection groups completed so far (set by the watcher thread below).
@@ -378,25 +381,27 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             }
         }
         if (batches.empty()) continue;
-        DBuf droff(&ctx, R.row_off.size() * 4), dspans(&ctx, std::max<size_t>(R.spans.size(), 1) * 4);
-        ctx.h2d(droff.get(), R.row_off.data(), R.row_off.size() * 4);
-        if (!R.spans.empty()) ctx.h2d(dspans.get(), R.spans.data(), R.spans.size() * 4);
         mark("rec " + std::to_string(r) + " crops built");
-        line_crop(ctx, R.crops, droff.as<int>(), dspans.as<int>(), st);
+        line_crop(ctx, R.crops, R.row_off, R.spans, st);
         const Recognizer::Dims d = I.rec.dims(batches.data(), int(batches.size()));
         R.tmax = d.tmax;
         R.ntot = d.ntot;
         R.lens.assign(size_t(d.ntot), 0);
         DBuf logits(&ctx, size_t(d.tmax) * d.ntot * d.classes * sizeof(float));
-        DBuf best(&ctx, size_t(d.tmax) * d.ntot * sizeof(uint32_t));
-        I.rec.recognize_device(batches.data(), int(batches.size()), logits.as<float>(), best.as<uint32_t>(),
+        R.best = DBuf(&ctx, size_t(d.tmax) * d.ntot * sizeof(uint32_t));
+        I.rec.recognize_device(batches.data(), int(batches.size()), logits.as<float>(), R.best.as<uint32_t>(),
                                R.lens.data());
         mark("rec " + std::to_string(r) + " enqueued");
+        // The arg-max goes to the host on the copy stream, so the next pass's kernels do not
+        // wait for the copy.
         I.best_host[size_t(r)].ensure(size_t(d.tmax) * d.ntot * sizeof(uint32_t));
-        OCR_HIP(hipMemcpyAsync(I.best_host[size_t(r)].p, best.get(), size_t(d.tmax) * d.ntot * sizeof(uint32_t),
-                               hipMemcpyDeviceToHost, st));
+        OCR_HIP(hipEventCreateWithFlags(&am_ev[size_t(r)], hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(am_ev[size_t(r)], st));
+        OCR_HIP(hipStreamWaitEvent(I.copy, am_ev[size_t(r)], 0));
+        OCR_HIP(hipMemcpyAsync(I.best_host[size_t(r)].p, R.best.get(), size_t(d.tmax) * d.ntot * sizeof(uint32_t),
+                               hipMemcpyDeviceToHost, I.copy));
         OCR_HIP(hipEventCreateWithFlags(&rec_ev[size_t(r)], hipEventDisableTiming));
-        OCR_HIP(hipEventRecord(rec_ev[size_t(r)], st));
+        OCR_HIP(hipEventRecord(rec_ev[size_t(r)], I.copy));
         stats_.rec_passes++;
         // 4. Greedy CTC on the host once the arg-max is back.
         {
@@ -405,19 +410,26 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         }
         hipEvent_t ev = rec_ev[size_t(r)];
         const uint32_t *bh = static_cast<const uint32_t *>(I.best_host[size_t(r)].p);
-        I.workers.submit([&, ev, bh, r, dev] {
+        const bool last = r == nrec - 1;
+        I.workers.submit([&, ev, bh, r, dev, last] {
             std::string err;
             double busy = 0;
             try {
                 (void)hipSetDevice(dev);
-                wait_event(ev);
+                wait_event(ev, last);
+                mark("ctc " + std::to_string(r) + " start");
                 const auto tc = Clock::now();
                 const RecPass &R2 = passes[size_t(r)];
-                for (size_t j = 0; j < R2.rows.size(); j++) {
-                    std::string s = ctc_decode(bh + j, int(R2.lens[j]), R2.ntot, R2.widths[j]);
-                    pages_[size_t(R2.rows[j].first)].lines[size_t(R2.rows[j].second)] = std::move(s);
-                }
+                // Lines in chunks on the loop pool (each line's text has a slot of its own).
+                const int nl = int(R2.rows.size()), chunks = std::min(nl, 32);
+                LoopPool::get().run(chunks, [&](int c) {
+                    for (int j = int(long(nl) * c / chunks); j < int(long(nl) * (c + 1) / chunks); j++) {
+                        std::string s = ctc_decode(bh + j, int(R2.lens[size_t(j)]), R2.ntot, R2.widths[size_t(j)]);
+                        pages_[size_t(R2.rows[size_t(j)].first)].lines[size_t(R2.rows[size_t(j)].second)] = std::move(s);
+                    }
+                }, -1);
                 busy = ms_since(tc);
+                mark("ctc " + std::to_string(r) + " done");
             } catch (const std::exception &e) {
                 err = e.what();
             }
@@ -432,12 +444,15 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         std::unique_lock<std::mutex> lk(mu);
         cv.wait(lk, [&] { return pending_tasks == 0; });
     }
+    mark("tasks done");
     (void)hipStreamSynchronize(I.copy);
     for (hipEvent_t e : det_ev)
         if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : ccl_ev)
         if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : rec_ev)
+        if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : am_ev)
         if (e) (void)hipEventDestroy(e);
     if (!error.empty()) fail("pipeline: " + error);
     ctx.sync();
