@@ -212,7 +212,12 @@ void Ctx::h2d(void *dst, const void *src, size_t bytes) {
         return;
     }
     std::lock_guard<std::mutex> lk(ring_mu_);
-    if (!ring_) OCR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ring_), RING_BYTES, hipHostMallocDefault));
+    if (!ring_) {
+        OCR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ring_), RING_BYTES, hipHostMallocDefault));
+        // Fault every page in now (a page's first CPU write runs at about 2 GB/s, later ones at
+        // memory speed), not while a run stages its tables.
+        std::memset(ring_, 0, RING_BYTES);
+    }
     const size_t need = (bytes + 255) & ~size_t(255);
     if (ring_head_ + need > RING_BYTES) ring_head_ = 0;
     const size_t b = ring_head_, e = b + need;
