@@ -156,6 +156,19 @@ def test_pipeline_merge_and_device_entry(detector, recognizer, ctx):
     assert a.stats()["lines"] == b.stats()["lines"]
 
 
+def test_pipeline_words_match_host_labelling(detector, recognizer):
+    # Eight full pages in one detection pass label their masks on the GPU concurrently; every
+    # page's word count equals the host labelling of the same mask (a component split, merged or
+    # given a wrong bottom row by a race would change it, or fail the run's own row checks).
+    pages = [synth.page(s) for s in range(20, 28)]
+    p = ocrhip.Pipeline(detector, recognizer, merge=8, det_batch=8)
+    p.run(pages)
+    for k, page in enumerate(pages):
+        print(f"page {k}", flush=True)
+        want = ocrhip.word_rects(detector.detect_page(page, 0.5), page.shape[1])
+        assert p.texts(k)[1] == len(want)
+
+
 def test_pipeline_blank_and_small_pages(detector, recognizer):
     blank = np.full((3300, 2550, 3), 255, np.uint8)
     small = np.ascontiguousarray(synth.page(7)[150:400, 100:900])

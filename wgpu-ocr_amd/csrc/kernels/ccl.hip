@@ -12,7 +12,8 @@
 // parent by its root and raises its root's bottom row; (6) a thread per root gives its component
 // a record and a block of row slots, one a row from top to bottom (an 8-connected component has
 // pixels in every row of its span); (7) a thread per run folds its first and last pixel into its
-// row's slot with atomic min / max. The host then reads each component's leftmost and rightmost
+// row's slot with atomic min / max (only the first and last of neighbouring runs of one component
+// in a row). The host then reads each component's leftmost and rightmost
 // pixel per row, the points its rectangle needs. A page with more runs, components or row slots
 // than the buffers hold gets none of them (its totals say so) and the host labels it from the
 // bits instead.
@@ -133,11 +134,25 @@ __global__ __launch_bounds__(256) void ccl_runs_kernel(const CclParams p) {
     }
 }
 
-__device__ inline int ccl_find(const int32_t *parent, int x) {
+// The root of x, read only (the flatten step: its stores of final roots must not be replaced by
+// a concurrent walk's shortcut).
+__device__ inline int ccl_root(const int32_t *parent, int x) {
     for (;;) {
         const int q = __atomic_load_n(parent + x, __ATOMIC_RELAXED);
         if (q == x) return x;
         x = q;
+    }
+}
+
+// The root of x, halving the path on the way (x's parent becomes its grandparent: an ancestor
+// either way, and only roots are ever linked, so the store never undoes a link). Union step only.
+__device__ inline int ccl_find(int32_t *parent, int x) {
+    for (;;) {
+        const int q = __atomic_load_n(parent + x, __ATOMIC_RELAXED);
+        if (q == x) return x;
+        const int qq = __atomic_load_n(parent + q, __ATOMIC_RELAXED);
+        if (qq != q) __atomic_store_n(parent + x, qq, __ATOMIC_RELAXED);
+        x = qq;
     }
 }
 
@@ -180,9 +195,13 @@ __global__ __launch_bounds__(256) void ccl_flatten_kernel(const CclParams p) {
     const int n = g.row_off[g.h];
     if (n > g.cap) return;
     for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
-        const int r = ccl_find(g.root, j);
+        const int r = ccl_root(g.root, j);
         g.root[j] = r;
-        if (r != j) atomicMax(g.cbot + r, int(g.ry[j]));
+        // The root's bottom row, from the last of neighbouring runs of one component in a row
+        // (a neighbour's parent equal to r means the same component: r is a root).
+        const int y = g.ry[j];
+        const bool last = j + 1 == n || int(g.ry[j + 1]) != y || __atomic_load_n(g.root + j + 1, __ATOMIC_RELAXED) != r;
+        if (r != j && last) atomicMax(g.cbot + r, y);
     }
 }
 
@@ -212,10 +231,15 @@ __global__ __launch_bounds__(256) void ccl_extremes_kernel(const CclParams p) {
     const int n = g.row_off[g.h];
     if (n > g.cap || g.total[1] > g.ccap || g.total[2] > g.scap) return;
     for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
-        const int r = g.root[j];
-        const int slot = g.cbot[r] + int(g.ry[j]) - int(g.ry[r]);
-        atomicMin(g.xmin + slot, uint32_t(g.x0[j]));
-        atomicMax(g.xmax + slot, uint32_t(g.x1[j]));
+        const int r = g.root[j], y = g.ry[j];
+        // Runs of a row go left to right: of neighbouring runs of one component in one row only
+        // the first can hold its leftmost pixel and only the last its rightmost.
+        const bool first = j == 0 || int(g.ry[j - 1]) != y || g.root[j - 1] != r;
+        const bool last = j + 1 == n || int(g.ry[j + 1]) != y || g.root[j + 1] != r;
+        if (!first && !last) continue;
+        const int slot = g.cbot[r] + y - int(g.ry[r]);
+        if (first) atomicMin(g.xmin + slot, uint32_t(g.x0[j]));
+        if (last) atomicMax(g.xmax + slot, uint32_t(g.x1[j]));
     }
 }
 
