@@ -587,6 +587,9 @@ void Graph::Exec::step(size_t i) {
             conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
             break;
         }
+        // Kernel = stride = 2 with few channels: the GEMM over the input pixels would be one
+        // 32-wide K chunk deep, so a float32 pass at HBM speed does better.
+        if (convt_k2s2(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st)) break;
         if (s.allph.whi) {
             // All phases as one GEMM over the input pixels.
             ConvArgs ca;

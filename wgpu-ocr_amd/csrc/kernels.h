@@ -114,6 +114,10 @@ bool conv1_mfma_multi(const Act *x, const Act *y, const Act *ypool, int count, c
 // ConvTranspose gather form (gpu.rs:424-460); w re-laid out as [ky][kx][cin][cout].
 void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride,
                     int act, hipStream_t s);
+// The same for kernel = stride = 2 with channel counts multiples of 4 and 4 cin cout <= 16384
+// (the weights in LDS): one float32 pass at HBM speed. False (nothing launched) otherwise.
+bool convt_k2s2(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride, int act,
+                hipStream_t s);
 void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s);
 void copy_act(const Act &x, const Act &y, int y0, int x0, hipStream_t s);  // Slice / Concat copies
 void activate(const Act &x, const Act &y, int act, hipStream_t s);

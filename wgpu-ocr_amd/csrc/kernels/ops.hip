@@ -133,6 +133,76 @@ __global__ void convt_kernel(const float *x, int n, int h, int w, int cin, int x
     y[pix * ycs + co] = act_f(acc + b[co], act);
 }
 
+// ConvTranspose with kernel = stride = 2 (gpu.rs:424-460 for this case): output pixel (oy, ox)
+// is input pixel (oy / 2, ox / 2) times the one tap (oy % 2, ox % 2), no overlapping taps. The
+// weights [ky][kx][cin][cout] sit in LDS. A thread makes four output channels (c0 .. c0 + 3) of
+// phase px in output row oy for four neighbouring input columns, so each weight read from LDS
+// serves 16 FMAs; neighbouring lanes take the channel quads, then the two phases, so a store
+// instruction writes whole neighbouring pixels. float32 FMAs over the input channels in order,
+// the bias added last as in convt_kernel. Grid-stride, so each workgroup fills its LDS once.
+constexpr int CT2_MAXW = 16384;  // weight floats in LDS (64 KB)
+
+__global__ __launch_bounds__(256) void convt_k2s2_kernel(const float *x, int h, int w, int cin, long xcs, float *y,
+                                                          long total, int oh, int ow, int cout, long ycs, int nxg,
+                                                          const float *wt, const float *b, int act) {
+    extern __shared__ float sw[];
+    for (int i = threadIdx.x; i < 4 * cin * cout; i += 256) sw[i] = wt[i];
+    __syncthreads();
+    const int cq = cout >> 2;
+    for (long g = long(blockIdx.x) * 256 + threadIdx.x; g < total; g += long(gridDim.x) * 256) {
+        const int q = int(g % cq);
+        long t = g / cq;
+        const int px = int(t & 1);
+        t >>= 1;
+        const int xg = int(t % nxg);
+        t /= nxg;
+        const int oy = int(t % oh), img = int(t / oh);
+        const float *xrow = x + (size_t(img) * h + (oy >> 1)) * w * xcs;
+        const float *xp[4];
+        bool live[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int ix = 4 * xg + k;
+            live[k] = ix < w && 2 * ix + px < ow;
+            xp[k] = xrow + size_t(live[k] ? ix : 0) * xcs;
+        }
+        const float4 *wp = reinterpret_cast<const float4 *>(sw + size_t(((oy & 1) * 2 + px) * cin) * cout) + q;
+        float acc[4][4] = {};
+        for (int ci = 0; ci < cin; ci += 4) {
+            float xs[4][4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float4 v = *reinterpret_cast<const float4 *>(xp[k] + ci);
+                xs[k][0] = v.x, xs[k][1] = v.y, xs[k][2] = v.z, xs[k][3] = v.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float4 wv = wp[size_t(ci + e) * cq];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    acc[k][0] = fmaf(xs[k][e], wv.x, acc[k][0]);
+                    acc[k][1] = fmaf(xs[k][e], wv.y, acc[k][1]);
+                    acc[k][2] = fmaf(xs[k][e], wv.z, acc[k][2]);
+                    acc[k][3] = fmaf(xs[k][e], wv.w, acc[k][3]);
+                }
+            }
+        }
+        const int c0 = 4 * q;
+        const float b0 = b[c0], b1 = b[c0 + 1], b2 = b[c0 + 2], b3 = b[c0 + 3];
+        float *yrow = y + (size_t(img) * oh + oy) * ow * ycs + c0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (!live[k]) continue;
+            float4 o;
+            o.x = act_f(acc[k][0] + b0, act);
+            o.y = act_f(acc[k][1] + b1, act);
+            o.z = act_f(acc[k][2] + b2, act);
+            o.w = act_f(acc[k][3] + b3, act);
+            *reinterpret_cast<float4 *>(yrow + size_t(2 * (4 * xg + k) + px) * ycs) = o;
+        }
+    }
+}
+
 // ---- maxpool (gpu.rs:462-482): kernel = stride, no padding, floor ---------------------------
 __global__ void maxpool_kernel(const float *x, int n, int h, int w, int c, int xcs, float *y, int oh, int ow, int ycs,
                                int kh, int kw) {
@@ -368,6 +438,26 @@ void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, 
     hipLaunchKernelGGL(convt_kernel, dim3(blocks_for(y.count())), dim3(256), 0, s, x.p, x.n, x.h, x.w, x.c, x.cs, y.p,
                        y.h, y.w, y.c, y.cs, w, b, kh, kw, stride, act);
     OCR_HIP(hipGetLastError());
+}
+
+bool convt_k2s2(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride, int act,
+                hipStream_t s) {
+    if (kh != 2 || kw != 2 || stride != 2 || !b) return false;
+    if (x.c % 4 || y.c % 4 || x.cs % 4 || y.cs % 4 || 4 * x.c * y.c > CT2_MAXW) return false;
+    if ((reinterpret_cast<uintptr_t>(x.p) & 15) || (reinterpret_cast<uintptr_t>(y.p) & 15)) return false;
+    if (x.n != y.n || y.h > 2 * x.h || y.w > 2 * x.w || y.h < 1 || y.w < 1) return false;
+    // Threads: channel quads x 2 phases x groups of 4 input columns (of the ceil(ow / 2) the row
+    // reads) x output rows x images.
+    const int nxg = ((y.w + 1) / 2 + 3) / 4;
+    const long total = long(y.n) * y.h * nxg * 2 * (y.c / 4);
+    ProbeScope probe("conv_transpose", s, 2.0 * double(y.pixels()) * x.c * y.c,
+                     4.0 * double(x.count() + y.count()));
+    // Four workgroups a CU: each fills its LDS once and walks several blocks of outputs.
+    const unsigned grid = unsigned(std::min<long>((total + 255) / 256, 1024));
+    hipLaunchKernelGGL(convt_k2s2_kernel, dim3(grid), dim3(256), size_t(4) * 4 * x.c * y.c, s, x.p, x.h, x.w, x.c,
+                       long(x.cs), y.p, total, y.h, y.w, y.c, long(y.cs), nxg, w, b, act);
+    OCR_HIP(hipGetLastError());
+    return true;
 }
 
 void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s) {
