@@ -158,6 +158,8 @@ def test_conv_transpose_2x3(ctx, tmp_path):
                                                         ((2, 2), 2, 40, 16, (6, 9), True),
                                                         ((2, 2), 2, 64, 32, (13, 37), True),
                                                         ((2, 2), 2, 32, 48, (1, 1), True),
+                                                        ((2, 2), 2, 128, 64, (5, 7), True),
+                                                        ((2, 2), 2, 256, 48, (3, 10), False),
                                                         ((3, 3), 3, 16, 16, (5, 4), True),
                                                         ((3, 3), 2, 16, 16, (5, 7), True),
                                                         ((2, 3), 2, 32, 16, (4, 5), True)])
