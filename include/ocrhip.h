@@ -135,9 +135,10 @@ int ocr_word_rects(const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out,
  * across the cuts): the same rectangles in the same order. The page pipeline's layout runs so. */
 int ocr_word_rects_mt(const uint32_t *bits, uint32_t w, uint32_t h, uint32_t threads, ocr_rrect *out, uint32_t cap,
                       uint32_t *count);
-/* The same with the mask's runs labelled on the GPU of ctx (the page pipeline's path: the host
- * only turns each component's row extremes into a rectangle). The same rectangles in the same
- * order; no counterpart in the reference, which finds the components on the host. */
+/* The same with the mask's components labelled on the GPU of ctx, down to each component's
+ * leftmost and rightmost pixel per row (the page pipeline's path: the host only turns those rows
+ * into a hull and a rectangle). The same rectangles in the same order; no counterpart in the
+ * reference, which finds the components on the host. */
 int ocr_word_rects_gpu(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out, uint32_t cap,
                        uint32_t *count);
 
