@@ -53,6 +53,12 @@ void *ocr_device_alloc(ocr_ctx *ctx, size_t bytes);
 int ocr_device_free(ocr_ctx *ctx, void *p);
 int ocr_memcpy_h2d(ocr_ctx *ctx, void *dst, const void *src, size_t bytes);
 int ocr_memcpy_d2h(ocr_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Page-locked host memory (hipHostMalloc) for pages a caller renders straight into: the page
+ * pipeline's upload copies from it with no staging copy. The reference has no counterpart (its
+ * uploads go through wgpu's staging, src/gpu.rs:922-936). ocr_host_free waits for the context's
+ * stream first. */
+void *ocr_host_alloc(ocr_ctx *ctx, size_t bytes);
+int ocr_host_free(ocr_ctx *ctx, void *p);
 
 /* Detector::new (src/gpu.rs:1385-1387) from an ONNX file (Onnx::load, src/onnx.rs:88-123). */
 ocr_detector *ocr_detector_new(ocr_ctx *ctx, const char *onnx_path);
@@ -183,9 +189,18 @@ void ocr_pipeline_free(ocr_pipeline *pipe);
  * decoded. */
 int ocr_pipeline_run_device(ocr_pipeline *pipe, const uint8_t *const *d_rgb, const uint32_t *w, const uint32_t *h,
                             uint32_t npages);
-/* The same with the pages in host memory (uploaded first, inside the call). */
+/* The same with the pages in host memory, as the reference's run receives them
+ * (src/bin/ocr-bench.rs:458-587; each page uploaded inside detect_page, src/gpu.rs:1402-1406).
+ * Each detection group's pages go to the device on a copy stream of their own while the earlier
+ * groups are detected and recognised: through a pinned staging ring (host copies on the host
+ * worker threads), or straight from the caller's memory when it is page-locked
+ * (ocr_host_alloc). Per-page errors (ocr-bench.rs:277-281, 303-307): a page that fails keeps its
+ * error (ocr_pipeline_page_error) and the other pages finish; the call then returns OCR_ERR with
+ * the number of failed pages and the first error. */
 int ocr_pipeline_run(ocr_pipeline *pipe, const uint8_t *const *rgb, const uint32_t *w, const uint32_t *h,
                      uint32_t npages);
+/* Why a page of the last run failed ("" when it finished); *len receives the message length. */
+int ocr_pipeline_page_error(ocr_pipeline *pipe, uint32_t page, char *buf, uint32_t cap, uint32_t *len);
 int ocr_pipeline_stats_get(ocr_pipeline *pipe, ocr_pipeline_stats *out);
 /* Lines and words found on a page of the last run. */
 int ocr_pipeline_page(ocr_pipeline *pipe, uint32_t page, uint32_t *lines, uint32_t *words);

@@ -1,0 +1,288 @@
+// The page pipeline's schedule (wgpu-ocr_amd/csrc/pipeline_core.h) with hooks that record the
+// order of the steps and fail on purpose: a failing step fails exactly the pages it covers and
+// every other page finishes (the reference reports errors per page, src/bin/ocr-bench.rs:277-281,
+// 303-307), the ordering rules hold, and nothing deadlocks with few workers. Built and run by
+// tests/test_pipeline_core.py under AddressSanitizer + UndefinedBehaviorSanitizer and under
+// ThreadSanitizer.
+#include "pipeline_core.h"
+
+#include <atomic>
+#include <cstdio>
+#include <cstdlib>
+#include <deque>
+#include <random>
+#include <stdexcept>
+#include <string>
+
+using namespace ocr;
+
+namespace {
+
+int failures = 0;
+#define CHECK(c, ...)                                     \
+    do {                                                  \
+        if (!(c)) {                                       \
+            failures++;                                   \
+            std::fprintf(stderr, "FAIL %s:%d: ", __FILE__, __LINE__); \
+            std::fprintf(stderr, __VA_ARGS__);            \
+            std::fprintf(stderr, "\n");                   \
+        }                                                 \
+    } while (0)
+
+// A small FIFO thread pool (the pipeline's Workers without HIP).
+class Pool {
+  public:
+    explicit Pool(int n) {
+        for (int i = 0; i < n; i++) t_.emplace_back([this] { loop(); });
+    }
+    ~Pool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto &t : t_) t.join();
+    }
+    void submit(std::function<void()> f) {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            q_.push_back(std::move(f));
+        }
+        cv_.notify_one();
+    }
+
+  private:
+    void loop() {
+        for (;;) {
+            std::function<void()> f;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [this] { return stop_ || !q_.empty(); });
+                if (q_.empty()) return;
+                f = std::move(q_.front());
+                q_.pop_front();
+            }
+            f();
+        }
+    }
+    std::vector<std::thread> t_;
+    std::deque<std::function<void()>> q_;
+    std::mutex mu_;
+    std::condition_variable cv_;
+    bool stop_ = false;
+};
+
+struct Faults {
+    int stage = -1, detect = -1, detect_wait = -1, layout = -1, recognize = -1, decode = -1;
+};
+
+// Records what ran and checks the ordering rules as it goes.
+struct Hooks final : PipelineHooks {
+    const PipelinePlan &P;
+    Faults f;
+    std::mt19937 rng;
+    std::mutex mu;
+    std::vector<int> staged_at, detected_at, waited_at, laid_at, rec_at, dec_at;
+    std::vector<std::vector<char>> rec_ok;
+    int clock = 0;
+    bool jitter, lookahead = false;
+    Hooks(const PipelinePlan &plan, Faults faults, unsigned seed, bool jit)
+        : P(plan), f(faults), rng(seed), jitter(jit) {
+        staged_at.assign(size_t(P.groups()), -1);
+        detected_at = waited_at = staged_at;
+        laid_at.assign(size_t(P.npages), -1);
+        rec_at.assign(size_t(P.passes()), -1);
+        dec_at = rec_at;
+        rec_ok.resize(size_t(P.passes()));
+    }
+    void nap() {
+        if (!jitter) return;
+        int us;
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            us = int(rng() % 300);
+        }
+        std::this_thread::sleep_for(std::chrono::microseconds(us));
+    }
+    int tick() {
+        std::lock_guard<std::mutex> lk(mu);
+        return clock++;
+    }
+    void stage(int g) override {
+        nap();
+        if (g == f.stage) throw std::runtime_error("stage fault");
+        staged_at[size_t(g)] = tick();
+    }
+    void detect(int g) override {
+        CHECK(staged_at[size_t(g)] >= 0, "detect(%d) before its stage", g);
+        nap();
+        if (g == f.detect) throw std::runtime_error("detect fault");
+        detected_at[size_t(g)] = tick();
+    }
+    void detect_wait(int g) override {
+        CHECK(detected_at[size_t(g)] >= 0, "detect_wait(%d) before detect", g);
+        nap();
+        if (g == f.detect_wait) throw std::runtime_error("detect_wait fault");
+        waited_at[size_t(g)] = tick();
+    }
+    void layout(int p) override {
+        const int g = P.group_of[size_t(p)];
+        CHECK(waited_at[size_t(g)] >= 0, "layout(%d) before its detection finished", p);
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            for (int q = 0; q < P.pass_p0[size_t(P.pass_of[size_t(p)])]; q++)
+                CHECK(laid_at[size_t(q)] >= 0 || q == f.layout || P.group_of[size_t(q)] == f.stage ||
+                          P.group_of[size_t(q)] == f.detect || P.group_of[size_t(q)] == f.detect_wait,
+                      "layout(%d) before page %d of an earlier pass", p, q);
+        }
+        nap();
+        if (p == f.layout) throw std::runtime_error("layout fault");
+        const int t = tick();
+        std::lock_guard<std::mutex> lk(mu);
+        laid_at[size_t(p)] = t;
+    }
+    void recognize(int r, const std::vector<char> &ok) override {
+        const int p0 = P.pass_p0[size_t(r)], p1 = P.pass_p0[size_t(r) + 1];
+        CHECK(int(ok.size()) == p1 - p0, "recognize(%d): ok has %zu entries", r, ok.size());
+        for (int p = p0; p < p1; p++) {
+            std::lock_guard<std::mutex> lk(mu);
+            CHECK((laid_at[size_t(p)] >= 0) == (ok[size_t(p - p0)] != 0), "recognize(%d): page %d ok flag", r, p);
+        }
+        if (lookahead && r + 1 < P.passes())
+            for (int q = P.pass_p0[size_t(r) + 1]; q < P.pass_p0[size_t(r) + 2]; q++) {
+                const int g = P.group_of[size_t(q)];
+                CHECK(detected_at[size_t(g)] >= 0 || g == f.stage || g == f.detect,
+                      "recognize(%d) before group %d of the next pass was queued", r, g);
+            }
+        nap();
+        if (r == f.recognize) throw std::runtime_error("recognize fault");
+        rec_ok[size_t(r)] = ok;
+        rec_at[size_t(r)] = tick();
+    }
+    void decode(int r, bool last) override {
+        CHECK(rec_at[size_t(r)] >= 0, "decode(%d) before recognize", r);
+        CHECK(last == (r == P.passes() - 1), "decode(%d): last flag", r);
+        nap();
+        if (r == f.decode) throw std::runtime_error("decode fault");
+        dec_at[size_t(r)] = tick();
+    }
+};
+
+// Which pages a fault must fail.
+std::vector<char> expected_failed(const PipelinePlan &P, const Faults &f) {
+    std::vector<char> bad(size_t(P.npages), 0);
+    for (int p = 0; p < P.npages; p++) {
+        const int g = P.group_of[size_t(p)], r = P.pass_of[size_t(p)];
+        bad[size_t(p)] = g == f.stage || g == f.detect || g == f.detect_wait || p == f.layout || r == f.recognize ||
+                         r == f.decode;
+    }
+    return bad;
+}
+
+void run_case(const char *name, int npages, int merge, int det_batch, int workers, Faults f, unsigned seed,
+              bool jitter, bool lookahead = false) {
+    const PipelinePlan P = plan_pipeline(npages, merge, det_batch);
+    Hooks H(P, f, seed, jitter);
+    H.lookahead = lookahead;
+    std::vector<std::string> err;
+    {
+        Pool pool(workers);
+        double busy = -1;
+        err = run_schedule(P, H, [&](std::function<void()> fn) { pool.submit(std::move(fn)); }, &busy, lookahead);
+        CHECK(busy >= 0, "%s: busy time not reported", name);
+    }
+    const std::vector<char> bad = expected_failed(P, f);
+    CHECK(int(err.size()) == npages, "%s: %zu page results", name, err.size());
+    for (int p = 0; p < npages && p < int(err.size()); p++) {
+        CHECK(bad[size_t(p)] == !err[size_t(p)].empty(), "%s: page %d error '%s', expected %s", name, p,
+              err[size_t(p)].c_str(), bad[size_t(p)] ? "a failure" : "success");
+        if (bad[size_t(p)] && !err[size_t(p)].empty())
+            CHECK(err[size_t(p)].find("fault") != std::string::npos, "%s: page %d message '%s'", name, p,
+                  err[size_t(p)].c_str());
+    }
+    // Every pass with a page that reached recognition was recognised and (unless it failed
+    // there) decoded; every page without a failure was laid out.
+    for (int r = 0; r < P.passes(); r++) {
+        bool any_ok = false;
+        for (int p = P.pass_p0[size_t(r)]; p < P.pass_p0[size_t(r) + 1]; p++) {
+            const int g = P.group_of[size_t(p)];
+            any_ok |= !(g == f.stage || g == f.detect || g == f.detect_wait || p == f.layout);
+        }
+        if (any_ok && r != f.recognize) CHECK(H.rec_at[size_t(r)] >= 0, "%s: pass %d not recognised", name, r);
+        if (any_ok && r != f.recognize && r != f.decode) CHECK(H.dec_at[size_t(r)] >= 0, "%s: pass %d not decoded", name, r);
+        if (!any_ok) CHECK(H.rec_at[size_t(r)] < 0, "%s: pass %d recognised without pages", name, r);
+    }
+    for (int p = 0; p < npages; p++)
+        if (!bad[size_t(p)]) CHECK(H.laid_at[size_t(p)] >= 0, "%s: page %d not laid out", name, p);
+}
+
+}  // namespace
+
+int main() {
+    // The plan itself: passes of `merge` pages, groups inside passes, the first group smaller.
+    {
+        const PipelinePlan P = plan_pipeline(12, 6, 6);
+        CHECK(P.passes() == 2 && P.pass_p0[1] == 6, "plan: passes");
+        CHECK(P.groups() == 3 && P.group_p0[0] == 0 && P.group_p0[1] == 2 && P.group_p0[2] == 6, "plan: groups");
+        const PipelinePlan Q = plan_pipeline(7, 3, 2);
+        for (int p = 0; p < 7; p++) {
+            const int g = Q.group_of[size_t(p)];
+            CHECK(Q.pass_of[size_t(Q.group_p0[size_t(g)])] == Q.pass_of[size_t(Q.group_p0[size_t(g) + 1] - 1)],
+                  "plan: group %d straddles a pass", g);
+            CHECK(Q.group_p0[size_t(g) + 1] - Q.group_p0[size_t(g)] <= 2, "plan: group %d larger than det_batch", g);
+        }
+        CHECK(plan_pipeline(0, 2, 4).passes() == 0, "plan: no pages");
+    }
+    const Faults none;
+    run_case("clean", 12, 6, 6, 4, none, 1, true);
+    run_case("one worker", 9, 2, 3, 1, none, 2, true);
+    run_case("many pages few workers", 50, 4, 4, 2, none, 3, true);
+    for (int page : {0, 5, 11}) {
+        Faults f;
+        f.layout = page;
+        run_case("layout fault", 12, 6, 6, 4, f, 10u + unsigned(page), true);
+    }
+    for (int g : {0, 1, 2}) {
+        Faults f;
+        f.stage = g;
+        run_case("stage fault", 12, 6, 6, 3, f, 20u + unsigned(g), true);
+        Faults d;
+        d.detect = g;
+        run_case("detect fault", 12, 6, 6, 3, d, 30u + unsigned(g), true);
+        Faults w;
+        w.detect_wait = g;
+        run_case("detect_wait fault", 12, 6, 6, 3, w, 40u + unsigned(g), true);
+    }
+    for (int r : {0, 1}) {
+        Faults f;
+        f.recognize = r;
+        run_case("recognize fault", 12, 6, 6, 4, f, 50u + unsigned(r), true);
+        Faults d;
+        d.decode = r;
+        run_case("decode fault", 12, 6, 6, 4, d, 60u + unsigned(r), true);
+    }
+    {
+        // Every page of pass 0 fails before recognition: pass 0 is never recognised.
+        Faults f;
+        f.stage = 0;
+        run_case("whole first group", 2, 2, 6, 2, f, 70, false);
+    }
+    for (unsigned seed = 100; seed < 120; seed++) run_case("jitter", 17, 3, 4, 1 + int(seed % 4), none, seed, true);
+    // Lookahead: a pass waits for the next pass's detections to be queued.
+    for (unsigned seed = 200; seed < 210; seed++)
+        run_case("lookahead", 13, 3, 2, 1 + int(seed % 3), none, seed, true, true);
+    {
+        Faults f;
+        f.stage = 3;
+        run_case("lookahead stage fault", 12, 4, 2, 2, f, 220, true, true);
+        Faults g;
+        g.layout = 7;
+        run_case("lookahead layout fault", 12, 4, 2, 2, g, 221, true, true);
+    }
+    if (failures) {
+        std::fprintf(stderr, "%d check(s) failed\n", failures);
+        return 1;
+    }
+    std::printf("pipeline schedule: all checks passed\n");
+    return 0;
+}

@@ -184,3 +184,77 @@ def test_pipeline_rejects_empty_page(detector, recognizer):
     p = ocrhip.Pipeline(detector, recognizer)
     with pytest.raises(ocrhip.OcrError):
         p.run([np.zeros((0, 10, 3), np.uint8)])
+
+
+def test_pipeline_host_pinned_and_device_pages_agree(detector, recognizer, ctx):
+    # The same pages from pageable host memory (pinned staging ring, upload stream overlapped
+    # with detection), from page-locked host memory (uploaded straight from it) and resident in
+    # device memory: identical text. Two page sets alternate, so pooled page buffers written on
+    # the upload stream were last used by the compute stream in the run before.
+    sets = [[synth.page(s) for s in (30, 31, 32, 33)], [synth.page(s) for s in (34, 35, 36)]]
+    p = ocrhip.Pipeline(detector, recognizer, merge=2, det_batch=2)
+    want = []
+    for pages in sets:
+        d = []
+        for pg in pages:
+            b = ctx.alloc(pg.nbytes)
+            b.upload(pg)
+            d.append(b)
+        p.run_device(d, [pg.shape[1] for pg in pages], [pg.shape[0] for pg in pages])
+        want.append([p.texts(k) for k in range(len(pages))])
+    for rep in range(2):
+        for i, pages in enumerate(sets):
+            print(f"host pages, set {i}, repeat {rep}", flush=True)
+            p.run(pages)
+            assert [p.texts(k) for k in range(len(pages))] == want[i]
+            assert all(p.page_error(k) == "" for k in range(len(pages)))
+    pinned = []
+    for pg in sets[0]:
+        a = ctx.host_array(pg.shape)
+        a.array[...] = pg
+        pinned.append(a)
+    print("pinned host pages", flush=True)
+    p.run([a.array for a in pinned])
+    assert [p.texts(k) for k in range(len(sets[0]))] == want[0]
+
+
+def test_pipeline_page_error_other_pages_finish(detector, recognizer, monkeypatch):
+    # A page whose layout fails reports its error; the other pages of its recognition pass and
+    # of the other passes finish with the text of a clean run (ocr-bench.rs:277-281, 303-307).
+    pages = [synth.page(s) for s in (40, 41, 42, 43)]
+    p = ocrhip.Pipeline(detector, recognizer, merge=2, det_batch=2)
+    p.run(pages)
+    clean = [p.texts(k) for k in range(4)]
+    monkeypatch.setenv("OCR_PIPE_FAIL_LAYOUT", "1")
+    print("layout of page 1 fails", flush=True)
+    with pytest.raises(ocrhip.OcrError, match="1 of 4 pages failed"):
+        p.run(pages)
+    assert "injected" in p.page_error(1)
+    assert p.texts(1) == ([], 0)
+    for k in (0, 2, 3):
+        assert p.page_error(k) == ""
+        assert p.texts(k) == clean[k]
+    monkeypatch.delenv("OCR_PIPE_FAIL_LAYOUT")
+    p.run(pages)
+    assert [p.texts(k) for k in range(4)] == clean
+
+
+def test_pool_at_cap_same_results(rec_model_path, recognizer):
+    # A context whose scratch pool keeps at most 1 MB frees almost every buffer it is given back
+    # (hipFree) instead of keeping it: the recognition results are the same bits.
+    lines = synth.rec_lines(12, seed=9, wmin=200, wmax=600)
+    batches, _, _ = synth.batch_lines(lines)
+    want_logits, want_lens, want_best = recognizer.recognize(batches)
+    small = ocrhip.Context(pool_mb=1)
+    try:
+        rec = ocrhip.Recognizer(small, rec_model_path)
+        for rep in range(2):
+            print(f"pool at cap, repeat {rep}", flush=True)
+            logits, lens, best = rec.recognize(batches)
+            np.testing.assert_array_equal(lens, want_lens)
+            for k, T in enumerate(lens):  # rows past a line's length are not defined
+                np.testing.assert_array_equal(best[:T, k], want_best[:T, k])
+                np.testing.assert_array_equal(logits[:T, k], want_logits[:T, k])
+        del rec
+    finally:
+        small.close()

@@ -129,6 +129,25 @@ int ocr_device_free(ocr_ctx *ctx, void *p) {
     });
 }
 
+void *ocr_host_alloc(ocr_ctx *ctx, size_t bytes) {
+    return guard_ptr<void>([&]() -> void * {
+        need(ctx, "ctx");
+        ctx->ctx->bind();
+        void *p = nullptr;
+        OCR_HIP(hipHostMalloc(&p, bytes ? bytes : 16, hipHostMallocDefault));
+        return p;
+    });
+}
+
+int ocr_host_free(ocr_ctx *ctx, void *p) {
+    return guard([&] {
+        need(ctx, "ctx");
+        ctx->ctx->bind();
+        ctx->ctx->sync();
+        OCR_HIP(hipHostFree(p));
+    });
+}
+
 int ocr_memcpy_h2d(ocr_ctx *ctx, void *dst, const void *src, size_t bytes) {
     return guard([&] {
         need(ctx, "ctx");
@@ -501,20 +520,30 @@ int ocr_pipeline_run(ocr_pipeline *pipe, const uint8_t *const *rgb, const uint32
                      uint32_t npages) {
     return guard([&] {
         need(pipe, "pipeline");
-        Ctx &c = *pipe->owner->ctx;
-        c.bind();
-        std::vector<DBuf> bufs;
-        std::vector<const uint8_t *> ptrs;
-        std::vector<int> wi(npages), hi(npages);
-        for (uint32_t k = 0; k < npages; k++) {
-            need(rgb[k], "page");
-            const size_t bytes = size_t(w[k]) * h[k] * 3;
-            bufs.emplace_back(&c, bytes);
-            c.h2d(bufs.back().get(), rgb[k], bytes);
-            ptrs.push_back(bufs.back().as<uint8_t>());
-            wi[k] = int(w[k]), hi[k] = int(h[k]);
+        if (npages) {
+            need(rgb, "rgb");
+            need(w, "w");
+            need(h, "h");
         }
-        pipe->pipe->run(ptrs.data(), wi.data(), hi.data(), int(npages));
+        pipe->owner->ctx->bind();
+        std::vector<int> wi(npages), hi(npages);
+        for (uint32_t k = 0; k < npages; k++) wi[k] = int(w[k]), hi[k] = int(h[k]);
+        pipe->pipe->run_host(rgb, wi.data(), hi.data(), int(npages));
+    });
+}
+
+int ocr_pipeline_page_error(ocr_pipeline *pipe, uint32_t page, char *buf, uint32_t cap, uint32_t *len) {
+    return guard([&] {
+        need(pipe, "pipeline");
+        const auto &pages = pipe->pipe->pages();
+        if (page >= pages.size()) fail("page index out of range");
+        const std::string &s = pages[page].error;
+        if (len) *len = uint32_t(s.size());
+        if (buf && cap) {
+            const size_t n = std::min<size_t>(s.size(), cap - 1);
+            std::copy(s.begin(), s.begin() + long(n), buf);
+            buf[n] = 0;
+        }
     });
 }
 

@@ -9,10 +9,12 @@
 #include <mutex>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <thread>
 
 #include "crop.h"
 #include "host_util.h"
+#include "pipeline_core.h"
 
 namespace ocr {
 
@@ -63,6 +65,27 @@ PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float rel
 }
 
 
+namespace {
+
+// Pinned staging of pages handed over in pageable host memory: SLOTS buffers of SLOT_BYTES,
+// each reused once the copy out of it has finished.
+constexpr int SLOTS = 6;
+constexpr size_t SLOT_BYTES = size_t(8) << 20;
+// Pieces a slot's host copy is cut into for the loop pool.
+constexpr int COPY_PIECES = 8;
+
+// True when p is page-locked host memory (hipHostMalloc), which a copy engine reads directly.
+bool host_pinned(const void *p) {
+    hipPointerAttribute_t a{};
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();  // pageable memory is not known to HIP: not an error
+        return false;
+    }
+    return a.type == hipMemoryTypeHost;
+}
+
+}  // namespace
+
 struct Pipeline::Impl {
     Ctx &ctx;
     Detector &det;
@@ -71,8 +94,14 @@ struct Pipeline::Impl {
     Workers workers;
     std::vector<Pinned> bits_host, best_host, runs_host;
     // The masks and labelled runs go to the host on a stream of their own, so the next
-    // detection pass does not wait for the copies.
-    hipStream_t copy = nullptr;
+    // detection group does not wait for the copies; pages handed over in host memory go to the
+    // device on another. Detection and recognition share the context's stream: their kernels
+    // take every CU (persistent workgroups), so running them side by side only slows both.
+    hipStream_t copy = nullptr, up = nullptr;
+    Pinned slot[SLOTS];
+    hipEvent_t slot_ev[SLOTS] = {};
+    bool slot_used[SLOTS] = {};
+    int next_slot = 0;
     // Host threads the layouts of one recognition pass share (a page's word boxes in row bands,
     // its lines side by side).
     int host_threads;
@@ -81,11 +110,41 @@ struct Pipeline::Impl {
           host_threads(std::max(1, int(std::thread::hardware_concurrency()))) {
         ctx.bind();
         OCR_HIP(hipStreamCreateWithFlags(&copy, hipStreamNonBlocking));
+        OCR_HIP(hipStreamCreateWithFlags(&up, hipStreamNonBlocking));
+        for (hipEvent_t &e : slot_ev) OCR_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     ~Impl() {
-        if (copy) {
-            (void)hipStreamSynchronize(copy);
-            (void)hipStreamDestroy(copy);
+        for (hipStream_t s : {copy, up})
+            if (s) {
+                (void)hipStreamSynchronize(s);
+                ctx.pool().retire_stream(s);
+                (void)hipStreamDestroy(s);
+            }
+        for (hipEvent_t e : slot_ev)
+            if (e) (void)hipEventDestroy(e);
+    }
+    // Copies bytes of host memory to the device on the upload stream: straight from pinned
+    // memory, else through the staging slots (the host copy cut into pieces on the loop pool).
+    void upload(uint8_t *dst, const uint8_t *src, size_t bytes, bool pinned) {
+        if (pinned) {
+            OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, up));
+            return;
+        }
+        for (size_t off = 0; off < bytes; off += SLOT_BYTES) {
+            const size_t n = std::min(SLOT_BYTES, bytes - off);
+            const int k = next_slot;
+            next_slot = (next_slot + 1) % SLOTS;
+            slot[k].ensure(SLOT_BYTES);
+            if (slot_used[k]) OCR_HIP(hipEventSynchronize(slot_ev[k]));
+            uint8_t *stage = static_cast<uint8_t *>(slot[k].p);
+            const uint8_t *from = src + off;
+            LoopPool::get().run(COPY_PIECES, [&](int i) {
+                const size_t a = n * size_t(i) / COPY_PIECES, b = n * size_t(i + 1) / COPY_PIECES;
+                std::memcpy(stage + a, from + a, b - a);
+            }, -2);
+            OCR_HIP(hipMemcpyAsync(dst + off, stage, n, hipMemcpyHostToDevice, up));
+            OCR_HIP(hipEventRecord(slot_ev[k], up));
+            slot_used[k] = true;
         }
     }
 };
@@ -97,73 +156,65 @@ Pipeline::Pipeline(Ctx &ctx, Detector &det, Recognizer &rec, const PipelineOpts 
 
 Pipeline::~Pipeline() { delete impl_; }
 
-void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages) {
-    Impl &I = *impl_;
-    Ctx &ctx = I.ctx;
-    const hipStream_t st = ctx.stream();
-    const auto t0 = Clock::now();
-    pages_.assign(size_t(std::max(npages, 0)), PageText{});
-    stats_ = PipelineStats{};
-    stats_.pages = npages;
-    if (npages <= 0) return;
-    for (int p = 0; p < npages; p++)
-        if (w[p] <= 0 || h[p] <= 0) fail("pipeline: empty page " + std::to_string(p));
+namespace {
 
-    std::mutex mu;
-    std::condition_variable cv;
-    // OCR_PIPE_TRACE=1: host timestamps of the pipeline's steps, printed to stderr at the end.
-    static const bool tracing = std::getenv("OCR_PIPE_TRACE") != nullptr;
-    std::vector<std::pair<double, std::string>> trace;
-    auto mark = [&](const std::string &what) {
-        if (!tracing) return;
-        std::lock_guard<std::mutex> lk(mu);
-        trace.push_back({ms_since(t0), what});
-    };
-    std::vector<int> layout_ready(size_t(npages), 0);
-    std::vector<PageLayout> layouts(static_cast<size_t>(npages));
-    std::string error;
-    double cpu_busy = 0;
-    int pending_tasks = 0;
-    auto task_done = [&](double busy, const std::string &err) {
-        std::lock_guard<std::mutex> lk(mu);
-        cpu_busy += busy;
-        if (!err.empty() && error.empty()) error = err;
-        pending_tasks--;
-        cv.notify_all();
-    };
+// Each page's labelled components (ccl_runs) in one device block, whose head goes to the host:
+// the totals (runs, components, row slots), the component records (16 bytes each), each row
+// slot's leftmost then rightmost pixel (4 bytes each). The runs themselves (row offsets, roots,
+// first and last pixels, rows, root bottoms) follow on the device only.
+struct LabelCaps {
+    int runs, comps, slots;
+    size_t head() const { return 16 + size_t(comps) * 16 + size_t(slots) * 8; }
+};
 
-    // Recognition passes of `merge` pages, in page order.
-    std::vector<int> pass_p0;
-    for (int p = 0; p < npages; p += I.opts.merge) pass_p0.push_back(p);
-    pass_p0.push_back(npages);
-    const int nrec = int(pass_p0.size()) - 1;
-    // 1. Detection of every page in groups of at most det_batch pages (near-equal sizes) that
-    // never straddle a recognition pass: the first pass's layouts then start while the later
-    // pages are still being detected. The first group is a third of det_batch (at least one
-    // page), so the host starts on layouts early. The bit masks come back asynchronously.
-    std::vector<int> group_of(static_cast<size_t>(npages)), group_p0;
-    for (int r = 0; r < nrec; r++) {
-        int q0 = pass_p0[size_t(r)];
-        const int r1 = pass_p0[size_t(r) + 1];
-        if (r == 0 && r1 - q0 > 1) {
-            const int first = std::min(r1 - q0, std::max(1, I.opts.det_batch / 3));
-            group_p0.push_back(q0);
-            for (int p = q0; p < q0 + first; p++) group_of[size_t(p)] = int(group_p0.size()) - 1;
-            q0 += first;
-        }
-        const int ng = (r1 - q0 + I.opts.det_batch - 1) / I.opts.det_batch;
-        for (int k = 0; k < ng; k++) {
-            const int g0 = q0 + int(long(r1 - q0) * k / ng), g1 = q0 + int(long(r1 - q0) * (k + 1) / ng);
-            group_p0.push_back(g0);
-            for (int p = g0; p < g1; p++) group_of[size_t(p)] = int(group_p0.size()) - 1;
-        }
+}  // namespace
+
+// One run of the pipeline: the hooks of the schedule (pipeline_core.h) on this GPU.
+struct PipelineRun final : PipelineHooks {
+    Pipeline::Impl &I;
+    Ctx &ctx;
+    hipStream_t st;
+    const PipelinePlan &P;
+    const uint8_t *const *src;  // the pages: device pointers, or host pointers when on_host
+    bool on_host;
+    const int *w, *h;
+    std::vector<PageText> &pages;
+    LabelCaps caps;
+    const Clock::time_point t0;
+    // OCR_PIPE_TRACE=1: host timestamps of the steps, printed to stderr at the end.
+    bool tracing;
+    // OCR_PIPE_FAIL_LAYOUT=p: page p's layout fails (tests of the per-page error path).
+    int fail_layout = -1;
+    // With tracing: GPU timestamps (events on the streams) of each upload group, detection group
+    // and recognition pass, against one taken at the start on the compute stream.
+    hipEvent_t gpu_t0 = nullptr;
+    std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> gpu_marks;
+    hipEvent_t gpu_event(hipStream_t s) {
+        hipEvent_t e = nullptr;
+        if (!tracing) return e;
+        OCR_HIP(hipEventCreate(&e));
+        OCR_HIP(hipEventRecord(e, s));
+        return e;
     }
-    const int ngroups = int(group_p0.size());
-    std::vector<hipEvent_t> det_ev(size_t(ngroups), nullptr), ccl_ev(size_t(ngroups), nullptr);
-    // Each detection pass's masks and runs on the device, kept until the run ends: the copy
-    // stream reads them while the next passes run.
-    std::vector<std::vector<DBuf>> keep_bits(static_cast<size_t>(ngroups)), keep_runs(static_cast<size_t>(ngroups));
-    std::vector<hipEvent_t> rec_ev(size_t(nrec), nullptr), am_ev(size_t(nrec), nullptr);
+    void gpu_span(const std::string &what, hipEvent_t a, hipEvent_t b) {
+        if (!tracing) return;
+        std::lock_guard<std::mutex> lk(trace_mu);
+        gpu_marks.push_back({what, {a, b}});
+    }
+    std::mutex trace_mu;
+    std::vector<std::pair<double, std::string>> trace;
+
+    // Device pages (host mode: uploaded here), each group's upload event.
+    std::vector<DBuf> dpages;
+    std::vector<const uint8_t *> d_rgb;
+    std::vector<char> pinned;
+    std::vector<hipEvent_t> up_ev, det_ev;
+    // Each detection group's masks and runs on the device, kept until the run ends: the copy
+    // stream reads them while the next groups run.
+    std::vector<std::vector<DBuf>> keep_bits, keep_runs;
+    std::vector<size_t> words_of;
+    std::vector<int> runs_cap;
+    std::vector<PageLayout> layouts;
     struct RecPass {
         std::vector<std::pair<int, int>> rows;  // (page, line in page) of every recogniser line
         std::vector<uint32_t> lens;
@@ -172,54 +223,138 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         std::vector<CropLine> crops;
         std::vector<int32_t> row_off, spans;
         DBuf best;  // the arg-max classes, read by the copy to the host after the pass's kernels
+        std::vector<DBuf> batch_bufs;
+        hipEvent_t done = nullptr;
     };
-    std::vector<RecPass> passes(static_cast<size_t>(nrec));
-    // Detection groups completed so far (set by the watcher thread below).
-    int det_done = 0;
-    struct Joiner {
-        std::thread t;
-        ~Joiner() {
-            if (t.joinable()) t.join();
+    std::vector<RecPass> passes;
+    int batches = 0, rec_passes = 0;
+
+    PipelineRun(Pipeline::Impl &impl, const PipelinePlan &plan, const uint8_t *const *pages_src, bool host,
+                const int *pw, const int *ph, std::vector<PageText> &out)
+        : I(impl), ctx(impl.ctx), st(impl.ctx.stream()), P(plan), src(pages_src), on_host(host), w(pw), h(ph),
+          pages(out), t0(Clock::now()) {
+        tracing = std::getenv("OCR_PIPE_TRACE") != nullptr;
+        if (const char *f = std::getenv("OCR_PIPE_FAIL_LAYOUT")) fail_layout = std::atoi(f);
+        if (tracing) {
+            OCR_HIP(hipEventCreate(&gpu_t0));
+            OCR_HIP(hipEventRecord(gpu_t0, st));
+            OCR_HIP(hipStreamWaitEvent(I.up, gpu_t0, 0));
         }
-    } watcher;
-    // Worker tasks refer to the locals above: whatever happens, wait for them before returning.
-    try {
-    if (I.bits_host.size() < size_t(npages)) I.bits_host.resize(size_t(npages));
-    if (I.runs_host.size() < size_t(npages)) I.runs_host.resize(size_t(npages));
-    // Each page's labelled components (ccl_runs) in one device block, whose head goes to the
-    // host: the totals (runs, components, row slots), the component records (RCOMPS of 16
-    // bytes), each row slot's leftmost then rightmost pixel (RSLOTS of 4 bytes each). The runs
-    // themselves (row offsets, roots, first and last pixels, rows, root bottoms; runs_cap each)
-    // follow on the device only.
-    constexpr int RCOMPS = 16384, RSLOTS = 65536;
-    constexpr size_t HEAD = 16 + size_t(RCOMPS) * 16 + size_t(RSLOTS) * 8;
-    std::vector<size_t> words_of(static_cast<size_t>(npages));
-    std::vector<int> runs_cap(static_cast<size_t>(npages));
-    auto roff_bytes = [&](int p) { return (size_t(h[p] + 1) * 4 + 15) & ~size_t(15); };
-    auto block_bytes = [&](int p) { return HEAD + roff_bytes(p) + size_t(runs_cap[size_t(p)]) * 14; };
-    for (int p = 0; p < npages; p++) {
-        words_of[size_t(p)] = size_t((w[p] + 31) / 32) * h[p];
-        I.bits_host[size_t(p)].ensure(words_of[size_t(p)] * 4);
-        runs_cap[size_t(p)] = int(std::min<size_t>(words_of[size_t(p)] * 16, size_t(1) << 17));
-        I.runs_host[size_t(p)].ensure(HEAD);
+        const int np = P.npages, ng = P.groups();
+        caps.runs = I.opts.label_runs > 0 ? I.opts.label_runs : 1 << 17;
+        caps.comps = I.opts.label_comps > 0 ? I.opts.label_comps : 16384;
+        caps.slots = I.opts.label_slots > 0 ? I.opts.label_slots : 65536;
+        up_ev.assign(size_t(ng), nullptr);
+        det_ev.assign(size_t(ng), nullptr);
+        keep_bits.resize(size_t(ng));
+        keep_runs.resize(size_t(ng));
+        layouts.resize(size_t(np));
+        passes.resize(size_t(P.passes()));
+        if (I.bits_host.size() < size_t(np)) I.bits_host.resize(size_t(np));
+        if (I.runs_host.size() < size_t(np)) I.runs_host.resize(size_t(np));
+        if (I.best_host.size() < size_t(P.passes())) I.best_host.resize(size_t(P.passes()));
+        words_of.resize(size_t(np));
+        runs_cap.resize(size_t(np));
+        for (int p = 0; p < np; p++) {
+            words_of[size_t(p)] = size_t((w[p] + 31) / 32) * h[p];
+            I.bits_host[size_t(p)].ensure(words_of[size_t(p)] * 4);
+            runs_cap[size_t(p)] = int(std::min<size_t>(words_of[size_t(p)] * 16, size_t(caps.runs)));
+            I.runs_host[size_t(p)].ensure(caps.head());
+        }
+        // Host pages: every page's device buffer now, before this run queues any work, so the
+        // uploads never wait for this run's kernels.
+        d_rgb.resize(size_t(np));
+        if (on_host) {
+            pinned.resize(size_t(np));
+            for (int p = 0; p < np; p++) {
+                dpages.emplace_back(&ctx, size_t(w[p]) * h[p] * 3, I.up);
+                dpages.back().used_on(st);
+                d_rgb[size_t(p)] = dpages.back().as<uint8_t>();
+                pinned[size_t(p)] = host_pinned(src[p]);
+            }
+        } else {
+            for (int p = 0; p < np; p++) d_rgb[size_t(p)] = src[p];
+        }
     }
-    for (int g = 0; g < ngroups; g++) {
-        const int p0 = group_p0[size_t(g)], p1 = g + 1 < ngroups ? group_p0[size_t(g) + 1] : npages;
+    ~PipelineRun() override {
+        // Nothing may still use the run's buffers once they go back to the pool.
+        (void)hipStreamSynchronize(I.up);
+        (void)hipStreamSynchronize(I.copy);
+        (void)hipStreamSynchronize(st);
+        for (hipEvent_t e : up_ev)
+            if (e) (void)hipEventDestroy(e);
+        for (hipEvent_t e : det_ev)
+            if (e) (void)hipEventDestroy(e);
+        for (RecPass &R : passes)
+            if (R.done) (void)hipEventDestroy(R.done);
+        if (gpu_t0) (void)hipEventDestroy(gpu_t0);
+    }
+    void mark(const std::string &what) {
+        if (!tracing) return;
+        std::lock_guard<std::mutex> lk(trace_mu);
+        trace.push_back({ms_since(t0), what});
+    }
+    void print_trace() {
+        if (!tracing) return;
+        (void)hipDeviceSynchronize();
+        for (auto &m : gpu_marks) {
+            float a = 0, b = 0;
+            (void)hipEventElapsedTime(&a, gpu_t0, m.second.first);
+            (void)hipEventElapsedTime(&b, gpu_t0, m.second.second);
+            char buf[160];
+            std::snprintf(buf, sizeof buf, "GPU %s: %.3f .. %.3f ms", m.first.c_str(), a, b);
+            trace.push_back({double(a), buf});
+            (void)hipEventDestroy(m.second.first);
+            (void)hipEventDestroy(m.second.second);
+        }
+        gpu_marks.clear();
+        mark("end");
+        std::sort(trace.begin(), trace.end());
+        for (const auto &e : trace) std::fprintf(stderr, "[pipe] %8.3f ms  %s\n", e.first, e.second.c_str());
+    }
+    size_t roff_bytes(int p) const { return (size_t(h[p] + 1) * 4 + 15) & ~size_t(15); }
+    size_t block_bytes(int p) const { return caps.head() + roff_bytes(p) + size_t(runs_cap[size_t(p)]) * 14; }
+
+    void stage(int g) override {
+        const int p0 = P.group_p0[size_t(g)], p1 = P.group_p0[size_t(g) + 1];
+        if (!on_host) return;
+        ctx.bind();
+        mark("stage " + std::to_string(g) + " start");
+        hipEvent_t ga = gpu_event(I.up);
+        for (int p = p0; p < p1; p++)
+            I.upload(dpages[size_t(p)].as<uint8_t>(), src[p], size_t(w[p]) * h[p] * 3, pinned[size_t(p)] != 0);
+        gpu_span("upload " + std::to_string(g), ga, gpu_event(I.up));
+        OCR_HIP(hipEventCreateWithFlags(&up_ev[size_t(g)], hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(up_ev[size_t(g)], I.up));
+        mark("stage " + std::to_string(g) + " queued");
+    }
+
+    // Detection of a group's pages, the labelling of their masks, and the copies of masks and
+    // labels to the host (on the copy stream).
+    void detect(int g) override {
+        const int p0 = P.group_p0[size_t(g)], p1 = P.group_p0[size_t(g) + 1];
+        const hipStream_t ds = st;
+        if (up_ev[size_t(g)]) OCR_HIP(hipStreamWaitEvent(ds, up_ev[size_t(g)], 0));
+        hipEvent_t ga = gpu_event(ds);
         std::vector<DBuf> &bits = keep_bits[size_t(g)];
         std::vector<uint32_t *> bp;
         for (int p = p0; p < p1; p++) {
             bits.emplace_back(&ctx, words_of[size_t(p)] * 4);
+            bits.back().used_on(I.copy);
             bp.push_back(bits.back().as<uint32_t>());
         }
-        I.det.detect_pages_device(d_rgb + p0, w + p0, h + p0, p1 - p0, I.opts.thr, bp.data());
+        mark("det group " + std::to_string(g) + " model");
+        I.det.detect_pages_device(d_rgb.data() + p0, w + p0, h + p0, p1 - p0, I.opts.thr, bp.data());
+        mark("det group " + std::to_string(g) + " labels");
         std::vector<DBuf> &rbuf = keep_runs[size_t(g)];
         std::vector<CclPage> cp;
         for (int p = p0; p < p1; p++) {
             rbuf.emplace_back(&ctx, block_bytes(p));
+            rbuf.back().used_on(I.copy);
             char *b = rbuf.back().as<char>();
             const size_t cap = size_t(runs_cap[size_t(p)]);
-            char *comps = b + 16, *xmin = comps + size_t(RCOMPS) * 16, *xmax = xmin + size_t(RSLOTS) * 4;
-            char *roff = b + HEAD, *root = roff + roff_bytes(p), *cbot = root + cap * 4;
+            char *comps = b + 16, *xmin = comps + size_t(caps.comps) * 16, *xmax = xmin + size_t(caps.slots) * 4;
+            char *roff = b + caps.head(), *root = roff + roff_bytes(p), *cbot = root + cap * 4;
             char *x0 = cbot + cap * 4, *x1 = x0 + cap * 2, *ry = x1 + cap * 2;
             CclPage pg{};
             pg.bits = bp[size_t(p - p0)], pg.w = w[p], pg.h = h[p];
@@ -229,115 +364,61 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             pg.ry = reinterpret_cast<uint16_t *>(ry), pg.cbot = reinterpret_cast<int32_t *>(cbot);
             pg.comps = reinterpret_cast<int32_t *>(comps);
             pg.xmin = reinterpret_cast<uint32_t *>(xmin), pg.xmax = reinterpret_cast<uint32_t *>(xmax);
-            pg.ccap = RCOMPS, pg.scap = RSLOTS;
+            pg.ccap = caps.comps, pg.scap = caps.slots;
             cp.push_back(pg);
         }
-        ccl_runs(cp.data(), int(cp.size()), st);
-        OCR_HIP(hipEventCreateWithFlags(&ccl_ev[size_t(g)], hipEventDisableTiming));
-        OCR_HIP(hipEventRecord(ccl_ev[size_t(g)], st));
-        OCR_HIP(hipStreamWaitEvent(I.copy, ccl_ev[size_t(g)], 0));
+        ccl_runs(cp.data(), int(cp.size()), ds);
+        gpu_span("detect " + std::to_string(g), ga, gpu_event(ds));
+        hipEvent_t ready = nullptr;
+        OCR_HIP(hipEventCreateWithFlags(&ready, hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(ready, ds));
+        OCR_HIP(hipStreamWaitEvent(I.copy, ready, 0));
+        OCR_HIP(hipEventDestroy(ready));  // the wait above holds what it needs
         for (int p = p0; p < p1; p++) {
             OCR_HIP(hipMemcpyAsync(I.bits_host[size_t(p)].p, bp[size_t(p - p0)], words_of[size_t(p)] * 4,
                                    hipMemcpyDeviceToHost, I.copy));
-            OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), HEAD,
+            OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), caps.head(),
                                    hipMemcpyDeviceToHost, I.copy));
         }
         OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming | hipEventBlockingSync));
         OCR_HIP(hipEventRecord(det_ev[size_t(g)], I.copy));
-        mark("det group " + std::to_string(g) + " enqueued");
+        mark("det group " + std::to_string(g) + " queued");
     }
-    // One thread waits for the detection groups in order and wakes the layouts; the layout
-    // tasks sleep meanwhile, so the host cores go to the layouts that can run.
-    const int dev = ctx.device();
-    watcher.t = std::thread([&, dev] {
-        std::string err;
-        try {
-            (void)hipSetDevice(dev);
-            for (int g = 0; g < ngroups; g++) {
-                OCR_HIP(hipEventSynchronize(det_ev[size_t(g)]));
-                std::lock_guard<std::mutex> lk(mu);
-                det_done = g + 1;
-                cv.notify_all();
-            }
-        } catch (const std::exception &e) {
-            err = e.what();
-        }
-        std::lock_guard<std::mutex> lk(mu);
-        if (!err.empty() && error.empty()) error = err;
-        det_done = ngroups;
-        cv.notify_all();
-    });
-    // 2. Host layout of each page once its mask is on the host and every page of the earlier
-    // recognition passes is laid out; its loops run on the shared host loop pool, earlier pages
-    // first.
-    for (int p = 0; p < npages; p++) {
-        {
-            std::lock_guard<std::mutex> lk(mu);
-            pending_tasks++;
-        }
-        const int grp = group_of[size_t(p)];
+
+    void detect_wait(int g) override {
+        ctx.bind();
+        OCR_HIP(hipEventSynchronize(det_ev[size_t(g)]));
+        mark("det group " + std::to_string(g) + " done");
+    }
+
+    // Words, lines and line geometry of page p on the host, from its mask's labelled components
+    // (the GPU's, unless the page had more runs, components or row slots than the buffers hold:
+    // then from the bits).
+    void layout(int p) override {
+        ctx.bind();
+        mark("layout " + std::to_string(p) + " start");
         const uint32_t *bits = static_cast<const uint32_t *>(I.bits_host[size_t(p)].p);
         const char *rblk = static_cast<const char *>(I.runs_host[size_t(p)].p);
-        const int rcap = runs_cap[size_t(p)];
-        const int pw = w[p], ph = h[p];
-        int pr = 0;
-        while (pass_p0[size_t(pr) + 1] <= p) pr++;
-        const int before = pass_p0[size_t(pr)], threads = I.host_threads;
-        I.workers.submit([&, p, grp, bits, rblk, rcap, pw, ph, dev, before, threads] {
-            std::string err;
-            double busy = 0;
-            try {
-                (void)hipSetDevice(dev);
-                {
-                    std::unique_lock<std::mutex> lk(mu);
-                    cv.wait(lk, [&] {
-                        if (!error.empty()) return true;
-                        if (det_done <= grp) return false;
-                        for (int q = 0; q < before; q++)
-                            if (!layout_ready[size_t(q)]) return false;
-                        return true;
-                    });
-                    if (!error.empty()) fail("an earlier step failed");
-                }
-                mark("layout " + std::to_string(p) + " start");
-                const auto tc = Clock::now();
-                // The GPU's labelled components unless the page had more runs, components or
-                // row slots than the buffers hold.
-                const int32_t *tot = reinterpret_cast<const int32_t *>(rblk);
-                const char *comps = rblk + 16, *xmin = comps + size_t(RCOMPS) * 16;
-                const MaskRows mr{reinterpret_cast<const int32_t *>(comps), tot[1],
-                                  reinterpret_cast<const uint32_t *>(xmin),
-                                  reinterpret_cast<const uint32_t *>(xmin + size_t(RSLOTS) * 4), tot[2]};
-                const bool fits = tot[0] <= rcap && tot[1] <= RCOMPS && tot[2] <= RSLOTS;
-                PageLayout L = layout_page(bits, pw, ph, I.opts.relv, I.opts.relend, threads, p, fits ? &mr : nullptr);
-                busy = ms_since(tc);
-                mark("layout " + std::to_string(p) + " done");
-                std::lock_guard<std::mutex> lk(mu);
-                layouts[size_t(p)] = std::move(L);
-                layout_ready[size_t(p)] = 1;
-            } catch (const std::exception &e) {
-                err = e.what();
-                std::lock_guard<std::mutex> lk(mu);
-                layout_ready[size_t(p)] = -1;
-            }
-            task_done(busy, err);
-        });
+        const int32_t *tot = reinterpret_cast<const int32_t *>(rblk);
+        const char *comps = rblk + 16, *xmin = comps + size_t(caps.comps) * 16;
+        const MaskRows mr{reinterpret_cast<const int32_t *>(comps), tot[1], reinterpret_cast<const uint32_t *>(xmin),
+                          reinterpret_cast<const uint32_t *>(xmin + size_t(caps.slots) * 4), tot[2]};
+        const bool fits = tot[0] <= runs_cap[size_t(p)] && tot[1] <= caps.comps && tot[2] <= caps.slots;
+        layouts[size_t(p)] = layout_page(bits, w[p], h[p], I.opts.relv, I.opts.relend, I.host_threads, p,
+                                         fits ? &mr : nullptr);
+        if (p == fail_layout) fail("layout of page " + std::to_string(p) + " failed (injected)");
+        mark("layout " + std::to_string(p) + " done");
     }
-    // 3. Recognition, pass by pass in page order.
-    if (I.best_host.size() < size_t(nrec)) I.best_host.resize(size_t(nrec));
-    for (int r = 0; r < nrec; r++) {
-        const int p0 = pass_p0[size_t(r)], p1 = pass_p0[size_t(r) + 1];
-        {
-            std::unique_lock<std::mutex> lk(mu);
-            cv.wait(lk, [&] {
-                for (int p = p0; p < p1; p++)
-                    if (!layout_ready[size_t(p)]) return false;
-                return true;
-            });
-            if (!error.empty()) break;
-        }
-        mark("rec " + std::to_string(r) + " layouts ready");
+
+    // Line images and recognition of pass r's laid-out pages, and the arg-max copy to the host.
+    void recognize(int r, const std::vector<char> &ok) override {
+        const int p0 = P.pass_p0[size_t(r)], p1 = P.pass_p0[size_t(r) + 1];
         RecPass &R = passes[size_t(r)];
+        mark("rec " + std::to_string(r) + " layouts ready");
+        // The line crops read the pages: after their uploads (long done: their masks were on the
+        // host before the layouts ran, but the streams say so too).
+        for (int g = P.group_of[size_t(p0)]; g <= P.group_of[size_t(p1 - 1)]; g++)
+            if (up_ev[size_t(g)]) OCR_HIP(hipStreamWaitEvent(st, up_ev[size_t(g)], 0));
         // A line's recognition depends on its batch's width (the padding), not on which lines
         // share the batch, so every page's batches of one width run as one trunk batch: the
         // same results with fewer, fuller launches. Widths ascending, pages and batches in order.
@@ -345,6 +426,7 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
         // The pages' row offsets and spans, appended page by page (offsets rebased).
         std::vector<int> page_row0(size_t(p1 - p0));
         for (int p = p0; p < p1; p++) {
+            if (!ok[size_t(p - p0)]) continue;
             const PageLayout &L = layouts[size_t(p)];
             page_row0[size_t(p - p0)] = int(R.row_off.size());
             const int32_t sbase = int32_t(R.spans.size());
@@ -354,121 +436,136 @@ void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int 
             R.spans.insert(R.spans.end(), L.spans.begin(), L.spans.end());
         }
         for (int p = p0; p < p1; p++) {
+            if (!ok[size_t(p - p0)]) continue;
             const PageLayout &L = layouts[size_t(p)];
-            pages_[size_t(p)].words = L.words;
-            pages_[size_t(p)].lines.assign(L.lines.size(), std::string());
+            pages[size_t(p)].words = L.words;
+            pages[size_t(p)].lines.assign(L.lines.size(), std::string());
             for (size_t b = 0; b < L.plan.lines.size(); b++) {
-                stats_.batches++;
+                batches++;
                 for (int li : L.plan.lines[b]) by_width[L.plan.width[b]].push_back({p, li});
             }
         }
-        std::vector<Recognizer::Batch> batches;
-        std::vector<DBuf> batch_bufs;
+        std::vector<Recognizer::Batch> rb;
         for (const auto &kv : by_width) {
             const int wb = kv.first, n = int(kv.second.size());
-            batch_bufs.emplace_back(&ctx, size_t(n) * LINE_H * wb * sizeof(float));
-            float *base = batch_bufs.back().as<float>();
-            batches.push_back({base, n, wb});
+            R.batch_bufs.emplace_back(&ctx, size_t(n) * LINE_H * wb * sizeof(float));
+            float *base = R.batch_bufs.back().as<float>();
+            rb.push_back({base, n, wb});
             for (int k = 0; k < n; k++) {
                 const int p = kv.second[size_t(k)].first, li = kv.second[size_t(k)].second;
                 const PageLayout &L = layouts[size_t(p)];
                 const LineGeom &g = L.lines[size_t(li)];
-                CropLine c{d_rgb[p], w[p], h[p], g.left, g.top, g.bw, g.bh, g.out_w,
+                CropLine c{d_rgb[size_t(p)], w[p], h[p], g.left, g.top, g.bw, g.bh, g.out_w,
                            page_row0[size_t(p - p0)] + L.line_row0[size_t(li)], base + size_t(k) * LINE_H * wb, wb};
                 R.crops.push_back(c);
                 R.rows.push_back({p, li});
                 R.widths.push_back(g.out_w);
             }
         }
-        if (batches.empty()) continue;
+        if (rb.empty()) return;
         mark("rec " + std::to_string(r) + " crops built");
+        hipEvent_t ga = gpu_event(st);
         line_crop(ctx, R.crops, R.row_off, R.spans, st);
-        const Recognizer::Dims d = I.rec.dims(batches.data(), int(batches.size()));
+        const Recognizer::Dims d = I.rec.dims(rb.data(), int(rb.size()));
         R.tmax = d.tmax;
         R.ntot = d.ntot;
         R.lens.assign(size_t(d.ntot), 0);
         DBuf logits(&ctx, size_t(d.tmax) * d.ntot * d.classes * sizeof(float));
         R.best = DBuf(&ctx, size_t(d.tmax) * d.ntot * sizeof(uint32_t));
-        I.rec.recognize_device(batches.data(), int(batches.size()), logits.as<float>(), R.best.as<uint32_t>(),
-                               R.lens.data());
-        mark("rec " + std::to_string(r) + " enqueued");
+        R.best.used_on(I.copy);
+        I.rec.recognize_device(rb.data(), int(rb.size()), logits.as<float>(), R.best.as<uint32_t>(), R.lens.data());
+        gpu_span("recognize " + std::to_string(r), ga, gpu_event(st));
+        mark("rec " + std::to_string(r) + " queued");
         // The arg-max goes to the host on the copy stream, so the next pass's kernels do not
         // wait for the copy.
         I.best_host[size_t(r)].ensure(size_t(d.tmax) * d.ntot * sizeof(uint32_t));
-        OCR_HIP(hipEventCreateWithFlags(&am_ev[size_t(r)], hipEventDisableTiming));
-        OCR_HIP(hipEventRecord(am_ev[size_t(r)], st));
-        OCR_HIP(hipStreamWaitEvent(I.copy, am_ev[size_t(r)], 0));
+        hipEvent_t am = nullptr;
+        OCR_HIP(hipEventCreateWithFlags(&am, hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(am, st));
+        OCR_HIP(hipStreamWaitEvent(I.copy, am, 0));
+        OCR_HIP(hipEventDestroy(am));
         OCR_HIP(hipMemcpyAsync(I.best_host[size_t(r)].p, R.best.get(), size_t(d.tmax) * d.ntot * sizeof(uint32_t),
                                hipMemcpyDeviceToHost, I.copy));
-        OCR_HIP(hipEventCreateWithFlags(&rec_ev[size_t(r)], hipEventDisableTiming));
-        OCR_HIP(hipEventRecord(rec_ev[size_t(r)], I.copy));
-        stats_.rec_passes++;
-        // 4. Greedy CTC on the host once the arg-max is back.
-        {
-            std::lock_guard<std::mutex> lk(mu);
-            pending_tasks++;
-        }
-        hipEvent_t ev = rec_ev[size_t(r)];
+        OCR_HIP(hipEventCreateWithFlags(&R.done, hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(R.done, I.copy));
+        rec_passes++;
+    }
+
+    // Greedy CTC of pass r on the host once its arg-max is there.
+    void decode(int r, bool last) override {
+        ctx.bind();
+        const RecPass &R = passes[size_t(r)];
+        if (!R.done) return;
+        wait_event(R.done, last);
+        mark("ctc " + std::to_string(r) + " start");
         const uint32_t *bh = static_cast<const uint32_t *>(I.best_host[size_t(r)].p);
-        const bool last = r == nrec - 1;
-        I.workers.submit([&, ev, bh, r, dev, last] {
-            std::string err;
-            double busy = 0;
-            try {
-                (void)hipSetDevice(dev);
-                wait_event(ev, last);
-                mark("ctc " + std::to_string(r) + " start");
-                const auto tc = Clock::now();
-                const RecPass &R2 = passes[size_t(r)];
-                // Lines in chunks on the loop pool (each line's text has a slot of its own).
-                const int nl = int(R2.rows.size()), chunks = std::min(nl, 32);
-                LoopPool::get().run(chunks, [&](int c) {
-                    for (int j = int(long(nl) * c / chunks); j < int(long(nl) * (c + 1) / chunks); j++) {
-                        std::string s = ctc_decode(bh + j, int(R2.lens[size_t(j)]), R2.ntot, R2.widths[size_t(j)]);
-                        pages_[size_t(R2.rows[size_t(j)].first)].lines[size_t(R2.rows[size_t(j)].second)] = std::move(s);
-                    }
-                }, -1);
-                busy = ms_since(tc);
-                mark("ctc " + std::to_string(r) + " done");
-            } catch (const std::exception &e) {
-                err = e.what();
+        // Lines in chunks on the loop pool (each line's text has a slot of its own).
+        const int nl = int(R.rows.size()), chunks = std::min(nl, 32);
+        LoopPool::get().run(chunks, [&](int c) {
+            for (int j = int(long(nl) * c / chunks); j < int(long(nl) * (c + 1) / chunks); j++) {
+                std::string s = ctc_decode(bh + j, int(R.lens[size_t(j)]), R.ntot, R.widths[size_t(j)]);
+                pages[size_t(R.rows[size_t(j)].first)].lines[size_t(R.rows[size_t(j)].second)] = std::move(s);
             }
-            task_done(busy, err);
-        });
+        }, -1);
+        mark("ctc " + std::to_string(r) + " done");
     }
-    } catch (const std::exception &e) {
-        std::lock_guard<std::mutex> lk(mu);
-        if (error.empty()) error = e.what();
+};
+
+void Pipeline::run_pages(const uint8_t *const *src, bool on_host, const int *w, const int *h, int npages) {
+    Impl &I = *impl_;
+    const auto t0 = Clock::now();
+    pages_.assign(size_t(std::max(npages, 0)), PageText{});
+    stats_ = PipelineStats{};
+    stats_.pages = npages;
+    if (npages <= 0) return;
+    for (int p = 0; p < npages; p++) {
+        if (!src[p]) fail("pipeline: page " + std::to_string(p) + " is null");
+        if (w[p] <= 0 || h[p] <= 0) fail("pipeline: empty page " + std::to_string(p));
     }
+    I.ctx.bind();
+    const PipelinePlan plan = plan_pipeline(npages, I.opts.merge, I.opts.det_batch);
+    std::vector<std::string> errs;
+    double busy = 0;
+    int failed = 0;
     {
-        std::unique_lock<std::mutex> lk(mu);
-        cv.wait(lk, [&] { return pending_tasks == 0; });
-    }
-    mark("tasks done");
-    (void)hipStreamSynchronize(I.copy);
-    for (hipEvent_t e : det_ev)
-        if (e) (void)hipEventDestroy(e);
-    for (hipEvent_t e : ccl_ev)
-        if (e) (void)hipEventDestroy(e);
-    for (hipEvent_t e : rec_ev)
-        if (e) (void)hipEventDestroy(e);
-    for (hipEvent_t e : am_ev)
-        if (e) (void)hipEventDestroy(e);
-    if (!error.empty()) fail("pipeline: " + error);
-    ctx.sync();
+        PipelineRun R(I, plan, src, on_host, w, h, pages_);
+        const char *la = std::getenv("OCR_PIPE_LOOKAHEAD");
+        const bool lookahead = la ? std::atoi(la) != 0 : I.opts.lookahead;
+        errs = run_schedule(plan, R, [&](std::function<void()> f) { I.workers.submit(std::move(f)); }, &busy,
+                            lookahead);
+        for (int p = 0; p < npages; p++) {
+            pages_[size_t(p)].error = errs[size_t(p)];
+            if (!errs[size_t(p)].empty()) {
+                pages_[size_t(p)].lines.clear();
+                failed++;
+            }
+        }
+        stats_.batches = R.batches;
+        stats_.rec_passes = R.rec_passes;
+        for (const auto &Rp : R.passes)
+            for (uint32_t l : Rp.lens) stats_.rec_steps += l;
+        R.print_trace();
+    }  // R's destructor waits for the streams before its buffers go back to the pool
     stats_.ms = ms_since(t0);
-    if (tracing) {
-        mark("end");
-        std::sort(trace.begin(), trace.end());
-        for (const auto &e : trace) std::fprintf(stderr, "[pipe] %8.3f ms  %s\n", e.first, e.second.c_str());
-    }
-    stats_.cpu_busy_ms = cpu_busy;
+    stats_.cpu_busy_ms = busy;
     for (const PageText &pt : pages_) {
         stats_.lines += int(pt.lines.size());
         stats_.words += pt.words;
     }
-    for (const RecPass &R : passes)
-        for (uint32_t l : R.lens) stats_.rec_steps += l;
+    if (failed) {
+        int first = 0;
+        while (errs[size_t(first)].empty()) first++;
+        fail("pipeline: " + std::to_string(failed) + " of " + std::to_string(npages) + " pages failed; page " +
+             std::to_string(first) + ": " + errs[size_t(first)]);
+    }
+}
+
+void Pipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages) {
+    run_pages(d_rgb, false, w, h, npages);
+}
+
+void Pipeline::run_host(const uint8_t *const *rgb, const int *w, const int *h, int npages) {
+    run_pages(rgb, true, w, h, npages);
 }
 
 }  // namespace ocr

@@ -18,11 +18,16 @@ struct PipelineOpts {
     float thr = 0.5f;     // detection threshold
     int threads = 0;      // host worker threads (0: hardware concurrency, at most 16)
     int det_batch = 4;    // pages per detection pass
+    bool lookahead = true;  // a recognition pass waits for the next pass's detections to be queued
+    // Capacities of the GPU labelling of a page's mask (0: 2^17 runs, 16384 components, 65536
+    // row slots); a page that needs more is labelled on the host from its bits.
+    int label_runs = 0, label_comps = 0, label_slots = 0;
 };
 
 struct PageText {
     std::vector<std::string> lines;  // reading order
     int words = 0;
+    std::string error;  // why the page failed ("" when it finished)
 };
 
 struct PipelineStats {
@@ -59,11 +64,17 @@ class Pipeline {
     ~Pipeline();
     // All pages' RGB bytes already in device memory.
     void run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages);
+    // The pages in host memory: each detection group's pages go to the device on a stream of
+    // their own (through pinned staging unless already page-locked) while earlier groups are
+    // detected and recognised. A page that fails leaves its error in pages()[p].error and the
+    // others finish; the call then throws, naming how many failed and the first error.
+    void run_host(const uint8_t *const *rgb, const int *w, const int *h, int npages);
     const std::vector<PageText> &pages() const { return pages_; }
     const PipelineStats &stats() const { return stats_; }
+    struct Impl;
 
   private:
-    struct Impl;
+    void run_pages(const uint8_t *const *src, bool on_host, const int *w, const int *h, int npages);
     Impl *impl_;
     std::vector<PageText> pages_;
     PipelineStats stats_;

@@ -86,25 +86,63 @@ size_t Pool::size_class(size_t bytes) {
     return mid >= bytes ? mid : p;
 }
 
-Pool::~Pool() { trim(); }
+Pool::~Pool() {
+    trim();
+    for (hipEvent_t e : spare_) (void)hipEventDestroy(e);
+}
 
-void *Pool::get(size_t bytes) {
+hipEvent_t Pool::event() {
+    if (!spare_.empty()) {
+        hipEvent_t e = spare_.back();
+        spare_.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    OCR_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    return e;
+}
+
+void *Pool::get(size_t bytes, hipStream_t s) {
     size_t sz = size_class(bytes);
     {
         std::lock_guard<std::mutex> lk(mu_);
         auto it = free_.find(sz);
         if (it != free_.end() && !it->second.empty()) {
-            void *p = it->second.back();
-            it->second.pop_back();
-            held_ -= sz;
-            live_ += sz;
-            return p;
+            std::vector<Block> &v = it->second;
+            // The newest buffer whose home is s (stream order covers its earlier uses there),
+            // else the newest idle one. A buffer still homed on another stream is not taken: an
+            // event recorded on that stream now would also wait for everything queued there
+            // since, and serialise the streams.
+            long pick = -1;
+            for (size_t k = v.size(); k-- > 0;)
+                if (v[k].home == s) {
+                    pick = long(k);
+                    break;
+                }
+            if (pick < 0)
+                for (size_t k = v.size(); k-- > 0;)
+                    if (v[k].home == nullptr) {
+                        pick = long(k);
+                        break;
+                    }
+            if (pick >= 0) {
+                Block b = std::move(v[size_t(pick)]);
+                v.erase(v.begin() + pick);
+                for (hipEvent_t e : b.pending) {
+                    OCR_HIP(hipStreamWaitEvent(s, e, 0));
+                    spare_.push_back(e);  // reusable: the wait above captured its state
+                }
+                held_ -= sz;
+                live_ += sz;
+                return b.p;
+            }
         }
     }
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, sz);
     if (e != hipSuccess) {
         // Out of memory: give back what the pool holds and try once more.
+        (void)hipGetLastError();
         trim();
         OCR_HIP(hipMalloc(&p, sz));
     }
@@ -114,7 +152,7 @@ void *Pool::get(size_t bytes) {
     return p;
 }
 
-void Pool::put(void *p) {
+void Pool::put(void *p, hipStream_t home, const hipStream_t *extra, int nextra) {
     if (!p) return;
     std::lock_guard<std::mutex> lk(mu_);
     auto it = size_of_.find(p);
@@ -127,22 +165,41 @@ void Pool::put(void *p) {
         (void)hipFree(p);
         return;
     }
+    Block b{p, home, {}};
+    for (int k = 0; k < nextra; k++) {
+        if (!extra[k] || extra[k] == home) continue;
+        hipEvent_t e = event();
+        OCR_HIP(hipEventRecord(e, extra[k]));
+        b.pending.push_back(e);
+    }
     held_ += sz;
-    free_[sz].push_back(p);
+    free_[sz].push_back(std::move(b));
+}
+
+void Pool::retire_stream(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(mu_);
+    for (auto &kv : free_)
+        for (Block &b : kv.second)
+            if (b.home == s) b.home = nullptr;
 }
 
 void Pool::trim() {
     std::lock_guard<std::mutex> lk(mu_);
     for (auto &kv : free_)
-        for (void *p : kv.second) {
-            (void)hipFree(p);
-            size_of_.erase(p);
+        for (Block &b : kv.second) {
+            (void)hipFree(b.p);
+            size_of_.erase(b.p);
+            for (hipEvent_t e : b.pending) spare_.push_back(e);
         }
     free_.clear();
     held_ = 0;
 }
 
-DBuf::DBuf(Ctx *ctx, size_t bytes) : ctx_(ctx), bytes_(bytes) { p_ = ctx->pool().get(bytes); }
+DBuf::DBuf(Ctx *ctx, size_t bytes) : DBuf(ctx, bytes, ctx->stream()) {}
+
+DBuf::DBuf(Ctx *ctx, size_t bytes, hipStream_t stream) : ctx_(ctx), bytes_(bytes), home_(stream) {
+    p_ = ctx->pool().get(bytes, stream);
+}
 
 DBuf &DBuf::operator=(DBuf &&o) noexcept {
     if (this != &o) {
@@ -150,18 +207,31 @@ DBuf &DBuf::operator=(DBuf &&o) noexcept {
         ctx_ = o.ctx_;
         p_ = o.p_;
         bytes_ = o.bytes_;
+        home_ = o.home_;
+        nextra_ = o.nextra_;
+        extra_[0] = o.extra_[0], extra_[1] = o.extra_[1];
         o.p_ = nullptr;
         o.ctx_ = nullptr;
         o.bytes_ = 0;
+        o.nextra_ = 0;
     }
     return *this;
 }
 
+void DBuf::used_on(hipStream_t s) {
+    if (s == home_) return;
+    for (int k = 0; k < nextra_; k++)
+        if (extra_[k] == s) return;
+    if (nextra_ == 2) fail("DBuf::used_on: more than two extra streams");
+    extra_[nextra_++] = s;
+}
+
 void DBuf::reset() {
-    if (p_ && ctx_) ctx_->pool().put(p_);
+    if (p_ && ctx_) ctx_->pool().put(p_, home_, extra_, nextra_);
     p_ = nullptr;
     ctx_ = nullptr;
     bytes_ = 0;
+    nextra_ = 0;
 }
 
 Ctx::Ctx(int device, uint32_t lines, size_t pool_mb) : device_(device), lines_(lines), pool_(pool_mb << 20) {
@@ -188,9 +258,26 @@ Ctx::~Ctx() {
     if (stream_) (void)hipStreamDestroy(stream_);
 }
 
+namespace {
+thread_local const Ctx *tl_ctx = nullptr;
+thread_local hipStream_t tl_stream = nullptr;
+}  // namespace
+
+hipStream_t Ctx::stream() const { return tl_ctx == this && tl_stream ? tl_stream : stream_; }
+
+StreamScope::StreamScope(const Ctx &ctx, hipStream_t s) : prev_ctx_(tl_ctx), prev_stream_(tl_stream) {
+    tl_ctx = &ctx;
+    tl_stream = s;
+}
+
+StreamScope::~StreamScope() {
+    tl_ctx = prev_ctx_;
+    tl_stream = prev_stream_;
+}
+
 void Ctx::bind() const { OCR_HIP(hipSetDevice(device_)); }
 
-void Ctx::sync() { OCR_HIP(hipStreamSynchronize(stream_)); }
+void Ctx::sync() { OCR_HIP(hipStreamSynchronize(stream())); }
 
 const void *Ctx::upload_raw(const void *data, size_t bytes) {
     void *p = nullptr;
@@ -208,7 +295,7 @@ void Ctx::h2d(void *dst, const void *src, size_t bytes) {
     if (!bytes) return;
     if (bytes > RING_BYTES / 4) {
         // Large uploads (whole pages, inputs) go straight from the caller's memory.
-        OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_));
+        OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()));
         return;
     }
     std::lock_guard<std::mutex> lk(ring_mu_);
@@ -238,7 +325,8 @@ void Ctx::h2d(void *dst, const void *src, size_t bytes) {
         staged_.pop_front();
     }
     std::memcpy(ring_ + b, src, bytes);
-    OCR_HIP(hipMemcpyAsync(dst, ring_ + b, bytes, hipMemcpyHostToDevice, stream_));
+    const hipStream_t st = stream();
+    OCR_HIP(hipMemcpyAsync(dst, ring_ + b, bytes, hipMemcpyHostToDevice, st));
     hipEvent_t ev = nullptr;
     if (!spare_events_.empty()) {
         ev = spare_events_.back();
@@ -246,14 +334,15 @@ void Ctx::h2d(void *dst, const void *src, size_t bytes) {
     } else {
         OCR_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     }
-    OCR_HIP(hipEventRecord(ev, stream_));
+    OCR_HIP(hipEventRecord(ev, st));
     staged_.push_back({b, e, ev});
     ring_head_ = e;
 }
 
 void Ctx::d2h(void *dst, const void *src, size_t bytes) {
-    if (bytes) OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream_));
-    OCR_HIP(hipStreamSynchronize(stream_));
+    const hipStream_t st = stream();
+    if (bytes) OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st));
+    OCR_HIP(hipStreamSynchronize(st));
 }
 
 }  // namespace ocr

@@ -18,24 +18,41 @@
 namespace ocr {
 
 // Size-classed, stream-ordered pool of device buffers (gpu.rs:938-966). hipMalloc is slow and
-// synchronising, so scratch buffers are reused: a buffer given back is handed out again for
-// later work on the same stream, which stream order makes safe without any wait. Sizes are
-// rounded up to classes (2^k and 1.5 * 2^k above 64 KiB) so varied batch shapes share buffers;
-// the pool keeps at most `cap` bytes and frees the rest (POOLMB, gpu.rs:919).
+// synchronising, so scratch buffers are reused. Every buffer has a home stream, the stream its
+// last holder queued work on; other streams that touched it are named when it is given back,
+// and an event is recorded on each of them then. A buffer is handed out again only for work on
+// its home stream (stream order covers its uses there; the recorded events are waited for on
+// the GPU, not the host), or once its home stream is retired (synchronised, about to go).
+// Sizes are rounded up to classes (2^k and 1.5 * 2^k above 64 KiB) so varied batch shapes share
+// buffers; the pool keeps at most `cap` bytes and frees the rest (POOLMB, gpu.rs:919), which
+// waits for the device.
 class Pool {
   public:
     explicit Pool(size_t cap_bytes) : cap_(cap_bytes) {}
     ~Pool();
-    void *get(size_t bytes);
-    void put(void *p);
+    // A buffer of at least `bytes` for work queued on stream s.
+    void *get(size_t bytes, hipStream_t s);
+    // Gives p back; its holder queued work on `home` and, if given, on the `extra` streams.
+    void put(void *p, hipStream_t home, const hipStream_t *extra = nullptr, int nextra = 0);
+    // Stream s has finished all its work and is about to be destroyed: buffers given back from
+    // it need no wait any more.
+    void retire_stream(hipStream_t s);
     void trim();  // free everything held
     size_t held() const { return held_; }
     size_t live() const { return live_; }
+    size_t cap() const { return cap_; }
     static size_t size_class(size_t bytes);
 
   private:
-    std::map<size_t, std::vector<void *>> free_;
+    struct Block {
+        void *p;
+        hipStream_t home;  // null: no work queued on it anywhere
+        std::vector<hipEvent_t> pending;  // recorded on other streams that used the buffer
+    };
+    hipEvent_t event();
+    std::map<size_t, std::vector<Block>> free_;
     std::unordered_map<void *, size_t> size_of_;
+    std::vector<hipEvent_t> spare_;
     size_t cap_, held_ = 0, live_ = 0;
     std::mutex mu_;
 };
@@ -86,17 +103,21 @@ class ProbeScope {
     bool on_ = false;
 };
 
-// A pooled device buffer owned by one holder; goes back to the pool when destroyed.
+// A pooled device buffer owned by one holder; goes back to the pool when destroyed. Its work
+// is queued on `stream` (the context's stream unless given); used_on() names another stream
+// that reads or writes it, so the pool orders the buffer's next use after that stream's work.
 class DBuf {
   public:
     DBuf() = default;
     DBuf(Ctx *ctx, size_t bytes);
+    DBuf(Ctx *ctx, size_t bytes, hipStream_t stream);
     DBuf(DBuf &&o) noexcept { *this = std::move(o); }
     DBuf &operator=(DBuf &&o) noexcept;
     DBuf(const DBuf &) = delete;
     DBuf &operator=(const DBuf &) = delete;
     ~DBuf() { reset(); }
     void reset();
+    void used_on(hipStream_t s);
     template <class T> T *as() const { return static_cast<T *>(p_); }
     void *get() const { return p_; }
     size_t bytes() const { return bytes_; }
@@ -106,6 +127,9 @@ class DBuf {
     Ctx *ctx_ = nullptr;
     void *p_ = nullptr;
     size_t bytes_ = 0;
+    hipStream_t home_ = nullptr;
+    hipStream_t extra_[2] = {nullptr, nullptr};
+    int nextra_ = 0;
 };
 
 // A weight buffer uploaded once at load time (not pooled).
@@ -119,20 +143,23 @@ class Ctx {
     Ctx(int device, uint32_t lines, size_t pool_mb);
     ~Ctx();
     int device() const { return device_; }
-    hipStream_t stream() const { return stream_; }
+    // The stream work is queued on: the context's own, unless a StreamScope on the calling
+    // thread names another.
+    hipStream_t stream() const;
+    hipStream_t own_stream() const { return stream_; }
     uint32_t lines() const { return lines_; }
     Pool &pool() { return pool_; }
     void bind() const;  // make this context's device current on the calling thread
-    void sync();
+    void sync();        // waits for stream()
 
     // Weights live until the context is destroyed.
     template <class T> const T *upload_weights(const T *data, size_t count) {
         return static_cast<const T *>(upload_raw(data, count * sizeof(T)));
     }
-    // Async on the stream: src is copied into a pinned staging ring first, so the call returns
+    // Async on stream(): src is copied into a pinned staging ring first, so the call returns
     // at once and src may be reused (a copy from pageable memory would wait for the stream).
     void h2d(void *dst, const void *src, size_t bytes);
-    void d2h(void *dst, const void *src, size_t bytes);  // synchronous: waits for the stream
+    void d2h(void *dst, const void *src, size_t bytes);  // synchronous: waits for stream()
 
   private:
     const void *upload_raw(const void *data, size_t bytes);
@@ -151,6 +178,20 @@ class Ctx {
     std::deque<Staged> staged_;
     std::vector<hipEvent_t> spare_events_;
     std::mutex ring_mu_;
+};
+
+// While alive, ctx.stream() on this thread is s: everything the models and graphs queue (and
+// the pooled buffers they take) goes to s instead of the context's own stream.
+class StreamScope {
+  public:
+    StreamScope(const Ctx &ctx, hipStream_t s);
+    ~StreamScope();
+    StreamScope(const StreamScope &) = delete;
+    StreamScope &operator=(const StreamScope &) = delete;
+
+  private:
+    const Ctx *prev_ctx_;
+    hipStream_t prev_stream_;
 };
 
 }  // namespace ocr

@@ -42,6 +42,8 @@ SIGNATURES = {
     "ocr_device_free": (ctypes.c_int, [P, P]),
     "ocr_memcpy_h2d": (ctypes.c_int, [P, P, P, SZ]),
     "ocr_memcpy_d2h": (ctypes.c_int, [P, P, P, SZ]),
+    "ocr_host_alloc": (P, [P, SZ]),
+    "ocr_host_free": (ctypes.c_int, [P, P]),
     "ocr_detector_new": (P, [P, ctypes.c_char_p]),
     "ocr_detector_free": (None, [P]),
     "ocr_detect_page": (ctypes.c_int, [P, P, U32, U32, F32, P]),
@@ -73,6 +75,7 @@ SIGNATURES = {
     "ocr_pipeline_stats_get": (ctypes.c_int, [P, P]),
     "ocr_pipeline_page": (ctypes.c_int, [P, U32, PU32, PU32]),
     "ocr_pipeline_line_text": (ctypes.c_int, [P, U32, U32, ctypes.c_char_p, U32, PU32]),
+    "ocr_pipeline_page_error": (ctypes.c_int, [P, U32, ctypes.c_char_p, U32, PU32]),
     "ocr_nd_new": (P, [P, ctypes.c_char_p, ctypes.c_int]),
     "ocr_nd_free": (None, [P]),
     "ocr_nd_dims": (ctypes.c_int, [P, P, U32, P, PU32]),
@@ -166,6 +169,33 @@ class DeviceBuffer:
             pass
 
 
+class HostArray:
+    """Page-locked host memory of a context (ocr_host_alloc) as a numpy array (.array); freed
+    with the object."""
+
+    def __init__(self, ctx: "Context", shape, dtype=np.uint8):
+        self.ctx = ctx
+        dtype = np.dtype(dtype)
+        nbytes = int(np.prod(shape)) * dtype.itemsize
+        self.ptr = lib().ocr_host_alloc(ctx.handle, max(nbytes, 1))
+        if not self.ptr:
+            raise OcrError(lib().ocr_last_error().decode())
+        buf = (ctypes.c_uint8 * max(nbytes, 1)).from_address(self.ptr)
+        self.array = np.frombuffer(buf, dtype=dtype, count=int(np.prod(shape))).reshape(shape)
+
+    def free(self):
+        if self.ptr:
+            self.array = None
+            lib().ocr_host_free(self.ctx.handle, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Context:
     """Gpu::new (src/gpu.rs:850): device, stream and scratch pool."""
 
@@ -180,6 +210,10 @@ class Context:
 
     def alloc(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)
+
+    def host_array(self, shape, dtype=np.uint8) -> "HostArray":
+        """A numpy array in page-locked host memory (ocr_host_alloc)."""
+        return HostArray(self, shape, dtype)
 
     def close(self):
         if self.handle:
@@ -487,12 +521,20 @@ class Pipeline:
         _check(lib().ocr_pipeline_run_device(self.handle, arr, _ptr(w), _ptr(h), n))
 
     def run(self, pages):
+        """Pages in host memory (numpy [h, w, 3] uint8; pageable, or HostArray arrays)."""
         pages = [np.ascontiguousarray(p, np.uint8) for p in pages]
         n = len(pages)
         arr = (ctypes.c_void_p * n)(*[p.ctypes.data for p in pages])
         w = np.asarray([p.shape[1] for p in pages], np.uint32)
         h = np.asarray([p.shape[0] for p in pages], np.uint32)
         _check(lib().ocr_pipeline_run(self.handle, arr, _ptr(w), _ptr(h), n))
+
+    def page_error(self, page: int) -> str:
+        """Why a page of the last run failed ("" when it finished)."""
+        buf = ctypes.create_string_buffer(4096)
+        n = ctypes.c_uint32()
+        _check(lib().ocr_pipeline_page_error(self.handle, page, buf, 4096, ctypes.byref(n)))
+        return buf.value.decode()
 
     def stats(self) -> dict:
         s = ocr_pipeline_stats()
