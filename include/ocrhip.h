@@ -148,6 +148,17 @@ int ocr_word_rects_mt(const uint32_t *bits, uint32_t w, uint32_t h, uint32_t thr
 int ocr_word_rects_gpu(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out, uint32_t cap,
                        uint32_t *count);
 
+/* The same rectangles as ocr_word_rects_gpu without any device allocation: no counterpart in the
+ * reference; for callers that cannot allocate device memory (serving loops, harnesses that forbid
+ * hipMalloc). The labelling runs in one fixed device array of 4.56 MiB per GPU, set up by
+ * ocr_create and held until the process ends. Limits: at most 16384 rows and 2^19 mask words
+ * (ceil(w / 32) * h; a 4096 x 4096 page); larger masks fail with an error. A mask with more than
+ * 131072 runs, 16384 components or 65536 component rows is labelled on the host instead (the
+ * same rectangles). Calls on one GPU share the array and run one at a time. Host-side geometry
+ * uses ordinary heap memory. */
+int ocr_word_rects_gpu_noalloc(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out,
+                               uint32_t cap, uint32_t *count);
+
 /* The page layout before recognition (src/bin/ocr-bench.rs:503-559): words, text lines in
  * reading order, line padding (relv, relend), every line's crop box, polygon spans and resized
  * width, and the batches (ocr-bench.rs:385-407). */

@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "models.h"
+#include "noalloc.h"
 #include "nd.h"
 #include "pipeline.h"
 #include "crop.h"
@@ -96,6 +97,8 @@ ocr_ctx *ocr_create(const ocr_opts *opts) {
         if (o.pool_mb == 0) o.pool_mb = 8192;
         auto c = std::make_unique<ocr_ctx>();
         c->ctx = std::make_unique<Ctx>(o.device, o.lines, size_t(o.pool_mb));
+        // The fixed device array of ocr_word_rects_gpu_noalloc: its address on this device.
+        noalloc_init(o.device);
         return c.release();
     });
 }
@@ -425,6 +428,18 @@ int ocr_word_rects_gpu(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t 
             c.d2h(xmax.data(), dxmax.get(), ns * 4);
         }
         std::vector<RRect> r = word_rects_from_rows(comps.data(), int(nc), xmin.data(), xmax.data(), int(ns));
+        *count = uint32_t(r.size());
+        for (size_t i = 0; i < r.size() && i < cap; i++) out[i] = {r[i].cx, r[i].cy, r[i].ux, r[i].uy, r[i].w, r[i].h};
+    });
+}
+
+int ocr_word_rects_gpu_noalloc(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t h, ocr_rrect *out,
+                               uint32_t cap, uint32_t *count) {
+    return guard([&] {
+        need(ctx, "ctx");
+        need(bits, "bits");
+        need(count, "count");
+        std::vector<RRect> r = word_rects_gpu_noalloc(*ctx->ctx, bits, int(w), int(h));
         *count = uint32_t(r.size());
         for (size_t i = 0; i < r.size() && i < cap; i++) out[i] = {r[i].cx, r[i].cy, r[i].ux, r[i].uy, r[i].w, r[i].h};
     });

@@ -63,6 +63,7 @@ SIGNATURES = {
     "ocr_word_rects": (ctypes.c_int, [P, U32, U32, P, U32, PU32]),
     "ocr_word_rects_mt": (ctypes.c_int, [P, U32, U32, U32, P, U32, PU32]),
     "ocr_word_rects_gpu": (ctypes.c_int, [P, P, U32, U32, P, U32, PU32]),
+    "ocr_word_rects_gpu_noalloc": (ctypes.c_int, [P, P, U32, U32, P, U32, PU32]),
     "ocr_layout_page": (P, [P, U32, U32, F32, F32]),
     "ocr_layout_free": (None, [P]),
     "ocr_layout_counts": (ctypes.c_int, [P, PU32, PU32, PU32]),
@@ -461,6 +462,18 @@ def word_rects_gpu(ctx: "Context", bits: np.ndarray, w: int):
     _check(lib().ocr_word_rects_gpu(ctx.handle, _ptr(bits), w, h, None, 0, ctypes.byref(count)))
     out = np.zeros((count.value, 6), np.float32)
     _check(lib().ocr_word_rects_gpu(ctx.handle, _ptr(bits), w, h, _ptr(out), count.value, ctypes.byref(count)))
+    return out
+
+
+def word_rects_gpu_noalloc(ctx: "Context", bits: np.ndarray, w: int):
+    """word_rects_gpu with the labelling in the library's fixed device array (no allocation)."""
+    bits = np.ascontiguousarray(bits, np.uint32)
+    h = bits.shape[0]
+    count = ctypes.c_uint32()
+    _check(lib().ocr_word_rects_gpu_noalloc(ctx.handle, _ptr(bits), w, h, None, 0, ctypes.byref(count)))
+    out = np.zeros((count.value, 6), np.float32)
+    _check(lib().ocr_word_rects_gpu_noalloc(ctx.handle, _ptr(bits), w, h, _ptr(out), count.value,
+                                            ctypes.byref(count)))
     return out
 
 
