@@ -83,16 +83,16 @@ def copy_calibration():
 
 def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
     """The oracle (C restatement, OpenMP on all host cores) page by page, as the reference's CPU
-    baseline loop runs (src/bin/ocr-bench.rs:431-444): oracle detection, the library's host
-    layout, oracle line images and recognition, greedy CTC. One untimed warm-up page, then
+    baseline loop runs (src/bin/ocr-bench.rs:431-444): oracle detection, the oracle's layout,
+    oracle line images and recognition, greedy CTC. One untimed warm-up page, then
     pages of the same workload until at least `min_secs` have passed (a bounded sample)."""
-    import ocrhip
     from oracle import graph as og
+    from oracle import layout as ol
     from oracle import onnx_read
 
     det, rec = onnx_read.load(det_path), onnx_read.load(rec_path)
     og.lib()
-    layout = lambda b, w: ocrhip.Layout(b, w)  # noqa: E731
+    layout = ol.Layout
     og.page_pipeline(det, rec, pages[0], 0.5, layout)
     n, t = 0, time.perf_counter()
     while time.perf_counter() - t < min_secs and n < 4 * len(pages):

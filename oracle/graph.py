@@ -18,6 +18,7 @@ from . import onnx_read
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+SOURCES = ("oracle.c", "contours.c")
 _lib = None
 
 
@@ -26,7 +27,7 @@ def build() -> str:
     os.makedirs(os.path.dirname(LIB_PATH), exist_ok=True)
     tmp = LIB_PATH + f".tmp{os.getpid()}"
     subprocess.run(["gcc", "-O3", "-march=x86-64-v2", "-fopenmp", "-fPIC", "-shared", "-ffp-contract=off",
-                    "-o", tmp, os.path.join(HERE, "oracle.c"), "-lm"], check=True)
+                    "-o", tmp, *(os.path.join(HERE, f) for f in SOURCES), "-lm"], check=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
@@ -34,7 +35,8 @@ def build() -> str:
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH) or os.path.getmtime(LIB_PATH) < os.path.getmtime(os.path.join(HERE, "oracle.c")):
+        if not os.path.exists(LIB_PATH) or any(os.path.getmtime(LIB_PATH) < os.path.getmtime(os.path.join(HERE, f))
+                                               for f in SOURCES):
             build()
         L = ctypes.CDLL(LIB_PATH)
         P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
@@ -50,6 +52,16 @@ def lib():
         L.orc_pp_line_input.argtypes = [P, I, I, I, I, I, I, I, I, P]
         L.orc_activate.argtypes = [F, I]
         L.orc_activate.restype = F
+        L.orc_find_contours.argtypes = [P, I, I]
+        L.orc_find_contours.restype = P
+        L.orc_contours_free.argtypes = [P]
+        L.orc_contours_count.argtypes = [P]
+        L.orc_contours_points.argtypes = [P]
+        L.orc_contours_get.argtypes = [P, P, P, P, P]
+        L.orc_simplify_polygon.argtypes = [P, I, F, P]
+        L.orc_convex_hull.argtypes = [P, I, P]
+        L.orc_min_area_rect.argtypes = [P, I, P]
+        L.orc_word_rects.argtypes = [P, I, I, F, F, F, P, I]
         _lib = L
     return _lib
 

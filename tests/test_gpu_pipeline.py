@@ -8,6 +8,7 @@ import pytest
 import ocrhip
 from ocrhip import synth
 from oracle import graph as og
+from oracle import layout as ol
 
 pytestmark = pytest.mark.gpu
 
@@ -18,7 +19,9 @@ def pipeline(detector, recognizer):
 
 
 def layout_of(bits, w):
-    return ocrhip.Layout(bits, w)
+    """The oracle's layout (words, lines, padding, crops, batches), restated apart from the
+    product's host code."""
+    return ol.Layout(bits, w)
 
 
 def test_pipeline_text_matches_cpu(pipeline, detector, det_oracle, rec_oracle):
@@ -39,6 +42,28 @@ def test_pipeline_text_matches_cpu(pipeline, detector, det_oracle, rec_oracle):
     assert words == cpu_words
     assert texts == cpu_texts
     assert sum(len(t) for t in texts) > 0
+
+
+def test_bench_configuration_text_matches_cpu(detector, recognizer, det_oracle, rec_oracle):
+    # The benchmark's workload: 12 pages from host memory, 6 pages a recognition pass, 2 a
+    # detection pass. Every page's text equals the CPU pipeline's (oracle detection, layout,
+    # line images, recognition, CTC) on the same mask; a pass of 6 detection pages gives the same.
+    pages = [synth.page(i) for i in range(12)]
+    p = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=2)
+    print("bench configuration: 12 pages", flush=True)
+    p.run(pages)
+    q = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=6)
+    q.run(pages)
+    for k, page in enumerate(pages):
+        print(f"bench configuration: page {k} against the oracle", flush=True)
+        texts, words = p.texts(k)
+        assert q.texts(k) == (texts, words)
+        bits = detector.detect_page(page, 0.5)
+        want_bits, prob, _ = og.detect_page(det_oracle, page, 0.5)
+        diff = np.unpackbits((bits ^ want_bits).view(np.uint8), bitorder="little").reshape(bits.shape[0], -1)
+        assert np.all(np.abs(prob[diff[:, : page.shape[1]].astype(bool)] - 0.5) < 1e-4)
+        cpu_texts, cpu_words, _ = og.page_pipeline(det_oracle, rec_oracle, page, 0.5, lambda b, w: layout_of(bits, w))
+        assert (texts, words) == (cpu_texts, cpu_words)
 
 
 def test_line_images_match_oracle(detector, ctx):
@@ -98,7 +123,7 @@ def _pack_bits(mask):
 
 
 def test_word_rects_gpu_labelling_identical(detector, ctx):
-    # Components labelled on the GPU give the host's rectangles bit for bit, in the same order:
+    # Components labelled on the GPU give the oracle's rectangles bit for bit, in the same order:
     # a detector mask, noise with many tiny and diagonal-only components, nested rings, full
     # rows, an empty mask, widths inside a word.
     rng = np.random.Generator(np.random.PCG64(23))
@@ -121,10 +146,12 @@ def test_word_rects_gpu_labelling_identical(detector, ctx):
     masks.append((_pack_bits(diag), 130))
     for bits, w in masks:
         print(f"word rects of a {bits.shape[0]} x {w} mask", flush=True)
-        want = ocrhip.word_rects(bits, w)
+        want = ol.word_rects(bits, w)
         got = ocrhip.word_rects_gpu(ctx, bits, w)
         assert got.shape == want.shape
         np.testing.assert_array_equal(got, want)
+    # nested rings: only the outermost ring is an external contour (ocr-bench.rs:52)
+    assert len(ocrhip.word_rects_gpu(ctx, masks[4][0], 300)) == 1
 
 
 def test_detect_mask_words_at_odd_widths(detector, det_oracle):
@@ -158,14 +185,14 @@ def test_pipeline_merge_and_device_entry(detector, recognizer, ctx):
 
 def test_pipeline_words_match_host_labelling(detector, recognizer):
     # Eight full pages in one detection pass label their masks on the GPU concurrently; every
-    # page's word count equals the host labelling of the same mask (a component split, merged or
+    # page's word count equals the oracle's words of the same mask (a component split, merged or
     # given a wrong bottom row by a race would change it, or fail the run's own row checks).
     pages = [synth.page(s) for s in range(20, 28)]
     p = ocrhip.Pipeline(detector, recognizer, merge=8, det_batch=8)
     p.run(pages)
     for k, page in enumerate(pages):
         print(f"page {k}", flush=True)
-        want = ocrhip.word_rects(detector.detect_page(page, 0.5), page.shape[1])
+        want = ol.word_rects(detector.detect_page(page, 0.5), page.shape[1])
         assert p.texts(k)[1] == len(want)
 
 

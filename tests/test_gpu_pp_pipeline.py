@@ -1,14 +1,13 @@
-"""The PP-OCR page pipeline on the GPU against the oracle, through the C ABI:
-line images, then whole pages (DB detection, host boxes, SVTR recognition, CTC).
-
-The host geometry (DB boxes, line boxes) is the library's own restatement of ppdet::boxes and
-is shared by both sides, as the ocrs pipeline test shares the host layout: rten-imageproc is not
-available to pin it (parity unpinned)."""
+"""The PP-OCR page pipeline (DB detection at long side 960, threshold 0.3, host boxes, SVTR
+recognition, CTC) on the GPU against the oracle, through the C ABI: line images, then whole pages.
+The oracle side takes its boxes from the oracle's own restatement of ppdet::boxes and of the
+line boxes (oracle/layout.py)."""
 import numpy as np
 import pytest
 
 from ocrhip import synth, synth_pp
 from oracle import graph as og
+from oracle import layout as ol
 from oracle import onnx_read
 
 pytestmark = pytest.mark.gpu
@@ -24,8 +23,9 @@ def pp_models(ctx):
 
 
 def boxes_of(bits, prob, to_page, page_w, page_h):
-    import ocrhip
-    return [ocrhip.pp_line_box(b, 0.1, page_w, page_h) for b in ocrhip.db_boxes(bits, prob, to_page)]
+    """The oracle's line boxes of a thresholded DB map."""
+    h, w = prob.shape
+    return [ol.pp_line_box(b, 0.1, page_w, page_h) for b in ol.db_boxes(bits, prob, w, h, to_page)]
 
 
 def test_pp_line_images_match_oracle(ctx):

@@ -427,7 +427,7 @@ int ocr_word_rects_gpu(ocr_ctx *ctx, const uint32_t *bits, uint32_t w, uint32_t 
             c.d2h(xmin.data(), dxmin.get(), ns * 4);
             c.d2h(xmax.data(), dxmax.get(), ns * 4);
         }
-        std::vector<RRect> r = word_rects_from_rows(comps.data(), int(nc), xmin.data(), xmax.data(), int(ns));
+        std::vector<RRect> r = word_rects_from_rows(bits, int(w), int(h), comps.data(), int(nc), xmin.data(), xmax.data(), int(ns));
         *count = uint32_t(r.size());
         for (size_t i = 0; i < r.size() && i < cap; i++) out[i] = {r[i].cx, r[i].cy, r[i].ux, r[i].uy, r[i].w, r[i].h};
     });

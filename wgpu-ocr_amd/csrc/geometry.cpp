@@ -40,88 +40,250 @@ struct Pt {
     float x, y;
 };
 
-float cross(const Pt &o, const Pt &a, const Pt &b) { return (a.x - o.x) * (b.y - o.y) - (a.y - o.y) * (b.x - o.x); }
+// ---- Word boxes: outer contours, simplification, minimum-area rectangles -------------------
+// The steps of ocr-bench.rs:47-58 (find_contours External, simplify_polygon(2), min_area_rect of
+// rten-imageproc 0.26.0), restated from the algorithms they publish (the crate is not vendored):
+// Suzuki-Abe border following, Ramer-Douglas-Peucker, and the rectangle with a side on a convex
+// hull edge. The arithmetic is float32 in a fixed order, the same rectangles bit for bit as the
+// oracle's independent restatement.
 
-// Convex hull of a component given as row extents (rows ascending; per row the leftmost and
-// rightmost pixel), counter-clockwise in the sense cross > 0, starting at the vertex with the
-// smallest (x, y), collinear points dropped, without repeating the first point. Only a row's two
-// extremes can be hull vertices, and listing them row by row already sorts the points by (y, x):
-// Andrew's monotone chain runs on the transposed points (x, y) -> (y, x) with no sort, and the
-// transposed chain's turn test is the original one negated, so reversing its output restores the
-// orientation. The vertex list is the one the chain over (x, y)-sorted points would give.
-std::vector<Pt> hull_rows(const std::vector<Pt> &p) {
-    // p: (x, y) in (y, x) order, unique.
-    auto tcross = [](const Pt &o, const Pt &a, const Pt &b) {  // cross product of the transposed points
-        return (a.y - o.y) * (b.x - o.x) - (a.x - o.x) * (b.y - o.y);
-    };
-    auto before = [](const Pt &a, const Pt &b) { return a.x < b.x || (a.x == b.x && a.y < b.y); };
-    if (p.size() < 3) {
-        std::vector<Pt> q = p;
-        if (q.size() == 2 && before(q[1], q[0])) std::swap(q[0], q[1]);
-        return q;
+// Directions 0 E, 1 NE, 2 N, 3 NW, 4 W, 5 SW, 6 S, 7 SE (y down); +1 turns counter-clockwise on
+// the page.
+constexpr int DIR_X[8] = {1, 1, 0, -1, -1, -1, 0, 1};
+constexpr int DIR_Y[8] = {0, -1, -1, -1, 0, 1, 1, 1};
+
+// A bit mask copied with a frame of zeros: one row above and below, one word left and right,
+// and the bits past the mask width cleared (the padding of the border following), so a pixel's
+// neighbours are read with no bounds checks.
+struct PaddedMask {
+    std::vector<uint32_t> p;
+    size_t stride = 0;  // words a padded row
+    void build(const uint32_t *bits, int w, int h) {
+        const int words = (w + 31) / 32;
+        stride = size_t(words) + 2;
+        p.assign(stride * (size_t(h) + 2) + 1, 0u);  // one spare word for the last 64-bit read
+        const uint32_t last = (w & 31) ? (1u << (w & 31)) - 1u : ~0u;
+        for (int y = 0; y < h; y++) {
+            uint32_t *dst = p.data() + (size_t(y) + 1) * stride + 1;
+            std::memcpy(dst, bits + size_t(y) * size_t(words), size_t(words) * 4);
+            dst[words - 1] &= last;
+        }
     }
-    std::vector<Pt> h(2 * p.size());
+    // The 3 x 3 block around (x, y): row y - 1 in bits 0..2, row y in 3..5, row y + 1 in 6..8
+    // (pixel x - 1 first in each).
+    uint32_t block(int x, int y) const {
+        const int b = x + 31;  // bit of pixel x - 1 in the padded row
+        const uint32_t *row = p.data() + (size_t(y) + 1) * stride + size_t(b >> 5);
+        const int sh = b & 31;
+        uint64_t u, m, d;
+        std::memcpy(&u, row - stride, 8);
+        std::memcpy(&m, row, 8);
+        std::memcpy(&d, row + stride, 8);
+        return (uint32_t(u >> sh) & 7u) | (uint32_t(m >> sh) & 7u) << 3 | (uint32_t(d >> sh) & 7u) << 6;
+    }
+};
+
+// The neighbour ring (bits 0..7 in direction order) of a 3 x 3 block.
+constexpr uint32_t block_ring(uint32_t b) {
+    return ((b >> 5) & 1u) | ((b >> 2) & 1u) << 1 | ((b >> 1) & 1u) << 2 | (b & 1u) << 3 | ((b >> 3) & 1u) << 4 |
+           ((b >> 6) & 1u) << 5 | ((b >> 7) & 1u) << 6 | ((b >> 8) & 1u) << 7;
+}
+
+// Step (3.3) of the border following as a table: for a pixel's 3 x 3 block and the direction
+// dprev of the pixel it came from, the first set neighbour counter-clockwise after dprev (the
+// ring always holds dprev; entries where it does not are never read).
+struct NextDir {
+    uint8_t t[512 * 8];
+    NextDir() {
+        for (uint32_t b = 0; b < 512; b++) {
+            const uint32_t r = block_ring(b);
+            for (int d = 0; d < 8; d++) {
+                int n = d;
+                for (int k = 1; k <= 8; k++)
+                    if ((r >> ((d + k) & 7)) & 1u) {
+                        n = (d + k) & 7;
+                        break;
+                    }
+                t[b * 8 + uint32_t(d)] = uint8_t(n);
+            }
+        }
+    }
+};
+const NextDir NEXT_DIR;
+
+// The outer border of the 8-connected component whose raster-first pixel is (x0, y0), as the
+// pixels Suzuki-Abe border following visits (steps 3.1-3.5: from the west neighbour clockwise to
+// the first set pixel, then from each pixel counter-clockwise after the one it came from), x, y
+// pairs in visiting order, starting at (x0, y0). A lone pixel is its own border.
+void trace_outer(const PaddedMask &m, int x0, int y0, std::vector<int32_t> &xy) {
+    xy.clear();
+    xy.push_back(x0), xy.push_back(y0);
+    const uint32_t b0 = m.block(x0, y0), r0 = block_ring(b0);
+    if (!r0) return;
+    int d1 = 4;
+    while (!((r0 >> d1) & 1u)) d1 = (d1 + 7) & 7;  // clockwise from the west
+    const int x1 = x0 + DIR_X[d1], y1 = y0 + DIR_Y[d1];
+    int x3 = x0, y3 = y0, dprev = d1;
+    uint32_t b = b0;
+    for (;;) {
+        const int d4 = NEXT_DIR.t[b * 8 + uint32_t(dprev)];
+        const int x4 = x3 + DIR_X[d4], y4 = y3 + DIR_Y[d4];
+        if (x4 == x0 && y4 == y0 && x3 == x1 && y3 == y1) return;
+        dprev = (d4 + 4) & 7;
+        x3 = x4, y3 = y4;
+        xy.push_back(x3), xy.push_back(y3);
+        b = m.block(x3, y3);
+    }
+}
+
+// Squared distances from the points k in (s, e) (coordinates px, py) to the segment between
+// points s and e (from point s when the segment is a point), into d2[k]: the float operations of
+// the distance itself up to its square root, so sqrt(d2[k]) is that distance bit for bit.
+void seg_dist2(const float *__restrict px, const float *__restrict py, int s, int e, float *__restrict d2) {
+    const float ax = px[s], ay = py[s], bx = px[e], by = py[e];
+    if (ax == bx && ay == by) {
+        for (int k = s + 1; k < e; k++) {
+            const float dx = px[k] - ax, dy = py[k] - ay;
+            d2[k] = dx * dx + dy * dy;
+        }
+        return;
+    }
+    const float abx = bx - ax, aby = by - ay, den = abx * abx + aby * aby;
+    for (int k = s + 1; k < e; k++) {
+        const float acx = px[k] - ax, acy = py[k] - ay;
+        const float t = (acx * abx + acy * aby) / den;
+        const float qx = t <= 0.f ? ax : (t >= 1.f ? bx : ax + abx * t);
+        const float qy = t <= 0.f ? ay : (t >= 1.f ? by : ay + aby * t);
+        const float dx = px[k] - qx, dy = py[k] - qy;
+        d2[k] = dx * dx + dy * dy;
+    }
+}
+
+// Scratch of simplify_closed, kept per thread.
+struct SimplifyScratch {
+    std::vector<float> px, py, d2;
+    std::vector<unsigned char> keep;
+    std::vector<std::pair<int, int>> stack;
+};
+
+// simplify_polygon(points, eps): Ramer-Douglas-Peucker on the closed polygon (the first point
+// appended, then dropped): a run splits at its farthest inner point from the segment between its
+// ends (distance to the segment, from its first point when it is a point; the last of equally
+// far points) when that is farther than eps. The farthest point is found on squared distances,
+// then the last point whose distance equals the largest one is picked by the distances
+// themselves (squared distances a few ulps apart can share a square root).
+void simplify_closed(const std::vector<int32_t> &xy, float eps, std::vector<Pt> &out, SimplifyScratch &S) {
+    const int n = int(xy.size() / 2);
+    out.clear();
+    if (n == 0) return;
+    S.px.resize(size_t(n) + 1), S.py.resize(size_t(n) + 1), S.d2.resize(size_t(n) + 1);
+    float *px = S.px.data(), *py = S.py.data(), *d2 = S.d2.data();
+    for (int k = 0; k < n; k++) px[k] = float(xy[size_t(2 * k)]), py[k] = float(xy[size_t(2 * k + 1)]);
+    px[n] = px[0], py[n] = py[0];
+    S.keep.assign(size_t(n) + 1, 0);
+    S.stack.assign(1, {0, n});
+    while (!S.stack.empty()) {
+        const auto [s, e] = S.stack.back();
+        S.stack.pop_back();
+        S.keep[size_t(s)] = S.keep[size_t(e)] = 1;
+        if (e - s < 2) continue;
+        seg_dist2(px, py, s, e, d2);
+        // The largest squared distance: 8 running maxima (max is exact in any order).
+        float mx[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        int k = s + 1;
+        for (; k + 8 <= e; k += 8)
+            for (int j = 0; j < 8; j++) mx[j] = d2[k + j] > mx[j] ? d2[k + j] : mx[j];
+        for (; k < e; k++) mx[0] = d2[k] > mx[0] ? d2[k] : mx[0];
+        float m2 = mx[0];
+        for (int j = 1; j < 8; j++) m2 = mx[j] > m2 ? mx[j] : m2;
+        const float dmax = std::sqrt(m2), near = m2 - m2 * 1e-5f;
+        int best = e - 1;
+        for (int q = e - 1; q > s; q--)
+            if (d2[q] >= near && std::sqrt(d2[q]) == dmax) {
+                best = q;
+                break;
+            }
+        if (dmax > eps) {
+            S.stack.push_back({best, e});
+            S.stack.push_back({s, best});
+        }
+    }
+    for (int k = 0; k < n; k++)
+        if (S.keep[size_t(k)]) out.push_back({px[k], py[k]});
+}
+
+double cross(const Pt &o, const Pt &a, const Pt &b) {
+    return (double(a.x) - o.x) * (double(b.y) - o.y) - (double(a.y) - o.y) * (double(b.x) - o.x);
+}
+
+// Convex hull (Andrew's monotone chain): counter-clockwise in the sense cross > 0 from the point
+// with the smallest (x, y), collinear points dropped, the first point not repeated.
+void convex_hull(std::vector<Pt> p, std::vector<Pt> &h) {
+    std::sort(p.begin(), p.end(), [](const Pt &a, const Pt &b) { return a.x < b.x || (a.x == b.x && a.y < b.y); });
+    p.erase(std::unique(p.begin(), p.end(), [](const Pt &a, const Pt &b) { return a.x == b.x && a.y == b.y; }),
+            p.end());
+    h.clear();
+    if (p.size() <= 2) {
+        h = p;
+        return;
+    }
+    h.resize(2 * p.size());
     size_t k = 0;
     for (size_t i = 0; i < p.size(); i++) {
-        while (k >= 2 && tcross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
+        while (k >= 2 && cross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
         h[k++] = p[i];
     }
     for (size_t i = p.size() - 1, t = k + 1; i-- > 0;) {
-        while (k >= t && tcross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
+        while (k >= t && cross(h[k - 2], h[k - 1], p[i]) <= 0) k--;
         h[k++] = p[i];
     }
     h.resize(k - 1);
-    if (h.size() == 2) {  // all points collinear: the two ends, smallest (x, y) first
-        if (before(h[1], h[0])) std::swap(h[0], h[1]);
-        return h;
-    }
-    std::reverse(h.begin(), h.end());
-    size_t first = 0;
-    for (size_t i = 1; i < h.size(); i++)
-        if (before(h[i], h[first])) first = i;
-    std::rotate(h.begin(), h.begin() + long(first), h.end());
-    return h;
 }
 
-// Minimum-area enclosing rectangle of a convex polygon: the best of the rectangles with a side
-// on one of its edges (rotating calipers). The up axis is the rectangle axis pointing most
-// towards -y, so near-horizontal boxes come out upright.
-RRect min_area_rect(const std::vector<Pt> &h) {
-    RRect best;
-    if (h.empty()) return best;
-    if (h.size() == 1) {
-        best.cx = h[0].x, best.cy = h[0].y, best.w = best.h = 0;
-        return best;
-    }
-    float best_area = INFINITY;
-    for (size_t i = 0; i < h.size(); i++) {
-        const Pt &a = h[i], &b = h[(i + 1) % h.size()];
-        float ex = b.x - a.x, ey = b.y - a.y, len = std::sqrt(ex * ex + ey * ey);
-        if (len == 0) continue;
+// min_area_rect: of the rectangles with a side on an edge of the convex hull (edges in hull
+// order), the first of the smallest area, then turned by a multiple of 90 degrees so its up axis
+// points most towards -y (the last of equally good turns: up, +90, +180, +270). False when the
+// points hold fewer than two distinct positions.
+bool min_area_rect(const std::vector<Pt> &pts, std::vector<Pt> &hull, RRect &out) {
+    convex_hull(pts, hull);
+    const size_t m = hull.size();
+    bool found = false;
+    float best = INFINITY;
+    for (size_t i = 0; i < m && m >= 2; i++) {
+        const float ax = hull[i].x, ay = hull[i].y, bx = hull[(i + 1) % m].x, by = hull[(i + 1) % m].y;
+        float ex = bx - ax, ey = by - ay;
+        const float len = std::sqrt(ex * ex + ey * ey);
+        if (len == 0.f) continue;
         ex /= len, ey /= len;
-        const float nx = -ey, ny = ex;
-        float e0 = INFINITY, e1 = -INFINITY, n0 = INFINITY, n1 = -INFINITY;
-        for (const Pt &p : h) {
-            const float pe = p.x * ex + p.y * ey, pn = p.x * nx + p.y * ny;
-            e0 = std::min(e0, pe), e1 = std::max(e1, pe), n0 = std::min(n0, pn), n1 = std::max(n1, pn);
+        const float nx = -ey, ny = ex;  // into the hull
+        float pmin = INFINITY, pmax = -INFINITY, qmax = -INFINITY;
+        for (size_t k = 0; k < m; k++) {
+            const float dx = hull[k].x - ax, dy = hull[k].y - ay;
+            const float par = dx * ex + dy * ey, perp = dx * nx + dy * ny;
+            if (par < pmin) pmin = par;
+            if (par > pmax) pmax = par;
+            if (perp > qmax) qmax = perp;
         }
-        const float area = (e1 - e0) * (n1 - n0);
-        if (area < best_area) {
-            best_area = area;
-            const float me = (e0 + e1) / 2, mn = (n0 + n1) / 2;
-            RRect r;
-            r.cx = ex * me + nx * mn, r.cy = ey * me + ny * mn;
-            // Candidate up axes: +-e (height = e extent) and +-n (height = n extent).
-            const float cand[4][3] = {{ex, ey, e1 - e0}, {-ex, -ey, e1 - e0}, {nx, ny, n1 - n0}, {-nx, -ny, n1 - n0}};
-            int k = 0;
-            for (int c = 1; c < 4; c++)
-                if (cand[c][1] < cand[k][1] - 1e-6f) k = c;
-            r.ux = cand[k][0], r.uy = cand[k][1], r.h = cand[k][2];
-            r.w = (k < 2) ? (n1 - n0) : (e1 - e0);
-            best = r;
+        const float width = pmax - pmin, height = qmax, area = width * height;
+        if (area < best) {
+            best = area;
+            found = true;
+            const float mid = (pmin + pmax) / 2.f, half = height / 2.f;
+            out.cx = ax + ex * mid + nx * half;
+            out.cy = ay + ey * mid + ny * half;
+            out.ux = nx, out.uy = ny, out.w = width, out.h = height;
         }
     }
-    return best;
+    if (!found) return false;
+    const float ux = out.ux, uy = out.uy, w = out.w, h = out.h;
+    const float cand[4][2] = {{ux, uy}, {uy, -ux}, {-ux, -uy}, {-uy, ux}};
+    int k = 0;
+    for (int c = 1; c < 4; c++)
+        if (-cand[c][1] >= -cand[k][1]) k = c;
+    out.ux = cand[k][0], out.uy = cand[k][1];
+    out.w = (k & 1) ? h : w;
+    out.h = (k & 1) ? w : h;
+    return true;
 }
 
 struct Run {
@@ -138,9 +300,9 @@ int find(std::vector<int> &parent, int a) {
 namespace {
 
 // The 8-connected components of rows [y0, y1) of a bit mask (ceil(w / 32) words a row), each as
-// its rows' leftmost and rightmost pixels, rows ascending (all the convex hull needs; see
-// hull_rows), in order of their first run; and the runs of the first and last rows with their
-// components, for joining neighbouring bands.
+// its rows' leftmost and rightmost pixels, rows ascending (its first pixel and bounding box), in
+// order of their first run; and the runs of the first and last rows with their components, for
+// joining neighbouring bands.
 struct BandComps {
     std::vector<std::vector<Pt>> pts;
     std::vector<Run> first, last;
@@ -342,58 +504,144 @@ static std::vector<std::vector<Pt>> component_points(const uint32_t *bits, int w
     return out;
 }
 
-// Each component's minimum-area rectangle, grown by expand on every side; those of at least
-// min_area, in component order.
-static std::vector<RRect> rects_of(const std::vector<std::vector<Pt>> &comps, float expand, float min_area,
-                                   int threads) {
-    std::vector<RRect> rects(comps.size());
-    parallel_for(int(comps.size()), threads, [&](int i) {
-        rects[size_t(i)] = min_area_rect(hull_rows(comps[size_t(i)]));
-        rects[size_t(i)].resize(rects[size_t(i)].w + 2 * expand, rects[size_t(i)].h + 2 * expand);
+namespace {
+
+// A component to trace: its raster-first pixel (the leftmost of its top row) and bounding box.
+struct Seed {
+    int fx, fy, x0, y0, x1, y1;
+};
+
+Seed seed_of_rows(const std::vector<Pt> &v) {
+    Seed s{int(v[0].x), int(v[0].y), int(v[0].x), int(v[0].y), int(v[0].x), int(v[0].y)};
+    for (const Pt &p : v) {
+        s.x0 = std::min(s.x0, int(p.x)), s.x1 = std::max(s.x1, int(p.x));
+        s.y0 = std::min(s.y0, int(p.y)), s.y1 = std::max(s.y1, int(p.y));
+    }
+    return s;
+}
+
+// Whether the outer border xy (a closed chain of 8-neighbours) winds around the pixel (qx, qy) an
+// odd number of times: the chain's steps across rows qy..qy+1 whose end on row qy lies left of qx.
+bool encloses(const std::vector<int32_t> &xy, int qx, int qy) {
+    const size_t n = xy.size() / 2;
+    bool odd = false;
+    for (size_t k = 0; k < n; k++) {
+        const size_t j = k + 1 == n ? 0 : k + 1;
+        const int ay = xy[2 * k + 1], by = xy[2 * j + 1];
+        if ((ay > qy) != (by > qy)) {
+            const int x = ay <= qy ? xy[2 * k] : xy[2 * j];
+            if (x < qx) odd = !odd;
+        }
+    }
+    return odd;
+}
+
+// The rectangles of the external components (ocr-bench.rs:47-55: find_contours External,
+// simplify_polygon(2), min_area_rect), given every 8-connected component of the mask by its seed
+// in raster order of first pixels; ok[i] is false for a component inside a hole of another one
+// and for one without a rectangle (a single pixel).
+//
+// A component is external when the background pixel west of its first pixel belongs to the
+// background reaching the frame. That pixel lies in a hole of some component exactly when an
+// outer border winds around it (a 4-connected background path cannot cross an outer border
+// through 8-neighbouring pixel centres), and the component whose hole it is spans it strictly in
+// both axes and comes earlier in raster order: only those are tested.
+void external_rects(const uint32_t *bits, int w, int h, const std::vector<Seed> &seeds, int threads,
+                    std::vector<RRect> &rects, std::vector<char> &ok) {
+    PaddedMask m;  // read by the worker threads too
+    m.build(bits, w, h);
+    const int n = int(seeds.size());
+    std::vector<std::vector<int32_t>> chains(static_cast<size_t>(n));
+    parallel_for(n, threads, [&](int i) { trace_outer(m, seeds[size_t(i)].fx, seeds[size_t(i)].fy, chains[size_t(i)]); });
+    ok.assign(size_t(n), 1);
+    std::vector<int> active;  // earlier components whose rows reach below the current row
+    for (int i = 0; i < n; i++) {
+        const Seed &c = seeds[size_t(i)];
+        const int qx = c.fx - 1, qy = c.fy;
+        size_t keep = 0;
+        for (int j : active)
+            if (seeds[size_t(j)].y1 > qy) active[keep++] = j;
+        active.resize(keep);
+        if (qx >= 0)
+            for (int j : active) {
+                const Seed &d = seeds[size_t(j)];
+                if (d.y0 < qy && d.x0 < qx && qx < d.x1 && encloses(chains[size_t(j)], qx, qy)) {
+                    ok[size_t(i)] = 0;
+                    break;
+                }
+            }
+        active.push_back(i);
+    }
+    rects.assign(size_t(n), RRect{});
+    parallel_for(n, threads, [&](int i) {
+        if (!ok[size_t(i)]) return;
+        thread_local std::vector<Pt> simp, hull;
+        thread_local SimplifyScratch scratch;
+        simplify_closed(chains[size_t(i)], 2.f, simp, scratch);
+        if (!min_area_rect(simp, hull, rects[size_t(i)])) ok[size_t(i)] = 0;
     });
+}
+
+std::vector<RRect> grown_rects(const uint32_t *bits, int w, int h, const std::vector<Seed> &seeds, float expand,
+                               float min_area, int threads) {
+    std::vector<RRect> rects;
+    std::vector<char> ok;
+    external_rects(bits, w, h, seeds, threads, rects, ok);
     std::vector<RRect> out;
-    for (const RRect &r : rects)
+    for (size_t i = 0; i < rects.size(); i++) {
+        if (!ok[i]) continue;
+        RRect r = rects[i];
+        r.resize(r.w + 2 * expand, r.h + 2 * expand);
         if (r.area() >= min_area) out.push_back(r);
+    }
     return out;
 }
 
+}  // namespace
+
 std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand, float min_area, int threads) {
-    return rects_of(component_points(bits, w, h, threads), expand, min_area, threads);
+    const auto comps = component_points(bits, w, h, threads);
+    std::vector<Seed> seeds;
+    seeds.reserve(comps.size());
+    for (const auto &v : comps) seeds.push_back(seed_of_rows(v));
+    return grown_rects(bits, w, h, seeds, expand, min_area, threads);
 }
 
-std::vector<RRect> word_rects_from_rows(const int32_t *comps, int ncomps, const uint32_t *xmin, const uint32_t *xmax,
-                                        int nslots, float expand, float min_area, int threads) {
-    // Components in order of first run: the order band_components lists them in.
+std::vector<RRect> word_rects_from_rows(const uint32_t *bits, int w, int h, const int32_t *comps, int ncomps,
+                                        const uint32_t *xmin, const uint32_t *xmax, int nslots, float expand,
+                                        float min_area, int threads) {
+    // Components in order of first run (row-major): the order of their first pixels.
     std::vector<int> order(size_t(std::max(ncomps, 0)));
     for (int c = 0; c < ncomps; c++) order[size_t(c)] = c;
     std::sort(order.begin(), order.end(), [&](int a, int b) { return comps[4 * a] < comps[4 * b]; });
-    std::vector<std::vector<Pt>> pts(order.size());
+    std::vector<Seed> seeds(order.size());
     for (size_t k = 0; k < order.size(); k++) {
         const int32_t *rec = comps + 4 * order[k];
         const int top = rec[1], rows = rec[2], b = rec[3];
-        if (rows < 1 || b < 0 || b + rows > nslots) fail("word_rects_from_rows: a component's row slots");
-        auto &v = pts[k];
-        v.reserve(size_t(rows) * 2);
+        if (rows < 1 || b < 0 || b + rows > nslots || top < 0 || top + rows > h)
+            fail("word_rects_from_rows: a component's row slots");
+        Seed &s = seeds[k];
+        s.fx = int(xmin[b]), s.fy = top, s.y0 = top, s.y1 = top + rows - 1;
+        s.x0 = INT32_MAX, s.x1 = -1;
         for (int r = 0; r < rows; r++) {
             const uint32_t x0 = xmin[b + r], x1 = xmax[b + r];
-            if (x0 > x1) fail("word_rects_from_rows: a component row without pixels");
-            const float fy = float(top + r);
-            v.push_back({float(x0), fy});
-            if (x1 != x0) v.push_back({float(x1), fy});
+            if (x0 > x1 || x1 >= uint32_t(w)) fail("word_rects_from_rows: a component row without pixels");
+            s.x0 = std::min(s.x0, int(x0)), s.x1 = std::max(s.x1, int(x1));
         }
     }
-    return rects_of(pts, expand, min_area, threads);
+    return grown_rects(bits, w, h, seeds, expand, min_area, threads);
 }
 
-// ppdet.rs:65-85: the mean probability of the map's pixels whose position lies inside r (its
-// height along the up axis, its width across it), scanning r's bounding box.
+// ppdet.rs:65-85: the mean probability (an f32 sum in row-major order) of the map's pixels whose
+// position lies inside r (its height along the up axis, its width across it), scanning r's
+// bounding box.
 static float db_score(const float *prob, int w, int h, const RRect &r) {
     float l, t, rr, b;
     r.bbox(l, t, rr, b);
     const int x0 = int(std::max(std::floor(l), 0.f)), y0 = int(std::max(std::floor(t), 0.f));
-    const int x1 = std::min(int(std::ceil(rr)), w - 1), y1 = std::min(int(std::ceil(b)), h - 1);
+    const int x1 = std::min(std::max(int(std::ceil(rr)), 0), w - 1), y1 = std::min(std::max(int(std::ceil(b)), 0), h - 1);
     const float hw = r.w / 2, hh = r.h / 2;
-    double sum = 0;
+    float sum = 0;
     long n = 0;
     for (int y = y0; y <= y1; y++)
         for (int x = x0; x <= x1; x++) {
@@ -404,14 +652,22 @@ static float db_score(const float *prob, int w, int h, const RRect &r) {
                 n++;
             }
         }
-    return n ? float(sum / double(n)) : 0.f;
+    return n ? sum / float(n) : 0.f;
 }
 
 std::vector<RRect> db_boxes(const uint32_t *bits, const float *prob, int w, int h, float to_page_x, float to_page_y,
                             const DbParams &db) {
+    const auto comps = component_points(bits, w, h);
+    std::vector<Seed> seeds;
+    seeds.reserve(comps.size());
+    for (const auto &v : comps) seeds.push_back(seed_of_rows(v));
+    std::vector<RRect> rects;
+    std::vector<char> ok;
+    external_rects(bits, w, h, seeds, 1, rects, ok);
     std::vector<RRect> out;
-    for (auto &v : component_points(bits, w, h)) {
-        const RRect r = min_area_rect(hull_rows(v));
+    for (size_t i = 0; i < rects.size(); i++) {
+        if (!ok[i]) continue;
+        const RRect &r = rects[i];
         if (std::min(r.w, r.h) < db.min_size || db_score(prob, w, h, r) < db.box_thresh) continue;
         // Unclip: grown by area * ratio / perimeter on every side (ppdet.rs:104-109).
         const float d = r.w * r.h * db.unclip_ratio / std::max(2.f * (r.w + r.h), 1e-6f);

@@ -27,18 +27,23 @@ struct RRect {
 // pool: lower runs first.
 void set_loop_priority(int prio);
 
-// word_rects (ocr-bench.rs:40-60): 8-connected components of the mask (h rows of ceil(w/32)
-// words), each component's minimum-area rectangle over its pixels, grown by `expand` on every
-// side, kept when its area is at least min_area; on `threads` threads (the same result).
+// word_rects (ocr-bench.rs:40-60): the external 8-connected components of the mask (h rows of
+// ceil(w/32) words; components inside a hole of another one are left out, as
+// find_contours(RetrievalMode::External) does), each one's outer border (Suzuki-Abe border
+// following) simplified by Douglas-Peucker with epsilon 2, its minimum-area rectangle grown by
+// `expand` on every side, kept when its area is at least min_area; in raster order of the
+// components' first pixels; on `threads` threads (the same result).
 std::vector<RRect> word_rects(const uint32_t *bits, int w, int h, float expand = 3.f, float min_area = 100.f,
                               int threads = 1);
 
 // The same rectangles from the mask's components as labelled on the GPU (kernels/ccl.hip):
 // comps holds ncomps records {first run, top row, rows, first slot} in any order, and row slot
 // i (of nslots) a component's leftmost and rightmost pixel xmin[i] .. xmax[i] in one row, its
-// rows' slots consecutive from the top. Components are listed in order of first run (row-major).
-std::vector<RRect> word_rects_from_rows(const int32_t *comps, int ncomps, const uint32_t *xmin, const uint32_t *xmax,
-                                        int nslots, float expand = 3.f, float min_area = 100.f, int threads = 1);
+// rows' slots consecutive from the top. The borders are traced in the mask bits from each
+// component's first pixel (the leftmost of its top row).
+std::vector<RRect> word_rects_from_rows(const uint32_t *bits, int w, int h, const int32_t *comps, int ncomps,
+                                        const uint32_t *xmin, const uint32_t *xmax, int nslots, float expand = 3.f,
+                                        float min_area = 100.f, int threads = 1);
 
 // Text lines from words, left to right within a line, lines top to bottom (the role of ocrs'
 // find_text_lines, ocr-bench.rs:516).
@@ -76,11 +81,10 @@ struct DbParams {
 };
 
 // ppdet::boxes (ppdet.rs:87-132) from the thresholded map (bits) and the map itself (prob, for
-// the box scores), both w x h: each 8-connected component's minimum-area rectangle, kept when
-// its shorter side is at least min_size and its mean probability at least box_thresh, grown by
-// the DB unclip offset, scaled to the page and put in reading order. The reference simplifies
-// each contour (Douglas-Peucker, 2 px) before its rectangle; here the rectangle encloses the
-// component's convex hull.
+// the box scores), both w x h: each external component's rectangle as word_rects finds it (outer
+// border, Douglas-Peucker with epsilon 2, minimum-area rectangle), kept when its shorter side is
+// at least min_size and its mean probability (an f32 sum) at least box_thresh, grown by the DB
+// unclip offset, scaled to the page and put in reading order.
 std::vector<RRect> db_boxes(const uint32_t *bits, const float *prob, int w, int h, float to_page_x, float to_page_y,
                             const DbParams &db = DbParams{});
 

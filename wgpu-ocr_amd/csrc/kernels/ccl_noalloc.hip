@@ -112,7 +112,7 @@ std::vector<RRect> word_rects_gpu_noalloc(Ctx &c, const uint32_t *bits, int w, i
         OCR_HIP(hipMemcpyAsync(xmax.data(), pg.xmax, ns * 4, hipMemcpyDeviceToHost, st));
         OCR_HIP(hipStreamSynchronize(st));
     }
-    return word_rects_from_rows(comps.data(), int(nc), xmin.data(), xmax.data(), int(ns));
+    return word_rects_from_rows(bits, w, h, comps.data(), int(nc), xmin.data(), xmax.data(), int(ns));
 }
 
 }  // namespace ocr

@@ -37,8 +37,8 @@ PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float rel
     set_loop_priority(page_prio);
     PageLayout L;
     std::vector<RRect> words =
-        rows ? word_rects_from_rows(rows->comps, rows->ncomps, rows->xmin, rows->xmax, rows->nslots, 3.f, 100.f,
-                                    threads)
+        rows ? word_rects_from_rows(bits, w, h, rows->comps, rows->ncomps, rows->xmin, rows->xmax, rows->nslots, 3.f,
+                                    100.f, threads)
              : word_rects(bits, w, h, 3.f, 100.f, threads);
     L.words = int(words.size());
     auto lines = find_text_lines(words);
