@@ -195,6 +195,9 @@ def nd_cases():
         y = np.zeros((3, 48, wb), np.float32)
         y[:, :, :out_w] = (q / 255.0 - 0.5) / 0.5
         c[name] = dict(rgb=page, line=np.array([left, top, cw, ch, out_w]), wb=np.array(wb), y=y)
+    # torch's hardsigmoid is ONNX HardSigmoid with alpha 1/6, beta 0.5 (ONNX's defaults are 0.2, 0.5)
+    x = np.concatenate([f32(200, scale=3.0), np.array([-3.0, 3.0, 0.0, -6.0, 6.0], np.float32)])
+    c["hardsigmoid"] = dict(x=x, y=F.hardsigmoid(t(x)).numpy())
     return c
 
 

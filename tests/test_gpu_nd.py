@@ -107,6 +107,18 @@ def test_se_gate_gelu_residual(ctx, tmp_path):
     check(ctx, p, RNG.standard_normal((2, 32, 3, 17)).astype(np.float32))
 
 
+def test_hardsigmoid_non_default_attributes(ctx, tmp_path):
+    # The SE gate with torch's hardsigmoid constants (alpha 1/6) and a standalone HardSigmoid with
+    # alpha 0.3, beta 0.4: the attributes, not ONNX's defaults, reach the kernels.
+    def fn(g, x):
+        se = g.add("GlobalAveragePool", [x])
+        se = g.add("HardSigmoid", [conv(g, se, 32, 32, k=1)], alpha=1.0 / 6.0, beta=0.5)
+        y = conv(g, g.add("Mul", [x, se]), 32, 32, k=1)
+        return g.add("HardSigmoid", [y], alpha=0.3, beta=0.4)
+    p = build(tmp_path, "hsig", fn, (2, 32, 3, 17))
+    check(ctx, p, (3 * RNG.standard_normal((2, 32, 3, 17))).astype(np.float32))
+
+
 def test_linear_silu_and_inexact_weights(ctx, tmp_path):
     def fn(g, x):
         y = g.add("MatMul", [x, w(g, (120, 240), 120)])

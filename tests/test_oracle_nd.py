@@ -75,6 +75,16 @@ def test_gelu_chain_and_silu():
     np.testing.assert_allclose(y, s["y"], rtol=1e-6, atol=1e-6)
 
 
+def test_hardsigmoid_attributes():
+    # F.hardsigmoid is HardSigmoid with alpha 1/6 and beta 0.5: the node's attributes, not ONNX's
+    # defaults (0.2, 0.5), must reach the arithmetic.
+    c = nd("hardsigmoid")
+    m = model([N("HardSigmoid", ["x"], ["y"], {"alpha": 1.0 / 6.0, "beta": 0.5})])
+    y, _ = graph.run(m, c["x"])
+    np.testing.assert_allclose(y, c["y"], rtol=1e-6, atol=1e-7)
+    assert c["y"].min() == 0 and c["y"].max() == 1  # both clamps reached
+
+
 def test_resize_nearest_x2():
     c = nd("resize2")
     m = model([N("Resize", ["x", "", "sc"], ["y"], {"mode": "nearest", "coordinate_transformation_mode": "asymmetric",

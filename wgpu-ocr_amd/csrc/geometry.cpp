@@ -628,6 +628,12 @@ std::vector<RRect> word_rects_from_rows(const uint32_t *bits, int w, int h, cons
             if (x0 > x1 || x1 >= uint32_t(w)) fail("word_rects_from_rows: a component row without pixels");
             s.x0 = std::min(s.x0, int(x0)), s.x1 = std::max(s.x1, int(x1));
         }
+        // The border following starts at a set pixel whose west neighbour is clear (a walk from
+        // anywhere else need not come back to its start).
+        const int words = (w + 31) / 32;
+        auto bit = [&](int x, int y) { return (bits[size_t(y) * size_t(words) + size_t(x >> 5)] >> (x & 31)) & 1u; };
+        if (!bit(s.fx, s.fy) || (s.fx > 0 && bit(s.fx - 1, s.fy)))
+            fail("word_rects_from_rows: a component's first pixel is not the start of a run");
     }
     return grown_rects(bits, w, h, seeds, expand, min_area, threads);
 }
