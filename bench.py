@@ -10,8 +10,10 @@ the ocrs architecture; data are synthetic.
 
 Prints one JSON line: value = pages/s over K timed steps (PCIe included), plus the same with the
 pages already resident in HBM and with the pages in page-locked host memory, recognition lines/s,
-the dominant kernel's roofline (HIP events on the kernel's own stream over the timed region), and
-a CPU baseline (the oracle: a C / numpy restatement of the same path, on a bounded sample).
+the dominant kernel's roofline (HIP events on the kernel's own stream over the timed region), the
+per-configuration figures (36-line recognition, the 800 x 600 detector, PP-OCR recognition), and
+a CPU baseline on a bounded sample: the same page loop with the graphs on torch-CPU (the stand-in
+for the reference's rten path), and the oracle's C restatement beside it.
 """
 import argparse
 import json
@@ -48,8 +50,14 @@ def roofline(kernels):
         achieved = k["bytes"] / secs / 1e9
         out = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                "frac": achieved / HBM_PEAK_GBS}
-    out.update({"kernel": fam, "calls": k["calls"], "avg_us": 1e3 * k["ms"] / max(k["calls"], 1),
-                "traffic": measured_traffic(fam)})
+    calls = max(k["calls"], 1)
+    out.update({"kernel": fam, "calls": k["calls"], "avg_us": 1e3 * k["ms"] / calls,
+                "traffic": measured_traffic(fam),
+                "algorithmic_bytes_per_launch": k["bytes"] / calls, "algorithmic_flops_per_launch": k["flops"] / calls,
+                # both views of the same launches: algorithmic bytes over HBM peak, algorithmic FLOPs
+                # over the dense f16 matrix-core peak
+                "frac_hbm": k["bytes"] / secs / (HBM_PEAK_GBS * 1e9),
+                "frac_mfma_f16": k["flops"] / secs / (F16_PEAK_TFLOPS * 1e12)})
     return out
 
 
@@ -105,6 +113,32 @@ def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
                       f"(oracle: C restatement with OpenMP, float32)"}
 
 
+def cpu_baseline_torch(det_path, rec_path, pages, min_secs=10.0):
+    """The same page loop with the detection and recognition graphs on torch-CPU (one library
+    call per ONNX node, float32, torch's threads on all host cores): the stand-in for the
+    reference's rten CPU path, which cannot run here. Grey resize, mask, layout, line crops and
+    CTC are the oracle's. One untimed warm-up page, then pages until min_secs have passed."""
+    import torch
+    from oracle import layout as ol
+    from oracle import onnx_read
+    from oracle import torch_cpu
+
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    det = torch_cpu.TorchGraph(onnx_read.load(det_path))
+    rec = torch_cpu.TorchGraph(onnx_read.load(rec_path))
+    torch_cpu.page_pipeline(det, rec, pages[0], 0.5, ol.Layout)
+    n, t = 0, time.perf_counter()
+    while time.perf_counter() - t < min_secs and n < 4 * len(pages):
+        torch_cpu.page_pipeline(det, rec, pages[n % len(pages)], 0.5, ol.Layout)
+        n += 1
+    secs = time.perf_counter() - t
+    return {"value": n / secs, "unit": "pages/s", "cores": cores, "kind": "port",
+            "sample": f"{n} of the synthetic 2550x3300 pages, whole pipeline page by page, {secs:.1f} s "
+                      f"(torch {torch.__version__} CPU for the detection and recognition graphs, float32; "
+                      f"the stand-in for rten)"}
+
+
 def pp_pipeline(ctx, d_pages, ws, hs, merge, steps=2):
     """The PP-OCR whole-page pipeline on the same resident pages (DB detector at long side 960,
     threshold 0.3, host boxes, SVTR recogniser with the 18 708-class head): a supplementary
@@ -130,6 +164,90 @@ def pp_pipeline(ctx, d_pages, ws, hs, merge, steps=2):
             "rec_lines_per_sec": lines / secs, "steps": steps}
 
 
+def _probed(families, fn):
+    """Runs fn once with every family probed; returns {family: probe} for those that ran."""
+    import ocrhip
+    for f in families:
+        ocrhip.probe_start(f)
+    fn()
+    out = {f: ocrhip.probe_stop(f) for f in families}
+    return {f: k for f, k in out.items() if k["calls"]}
+
+
+def _timed(ctx, fn, reps, warmup=3):
+    for _ in range(warmup):
+        fn()
+    ctx.synchronize()
+    t = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    ctx.synchronize()
+    return (time.perf_counter() - t) / reps
+
+
+def _kernel_summary(kernels, units):
+    """Per-family ms per unit, the dominant family, and its roofline (algorithmic work over its
+    summed launch time)."""
+    top = max(kernels, key=lambda f: kernels[f]["ms"])
+    return {"kernels_ms": {f: round(k["ms"] / units, 4) for f, k in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])},
+            "dominant": roofline({top: kernels[top]})}
+
+
+def config_figures(ctx, det, rec, reps=20):
+    """The per-configuration figures (the reference reports them per stage: src/bin/stages.rs,
+    ppocr-bench.rs): inputs resident in device memory where the entry point takes them."""
+    import ocrhip
+    from ocrhip import synth, synth_pp
+    out = {}
+    # 36 grey line images, height 64, widths uniform in [200, 800] (ocrs batching: width rounded
+    # up to 50, at most 20 a batch): the CNN trunk, 2 x BiGRU(256), projection, arg-max.
+    lines = synth.rec_lines(36, seed=0, wmin=200, wmax=800)
+    batches, _, _ = synth.batch_lines(lines)
+    dev = []
+    for data, n, w in batches:
+        b = ctx.alloc(data.nbytes)
+        b.upload(np.ascontiguousarray(data))
+        dev.append((b, n, w))
+    tmax, ntot, _ = rec.dims(dev)
+    d_best = ctx.alloc(tmax * ntot * 4)
+    secs = _timed(ctx, lambda: rec.recognize_device(dev, d_best=d_best), reps)
+    kern = _probed(ocrhip.FAMILIES, lambda: (rec.recognize_device(dev, d_best=d_best), ctx.synchronize()))
+    gru = kern.get("gru", {"ms": 0.0, "calls": 0})
+    out["rec_36_lines"] = {
+        "workload": "36 grey lines 64 x [200, 800], ocrs batching, CNN trunk + 2 x BiGRU(256) + 97-class head",
+        "ms_per_batch": 1e3 * secs, "lines_per_sec": 36 / secs, "gru_steps": 2 * tmax,
+        "us_per_gru_step": 1e3 * gru["ms"] / max(gru["calls"] * tmax, 1),
+        "gflop_per_batch": sum(k["flops"] for k in kern.values()) / 1e9, **_kernel_summary(kern, 1)}
+    # The detection U-Net on one [1, 1, 800, 600] grey image (host in, probabilities out).
+    img = synth.det_input(0)
+    secs = _timed(ctx, lambda: det.detect(img), reps)
+    kern = _probed(ocrhip.FAMILIES, lambda: det.detect(img))
+    out["det_800x600"] = {"workload": "ocrs-architecture U-Net 16-256 on [1, 1, 800, 600] (host in and out)",
+                          "ms_per_page": 1e3 * secs, "gflop_per_page": sum(k["flops"] for k in kern.values()) / 1e9,
+                          **_kernel_summary(kern, 1)}
+    # PP-OCRv6-architecture recognition: 36 RGB lines 3 x 48 x [160, 960], 16 a batch, SVTR neck,
+    # 18 708-class CTC head (arg-max fused: the logits are never written).
+    prec = ocrhip.NdGraph(ctx, synth_pp.model_path("rec"), stop_before_softmax=True)
+    pb, _ = synth_pp.batch_lines(synth_pp.rec_lines(36, seed=0))
+    pdev = []
+    for data, n, w in pb:
+        b = ctx.alloc(data.nbytes)
+        b.upload(np.ascontiguousarray(data))
+        bb = ctx.alloc(int(np.prod(prec.dims(data.shape)[:-1])) * 4)
+        pdev.append((b, data.shape, bb))
+
+    def pp_rec():
+        for b, shape, bb in pdev:
+            prec.argmax_device(b, shape, bb)
+    secs = _timed(ctx, pp_rec, reps)
+    kern = _probed(ocrhip.ND_FAMILIES, lambda: (pp_rec(), ctx.synchronize()))
+    out["pp_rec_36_lines"] = {"workload": "PP-OCRv6-architecture rec, 36 RGB lines 3 x 48 x [160, 960], 16 a batch",
+                              "ms_per_batch": 1e3 * secs, "lines_per_sec": 36 / secs,
+                              "gflop_per_batch": sum(k["flops"] for k in kern.values()) / 1e9,
+                              **_kernel_summary(kern, 1)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -140,6 +258,7 @@ def main():
     ap.add_argument("--det-batch", type=int, default=2, help="pages per detection pass")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-pp", action="store_true", help="skip the PP-OCR pipeline measurement")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration figures")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device to device (the reference for traffic counters)")
     args = ap.parse_args()
@@ -262,8 +381,11 @@ def main():
     }
     if not args.no_pp:
         out["pp_pipeline"] = pp_pipeline(ctx, d_pages, ws, hs, args.merge)
+    if not args.no_configs:
+        out["configs"] = config_figures(ctx, det, rec)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(det_path, rec_path, pages)
+        out["cpu_baseline"] = cpu_baseline_torch(det_path, rec_path, pages)
+        out["cpu_oracle"] = cpu_baseline(det_path, rec_path, pages)
     print(json.dumps(out))
 
 

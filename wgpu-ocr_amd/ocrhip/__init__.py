@@ -332,6 +332,12 @@ class NdGraph:
         _check(lib().ocr_nd_argmax(self.handle, _ptr(x), _ptr(s), len(s), _ptr(best)))
         return best
 
+    def argmax_device(self, d_x: "DeviceBuffer", shape, d_best: "DeviceBuffer"):
+        """argmax with input and output in device memory, queued on the context's stream."""
+        s = np.asarray(shape, np.int64)
+        _check(lib().ocr_nd_argmax_device(self.handle, ctypes.c_void_p(d_x.ptr), _ptr(s), len(s),
+                                          ctypes.c_void_p(d_best.ptr)))
+
     def __del__(self):
         try:
             if self.handle:
@@ -423,7 +429,7 @@ class Recognizer:
 
 
 FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_narrow", "conv_igemm", "conv_mfma", "gru", "conv_transpose", "conv_direct", "conv_generic", "maxpool", "mask_up",
-            "grey_resize", "line_crop", "avgpool_t", "argmax", "copy")
+            "grey_resize", "line_crop", "avgpool_t", "argmax", "copy", "ccl")
 ND_FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_narrow", "conv_igemm", "conv_mfma", "nd_bgemm", "nd_conv_generic", "nd_conv_transpose", "nd_elementwise", "nd_copy",
                "nd_reduce", "nd_layer_norm", "nd_softmax", "nd_argmax", "nd_pool", "nd_resize", "nd_det_prep",
                "nd_threshold")
