@@ -60,8 +60,57 @@ int ocr_memcpy_d2h(ocr_ctx *ctx, void *dst, const void *src, size_t bytes);
 void *ocr_host_alloc(ocr_ctx *ctx, size_t bytes);
 int ocr_host_free(ocr_ctx *ctx, void *p);
 
+/* ---- A graph parsed on the host ---------------------------------------------------------------
+ * The reference parses the .onnx file on its own side (Onnx::load, src/onnx.rs:88-123) and hands
+ * the parsed Onnx to the constructors (Detector::new(&Gpu, &Onnx), src/gpu.rs:1385). These
+ * structs carry the same content (src/onnx.rs:8-56): nodes with their attributes (Constant nodes
+ * already turned into weights or integer lists), float weights, int64 constants, the input and
+ * output names. Everything is copied during the constructor call; the caller's memory may be
+ * released afterwards. */
+typedef struct ocr_onnx_attr {
+    const char *name;
+    int32_t type;     /* ONNX AttributeProto type: 1 FLOAT, 2 INT, 3 STRING, 6 FLOATS, 7 INTS */
+    float f;          /* FLOAT */
+    int64_t i;        /* INT */
+    const char *s;    /* STRING (NUL-terminated) */
+    const float *floats;  /* FLOATS */
+    const int64_t *ints;  /* INTS */
+    uint32_t count;       /* entries of floats or ints */
+} ocr_onnx_attr;
+
+typedef struct ocr_onnx_node {
+    const char *op;
+    const char *const *inputs;  /* "" for an omitted optional input */
+    uint32_t ninputs;
+    const char *const *outputs;
+    uint32_t noutputs;
+    const ocr_onnx_attr *attrs;
+    uint32_t nattrs;
+} ocr_onnx_node;
+
+/* One named tensor: float32 data (Onnx::weights) or int64 values (Onnx::ints), count entries. */
+typedef struct ocr_onnx_tensor {
+    const char *name;
+    const int64_t *dims;
+    uint32_t rank;
+    const float *data;   /* float32 weights, or NULL */
+    const int64_t *ints; /* int64 constants, or NULL */
+    uint64_t count;
+} ocr_onnx_tensor;
+
+typedef struct ocr_onnx {
+    const ocr_onnx_node *nodes;
+    uint32_t nnodes;
+    const ocr_onnx_tensor *tensors;
+    uint32_t ntensors;
+    const char *input;
+    const char *output;
+} ocr_onnx;
+
 /* Detector::new (src/gpu.rs:1385-1387) from an ONNX file (Onnx::load, src/onnx.rs:88-123). */
 ocr_detector *ocr_detector_new(ocr_ctx *ctx, const char *onnx_path);
+/* Detector::new(&Gpu, &Onnx) (src/gpu.rs:1385) from a graph the host has parsed. */
+ocr_detector *ocr_detector_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph);
 void ocr_detector_free(ocr_detector *det);
 
 /* Detector::detect_page (src/gpu.rs:1393-1422): rgb is h x w x 3 bytes (host); bits receives
@@ -82,6 +131,8 @@ int ocr_detect(ocr_detector *det, const float *input, uint32_t h, uint32_t w, fl
  * first node of type stop_op (NULL: the whole graph). The same operator contract as Detector. */
 typedef struct ocr_graph ocr_graph;
 ocr_graph *ocr_graph_new(ocr_ctx *ctx, const char *onnx_path, const char *stop_op);
+/* The same from a graph the host has parsed (Graph::build takes &Onnx, src/gpu.rs:1104). */
+ocr_graph *ocr_graph_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph, const char *stop_op);
 void ocr_graph_free(ocr_graph *g);
 /* Output shape [n, c, h, w] of the graph for an input of shape [n, c, h, w]. */
 int ocr_graph_dims(ocr_graph *g, uint32_t n, uint32_t c, uint32_t h, uint32_t w, uint32_t *out_nchw);
@@ -91,6 +142,8 @@ int ocr_graph_run(ocr_graph *g, const float *in, uint32_t n, uint32_t c, uint32_
 
 /* Recognizer::new (src/gpu.rs:1452-1506). lines as in ocr_opts. */
 ocr_recognizer *ocr_recognizer_new(ocr_ctx *ctx, const char *onnx_path, uint32_t lines);
+/* Recognizer::new(&Gpu, &Onnx, lines) (src/gpu.rs:1452) from a graph the host has parsed. */
+ocr_recognizer *ocr_recognizer_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph, uint32_t lines);
 void ocr_recognizer_free(ocr_recognizer *rec);
 
 /* One batch of n line images [n][64][w] (float, the ocrs input convention). */
@@ -226,6 +279,8 @@ typedef struct ocr_nd ocr_nd;
  * load-time fusions. stop_before_softmax: the run returns the logits a final Softmax would read
  * (the arg-max needs no Softmax). */
 ocr_nd *ocr_nd_new(ocr_ctx *ctx, const char *onnx_path, int stop_before_softmax);
+/* NdGraph::new(&Gpu, &Onnx, stop_before_softmax) (src/nd.rs:505) from a graph the host has parsed. */
+ocr_nd *ocr_nd_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph, int stop_before_softmax);
 void ocr_nd_free(ocr_nd *g);
 /* Output shape (rank <= 6) for an input shape, without running the graph. */
 int ocr_nd_dims(ocr_nd *g, const int64_t *in_shape, uint32_t rank, int64_t *out_shape, uint32_t *out_rank);

@@ -84,6 +84,76 @@ std::vector<Recognizer::Batch> to_batches(const ocr_batch *b, uint32_t count) {
 
 }  // namespace
 
+namespace {
+
+// The host-parsed graph of the C ABI as this library's Onnx (the reference's onnx.rs struct),
+// every string and array copied.
+Onnx onnx_of(const ocr_onnx *g) {
+    need(g, "graph");
+    auto str = [](const char *p, const char *what) -> std::string {
+        if (!p) fail(std::string("graph: missing ") + what);
+        return std::string(p);
+    };
+    Onnx m;
+    if (g->nnodes) need(g->nodes, "graph nodes");
+    if (g->ntensors) need(g->tensors, "graph tensors");
+    m.input = str(g->input, "input name");
+    m.output = str(g->output, "output name");
+    for (uint32_t k = 0; k < g->ntensors; k++) {
+        const ocr_onnx_tensor &t = g->tensors[k];
+        const std::string name = str(t.name, "tensor name");
+        if (t.rank && !t.dims) fail("graph: tensor " + name + " has a rank but no dims");
+        uint64_t n = 1;
+        std::vector<int64_t> dims(t.dims, t.dims + t.rank);
+        for (int64_t d : dims) {
+            if (d < 0) fail("graph: tensor " + name + " has a negative dimension");
+            n *= uint64_t(d);
+        }
+        if ((t.data != nullptr) == (t.ints != nullptr)) fail("graph: tensor " + name + " needs exactly one of data, ints");
+        if (t.data) {
+            if (n != t.count) fail("graph: tensor " + name + ": " + std::to_string(t.count) + " values for its dims");
+            m.weights[name] = Weight{dims, std::vector<float>(t.data, t.data + t.count)};
+        } else {
+            m.ints[name] = std::vector<int64_t>(t.ints, t.ints + t.count);
+        }
+    }
+    for (uint32_t k = 0; k < g->nnodes; k++) {
+        const ocr_onnx_node &cn = g->nodes[k];
+        Node n;
+        n.op = str(cn.op, "node op");
+        if (cn.ninputs) need(cn.inputs, "node inputs");
+        if (cn.noutputs) need(cn.outputs, "node outputs");
+        if (cn.nattrs) need(cn.attrs, "node attributes");
+        for (uint32_t i = 0; i < cn.ninputs; i++) n.inputs.push_back(cn.inputs[i] ? cn.inputs[i] : "");
+        for (uint32_t i = 0; i < cn.noutputs; i++) n.outputs.push_back(str(cn.outputs[i], "node output"));
+        for (uint32_t i = 0; i < cn.nattrs; i++) {
+            const ocr_onnx_attr &ca = cn.attrs[i];
+            Attr a;
+            a.name = str(ca.name, "attribute name");
+            a.type = ca.type;
+            switch (ca.type) {
+            case 1: a.f = ca.f, a.has_f = true; break;
+            case 2: a.i = ca.i, a.has_i = true; break;
+            case 3: a.s = str(ca.s, "string attribute"), a.has_s = true; break;
+            case 6:
+                if (ca.count) need(ca.floats, "float list attribute");
+                a.floats.assign(ca.floats, ca.floats + ca.count);
+                break;
+            case 7:
+                if (ca.count) need(ca.ints, "int list attribute");
+                a.ints.assign(ca.ints, ca.ints + ca.count);
+                break;
+            default: fail("graph: attribute " + a.name + " of unsupported type " + std::to_string(ca.type));
+            }
+            n.attrs.push_back(std::move(a));
+        }
+        m.nodes.push_back(std::move(n));
+    }
+    return m;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char *ocr_last_error(void) { return g_error.c_str(); }
@@ -164,6 +234,54 @@ int ocr_memcpy_d2h(ocr_ctx *ctx, void *dst, const void *src, size_t bytes) {
         need(ctx, "ctx");
         ctx->ctx->bind();
         ctx->ctx->d2h(dst, src, bytes);
+    });
+}
+
+ocr_detector *ocr_detector_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph) {
+    return guard_ptr<ocr_detector>([&] {
+        need(ctx, "ctx");
+        Onnx m = onnx_of(graph);
+        ctx->ctx->bind();
+        auto d = std::make_unique<ocr_detector>();
+        d->owner = ctx;
+        d->det = std::make_unique<Detector>(*ctx->ctx, m);
+        return d.release();
+    });
+}
+
+ocr_graph *ocr_graph_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph, const char *stop_op) {
+    return guard_ptr<ocr_graph>([&] {
+        need(ctx, "ctx");
+        Onnx m = onnx_of(graph);
+        ctx->ctx->bind();
+        auto g = std::make_unique<ocr_graph>();
+        g->owner = ctx;
+        g->graph = Graph::build(*ctx->ctx, m, stop_op, nullptr, nullptr);
+        return g.release();
+    });
+}
+
+ocr_recognizer *ocr_recognizer_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph, uint32_t lines) {
+    return guard_ptr<ocr_recognizer>([&] {
+        need(ctx, "ctx");
+        Onnx m = onnx_of(graph);
+        ctx->ctx->bind();
+        auto r = std::make_unique<ocr_recognizer>();
+        r->owner = ctx;
+        r->rec = std::make_unique<Recognizer>(*ctx->ctx, m, lines ? lines : 8);
+        return r.release();
+    });
+}
+
+ocr_nd *ocr_nd_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph, int stop_before_softmax) {
+    return guard_ptr<ocr_nd>([&] {
+        need(ctx, "ctx");
+        Onnx m = onnx_of(graph);
+        ctx->ctx->bind();
+        auto g = std::make_unique<ocr_nd>();
+        g->owner = ctx;
+        g->graph = NdGraph::build(*ctx->ctx, m, stop_before_softmax != 0);
+        return g.release();
     });
 }
 

@@ -60,6 +60,10 @@ SIGNATURES = {
     "ocr_recognize_device": (ctypes.c_int, [P, P, U32, P, P, P]),
     "ocr_probe_start": (ctypes.c_int, [ctypes.c_char_p]),
     "ocr_probe_stop": (ctypes.c_int, [ctypes.c_char_p, PU32, P, P, P]),
+    "ocr_detector_new_onnx": (P, [P, P]),
+    "ocr_graph_new_onnx": (P, [P, P, ctypes.c_char_p]),
+    "ocr_recognizer_new_onnx": (P, [P, P, U32]),
+    "ocr_nd_new_onnx": (P, [P, P, ctypes.c_int]),
     "ocr_word_rects": (ctypes.c_int, [P, U32, U32, P, U32, PU32]),
     "ocr_word_rects_mt": (ctypes.c_int, [P, U32, U32, U32, P, U32, PU32]),
     "ocr_word_rects_gpu": (ctypes.c_int, [P, P, U32, U32, P, U32, PU32]),
@@ -101,6 +105,93 @@ SIGNATURES = {
     "ocr_pp_line_images": (ctypes.c_int, [P, P, U32, U32, P, U32, U32, P]),
     "ocr_line_images": (ctypes.c_int, [P, P, U32, U32, P, U32, P, U32, P, U32, U32, P]),
 }
+
+
+class ocr_onnx_attr(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int32), ("f", ctypes.c_float), ("i", ctypes.c_int64),
+                ("s", ctypes.c_char_p), ("floats", ctypes.c_void_p), ("ints", ctypes.c_void_p), ("count", ctypes.c_uint32)]
+
+
+class ocr_onnx_node(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_char_p), ("inputs", ctypes.c_void_p), ("ninputs", ctypes.c_uint32),
+                ("outputs", ctypes.c_void_p), ("noutputs", ctypes.c_uint32), ("attrs", ctypes.c_void_p),
+                ("nattrs", ctypes.c_uint32)]
+
+
+class ocr_onnx_tensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dims", ctypes.c_void_p), ("rank", ctypes.c_uint32),
+                ("data", ctypes.c_void_p), ("ints", ctypes.c_void_p), ("count", ctypes.c_uint64)]
+
+
+class ocr_onnx(ctypes.Structure):
+    _fields_ = [("nodes", ctypes.c_void_p), ("nnodes", ctypes.c_uint32), ("tensors", ctypes.c_void_p),
+                ("ntensors", ctypes.c_uint32), ("input", ctypes.c_char_p), ("output", ctypes.c_char_p)]
+
+
+class ParsedGraph:
+    """A graph the host has parsed (the reference's Onnx, src/onnx.rs:44-56) as the C ABI's
+    ocr_onnx: nodes = [(op, inputs, outputs, {attribute: value})] (value a float, int, str or a
+    list of ints or floats), weights = {name: float32 array}, ints = {name: int64 array}. Keeps
+    every buffer alive for as long as the object lives."""
+
+    def __init__(self, nodes, weights, ints, input_name: str, output_name: str):
+        keep = self._keep = []
+
+        def cstr(v):
+            b = v.encode()
+            keep.append(b)
+            return b
+
+        def strs(names):
+            arr = (ctypes.c_char_p * max(len(names), 1))(*[cstr(n) for n in names])
+            keep.append(arr)
+            return ctypes.cast(arr, ctypes.c_void_p)
+
+        cnodes = (ocr_onnx_node * max(len(nodes), 1))()
+        for k, (op, ins, outs, attrs) in enumerate(nodes):
+            attrs = {k: v for k, v in attrs.items() if v is not None}
+            catt = (ocr_onnx_attr * max(len(attrs), 1))()
+            for j, (name, v) in enumerate(attrs.items()):
+                a = catt[j]
+                a.name = cstr(name)
+                if isinstance(v, bool) or isinstance(v, (int, np.integer)):
+                    a.type, a.i = 2, int(v)
+                elif isinstance(v, (float, np.floating)):
+                    a.type, a.f = 1, float(v)
+                elif isinstance(v, (str, bytes)):
+                    a.type, a.s = 3, cstr(v if isinstance(v, str) else v.decode())
+                else:
+                    vals = list(np.asarray(v).reshape(-1))
+                    if vals and all(isinstance(x, (float, np.floating)) for x in vals):
+                        arr = np.ascontiguousarray(vals, np.float32)
+                        a.type, a.floats = 6, arr.ctypes.data
+                    else:
+                        arr = np.ascontiguousarray(vals, np.int64)
+                        a.type, a.ints = 7, arr.ctypes.data
+                    keep.append(arr)
+                    a.count = len(vals)
+            keep.append(catt)
+            cnodes[k] = ocr_onnx_node(cstr(op), strs(list(ins)), len(ins), strs(list(outs)), len(outs),
+                                      ctypes.cast(catt, ctypes.c_void_p), len(attrs))
+        keep.append(cnodes)
+        tensors = []
+        for name, arr in weights.items():
+            a = np.ascontiguousarray(arr, np.float32)
+            d = np.ascontiguousarray(a.shape, np.int64)
+            keep += [a, d]
+            tensors.append(ocr_onnx_tensor(cstr(name), d.ctypes.data, a.ndim, a.ctypes.data, None, a.size))
+        for name, arr in ints.items():
+            a = np.ascontiguousarray(arr, np.int64).reshape(-1)
+            d = np.ascontiguousarray([a.size], np.int64)
+            keep += [a, d]
+            tensors.append(ocr_onnx_tensor(cstr(name), d.ctypes.data, 1, None, a.ctypes.data, a.size))
+        ctens = (ocr_onnx_tensor * max(len(tensors), 1))(*tensors)
+        keep.append(ctens)
+        self.struct = ocr_onnx(ctypes.cast(cnodes, ctypes.c_void_p), len(nodes), ctypes.cast(ctens, ctypes.c_void_p),
+                               len(tensors), cstr(input_name), cstr(output_name))
+
+    def ref(self):
+        return ctypes.byref(self.struct)
 
 
 class ocr_pipeline_opts(ctypes.Structure):
@@ -231,9 +322,12 @@ class Context:
 class Detector:
     """Detector (src/gpu.rs:1380-1431)."""
 
-    def __init__(self, ctx: Context, onnx_path: str):
+    def __init__(self, ctx: Context, onnx_path: "str | ParsedGraph"):
         self.ctx = ctx
-        self.handle = lib().ocr_detector_new(ctx.handle, onnx_path.encode())
+        if isinstance(onnx_path, ParsedGraph):
+            self.handle = lib().ocr_detector_new_onnx(ctx.handle, onnx_path.ref())
+        else:
+            self.handle = lib().ocr_detector_new(ctx.handle, onnx_path.encode())
         if not self.handle:
             raise OcrError(lib().ocr_last_error().decode())
 
@@ -273,9 +367,13 @@ class Detector:
 class Graph:
     """Graph (src/gpu.rs:1077-1378): a convolutional ONNX graph on the GPU."""
 
-    def __init__(self, ctx: Context, onnx_path: str, stop_op: str | None = None):
+    def __init__(self, ctx: Context, onnx_path: "str | ParsedGraph", stop_op: str | None = None):
         self.ctx = ctx
-        self.handle = lib().ocr_graph_new(ctx.handle, onnx_path.encode(), stop_op.encode() if stop_op else None)
+        stop = stop_op.encode() if stop_op else None
+        if isinstance(onnx_path, ParsedGraph):
+            self.handle = lib().ocr_graph_new_onnx(ctx.handle, onnx_path.ref(), stop)
+        else:
+            self.handle = lib().ocr_graph_new(ctx.handle, onnx_path.encode(), stop)
         if not self.handle:
             raise OcrError(lib().ocr_last_error().decode())
 
@@ -303,9 +401,12 @@ class Graph:
 class NdGraph:
     """NdGraph (src/nd.rs:428-1394): an ONNX graph of the N-D operator set on the GPU."""
 
-    def __init__(self, ctx: Context, onnx_path: str, stop_before_softmax: bool = False):
+    def __init__(self, ctx: Context, onnx_path: "str | ParsedGraph", stop_before_softmax: bool = False):
         self.ctx = ctx
-        self.handle = lib().ocr_nd_new(ctx.handle, onnx_path.encode(), int(bool(stop_before_softmax)))
+        if isinstance(onnx_path, ParsedGraph):
+            self.handle = lib().ocr_nd_new_onnx(ctx.handle, onnx_path.ref(), int(bool(stop_before_softmax)))
+        else:
+            self.handle = lib().ocr_nd_new(ctx.handle, onnx_path.encode(), int(bool(stop_before_softmax)))
         if not self.handle:
             raise OcrError(lib().ocr_last_error().decode())
 
@@ -377,9 +478,12 @@ def db_threshold(ctx: Context, prob: np.ndarray, thr: float) -> np.ndarray:
 class Recognizer:
     """Recognizer (src/gpu.rs:1441-1603)."""
 
-    def __init__(self, ctx: Context, onnx_path: str, lines: int = 8):
+    def __init__(self, ctx: Context, onnx_path: "str | ParsedGraph", lines: int = 8):
         self.ctx = ctx
-        self.handle = lib().ocr_recognizer_new(ctx.handle, onnx_path.encode(), lines)
+        if isinstance(onnx_path, ParsedGraph):
+            self.handle = lib().ocr_recognizer_new_onnx(ctx.handle, onnx_path.ref(), lines)
+        else:
+            self.handle = lib().ocr_recognizer_new(ctx.handle, onnx_path.encode(), lines)
         if not self.handle:
             raise OcrError(lib().ocr_last_error().decode())
 
