@@ -139,6 +139,14 @@ void trace_outer(const PaddedMask &m, int x0, int y0, std::vector<int32_t> &xy) 
 // Squared distances from the points k in (s, e) (coordinates px, py) to the segment between
 // points s and e (from point s when the segment is a point), into d2[k]: the float operations of
 // the distance itself up to its square root, so sqrt(d2[k]) is that distance bit for bit.
+// Built for AVX2 and for the baseline ISA (the loader picks one); the same IEEE operations either
+// way, no fused multiply-adds. (Host code only: the device pass of this file compiles nothing.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define OCR_HOST_CLONES
+#else
+#define OCR_HOST_CLONES __attribute__((target_clones("avx2", "default")))
+#endif
+OCR_HOST_CLONES
 void seg_dist2(const float *__restrict px, const float *__restrict py, int s, int e, float *__restrict d2) {
     const float ax = px[s], ay = py[s], bx = px[e], by = py[e];
     if (ax == bx && ay == by) {
@@ -551,9 +559,10 @@ void external_rects(const uint32_t *bits, int w, int h, const std::vector<Seed> 
     PaddedMask m;  // read by the worker threads too
     m.build(bits, w, h);
     const int n = int(seeds.size());
-    std::vector<std::vector<int32_t>> chains(static_cast<size_t>(n));
-    parallel_for(n, threads, [&](int i) { trace_outer(m, seeds[size_t(i)].fx, seeds[size_t(i)].fy, chains[size_t(i)]); });
-    ok.assign(size_t(n), 1);
+    // Components that could enclose the pixel west of a component's first pixel: earlier ones
+    // (in raster order) whose bounding box holds it strictly. Rare on text pages.
+    std::vector<std::pair<int, int>> cand;  // (component, possible encloser)
+    std::vector<char> encloser(size_t(n), 0);
     std::vector<int> active;  // earlier components whose rows reach below the current row
     for (int i = 0; i < n; i++) {
         const Seed &c = seeds[size_t(i)];
@@ -565,21 +574,28 @@ void external_rects(const uint32_t *bits, int w, int h, const std::vector<Seed> 
         if (qx >= 0)
             for (int j : active) {
                 const Seed &d = seeds[size_t(j)];
-                if (d.y0 < qy && d.x0 < qx && qx < d.x1 && encloses(chains[size_t(j)], qx, qy)) {
-                    ok[size_t(i)] = 0;
-                    break;
-                }
+                if (d.y0 < qy && d.x0 < qx && qx < d.x1) cand.push_back({i, j}), encloser[size_t(j)] = 1;
             }
         active.push_back(i);
     }
+    // Every component's border, simplification and rectangle in one pass; the borders of
+    // possible enclosers are kept for the winding test.
+    std::vector<std::vector<int32_t>> chains(static_cast<size_t>(n));
     rects.assign(size_t(n), RRect{});
+    ok.assign(size_t(n), 1);
     parallel_for(n, threads, [&](int i) {
-        if (!ok[size_t(i)]) return;
+        thread_local std::vector<int32_t> chain;
         thread_local std::vector<Pt> simp, hull;
         thread_local SimplifyScratch scratch;
-        simplify_closed(chains[size_t(i)], 2.f, simp, scratch);
+        std::vector<int32_t> &xy = encloser[size_t(i)] ? chains[size_t(i)] : chain;
+        trace_outer(m, seeds[size_t(i)].fx, seeds[size_t(i)].fy, xy);
+        simplify_closed(xy, 2.f, simp, scratch);
         if (!min_area_rect(simp, hull, rects[size_t(i)])) ok[size_t(i)] = 0;
     });
+    // A component inside a hole of another one is left out (an outer border winds around the
+    // background pixel west of its first pixel).
+    for (const auto &[i, j] : cand)
+        if (ok[size_t(i)] && encloses(chains[size_t(j)], seeds[size_t(i)].fx - 1, seeds[size_t(i)].fy)) ok[size_t(i)] = 0;
 }
 
 std::vector<RRect> grown_rects(const uint32_t *bits, int w, int h, const std::vector<Seed> &seeds, float expand,

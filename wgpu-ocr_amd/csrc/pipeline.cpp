@@ -36,13 +36,18 @@ PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float rel
                        const MaskRows *rows) {
     set_loop_priority(page_prio);
     PageLayout L;
+    const auto t0 = Clock::now();
     std::vector<RRect> words =
         rows ? word_rects_from_rows(bits, w, h, rows->comps, rows->ncomps, rows->xmin, rows->xmax, rows->nslots, 3.f,
                                     100.f, threads)
              : word_rects(bits, w, h, 3.f, 100.f, threads);
     L.words = int(words.size());
+    L.ms_words = ms_since(t0);
+    const auto t1 = Clock::now();
     auto lines = find_text_lines(words);
     pad_lines(lines, relv, relend);
+    L.ms_lines = ms_since(t1);
+    const auto t2 = Clock::now();
     lines.erase(std::remove_if(lines.begin(), lines.end(), [](const std::vector<RRect> &l) { return l.empty(); }),
                 lines.end());
     L.lines.resize(lines.size());
@@ -55,6 +60,7 @@ PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float rel
     std::vector<int> out_w;
     for (const LineGeom &g : L.lines) out_w.push_back(g.out_w);
     L.plan = plan_batches(out_w);
+    L.ms_geom = ms_since(t2);
     for (const LineGeom &g : L.lines) {
         L.line_row0.push_back(int32_t(L.row_off.size()));
         const int32_t sbase = int32_t(L.spans.size());
@@ -407,7 +413,13 @@ struct PipelineRun final : PipelineHooks {
         layouts[size_t(p)] = layout_page(bits, w[p], h[p], I.opts.relv, I.opts.relend, I.host_threads, p,
                                          fits ? &mr : nullptr);
         if (p == fail_layout) fail("layout of page " + std::to_string(p) + " failed (injected)");
-        mark("layout " + std::to_string(p) + " done");
+        if (tracing) {
+            const PageLayout &L = layouts[size_t(p)];
+            char buf[128];
+            std::snprintf(buf, sizeof buf, "layout %d done (words %.3f, lines %.3f, geometry %.3f ms)", p, L.ms_words,
+                          L.ms_lines, L.ms_geom);
+            mark(buf);
+        }
     }
 
     // Line images and recognition of pass r's laid-out pages, and the arg-max copy to the host.

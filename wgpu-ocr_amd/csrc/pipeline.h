@@ -40,6 +40,7 @@ struct PipelineStats {
 // recogniser), as ocr-bench.rs:503-559 does it per page.
 struct PageLayout {
     int words = 0;
+    double ms_words = 0, ms_lines = 0, ms_geom = 0;  // wall time of the three steps
     std::vector<LineGeom> lines;
     BatchPlan plan;
     // Every line's row offsets and spans one after another: line i's offsets start at
