@@ -184,11 +184,20 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     }
 
     // Weights of slice c, kernel row ky: block b = kx * NTW + j (n-tile nt0 + j); instruction i.
+    // The lane's byte offset of each instruction's fragment is fixed (n-tile, tap column, lane);
+    // a stage only moves the uniform base by its slice and kernel row. An n-tile past the last
+    // (16-channel layers in a 32-channel block) reads the last one's weights: its outputs are
+    // never stored.
+    unsigned woff[NWI];
+#pragma unroll
+    for (int i = 0; i < NWI; i++) {
+        const int b = min(i * 8 + wave, WBLK - 1), kx = b / NTW, j = b - kx * NTW, nt = min(nt0 + j, p.ntiles - 1);
+        woff[i] = (unsigned(nt * p.chunks * 9 + kx) * 64u + unsigned(lane)) * 16u;
+    }
     auto dma_w = [&](half8 *dst, int c, int ky, int i) __attribute__((always_inline)) {
-        const int b = min(i * 8 + wave, WBLK - 1), kx = b / NTW, j = b - kx * NTW, nt = nt0 + j;
-        const half8 *src = reinterpret_cast<const half8 *>(p.zero);
-        if (nt < p.ntiles) src = p.wt + ((size_t(nt) * p.chunks + c) * 9 + ky * 3 + kx) * 64 + lane;
-        dma16(src, dst + b * 64);
+        const int b = min(i * 8 + wave, WBLK - 1);
+        const char *base = reinterpret_cast<const char *>(p.wt) + size_t(c * 9 + ky * 3) * 1024;
+        dma16s(base, woff[i], dst + b * 64);
     };
     // Halo of position s into HF, instruction i.
     auto dma_h = [&](const Seq &s, int i) __attribute__((always_inline)) {
@@ -465,7 +474,8 @@ int c3_accepts(const ConvArgs &a) {
 void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     const ConvArgs &a = args[0];
     const ConvPack &pk = a.pk;
-    const int cout = a.y.c, nt = cout > 64 ? 4 : cout > 32 ? 2 : 1, bn = 32 * nt;
+    const int cout = a.y.c;
+    int nt = cout > 64 ? 4 : cout > 32 ? 2 : 1;
     C3Params p{};
     p.h = a.x.h;
     p.cin = a.x.c;
@@ -529,6 +539,12 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     p.nseg = count;
     p.tiles = int(tiles);
     if (p.tiles == 0) return;
+    // Narrower channel blocks (fewer n-tiles a wavefront) when the launch has so few tiles that
+    // most CUs would get no workgroup (the detector's deepest level at a few pages); a narrower
+    // block reuses each input fragment for fewer outputs, so only then.
+    const int cus = cu_count3();
+    while (nt > 1 && double(p.tiles) * ((cout + 32 * nt - 1) / (32 * nt)) < 0.15 * cus) nt /= 2;
+    const int bn = 32 * nt;
     p.nblocks = (cout + bn - 1) / bn;
     p.runs = std::max(1, std::min(p.tiles, cu_count3() / p.nblocks));
     p.zero = zero_block();

@@ -21,6 +21,13 @@ __device__ inline void dma16(const void *src, void *dst) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
+// The same with the address as a uniform 64-bit base plus a per-lane 32-bit byte offset (the
+// scalar-base addressing form: the per-lane part stays fixed while the base moves).
+__device__ inline void dma16s(const void *base, unsigned voff, void *dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(unsigned(reinterpret_cast<size_t>((lds_ptr)dst)));
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m0) : "memory");
+}
+
 // Workgroup barrier for LDS: this wavefront's LDS operations are complete and no memory operation
 // moves across it; global loads, stores and LDS DMA stay in flight.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
