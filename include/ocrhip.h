@@ -230,7 +230,11 @@ int ocr_layout_batch(ocr_layout *lay, uint32_t i, uint32_t *width, uint32_t *lin
 
 /* merge: pages per recognition pass (MERGE); relv / relend: line padding (RELV, RELEND);
  * thr: detection threshold; threads: host worker threads (0 = up to 16); det_batch: pages per
- * detection pass. Zeros take the defaults 2, 0.15, 0.1, 0.5, 0, 4. */
+ * detection pass. Zeros take the defaults 2, 0.15, 0.1, 0.5, 0, 4.
+ * label_runs / label_comps / label_slots: capacities of the GPU labelling of a page's mask
+ * (0 = 131072 runs, 16384 components, 65536 component rows). A page that needs more, or is
+ * wider or taller than 65536 pixels, is labelled on the host from its mask bits instead, with
+ * the same words. */
 typedef struct ocr_pipeline_opts {
     uint32_t merge;
     float relv;
@@ -238,13 +242,17 @@ typedef struct ocr_pipeline_opts {
     float thr;
     uint32_t threads;
     uint32_t det_batch;
+    uint32_t label_runs;
+    uint32_t label_comps;
+    uint32_t label_slots;
 } ocr_pipeline_opts;
 
 typedef struct ocr_pipeline_stats {
     double ms;           /* wall time of the last run */
     double cpu_busy_ms;  /* host worker time spent on layout and decoding */
     uint32_t pages, lines, words, batches, rec_passes;
-    uint64_t rec_steps;  /* GRU steps summed over lines */
+    uint64_t rec_steps;      /* GRU steps summed over lines */
+    uint32_t host_labelled;  /* pages whose mask was labelled on the host (over the capacities) */
 } ocr_pipeline_stats;
 
 ocr_pipeline *ocr_pipeline_new(ocr_detector *det, ocr_recognizer *rec, const ocr_pipeline_opts *opts);

@@ -196,6 +196,26 @@ def test_pipeline_words_match_host_labelling(detector, recognizer):
         assert p.texts(k)[1] == len(want)
 
 
+def test_pipeline_label_capacity_fallback(detector, recognizer):
+    # Labelling capacities too small for a full page's mask: those pages are labelled on the
+    # host from their bits, the small page beside them in the same detection group still on the
+    # GPU, and every page's text equals the run with the default capacities.
+    pages = [synth.page(30), np.ascontiguousarray(synth.page(31)[150:400, 100:900]), synth.page(32)]
+    base = ocrhip.Pipeline(detector, recognizer, merge=2, det_batch=2)
+    print("label fallback: default capacities", flush=True)
+    base.run(pages)
+    assert base.stats()["host_labelled"] == 0
+    want = [base.texts(k) for k in range(3)]
+    assert want[0][1] > 200 and want[2][1] > 200 and 0 < want[1][1] < 100
+    for caps in ({"label_comps": 200}, {"label_runs": 4000, "label_slots": 4000}):
+        print(f"label fallback: {caps}", flush=True)
+        p = ocrhip.Pipeline(detector, recognizer, merge=2, det_batch=2, **caps)
+        p.run(pages)
+        assert [p.texts(k) for k in range(3)] == want
+        n = p.stats()["host_labelled"]
+        assert n == 2 if "label_comps" in caps else n >= 2
+
+
 def test_pipeline_blank_and_small_pages(detector, recognizer):
     blank = np.full((3300, 2550, 3), 255, np.uint8)
     small = np.ascontiguousarray(synth.page(7)[150:400, 100:900])

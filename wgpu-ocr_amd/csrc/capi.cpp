@@ -622,6 +622,11 @@ ocr_pipeline *ocr_pipeline_new(ocr_detector *det, ocr_recognizer *rec, const ocr
             if (opts->thr != 0.f) o.thr = opts->thr;
             o.threads = int(opts->threads);
             if (opts->det_batch) o.det_batch = int(opts->det_batch);
+            if (opts->label_runs > (1u << 30) || opts->label_comps > (1u << 30) || opts->label_slots > (1u << 30))
+                fail("label capacities above 2^30");
+            o.label_runs = int(opts->label_runs);
+            o.label_comps = int(opts->label_comps);
+            o.label_slots = int(opts->label_slots);
         }
         det->owner->ctx->bind();
         auto p = std::make_unique<ocr_pipeline>();
@@ -686,7 +691,7 @@ int ocr_pipeline_stats_get(ocr_pipeline *pipe, ocr_pipeline_stats *out) {
         need(out, "out");
         const PipelineStats &s = pipe->pipe->stats();
         *out = {s.ms, s.cpu_busy_ms, uint32_t(s.pages), uint32_t(s.lines), uint32_t(s.words), uint32_t(s.batches),
-                uint32_t(s.rec_passes), uint64_t(s.rec_steps)};
+                uint32_t(s.rec_passes), uint64_t(s.rec_steps), uint32_t(s.host_labelled)};
     });
 }
 
@@ -992,7 +997,7 @@ int ocr_pp_pipeline_stats_get(ocr_pp_pipeline *pipe, ocr_pipeline_stats *out) {
         need(out, "out");
         const PipelineStats &s = pipe->pipe->stats();
         *out = ocr_pipeline_stats{s.ms, s.cpu_busy_ms, uint32_t(s.pages), uint32_t(s.lines), uint32_t(s.words),
-                                  uint32_t(s.batches), uint32_t(s.rec_passes), uint64_t(s.rec_steps)};
+                                  uint32_t(s.batches), uint32_t(s.rec_passes), uint64_t(s.rec_steps), 0u};
     });
 }
 

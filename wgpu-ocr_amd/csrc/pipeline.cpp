@@ -1,8 +1,9 @@
 #include "pipeline.h"
 
 #include <algorithm>
-#include <map>
+#include <atomic>
 #include <chrono>
+#include <map>
 #include <condition_variable>
 #include <deque>
 #include <functional>
@@ -220,6 +221,10 @@ struct PipelineRun final : PipelineHooks {
     std::vector<std::vector<DBuf>> keep_bits, keep_runs;
     std::vector<size_t> words_of;
     std::vector<int> runs_cap;
+    // Pages whose mask the GPU labels (the labelling stores columns and rows as 16 bits): the
+    // others are labelled on the host from their bits.
+    std::vector<char> gpu_label;
+    std::atomic<int> host_labelled{0};
     std::vector<PageLayout> layouts;
     struct RecPass {
         std::vector<std::pair<int, int>> rows;  // (page, line in page) of every recogniser line
@@ -261,7 +266,9 @@ struct PipelineRun final : PipelineHooks {
         if (I.best_host.size() < size_t(P.passes())) I.best_host.resize(size_t(P.passes()));
         words_of.resize(size_t(np));
         runs_cap.resize(size_t(np));
+        gpu_label.resize(size_t(np));
         for (int p = 0; p < np; p++) {
+            gpu_label[size_t(p)] = w[p] <= 65536 && h[p] <= 65536;
             words_of[size_t(p)] = size_t((w[p] + 31) / 32) * h[p];
             I.bits_host[size_t(p)].ensure(words_of[size_t(p)] * 4);
             runs_cap[size_t(p)] = int(std::min<size_t>(words_of[size_t(p)] * 16, size_t(caps.runs)));
@@ -355,6 +362,10 @@ struct PipelineRun final : PipelineHooks {
         std::vector<DBuf> &rbuf = keep_runs[size_t(g)];
         std::vector<CclPage> cp;
         for (int p = p0; p < p1; p++) {
+            if (!gpu_label[size_t(p)]) {
+                rbuf.emplace_back();
+                continue;
+            }
             rbuf.emplace_back(&ctx, block_bytes(p));
             rbuf.back().used_on(I.copy);
             char *b = rbuf.back().as<char>();
@@ -383,8 +394,9 @@ struct PipelineRun final : PipelineHooks {
         for (int p = p0; p < p1; p++) {
             OCR_HIP(hipMemcpyAsync(I.bits_host[size_t(p)].p, bp[size_t(p - p0)], words_of[size_t(p)] * 4,
                                    hipMemcpyDeviceToHost, I.copy));
-            OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), caps.head(),
-                                   hipMemcpyDeviceToHost, I.copy));
+            if (gpu_label[size_t(p)])
+                OCR_HIP(hipMemcpyAsync(I.runs_host[size_t(p)].p, rbuf[size_t(p - p0)].get(), caps.head(),
+                                       hipMemcpyDeviceToHost, I.copy));
         }
         OCR_HIP(hipEventCreateWithFlags(&det_ev[size_t(g)], hipEventDisableTiming | hipEventBlockingSync));
         OCR_HIP(hipEventRecord(det_ev[size_t(g)], I.copy));
@@ -409,7 +421,9 @@ struct PipelineRun final : PipelineHooks {
         const char *comps = rblk + 16, *xmin = comps + size_t(caps.comps) * 16;
         const MaskRows mr{reinterpret_cast<const int32_t *>(comps), tot[1], reinterpret_cast<const uint32_t *>(xmin),
                           reinterpret_cast<const uint32_t *>(xmin + size_t(caps.slots) * 4), tot[2]};
-        const bool fits = tot[0] <= runs_cap[size_t(p)] && tot[1] <= caps.comps && tot[2] <= caps.slots;
+        const bool fits = gpu_label[size_t(p)] && tot[0] <= runs_cap[size_t(p)] && tot[1] <= caps.comps &&
+                          tot[2] <= caps.slots;
+        if (!fits) host_labelled++;
         layouts[size_t(p)] = layout_page(bits, w[p], h[p], I.opts.relv, I.opts.relend, I.host_threads, p,
                                          fits ? &mr : nullptr);
         if (p == fail_layout) fail("layout of page " + std::to_string(p) + " failed (injected)");
@@ -554,6 +568,7 @@ void Pipeline::run_pages(const uint8_t *const *src, bool on_host, const int *w, 
         }
         stats_.batches = R.batches;
         stats_.rec_passes = R.rec_passes;
+        stats_.host_labelled = R.host_labelled.load();
         for (const auto &Rp : R.passes)
             for (uint32_t l : Rp.lens) stats_.rec_steps += l;
         R.print_trace();

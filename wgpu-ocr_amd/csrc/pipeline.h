@@ -20,7 +20,8 @@ struct PipelineOpts {
     int det_batch = 4;    // pages per detection pass
     bool lookahead = true;  // a recognition pass waits for the next pass's detections to be queued
     // Capacities of the GPU labelling of a page's mask (0: 2^17 runs, 16384 components, 65536
-    // row slots); a page that needs more is labelled on the host from its bits.
+    // row slots); a page that needs more, or is wider or taller than 65536 pixels, is labelled
+    // on the host from its bits.
     int label_runs = 0, label_comps = 0, label_slots = 0;
 };
 
@@ -34,6 +35,7 @@ struct PipelineStats {
     double ms = 0, cpu_busy_ms = 0;
     int pages = 0, lines = 0, words = 0, batches = 0, rec_passes = 0;
     long long rec_steps = 0;  // sum over lines of their GRU steps
+    int host_labelled = 0;    // pages whose mask was labelled on the host (over the GPU capacities)
 };
 
 // Words -> lines -> padding -> line images -> batches for one page (all host work before the

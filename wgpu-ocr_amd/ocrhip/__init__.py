@@ -196,13 +196,14 @@ class ParsedGraph:
 
 class ocr_pipeline_opts(ctypes.Structure):
     _fields_ = [("merge", ctypes.c_uint32), ("relv", ctypes.c_float), ("relend", ctypes.c_float),
-                ("thr", ctypes.c_float), ("threads", ctypes.c_uint32), ("det_batch", ctypes.c_uint32)]
+                ("thr", ctypes.c_float), ("threads", ctypes.c_uint32), ("det_batch", ctypes.c_uint32),
+                ("label_runs", ctypes.c_uint32), ("label_comps", ctypes.c_uint32), ("label_slots", ctypes.c_uint32)]
 
 
 class ocr_pipeline_stats(ctypes.Structure):
     _fields_ = [("ms", ctypes.c_double), ("cpu_busy_ms", ctypes.c_double), ("pages", ctypes.c_uint32),
                 ("lines", ctypes.c_uint32), ("words", ctypes.c_uint32), ("batches", ctypes.c_uint32),
-                ("rec_passes", ctypes.c_uint32), ("rec_steps", ctypes.c_uint64)]
+                ("rec_passes", ctypes.c_uint32), ("rec_steps", ctypes.c_uint64), ("host_labelled", ctypes.c_uint32)]
 
 
 def lib():
@@ -629,10 +630,10 @@ class Pipeline:
     """The whole-page pipeline (ocr-bench.rs:133-310, 458-585)."""
 
     def __init__(self, det: Detector, rec: Recognizer, merge=2, relv=0.15, relend=0.1, thr=0.5, threads=0,
-                 det_batch=4):
+                 det_batch=4, label_runs=0, label_comps=0, label_slots=0):
         self.ctx = det.ctx
         self._keep = (det, rec)
-        opts = ocr_pipeline_opts(merge, relv, relend, thr, threads, det_batch)
+        opts = ocr_pipeline_opts(merge, relv, relend, thr, threads, det_batch, label_runs, label_comps, label_slots)
         self.handle = lib().ocr_pipeline_new(det.handle, rec.handle, ctypes.byref(opts))
         if not self.handle:
             raise OcrError(lib().ocr_last_error().decode())
