@@ -157,11 +157,13 @@ void seg_dist2(const float *__restrict px, const float *__restrict py, int s, in
         return;
     }
     const float abx = bx - ax, aby = by - ay, den = abx * abx + aby * aby;
+    // Branch-free (both ends and the projection computed, then selected) so it vectorises.
     for (int k = s + 1; k < e; k++) {
         const float acx = px[k] - ax, acy = py[k] - ay;
         const float t = (acx * abx + acy * aby) / den;
-        const float qx = t <= 0.f ? ax : (t >= 1.f ? bx : ax + abx * t);
-        const float qy = t <= 0.f ? ay : (t >= 1.f ? by : ay + aby * t);
+        float qx = ax + abx * t, qy = ay + aby * t;
+        qx = t >= 1.f ? bx : qx, qy = t >= 1.f ? by : qy;
+        qx = t <= 0.f ? ax : qx, qy = t <= 0.f ? ay : qy;
         const float dx = px[k] - qx, dy = py[k] - qy;
         d2[k] = dx * dx + dy * dy;
     }
