@@ -475,7 +475,8 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     const ConvArgs &a = args[0];
     const ConvPack &pk = a.pk;
     const int cout = a.y.c;
-    int nt = cout > 64 ? 4 : cout > 32 ? 2 : 1;
+    const int nt_max = cout > 64 ? 4 : cout > 32 ? 2 : 1;
+    int nt = nt_max;
     C3Params p{};
     p.h = a.x.h;
     p.cin = a.x.c;
@@ -490,23 +491,36 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     p.cout = cout;
     p.chunks = pk.chunks;
     p.bias = a.bias;
-    // Tile: 16 blocks of 2 x 8 pixels; the shape wasting the fewest pixels (over all segments)
-    // whose halo fits.
+    // Tile shape (16 blocks of 2 x 8 pixels) and channel block (NT n-tiles a wavefront) chosen
+    // together. A workgroup walks ceil(tiles / runs) tiles, runs = CUs / blocks, so the launch
+    // takes that many rounds of a tile each; a tile costs about (1.5 + NT) units (per-stage
+    // overhead, then matrix work per n-tile: measured on the detector's 256 -> 128 layer) times
+    // its halo's share of extra pixels. Few tiles (the detector's deep levels at a few pages)
+    // favour narrower blocks and shapes whose count fits one round; many tiles the widest block.
     p.tm = a.tm;
     p.tm_ntot = a.tm_ntot;
+    const int cus = cu_count3();
     double best = 1e300;
+    bool fits = false;
     for (int mxc : {1, 2, 4, 8}) {
         if (pool == 3 && mxc != 8) continue;  // four rows: the whole output height in one tile
         const int tw = 8 * mxc, th = 2 * (16 / mxc), hw = tw + 2, hh = th + 2;
         const int rs = 9 * hw + (24 - 9 * hw % 16) % 16;  // 8 mod 16 units
         if (hh * hw > HPX || hh * rs > HSU) continue;
-        double cost = 0;
+        fits = true;
+        double ntl = 0;
         for (int k = 0; k < count; k++)
-            cost += double(args[k].y.n) * ((p.oh + th - 1) / th * th) * ((args[k].y.w + tw - 1) / tw * tw) *
-                    double(hh * hw) / (th * tw);
-        if (cost < best) best = cost, p.tw = tw, p.th = th, p.mx = mxc, p.rs = rs;
+            ntl += double(args[k].y.n) * ((p.oh + th - 1) / th) * ((args[k].y.w + tw - 1) / tw);
+        if (ntl < 1) continue;
+        for (int q = nt_max; q >= 1; q /= 2) {
+            const double blocks = (cout + 32 * q - 1) / (32 * q);
+            const double runs = std::max(1.0, std::min(ntl, std::floor(cus / blocks)));
+            const double cost = std::ceil(ntl / runs) * (1.5 + q) * double(hh * hw) / (th * tw);
+            if (cost < best) best = cost, p.tw = tw, p.th = th, p.mx = mxc, p.rs = rs, nt = q;
+        }
     }
-    if (best == 1e300) fail("conv3x3_dma: no tile fits");
+    if (!fits) fail("conv3x3_dma: no tile fits");
+    if (best == 1e300) return;  // no output pixels
     p.hw = p.tw + 2;
     p.hh = p.th + 2;
     p.npx = p.hh * p.hw;
@@ -539,14 +553,9 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     p.nseg = count;
     p.tiles = int(tiles);
     if (p.tiles == 0) return;
-    // Narrower channel blocks (fewer n-tiles a wavefront) when the launch has so few tiles that
-    // most CUs would get no workgroup (the detector's deepest level at a few pages); a narrower
-    // block reuses each input fragment for fewer outputs, so only then.
-    const int cus = cu_count3();
-    while (nt > 1 && double(p.tiles) * ((cout + 32 * nt - 1) / (32 * nt)) < 0.15 * cus) nt /= 2;
     const int bn = 32 * nt;
     p.nblocks = (cout + bn - 1) / bn;
-    p.runs = std::max(1, std::min(p.tiles, cu_count3() / p.nblocks));
+    p.runs = std::max(1, std::min(p.tiles, cus / p.nblocks));
     p.zero = zero_block();
     const int grid = p.runs * p.nblocks;
     ProbeScope probe("conv3x3_dma", s, flops, bytes);
