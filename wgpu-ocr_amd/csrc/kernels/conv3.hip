@@ -194,21 +194,32 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
         const int b = min(i * 8 + wave, WBLK - 1), kx = b / NTW, j = b - kx * NTW, nt = min(nt0 + j, p.ntiles - 1);
         woff[i] = (unsigned(nt * p.chunks * 9 + kx) * 64u + unsigned(lane)) * 16u;
     }
-    auto dma_w = [&](half8 *dst, int c, int ky, int i) __attribute__((always_inline)) {
+    // LDS byte addresses of the DMA destinations (the copies take them, not pointers).
+    const unsigned w0a = lds_addr(W0), w1a = lds_addr(W1), hfa = lds_addr(HF);
+    auto dma_w = [&](unsigned dst, int c, int ky, int i) __attribute__((always_inline)) {
         const int b = min(i * 8 + wave, WBLK - 1);
         const char *base = reinterpret_cast<const char *>(p.wt) + size_t(c * 9 + ky * 3) * 1024;
-        dma16s(base, woff[i], dst + b * 64);
+        dma16s_to(base, woff[i], dst + unsigned(b) * 1024u);
     };
-    // Halo of position s into HF, instruction i.
-    auto dma_h = [&](const Seq &s, int i) __attribute__((always_inline)) {
+    // The halo of a position: its image's slice base, corner and width, computed once for the
+    // position's NHI copies; instruction i copies this lane's slot (zeros outside the image and
+    // past the input channels), the choice made by a select rather than a branch.
+    struct Halo {
+        const float *base;
+        int iy0, ix0, w, cleft;
+    };
+    auto halo_of = [&](const Seq &s) __attribute__((always_inline)) {
         const C3Seg &sd = p.seg[s.sg];
-        const float *base = sd.x + size_t(s.img) * p.h * sd.w * p.xcs + s.c * 32;
+        return Halo{sd.x + size_t(s.img) * p.h * sd.w * p.xcs + s.c * 32, s.ty * p.th - 1, s.tx * p.tw - 1, sd.w,
+                    p.cin - s.c * 32};
+    };
+    auto dma_h = [&](const Halo &hl, int i) __attribute__((always_inline)) {
         const int b = min(i * 8 + wave, p.hblocks - 1);
-        const int iy = s.ty * p.th - 1 + dhy[i], ix = s.tx * p.tw - 1 + dhx[i];
-        const void *src = p.zero;
-        if (dhy[i] >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(sd.w) && s.c * 32 + dch[i] < p.cin)
-            src = base + unsigned((iy * sd.w + ix) * p.xcs + dch[i]);
-        dma16(src, HF + b * 64);
+        const int iy = hl.iy0 + dhy[i], ix = hl.ix0 + dhx[i];
+        const bool ok = dhy[i] >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(hl.w) && dch[i] < hl.cleft;
+        const int off = ok ? (iy * hl.w + ix) * p.xcs + dch[i] : 0;
+        const void *src = ok ? static_cast<const void *>(hl.base + unsigned(off)) : static_cast<const void *>(p.zero);
+        dma16_to(src, hfa + unsigned(b) * 1024u);
     };
     // HF -> HS, once a slice: hi part q (channels 8q..8q+7) of a pixel at its unit + q, lo at
     // + 4 + q; lo = x - hi rounded to float16 (x = hi + lo to about 2^-22).
@@ -375,17 +386,20 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     auto stage = [&](auto KYc, auto HPc) __attribute__((always_inline)) -> bool {
         constexpr int KY = decltype(KYc)::value, HP = decltype(HPc)::value;
         constexpr int WP = (KY + HP) & 1;
-        half8 *Wc = WP ? W1 : W0, *Wn = WP ? W0 : W1;
+        half8 *Wc = WP ? W1 : W0;
+        const unsigned Wna = WP ? w0a : w1a;
         const bool more = nxt.t < t_end;
         // The next stage's weights (steps 0..NWI-1), then at a slice's first row the next slice's
         // halo (steps NWI..NWI+NHI-1), one DMA instruction per step between the MFMAs.
         const bool wnext = KY < 2 || more, hnext = KY == 0 && more;
         const int wc = KY < 2 ? cur.c : nxt.c, wky = KY < 2 ? KY + 1 : 0;
+        Halo hn{};
+        if (hnext) hn = halo_of(nxt);
         compute(Wc, KY, [&](int st) __attribute__((always_inline)) {
             if (st < NWI) {
-                if (wnext) dma_w(Wn, wc, wky, st);
+                if (wnext) dma_w(Wna, wc, wky, st);
             } else if (st < NWI + NHI) {
-                if (hnext) dma_h(nxt, st - NWI);
+                if (hnext) dma_h(hn, st - NWI);
             }
         });
         if (KY == 2 && cur.c == p.chunks - 1) epilogue(cur);
@@ -403,9 +417,12 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     };
 
 #pragma unroll
-    for (int i = 0; i < NWI; i++) dma_w(W0, 0, 0, i);
+    for (int i = 0; i < NWI; i++) dma_w(w0a, 0, 0, i);
+    {
+        const Halo h0 = halo_of(cur);
 #pragma unroll
-    for (int i = 0; i < NHI; i++) dma_h(cur, i);
+        for (int i = 0; i < NHI; i++) dma_h(h0, i);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
     split();

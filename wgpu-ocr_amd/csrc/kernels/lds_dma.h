@@ -28,6 +28,22 @@ __device__ inline void dma16s(const void *base, unsigned voff, void *dst) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m0) : "memory");
 }
 
+// The byte address in LDS of p, a pointer into __shared__ memory.
+__device__ inline unsigned lds_addr(const void *p) { return unsigned(reinterpret_cast<size_t>((lds_ptr)p)); }
+
+// The same copies with the LDS destination as a byte address (uniform) and no memory clobber:
+// the compiler keeps values it loaded across them (kernel arguments, tables) instead of loading
+// them again, and may move ordinary loads and stores across them. Only for copies into a buffer
+// that nothing reads or writes before the explicit wait and the barrier that publish it; the
+// copies keep their order with respect to every other asm statement (the waits, the barriers).
+__device__ inline void dma16_to(const void *src, unsigned lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)));
+}
+__device__ inline void dma16s_to(const void *base, unsigned voff, unsigned lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(lds)));
+}
+
 // Workgroup barrier for LDS: this wavefront's LDS operations are complete and no memory operation
 // moves across it; global loads, stores and LDS DMA stay in flight.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
