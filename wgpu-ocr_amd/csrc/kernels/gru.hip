@@ -42,6 +42,11 @@ __device__ inline float fast_exp(float v) { return __builtin_amdgcn_exp2f(v * 1.
 __device__ inline float sigm(float v) { return __builtin_amdgcn_rcpf(1.f + fast_exp(-v)); }
 __device__ inline float tanh_f(float v) { return 1.f - 2.f * __builtin_amdgcn_rcpf(1.f + fast_exp(2.f * v)); }
 
+// a where the mask's bits are set, b elsewhere (v_bfi_b32): a per-lane choice of a register.
+__device__ inline float sel_bits(unsigned m, float a, float b) {
+    return __uint_as_float((m & __float_as_uint(a)) | (~m & __float_as_uint(b)));
+}
+
 // Lane r of each 16-lane row receives the value of lane (r + 8) mod 16 (DPP row_ror:8).
 __device__ inline float ror8(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));
@@ -85,6 +90,7 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
     // This lane's line and the two units (of each 16-row tile) it updates: lane r < 8 takes
     // units 4g, 4g+1 of line r, lane r >= 8 units 4g+2, 4g+3 of line r - 8.
     const bool upper = r >= LINES;
+    const unsigned umask = upper ? ~0u : 0u;
     const int lr = upper ? r - LINES : r;
     const int line = n0 + lr;
     const int len = line < ntot ? int(lens[line]) : 0;
@@ -141,10 +147,13 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
             float rh[3][2];
 #pragma unroll
             for (int q = 0; q < 3; q++) {
-                const float send0 = upper ? acc[q][rt][0] : acc[q][rt][2];
-                const float send1 = upper ? acc[q][rt][1] : acc[q][rt][3];
-                const float keep0 = upper ? acc[q][rt][2] : acc[q][rt][0];
-                const float keep1 = upper ? acc[q][rt][3] : acc[q][rt][1];
+                // The lane's choice between rows 0, 1 and 2, 3 as bit selects on the upper-lane
+                // mask (one bitfield insert each; a ternary on `upper` is compiled as a dynamic
+                // index into the accumulator, a chain of compares and selects).
+                const float send0 = sel_bits(umask, acc[q][rt][0], acc[q][rt][2]);
+                const float send1 = sel_bits(umask, acc[q][rt][1], acc[q][rt][3]);
+                const float keep0 = sel_bits(umask, acc[q][rt][2], acc[q][rt][0]);
+                const float keep1 = sel_bits(umask, acc[q][rt][3], acc[q][rt][1]);
                 rh[q][0] = keep0 + ror8(send0);
                 rh[q][1] = keep1 + ror8(send1);
             }
