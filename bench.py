@@ -19,6 +19,7 @@ import argparse
 import json
 import os
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -87,6 +88,68 @@ def copy_calibration():
         y.copy_(x)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": 4 * n, "copies": 3}))
+
+
+def conv_layer(spec, reps=5):
+    """One 3x3 convolution (+ ReLU, optional max pool) as a one-node graph: CIN,COUT,N,H,W[,PHxPW].
+    Random float16-exact weights, random input; one warm-up launch, then `reps` launches with
+    every kernel family probed. Prints the launch time per family (the single-layer figures and
+    the single-layer counter profiles run this)."""
+    import ocrhip
+    from ocrhip import onnx_write as ow
+    f = spec.split(",")
+    cin, cout, n, h, w = (int(v) for v in f[:5])
+    pool = tuple(int(v) for v in f[5].split("x")) if len(f) > 5 else None
+    rng = np.random.default_rng(0)
+    g = ow.Graph("layer")
+    wt = g.init("w", (rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2 / (cin * 9))).astype(np.float16)
+                .astype(np.float32))
+    b = g.init("b", (rng.standard_normal(cout) * 0.01).astype(np.float16).astype(np.float32))
+    y = g.add("Relu", [g.add("Conv", ["x", wt, b], kernel_shape=[3, 3], pads=[1, 1, 1, 1])])
+    oh, ow_ = h, w
+    if pool:
+        y = g.add("MaxPool", [y], kernel_shape=list(pool), strides=list(pool))
+        oh, ow_ = h // pool[0], w // pool[1]
+    path = os.path.join(tempfile.gettempdir(), f"ocrhip_layer_{os.getpid()}.onnx")
+    with open(path, "wb") as fh:
+        fh.write(g.model("x", [n, cin, h, w], y, [n, cout, oh, ow_]))
+    ctx = ocrhip.Context()
+    graph = ocrhip.Graph(ctx, path)
+    os.unlink(path)
+    x = rng.standard_normal((n, cin, h, w)).astype(np.float32)
+    graph.run(x)
+    kern = _probed(ocrhip.FAMILIES, lambda: [graph.run(x) for _ in range(reps)])
+    out = {"layer": spec, "flops": 2.0 * n * h * w * cin * cout * 9}
+    for fam, k in kern.items():
+        if k["calls"]:
+            us = 1e3 * k["ms"] / k["calls"]
+            out[fam] = {"us_per_launch": us, "launches_per_run": k["calls"] / reps,
+                        "tflops": k["flops"] / k["ms"] / 1e9 if k["flops"] else None,
+                        "gbps": k["bytes"] / k["ms"] / 1e6 if k["bytes"] else None}
+    print(json.dumps(out))
+
+
+def gru_lines(nlines, reps=5):
+    """The recogniser on `nlines` synthetic lines (widths in [200, 800]) resident in device
+    memory: one warm-up pass, then `reps` passes; prints the GRU's time per launch and per step."""
+    import ocrhip
+    from ocrhip import synth
+    ctx = ocrhip.Context()
+    rec = ocrhip.Recognizer(ctx, synth.model_path("rec"))
+    batches, _, _ = synth.batch_lines(synth.rec_lines(nlines, seed=0, wmin=200, wmax=800))
+    dev = []
+    for data, n, w in batches:
+        buf = ctx.alloc(data.nbytes)
+        buf.upload(np.ascontiguousarray(data))
+        dev.append((buf, n, w))
+    tmax, ntot, _ = rec.dims(dev)
+    d_best = ctx.alloc(tmax * ntot * 4)
+    rec.recognize_device(dev, d_best=d_best)
+    ctx.synchronize()
+    kern = _probed(["gru"], lambda: [rec.recognize_device(dev, d_best=d_best) for _ in range(reps)])
+    k = kern["gru"]
+    us = 1e3 * k["ms"] / k["calls"]
+    print(json.dumps({"lines": nlines, "steps": tmax, "gru_us_per_launch": us, "gru_us_per_step": us / tmax}))
 
 
 def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
@@ -261,9 +324,18 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration figures")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device to device (the reference for traffic counters)")
+    ap.add_argument("--conv-layer", metavar="CIN,COUT,N,H,W[,PHxPW]",
+                    help="only time one 3x3 convolution layer (+ ReLU, optional max pool)")
+    ap.add_argument("--gru-lines", type=int, metavar="N", help="only time the GRU on N recognised lines")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.conv_layer:
+        conv_layer(args.conv_layer)
+        return
+    if args.gru_lines:
+        gru_lines(args.gru_lines)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the pipeline shards by page with no exchange, so N GPUs run N "
