@@ -162,11 +162,14 @@ def test_conv_transpose_2x3(ctx, tmp_path):
                                                         ((2, 2), 2, 256, 48, (3, 10), False),
                                                         ((3, 3), 3, 16, 16, (5, 4), True),
                                                         ((3, 3), 2, 16, 16, (5, 7), True),
-                                                        ((2, 3), 2, 32, 16, (4, 5), True)])
+                                                        ((2, 3), 2, 32, 16, (4, 5), True),
+                                                        ((2, 3), 2, 256, 128, (5, 7), True),
+                                                        ((3, 3), 2, 128, 32, (4, 6), True)])
 def test_conv_transpose_phases(ctx, tmp_path, k, stride, cin, cout, hw, exact):
     """Sub-pixel phases on the matrix cores (any kernel at least the stride; kernel = stride with
-    float16-exact weights as one GEMM over the input pixels), and the scalar kernel when a phase
-    has no taps (1 x 1 with stride 2)."""
+    float16-exact weights as one GEMM over the input pixels), the scalar kernel when a phase has
+    no taps (1 x 1 with stride 2); the detector's 2 x 3 upsampler at 256 -> 128 and a 3 x 3 kernel
+    with stride 2 (up to four taps on one output) among them."""
     def net(g, x):
         wt = RNG.standard_normal((cin, cout, *k)).astype(np.float32) * 0.3
         if exact:

@@ -5,10 +5,11 @@
 // For every page of a detection pass: (1) a wavefront per mask row counts the row's runs (set
 // pixels whose left neighbour is clear); (2) a workgroup per page turns the counts into row
 // offsets; (3) a wavefront per row writes its runs, left to right, each run its own parent; (4)
-// a thread per run joins it with every run of the row above that touches it with 8-connectivity
-// (x ranges overlapping or adjacent; the runs above found by binary search), linking the larger root under the smaller with a
-// compare-and-swap, so every component's root is its smallest run index: its first run in
-// row-major order, the order the host lists components in; (5) a thread per run replaces its
+// every run is joined with every run of the row above that touches it with 8-connectivity
+// (x ranges overlapping or adjacent; the runs above found by binary search), linking the larger
+// root under the smaller with a compare-and-swap, so every component's root is its smallest run
+// index: its first run in row-major order, the order the host lists components in (within bands
+// of rows in LDS first, then across the bands' edges); (5) a thread per run replaces its
 // parent by its root and raises its root's bottom row; (6) a thread per root gives its component
 // a record and a block of row slots, one a row from top to bottom (an 8-connected component has
 // pixels in every row of its span); (7) a thread per run folds its first and last pixel into its
@@ -156,38 +157,123 @@ __device__ inline int ccl_find(int32_t *parent, int x) {
     }
 }
 
-__global__ __launch_bounds__(256) void ccl_union_kernel(const CclParams p) {
+// Joins run j (row y > 0) with every run of the row above that touches it, on the global
+// parents: the larger root linked under the smaller with a compare-and-swap.
+__device__ inline void ccl_join_above(const CclPage &g, int j, int y) {
+    const int lo = g.row_off[y - 1], hi = g.row_off[y];
+    const int a0 = g.x0[j], a1 = g.x1[j];
+    // First run above whose right end reaches a0 - 1 (right ends increase along a row).
+    int l = lo, r = hi;
+    while (l < r) {
+        const int m = (l + r) >> 1;
+        if (int(g.x1[m]) + 1 >= a0) r = m;
+        else l = m + 1;
+    }
+    for (int i = l; i < hi && int(g.x0[i]) <= a1 + 1; i++) {
+        int u = i, v = j;
+        for (;;) {
+            u = ccl_find(g.root, u);
+            v = ccl_find(g.root, v);
+            if (u == v) break;
+            if (u > v) {
+                const int t = u;
+                u = v;
+                v = t;
+            }
+            // Link root v under the smaller root u, if v is still a root.
+            if (atomicCAS(g.root + v, v, u) == v) break;
+        }
+    }
+}
+
+// Step (4) in two parts. Bands of CCL_BAND rows first: a workgroup a band joins every run with
+// the runs of the row above inside the band, with the runs' ranges and parents in LDS (binary
+// searches, parent walks and compare-and-swaps at LDS latency instead of a chain of dependent
+// global loads), then sets each run's parent to its band root, the band's smallest run index of
+// its component. A band with more runs than CCL_BAND_CAP does the same on the global parents.
+// Then ccl_union_bounds_kernel joins the first row of each band with the row above it.
+constexpr int CCL_BAND = 32, CCL_BAND_CAP = 4096;
+
+// The root of local run x in the LDS parents, halving the path (as ccl_find).
+__device__ inline int ccl_find_lds(int *par, int x) {
+    for (;;) {
+        const int q = __hip_atomic_load(par + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (q == x) return x;
+        const int qq = __hip_atomic_load(par + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (qq != q) __hip_atomic_store(par + x, qq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        x = qq;
+    }
+}
+
+__global__ __launch_bounds__(512) void ccl_union_band_kernel(const CclParams p) {
     const CclPage &g = p.pg[blockIdx.y];
     const int n = g.row_off[g.h];
-    if (n > g.cap) return;
-    for (int j = int(blockIdx.x) * 256 + int(threadIdx.x); j < n; j += int(gridDim.x) * 256) {
-        const int y = g.ry[j];
-        if (y == 0) continue;
-        const int lo = g.row_off[y - 1], hi = g.row_off[y];
-        const int a0 = g.x0[j], a1 = g.x1[j];
-        // First run above whose right end reaches a0 - 1 (right ends increase along a row).
+    const int y0 = int(blockIdx.x) * CCL_BAND;
+    if (n > g.cap || y0 >= g.h) return;
+    const int y1 = min(g.h, y0 + CCL_BAND), r0 = g.row_off[y0], nb = g.row_off[y1] - r0;
+    const int tid = threadIdx.x;
+    if (nb > CCL_BAND_CAP) {
+        for (int j = r0 + tid; j < r0 + nb; j += 512) {
+            const int y = g.ry[j];
+            if (y > y0) ccl_join_above(g, j, y);
+        }
+        return;
+    }
+    __shared__ uint16_t s_x0[CCL_BAND_CAP], s_x1[CCL_BAND_CAP];
+    __shared__ uint8_t s_row[CCL_BAND_CAP];  // row within the band
+    __shared__ int s_par[CCL_BAND_CAP];
+    __shared__ int s_off[CCL_BAND + 1];      // band-local index of each row's first run
+    for (int k = tid; k < nb; k += 512) {
+        s_x0[k] = g.x0[r0 + k];
+        s_x1[k] = g.x1[r0 + k];
+        s_row[k] = uint8_t(g.ry[r0 + k] - y0);
+        s_par[k] = k;
+    }
+    for (int t = tid; t <= y1 - y0; t += 512) s_off[t] = g.row_off[y0 + t] - r0;
+    __syncthreads();
+    for (int k = tid; k < nb; k += 512) {
+        const int yl = s_row[k];
+        if (yl == 0) continue;
+        const int lo = s_off[yl - 1], hi = s_off[yl];
+        const int a0 = s_x0[k], a1 = s_x1[k];
         int l = lo, r = hi;
         while (l < r) {
             const int m = (l + r) >> 1;
-            if (int(g.x1[m]) + 1 >= a0) r = m;
+            if (int(s_x1[m]) + 1 >= a0) r = m;
             else l = m + 1;
         }
-        for (int i = l; i < hi && int(g.x0[i]) <= a1 + 1; i++) {
-            int u = i, v = j;
+        for (int i = l; i < hi && int(s_x0[i]) <= a1 + 1; i++) {
+            int u = i, v = k;
             for (;;) {
-                u = ccl_find(g.root, u);
-                v = ccl_find(g.root, v);
+                u = ccl_find_lds(s_par, u);
+                v = ccl_find_lds(s_par, v);
                 if (u == v) break;
                 if (u > v) {
                     const int t = u;
                     u = v;
                     v = t;
                 }
-                // Link root v under the smaller root u, if v is still a root.
-                if (atomicCAS(g.root + v, v, u) == v) break;
+                if (atomicCAS(s_par + v, v, u) == v) break;
             }
         }
     }
+    __syncthreads();
+    // No links are made any more: a plain walk to the band root.
+    for (int k = tid; k < nb; k += 512) {
+        int x = k;
+        while (s_par[x] != x) x = s_par[x];
+        g.root[r0 + k] = r0 + x;
+    }
+}
+
+// The first row of every band but the first, joined with the last row of the band above (the
+// parents are then at most one link from a band root within each band).
+__global__ __launch_bounds__(256) void ccl_union_bounds_kernel(const CclParams p) {
+    const CclPage &g = p.pg[blockIdx.y];
+    const int n = g.row_off[g.h];
+    const int y = (int(blockIdx.x) + 1) * CCL_BAND;
+    if (n > g.cap || y >= g.h) return;
+    for (int j = g.row_off[y] + int(threadIdx.x); j < g.row_off[y + 1]; j += 256) ccl_join_above(g, j, y);
 }
 
 __global__ __launch_bounds__(256) void ccl_flatten_kernel(const CclParams p) {
@@ -267,7 +353,9 @@ void ccl_runs(const CclPage *pages, int count, hipStream_t s) {
         hipLaunchKernelGGL(ccl_runs_kernel, rows, dim3(256), 0, s, p);
         // A thread per run (up to the capacity; threads past a page's run count return).
         const dim3 runs_grid(unsigned(std::min(2048, (maxcap + 255) / 256)), unsigned(cnt));
-        hipLaunchKernelGGL(ccl_union_kernel, runs_grid, dim3(256), 0, s, p);
+        const unsigned bands = unsigned((maxh + CCL_BAND - 1) / CCL_BAND);
+        hipLaunchKernelGGL(ccl_union_band_kernel, dim3(bands, unsigned(cnt)), dim3(512), 0, s, p);
+        if (bands > 1) hipLaunchKernelGGL(ccl_union_bounds_kernel, dim3(bands - 1, unsigned(cnt)), dim3(256), 0, s, p);
         hipLaunchKernelGGL(ccl_flatten_kernel, runs_grid, dim3(256), 0, s, p);
         hipLaunchKernelGGL(ccl_comps_kernel, runs_grid, dim3(256), 0, s, p);
         hipLaunchKernelGGL(ccl_extremes_kernel, runs_grid, dim3(256), 0, s, p);
