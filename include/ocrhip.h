@@ -60,6 +60,18 @@ int ocr_memcpy_d2h(ocr_ctx *ctx, void *dst, const void *src, size_t bytes);
 void *ocr_host_alloc(ocr_ctx *ctx, size_t bytes);
 int ocr_host_free(ocr_ctx *ctx, void *p);
 
+/* ---- Page images ------------------------------------------------------------------------------
+ * The reference's page decode, image::open(p)?.into_rgb8() (src/bin/ocr-bench.rs:424, also
+ * src/bin/stages.rs:94 and src/bin/ppocr-bench.rs:69; image 0.25.10 over png 0.18.1), for PNG
+ * files given as their bytes. ocr_png_dims reads the signature and the IHDR chunk. ocr_png_decode
+ * writes w x h RGB triples, row by row, into rgb (cap bytes, at least w * h * 3; memory from
+ * ocr_host_alloc is uploaded by the page pipeline with no staging copy). Every colour type, bit
+ * depth and Adam7 interlacing: grey replicated, alpha dropped, 16-bit samples rounded to 8 bits.
+ * Chunk CRCs are checked. Host only and thread-safe, so pages decode side by side on the caller's
+ * threads; no context is needed. */
+int ocr_png_dims(const uint8_t *png, size_t n, uint32_t *w, uint32_t *h);
+int ocr_png_decode(const uint8_t *png, size_t n, uint8_t *rgb, size_t cap, uint32_t *w, uint32_t *h);
+
 /* ---- A graph parsed on the host ---------------------------------------------------------------
  * The reference parses the .onnx file on its own side (Onnx::load, src/onnx.rs:88-123) and hands
  * the parsed Onnx to the constructors (Detector::new(&Gpu, &Onnx), src/gpu.rs:1385). These

@@ -265,6 +265,35 @@ def test_pipeline_host_pinned_and_device_pages_agree(detector, recognizer, ctx):
     assert [p.texts(k) for k in range(len(sets[0]))] == want[0]
 
 
+def test_pipeline_from_png_pages(detector, recognizer, ctx):
+    # Pages as PNG files (the reference decodes them with image::open(p)?.into_rgb8() before its
+    # timed run, ocr-bench.rs:421-428): decoded by the library on host threads straight into
+    # page-locked memory, then run; the text is that of the same pixels given as arrays. One page
+    # is greyscale (decoded to R = G = B).
+    import io
+    Image = pytest.importorskip("PIL.Image")
+    pages = [synth.page(s) for s in (40, 41)]
+    pages.append(np.repeat(synth.page(42)[:, :, 1:2], 3, axis=2))
+    pngs = []
+    for i, pg in enumerate(pages):
+        buf = io.BytesIO()
+        (Image.fromarray(pg[:, :, 0], "L") if i == 2 else Image.fromarray(pg, "RGB")).save(buf, "PNG")
+        pngs.append(buf.getvalue())
+    p = ocrhip.Pipeline(detector, recognizer, merge=2, det_batch=2)
+    p.run(pages)
+    want = [p.texts(k) for k in range(len(pages))]
+    pinned = [ctx.host_array(ocrhip.png_dims(b)[::-1] + (3,)) for b in pngs]
+    import concurrent.futures as cf
+    with cf.ThreadPoolExecutor(3) as ex:
+        decoded = list(ex.map(lambda a: ocrhip.decode_png(a[0], out=a[1].array), zip(pngs, pinned)))
+    for d, pg in zip(decoded, pages):
+        np.testing.assert_array_equal(d, pg)
+    print("pages decoded from PNG into pinned memory", flush=True)
+    p.run([a.array for a in pinned])
+    assert [p.texts(k) for k in range(len(pages))] == want
+    assert sum(len(t[0]) for t in want) > 40
+
+
 def test_pipeline_page_error_other_pages_finish(detector, recognizer, monkeypatch):
     # A page whose layout fails reports its error; the other pages of its recognition pass and
     # of the other passes finish with the text of a clean run (ocr-bench.rs:277-281, 303-307).

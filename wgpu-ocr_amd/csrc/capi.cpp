@@ -9,6 +9,7 @@
 #include "noalloc.h"
 #include "nd.h"
 #include "pipeline.h"
+#include "png.h"
 #include "crop.h"
 #include "pp_pipeline.h"
 
@@ -218,6 +219,24 @@ int ocr_host_free(ocr_ctx *ctx, void *p) {
         ctx->ctx->bind();
         ctx->ctx->sync();
         OCR_HIP(hipHostFree(p));
+    });
+}
+
+int ocr_png_dims(const uint8_t *png, size_t n, uint32_t *w, uint32_t *h) {
+    return guard([&] {
+        need(w, "w");
+        need(h, "h");
+        const PngHeader hd = png_header(png, n);
+        *w = hd.w;
+        *h = hd.h;
+    });
+}
+
+int ocr_png_decode(const uint8_t *png, size_t n, uint8_t *rgb, size_t cap, uint32_t *w, uint32_t *h) {
+    return guard([&] {
+        const PngHeader hd = png_decode_rgb(png, n, rgb, cap);
+        if (w) *w = hd.w;
+        if (h) *h = hd.h;
     });
 }
 

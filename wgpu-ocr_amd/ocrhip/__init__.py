@@ -44,6 +44,8 @@ SIGNATURES = {
     "ocr_memcpy_d2h": (ctypes.c_int, [P, P, P, SZ]),
     "ocr_host_alloc": (P, [P, SZ]),
     "ocr_host_free": (ctypes.c_int, [P, P]),
+    "ocr_png_dims": (ctypes.c_int, [P, SZ, PU32, PU32]),
+    "ocr_png_decode": (ctypes.c_int, [P, SZ, P, SZ, PU32, PU32]),
     "ocr_detector_new": (P, [P, ctypes.c_char_p]),
     "ocr_detector_free": (None, [P]),
     "ocr_detect_page": (ctypes.c_int, [P, P, U32, U32, F32, P]),
@@ -550,6 +552,44 @@ def probe_stop(family: str) -> dict:
     _check(lib().ocr_probe_stop(family.encode(), ctypes.byref(calls), ctypes.byref(ms), ctypes.byref(flops),
                                 ctypes.byref(nbytes)))
     return {"calls": calls.value, "ms": ms.value, "flops": flops.value, "bytes": nbytes.value}
+
+
+# ---- page images (no GPU) ------------------------------------------------------------------
+def _png_bytes(src) -> np.ndarray:
+    if isinstance(src, (str, os.PathLike)):
+        with open(src, "rb") as f:
+            src = f.read()
+    return np.frombuffer(src, np.uint8) if not isinstance(src, np.ndarray) else np.ascontiguousarray(src, np.uint8)
+
+
+def png_dims(src) -> tuple:
+    """(width, height) of a PNG (a path or its bytes) from its IHDR chunk (ocr_png_dims)."""
+    data = _png_bytes(src)
+    w, h = ctypes.c_uint32(), ctypes.c_uint32()
+    _check(lib().ocr_png_dims(_ptr(data), data.size, ctypes.byref(w), ctypes.byref(h)))
+    return w.value, h.value
+
+
+def decode_png(src, out: np.ndarray | None = None) -> np.ndarray:
+    """A PNG page (a path or its bytes) as an [h, w, 3] uint8 RGB array, as the reference's
+    image::open(p)?.into_rgb8() (ocr-bench.rs:424). out, if given, is a C-contiguous uint8 array
+    of at least w * h * 3 bytes (page-locked memory from Context.host_array suits the pipeline);
+    the result is then a view of it."""
+    data = _png_bytes(src)
+    w, h = png_dims(data)
+    if out is None:
+        out = np.empty((h, w, 3), np.uint8)
+    if out.dtype != np.uint8 or not out.flags.c_contiguous:
+        raise OcrError("decode_png: out must be a C-contiguous uint8 array")
+    _check(lib().ocr_png_decode(_ptr(data), data.size, _ptr(out), out.nbytes, None, None))
+    return out.reshape(-1)[: w * h * 3].reshape(h, w, 3)
+
+
+def decode_pngs(srcs, threads: int = 8) -> list:
+    """Several PNG pages decoded side by side on host threads (the decode releases the GIL)."""
+    import concurrent.futures as cf
+    with cf.ThreadPoolExecutor(max(1, threads)) as ex:
+        return list(ex.map(decode_png, srcs))
 
 
 # ---- host geometry (no GPU) -----------------------------------------------------------------
