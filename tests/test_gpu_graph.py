@@ -47,7 +47,7 @@ def conv(g, x, cin, cout, k=(3, 3), pads=(1, 1, 1, 1), strides=(1, 1), group=1, 
 
 
 @pytest.mark.parametrize("cin,cout,h,w", [(5, 7, 9, 11), (16, 32, 20, 33), (40, 70, 6, 21), (64, 64, 8, 50),
-                                          (128, 256, 4, 37), (32, 16, 33, 17)])
+                                          (128, 256, 4, 37), (32, 16, 33, 17), (64, 32, 19, 41), (48, 20, 12, 35)])
 def test_conv3x3_mfma(ctx, tmp_path, cin, cout, h, w):
     p = build(tmp_path, "c", lambda g, x: conv(g, x, cin, cout, act="Relu"), (2, cin, h, w))
     check(ctx, p, RNG.standard_normal((2, cin, h, w)).astype(np.float32))
@@ -223,7 +223,8 @@ def test_shape_errors(ctx, tmp_path):
 
 @pytest.mark.parametrize("cin,cout,h,w,pool,two", [(32, 64, 17, 45, (2, 2), False), (64, 128, 16, 37, (2, 1), False),
                                                    (128, 256, 4, 53, (2, 1), False), (16, 97, 9, 23, (2, 1), True),
-                                                   (256, 128, 13, 19, (2, 2), True), (20, 48, 31, 70, (2, 2), False)])
+                                                   (256, 128, 13, 19, (2, 2), True), (20, 48, 31, 70, (2, 2), False),
+                                                   (64, 32, 15, 29, (2, 2), True)])
 def test_conv_pool_fusion_shapes(ctx, tmp_path, cin, cout, h, w, pool, two):
     """MaxPool fused into the conv epilogue over odd sizes, several channel blocks (cout not a
     multiple of the block), several input slices and partial slices; `two`: the full output is
