@@ -35,7 +35,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int H = 256, LINES = 8, HROW = H + 8;  // LDS row of the B operand: 256 units + padding
+// LDS row of the B operand: 256 units + 16 of padding (34 16-byte units, so the B reads of a step
+// meet distinct bank groups in every access pass and the state writes distinct banks).
+constexpr int H = 256, LINES = 8, HROW = H + 16;
 
 // exp through the hardware base-2 exponential; 1/x through the hardware reciprocal (1 ulp).
 __device__ inline float fast_exp(float v) { return __builtin_amdgcn_exp2f(v * 1.4426950408889634f); }
@@ -49,7 +51,9 @@ __device__ inline float sel_bits(unsigned m, float a, float b) {
 
 // Lane r of each 16-lane row receives the value of lane (r + 8) mod 16 (DPP row_ror:8).
 __device__ inline float ror8(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));
+    // (a row rotation has no out-of-row lanes, so bound_ctrl changes nothing; with it the
+    // compiler folds the move into the add that uses it)
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, true));
 }
 
 template <int UPW>
