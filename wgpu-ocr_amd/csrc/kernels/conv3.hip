@@ -33,10 +33,12 @@
 // the reads of another. Tile bookkeeping is incremental and uniform, addresses are 32-bit
 // offsets from per-tile bases: the VALU work per MFMA stays small.
 //
-// Work split: a persistent workgroup of 8 wavefronts (2 per SIMD) per CU walks a contiguous run
-// of TH x TW output tiles (runs of neighbouring tiles on one XCD) for one block of BN output
-// channels; wavefront (wm, wn) computes 64 pixels (four 2 x 8 row tiles, each four 2 x 2
-// squares, so a fused MaxPool reduces a lane's own accumulators) x 16 * NT channels.
+// Work split: a persistent workgroup of 16 wavefronts (4 per SIMD, so the matrix core of a SIMD
+// has another wavefront to serve while one waits on LDS or its DMA) per CU walks a contiguous
+// run of TH x TW output tiles (runs of neighbouring tiles on one XCD) for one block of BN output
+// channels; a tile is 16 row tiles of 2 x 8 pixels (each four 2 x 2 squares, so a fused MaxPool
+// reduces a lane's own accumulators), and wavefront (wm, wn) of the WM x WN grid computes 16 / WM
+// of them x 16 * NT channels.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -54,13 +56,10 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int MT = 4;                // row tiles (of 16 pixels) per wavefront
+constexpr int RTT = 16;              // row tiles (of 16 pixels) per tile
 constexpr int HMAX = 51;             // halo staging size in 1 KiB blocks (8 pixels of 32 channels)
 constexpr int HPX = HMAX * 8;        // halo pixels at most
-constexpr int NHI = (HMAX + 7) / 8;  // halo DMA instructions per wavefront and slice
 constexpr int HSP = 1632;            // units (16 bytes) of each hi / lo plane: halo rows x rs at most
-constexpr int NSI = 4;               // split items (pixel, 8 channels) per thread and slice
-static_assert((HPX + 15) / 16 * 64 <= NSI * 512, "split items fit");
 
 // One segment: a tensor of n images of width w (output width ow, pooled pow_); every segment of
 // a launch has the same height, channels and weights (the width batches of one recogniser pass).
@@ -110,10 +109,14 @@ struct Seq {
 // tap of every slice is copied into W0 once, a slice's three kernel rows run without a barrier
 // between them, and the next slice's halo has the whole slice to land.
 template <int WM, int WN, int NT, int ACT, int RC>
-__global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
-    constexpr int NTW = NT * WN, WBLK = 3 * NTW, NWI = (WBLK + 7) / 8;
-    constexpr int WRB = RC ? 9 * RC * NTW : WBLK, NRI = (WRB + 7) / 8;
-    static_assert(WM * WN == 8, "8 wavefronts");
+__global__ __launch_bounds__(64 * WM * WN, 1) void conv3_dma_kernel(C3Params p) {
+    constexpr int NW = WM * WN, MT = RTT / WM;  // wavefronts; row tiles per wavefront
+    constexpr int NTW = NT * WN, WBLK = 3 * NTW, NWI = (WBLK + NW - 1) / NW;
+    constexpr int WRB = RC ? 9 * RC * NTW : WBLK, NRI = (WRB + NW - 1) / NW;
+    constexpr int NHI = (HMAX + NW - 1) / NW;         // halo DMA instructions per wavefront and slice
+    constexpr int NSI = (HPX + 16 * NW - 1) / (16 * NW);  // split items (pixel, 8 channels) per thread
+    static_assert(NW == 8 || NW == 16, "8 or 16 wavefronts");
+    static_assert(RTT % WM == 0 && MT % 2 == 0, "whole row-tile pairs per wavefront");
     static_assert(NWI + NHI <= 3 * MT, "a stage's DMA instructions fit its steps");
     __shared__ __align__(16) half8 W0[WRB * 64];
     __shared__ __align__(16) half8 W1[RC ? 64 : WBLK * 64];
@@ -149,14 +152,13 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     // This lane's halo slot (row, column, channel part) for each halo DMA instruction; row -1
     // for padding slots. Unit U = 8 P + (u ^ ((P >> 1) & 1)) of HF holds channels 4u..4u+3 of
     // slot P = row * hw + column.
-    int dhy[NHI], dhx[NHI], dch[NHI];
+    // Packed in one register: column (bits 0-7), row (8-15), channel quad (16-18); -1: padding.
+    int dhs[NHI];
 #pragma unroll
     for (int i = 0; i < NHI; i++) {
-        const int b = min(i * 8 + wave, p.hblocks - 1), U = b * 64 + lane, P = U >> 3;
+        const int b = min(i * NW + wave, p.hblocks - 1), U = b * 64 + lane, P = U >> 3;
         const int hy = P / p.hw, hx = P - hy * p.hw;
-        dhy[i] = P < p.npx ? hy : -1;
-        dhx[i] = hx;
-        dch[i] = 4 * ((U & 7) ^ ((P >> 1) & 1));
+        dhs[i] = P < p.npx ? hx | hy << 8 | ((U & 7) ^ ((P >> 1) & 1)) << 16 : -1;
     }
     // This thread's split items: item k of lane l in wavefront w covers pixel
     // (l & 3) + 4 (l >> 4) + 16 (w + 8 k), channels 8q..8q+7 with q = (l >> 2) & 3: the four
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     int sf[NSI], ss[NSI];
 #pragma unroll
     for (int k = 0; k < NSI; k++) {
-        const int P = (lane & 3) + 4 * (lane >> 4) + 16 * (wave + 8 * k), q = (lane >> 2) & 3;
+        const int P = (lane & 3) + 4 * (lane >> 4) + 16 * (wave + NW * k), q = (lane >> 2) & 3;
         const int hy = P / p.hw, hx = P - hy * p.hw;
         sf[k] = 8 * P + ((2 * q) ^ ((P >> 1) & 1));
         ss[k] = P < p.npx ? hy * p.rs + hx * 4 + (q ^ ((hy & 1) << 1)) : -1;
@@ -207,13 +209,13 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
     unsigned woff[NWI];
 #pragma unroll
     for (int i = 0; i < NWI; i++) {
-        const int b = min(i * 8 + wave, WBLK - 1), kx = b / NTW, j = b - kx * NTW, nt = min(nt0 + j, p.ntiles - 1);
+        const int b = min(i * NW + wave, WBLK - 1), kx = b / NTW, j = b - kx * NTW, nt = min(nt0 + j, p.ntiles - 1);
         woff[i] = (unsigned(nt * p.chunks * 9 + kx) * 64u + unsigned(lane)) * 16u;
     }
     // LDS byte addresses of the DMA destinations (the copies take them, not pointers).
     const unsigned w0a = lds_addr(W0), w1a = lds_addr(W1), hfa = lds_addr(HF);
     auto dma_w = [&](unsigned dst, int c, int ky, int i) __attribute__((always_inline)) {
-        const int b = min(i * 8 + wave, WBLK - 1);
+        const int b = min(i * NW + wave, WBLK - 1);
         const char *base = reinterpret_cast<const char *>(p.wt) + size_t(c * 9 + ky * 3) * 1024;
         dma16s_to(base, woff[i], dst + unsigned(b) * 1024u);
     };
@@ -230,10 +232,11 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
                     p.cin - s.c * 32};
     };
     auto dma_h = [&](const Halo &hl, int i) __attribute__((always_inline)) {
-        const int b = min(i * 8 + wave, p.hblocks - 1);
-        const int iy = hl.iy0 + dhy[i], ix = hl.ix0 + dhx[i];
-        const bool ok = dhy[i] >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(hl.w) && dch[i] < hl.cleft;
-        const int off = ok ? (iy * hl.w + ix) * p.xcs + dch[i] : 0;
+        const int b = min(i * NW + wave, p.hblocks - 1);
+        const int d = dhs[i], ch = 4 * ((d >> 16) & 7);
+        const int iy = hl.iy0 + ((d >> 8) & 255), ix = hl.ix0 + (d & 255);
+        const bool ok = d >= 0 && unsigned(iy) < unsigned(p.h) && unsigned(ix) < unsigned(hl.w) && ch < hl.cleft;
+        const int off = ok ? (iy * hl.w + ix) * p.xcs + ch : 0;
         const void *src = ok ? static_cast<const void *>(hl.base + unsigned(off)) : static_cast<const void *>(p.zero);
         dma16_to(src, hfa + unsigned(b) * 1024u);
     };
@@ -462,7 +465,7 @@ __global__ __launch_bounds__(512, 1) void conv3_dma_kernel(C3Params p) {
         const int nwb = 9 * p.chunks * NTW;
 #pragma unroll
         for (int i = 0; i < NRI; i++) {
-            const int b = min(i * 8 + wave, nwb - 1), j = b % NTW, tap = b / NTW;
+            const int b = min(i * NW + wave, nwb - 1), j = b % NTW, tap = b / NTW;
             const int c = tap / 9, t9 = tap - c * 9, nt = min(nt0 + j, p.ntiles - 1);
             dma16_to(p.wt + (size_t(nt * p.chunks + c) * 9 + t9) * 64 + lane, w0a + unsigned(b) * 1024u);
         }
@@ -566,10 +569,10 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     p.cout = cout;
     p.chunks = pk.chunks;
     p.bias = a.bias;
-    // Tile shape (16 blocks of 2 x 8 pixels) and channel block (NT n-tiles a wavefront) chosen
+    // Tile shape (16 blocks of 2 x 8 pixels) and channel block (32 nt channels) chosen
     // together. A workgroup walks ceil(tiles / runs) tiles, runs = CUs / blocks, so the launch
-    // takes that many rounds of a tile each; a tile costs about (1.5 + NT) units (per-stage
-    // overhead, then matrix work per n-tile: measured on the detector's 256 -> 128 layer) times
+    // takes that many rounds of a tile each; a tile costs about (1.5 + nt) units (per-stage
+    // overhead, then matrix work per 32 channels: measured on the detector's 256 -> 128 layer) times
     // its halo's share of extra pixels. Few tiles (the detector's deep levels at a few pages)
     // favour narrower blocks and shapes whose count fits one round; many tiles the widest block.
     p.tm = a.tm;
@@ -636,13 +639,15 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     ProbeScope probe("conv3x3_dma", s, flops, bytes);
     auto launch = [&](auto ACTc) {
         constexpr int A = decltype(ACTc)::value;
-        const dim3 gd{unsigned(grid)}, bd{512};
-        if (nt == 4) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 4, A, 0>), gd, bd, 0, s, p);
-        else if (nt == 2 && p.chunks == 1) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 2, A, 1>), gd, bd, 0, s, p);
-        else if (nt == 2) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 2, A, 0>), gd, bd, 0, s, p);
-        else if (p.chunks == 1) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 1, A, 1>), gd, bd, 0, s, p);
-        else if (p.chunks == 2) hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 1, A, 2>), gd, bd, 0, s, p);
-        else hipLaunchKernelGGL((conv3_dma_kernel<4, 2, 1, A, 0>), gd, bd, 0, s, p);
+        // 16 wavefronts (4 a SIMD): 128-channel blocks as 4 x 4 wavefronts of 2 n-tiles, 64-channel
+        // blocks as 4 x 4 of one, 32-channel blocks as 8 x 2 of one (two row tiles each).
+        const dim3 gd{unsigned(grid)}, bd{1024};
+        if (nt == 4) hipLaunchKernelGGL((conv3_dma_kernel<4, 4, 2, A, 0>), gd, bd, 0, s, p);
+        else if (nt == 2 && p.chunks == 1) hipLaunchKernelGGL((conv3_dma_kernel<4, 4, 1, A, 1>), gd, bd, 0, s, p);
+        else if (nt == 2) hipLaunchKernelGGL((conv3_dma_kernel<4, 4, 1, A, 0>), gd, bd, 0, s, p);
+        else if (p.chunks == 1) hipLaunchKernelGGL((conv3_dma_kernel<8, 2, 1, A, 1>), gd, bd, 0, s, p);
+        else if (p.chunks == 2) hipLaunchKernelGGL((conv3_dma_kernel<8, 2, 1, A, 2>), gd, bd, 0, s, p);
+        else hipLaunchKernelGGL((conv3_dma_kernel<8, 2, 1, A, 0>), gd, bd, 0, s, p);
     };
     if (a.act == ACT_RELU) launch(std::integral_constant<int, ACT_RELU>{});
     else if (a.act == ACT_SIGMOID) launch(std::integral_constant<int, ACT_SIGMOID>{});
