@@ -4,6 +4,7 @@
 // 303-307), the ordering rules hold, and nothing deadlocks with few workers. Built and run by
 // tests/test_pipeline_core.py under AddressSanitizer + UndefinedBehaviorSanitizer and under
 // ThreadSanitizer.
+#include <algorithm>
 #include "pipeline_core.h"
 
 #include <atomic>
@@ -85,7 +86,8 @@ struct Hooks final : PipelineHooks {
     std::vector<int> staged_at, detected_at, waited_at, laid_at, rec_at, dec_at;
     std::vector<std::vector<char>> rec_ok;
     int clock = 0;
-    bool jitter, lookahead = false;
+    bool jitter, lookahead = false, interleave = false;
+    int polled_groups = 0;  // groups a recognition pass queued between its stages
     Hooks(const PipelinePlan &plan, Faults faults, unsigned seed, bool jit)
         : P(plan), f(faults), rng(seed), jitter(jit) {
         staged_at.assign(size_t(P.groups()), -1);
@@ -156,6 +158,18 @@ struct Hooks final : PipelineHooks {
             }
         nap();
         if (r == f.recognize) throw std::runtime_error("recognize fault");
+        if (interleave) {
+            // Three stages, the groups staged meanwhile queued between them.
+            CHECK(bool(poll_detections), "recognize(%d): no poll_detections", r);
+            for (int k = 0; k < 3 && poll_detections; k++) {
+                const int before = int(std::count_if(detected_at.begin(), detected_at.end(), [](int t) { return t >= 0; }));
+                const bool any = poll_detections();
+                const int after = int(std::count_if(detected_at.begin(), detected_at.end(), [](int t) { return t >= 0; }));
+                if (f.detect < 0) CHECK(any == (after > before), "recognize(%d): poll result %d, %d -> %d groups", r, int(any), before, after);
+                polled_groups += after - before;
+                nap();
+            }
+        }
         rec_ok[size_t(r)] = ok;
         rec_at[size_t(r)] = tick();
     }
@@ -179,11 +193,12 @@ std::vector<char> expected_failed(const PipelinePlan &P, const Faults &f) {
     return bad;
 }
 
-void run_case(const char *name, int npages, int merge, int det_batch, int workers, Faults f, unsigned seed,
-              bool jitter, bool lookahead = false) {
+int run_case(const char *name, int npages, int merge, int det_batch, int workers, Faults f, unsigned seed,
+             bool jitter, bool lookahead = false, bool interleave = false) {
     const PipelinePlan P = plan_pipeline(npages, merge, det_batch);
     Hooks H(P, f, seed, jitter);
     H.lookahead = lookahead;
+    H.interleave = interleave;
     std::vector<std::string> err;
     {
         Pool pool(workers);
@@ -214,6 +229,8 @@ void run_case(const char *name, int npages, int merge, int det_batch, int worker
     }
     for (int p = 0; p < npages; p++)
         if (!bad[size_t(p)]) CHECK(H.laid_at[size_t(p)] >= 0, "%s: page %d not laid out", name, p);
+    CHECK(!H.poll_detections, "%s: poll_detections left set after the run", name);
+    return H.polled_groups;
 }
 
 }  // namespace
@@ -278,6 +295,22 @@ int main() {
         Faults g;
         g.layout = 7;
         run_case("lookahead layout fault", 12, 4, 2, 2, g, 221, true, true);
+    }
+    // Interleaved: recognition passes queue the groups staged meanwhile between their stages.
+    {
+        int polled = 0;
+        for (unsigned seed = 300; seed < 320; seed++)
+            polled += run_case("interleave", 12 + int(seed % 6), 3, 2, 1 + int(seed % 3), none, seed, true, false, true);
+        for (unsigned seed = 320; seed < 330; seed++)
+            polled += run_case("interleave merge 6", 12 + int(seed % 7), 6, 2, 1 + int(seed % 3), none, seed, true,
+                               false, true);
+        CHECK(polled > 0, "interleave: no group was ever queued from inside a pass");
+        Faults d;
+        d.detect = 4;
+        run_case("interleave detect fault", 12, 3, 2, 2, d, 330, true, false, true);
+        Faults st;
+        st.stage = 5;
+        run_case("interleave stage fault", 12, 3, 2, 2, st, 331, true, false, true);
     }
     if (failures) {
         std::fprintf(stderr, "%d check(s) failed\n", failures);

@@ -170,7 +170,8 @@ Recognizer::Dims Recognizer::dims(const Batch *batches, int count) const {
     return d;
 }
 
-void Recognizer::recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens) {
+void Recognizer::recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens,
+                                  const std::function<void()> &between) {
     const hipStream_t st = ctx_.stream();
     const Dims d = dims(batches, count);
     if (d.ntot == 0) return;
@@ -239,6 +240,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         avgpool_t(feats.data(), count, pool_kh_, X.as<float>(), d.ntot, st);
     }
     trunks.clear();
+    if (between) between();
     DBuf G(&ctx_, size_t(M) * 1536 * sizeof(float));
     DBuf Y[2] = {DBuf(&ctx_, size_t(M) * 512 * sizeof(float)), DBuf(&ctx_, size_t(M) * 512 * sizeof(float))};
     const float *in = X.as<float>();
@@ -259,6 +261,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd, ntot, tmax, steps, st);
         in = Y[l].as<float>();
         in_c = 512;
+        if (between) between();
     }
     ConvArgs ca;
     ca.x = Act{const_cast<float *>(in), 1, 1, P, 512, 512};

@@ -1,6 +1,7 @@
 // The ocrs detection and recognition models on the GPU (src/gpu.rs:1380-1603).
 #pragma once
 
+#include <functional>
 #include <memory>
 #include <vector>
 
@@ -44,8 +45,11 @@ class Recognizer {
     // Recognizer::recognize (gpu.rs:1510-1602) with the batches' data in device memory.
     // logits: device [tmax][ntot][classes] raw logits (rows t >= lens[line] are not defined);
     // best: device [tmax][ntot] arg-max per row (last index on ties), may be null; lens: host
-    // [ntot], every line's step count (its batch's trunk width, gpu.rs:1552).
-    void recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens);
+    // [ntot], every line's step count (its batch's trunk width, gpu.rs:1552). between, if given,
+    // is called after the trunk's and after each GRU layer's kernels are queued (a caller that
+    // interleaves other work on the stream).
+    void recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens,
+                          const std::function<void()> &between = {});
     int classes() const { return classes_; }
     bool recurrent_exact() const { return r_exact_; }
     uint32_t lines() const { return lines_; }

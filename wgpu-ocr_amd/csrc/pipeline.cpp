@@ -280,6 +280,7 @@ struct PipelineRun final : PipelineHooks {
     const Clock::time_point t0;
     // OCR_PIPE_TRACE=1: host timestamps of the steps, printed to stderr at the end.
     bool tracing;
+    bool interleave = false;  // recognition passes queued in stages, detections between them
     // OCR_PIPE_FAIL_LAYOUT=p: page p's layout fails (tests of the per-page error path).
     int fail_layout = -1;
     // With tracing: GPU timestamps (events on the streams) of each upload group, detection group
@@ -589,7 +590,30 @@ struct PipelineRun final : PipelineHooks {
         DBuf logits(&ctx, size_t(d.tmax) * d.ntot * d.classes * sizeof(float));
         R.best = DBuf(&ctx, size_t(d.tmax) * d.ntot * sizeof(uint32_t));
         R.best.used_on(I.copy);
-        I.rec.recognize_device(rb.data(), int(rb.size()), logits.as<float>(), R.best.as<uint32_t>(), R.lens.data());
+        // Between the recogniser's stages (trunk, each GRU layer): the groups staged meanwhile
+        // are queued right behind the stage just queued, and the next stage waits until the one
+        // before it has finished, so at most one stage is ahead of a group that lands late.
+        std::vector<hipEvent_t> stage_ev;
+        auto between = [&]() {
+            if (!interleave) return;
+            hipEvent_t e = nullptr;
+            OCR_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+            OCR_HIP(hipEventRecord(e, st));
+            stage_ev.push_back(e);
+            if (poll_detections) poll_detections();
+            if (stage_ev.size() < 2) return;
+            const hipEvent_t prev = stage_ev[stage_ev.size() - 2];
+            for (;;) {
+                const hipError_t q = hipEventQuery(prev);
+                if (q == hipSuccess) break;
+                if (q != hipErrorNotReady) OCR_HIP(q);
+                if (poll_detections) poll_detections();
+                std::this_thread::sleep_for(std::chrono::microseconds(20));
+            }
+        };
+        I.rec.recognize_device(rb.data(), int(rb.size()), logits.as<float>(), R.best.as<uint32_t>(), R.lens.data(),
+                               between);
+        for (hipEvent_t e : stage_ev) OCR_HIP(hipEventDestroy(e));
         gpu_span("recognize " + std::to_string(r), ga, gpu_event(st));
         mark("rec " + std::to_string(r) + " queued");
         // The arg-max goes to the host on the copy stream, so the next pass's kernels do not
@@ -645,8 +669,14 @@ void Pipeline::run_pages(const uint8_t *const *src, bool on_host, const int *w, 
     int failed = 0;
     {
         PipelineRun R(I, plan, src, on_host, w, h, pages_);
+        // Pages from host memory reach the device one group at a time; a recognition pass then
+        // goes out as soon as its pages are laid out, in stages with the groups that have landed
+        // meanwhile queued between them (OCR_PIPE_INTERLEAVE=0: the whole pass at once, after
+        // the next pass's detections). Device-resident pages keep the lookahead order.
+        const char *il = std::getenv("OCR_PIPE_INTERLEAVE");
+        R.interleave = on_host && !(il && std::atoi(il) == 0);
         const char *la = std::getenv("OCR_PIPE_LOOKAHEAD");
-        const bool lookahead = la ? std::atoi(la) != 0 : I.opts.lookahead;
+        const bool lookahead = la ? std::atoi(la) != 0 : (R.interleave ? false : I.opts.lookahead);
         errs = run_schedule(plan, R, [&](std::function<void()> f) { I.workers.submit(std::move(f)); }, &busy,
                             lookahead);
         for (int p = 0; p < npages; p++) {

@@ -6,7 +6,9 @@
 //
 //   stager thread:  stage(g)        groups in order (the pages' bytes onto the device)
 //   main thread:    detect(g)       once g is staged; recognize(r) once pass r's pages are laid
-//                                   out (a staged detection goes first)
+//                                   out (a staged detection goes first); a pass may call
+//                                   poll_detections() between its stages to queue the groups
+//                                   staged meanwhile
 //   watcher thread: detect_wait(g)  groups in order, once queued
 //   worker threads: layout(p)       once p's group is detected and every page of the earlier
 //                                   passes is laid out; decode(r) once pass r is queued
@@ -76,6 +78,11 @@ class PipelineHooks {
     // ok[p - first page of r]: page p has a layout (pages without one are left out).
     virtual void recognize(int r, const std::vector<char> &ok) = 0;
     virtual void decode(int r, bool last) = 0;
+    // Set by run_schedule while it runs (main thread only): queues every detection group that is
+    // staged and not yet queued, returns whether it queued any. A recognition pass may call it
+    // between its stages, so that pages which reach the device meanwhile are detected after the
+    // stage in flight rather than after the whole pass.
+    std::function<bool()> poll_detections;
 };
 
 // Runs fn on a worker thread (the caller's pool); must not block the calling thread.
@@ -201,6 +208,42 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
     }
     // Main thread: detections as soon as staged, recognition passes as soon as laid out.
     int next_det = 0, next_rec = 0;
+    // Queues detection group g (next_det already moved past it, mu not held).
+    auto queue_group = [&](int g) {
+        std::string m;
+        try {
+            H.detect(g);
+        } catch (...) {
+            m = what(std::current_exception());
+        }
+        std::lock_guard<std::mutex> lk(mu);
+        if (!m.empty()) {
+            int p0, p1;
+            group_pages(g, p0, p1);
+            fail_pages(p0, p1, m);
+            group_failed[size_t(g)] = 1;
+        }
+        queued = next_det;
+        cv.notify_all();
+    };
+    H.poll_detections = [&]() -> bool {
+        bool any = false;
+        for (;;) {
+            int g;
+            {
+                std::lock_guard<std::mutex> lk(mu);
+                if (next_det >= ng || staged <= next_det) return any;
+                g = next_det++;
+                if (group_failed[size_t(g)]) {
+                    queued = next_det;
+                    cv.notify_all();
+                    continue;
+                }
+            }
+            queue_group(g);
+            any = true;
+        }
+    };
     while (next_rec < nr) {
         int do_det = -1, do_rec = -1;
         std::vector<char> pass_ok;
@@ -234,21 +277,7 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
             }
         }
         if (do_det >= 0) {
-            std::string m;
-            try {
-                H.detect(do_det);
-            } catch (...) {
-                m = what(std::current_exception());
-            }
-            std::lock_guard<std::mutex> lk(mu);
-            if (!m.empty()) {
-                int p0, p1;
-                group_pages(do_det, p0, p1);
-                fail_pages(p0, p1, m);
-                group_failed[size_t(do_det)] = 1;
-            }
-            queued = next_det;
-            cv.notify_all();
+            queue_group(do_det);
             continue;
         }
         const int r = do_rec, p0 = P.pass_p0[size_t(r)], p1 = P.pass_p0[size_t(r) + 1];
@@ -285,6 +314,7 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
             cv.notify_all();
         });
     }
+    H.poll_detections = nullptr;
     // Detections queued after the last pass (none in a valid plan), then every task and thread.
     {
         std::unique_lock<std::mutex> lk(mu);
