@@ -32,6 +32,9 @@ __device__ inline float grey_px(const uint8_t *rgb, int w, int h, int x, int y) 
     return g + float(q[2]) * (0.114f / 255.f);
 }
 
+// Four 32-bit words read from a 4-byte boundary (the 16 bytes around a run of 4 RGB pixels).
+typedef unsigned u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
 constexpr int CROP_WIN = 6144;   // grey values of a block's source window in LDS
 constexpr int CROP_SPANS = 512;  // polygon span bounds of the window's rows in LDS
 constexpr int CROP_ROWS = 256;   // window rows
@@ -83,24 +86,62 @@ __global__ __launch_bounds__(256) void line_crop_kernel(const CropLine *lines, c
         for (int i = tid; i <= wr; i += 256) s_roff[i] = row_off[L.row_base + wy0 + i] - sp0;
         for (int i = tid; i < nsp; i += 256) s_span[i] = spans[sp0 + i];
         __syncthreads();
-        // Grey of the window, four pixels a thread at a time with all their loads issued first.
-        const int n = wr * wc;
-        for (int i0 = tid; i0 < n; i0 += 4 * 256) {
-            float g[4];
+        // Grey of the window in items of four neighbouring pixels of one row, IPT items a thread
+        // with all their loads issued before any is used. An item whose 12 bytes lie inside the
+        // page row and inside the buffer is one 16-byte load from the 4-byte boundary at or below
+        // its first byte, realigned with alignbyte; any other item reads its pixels one by one.
+        constexpr int IPT = 6;
+        const int nq = (wc + 3) >> 2, n = wr * nq;
+        const uintptr_t buf0 = reinterpret_cast<uintptr_t>(L.rgb);
+        const uintptr_t buf1 = buf0 + size_t(L.pw) * L.ph * 3;
+        for (int j0 = 0; j0 < n; j0 += IPT * 256) {
+            u32x4a raw[IPT];
+            int off[IPT];
+            bool fast[IPT];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int i = i0 + k * 256;
-                const int r = i / wc, c = i - r * wc;
-                g[k] = i < n ? grey_px(L.rgb, L.pw, L.ph, L.left + wx0 + c, L.top + wy0 + r) : -0.5f;
+            for (int k = 0; k < IPT; k++) {
+                const int j = j0 + k * 256 + tid;
+                const int r = j / nq, c = 4 * (j - r * nq);
+                const int x0 = L.left + wx0 + c, y = L.top + wy0 + r;
+                const uintptr_t a = buf0 + (size_t(y) * L.pw + x0) * 3, al = a & ~uintptr_t(3);
+                fast[k] = j < n && y >= 0 && y < L.ph && x0 >= 0 && x0 + 4 <= L.pw && al >= buf0 && al + 16 <= buf1;
+                off[k] = int(a & 3);
+                raw[k] = fast[k] ? *reinterpret_cast<const u32x4a *>(al) : u32x4a{0u, 0u, 0u, 0u};
             }
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int i = i0 + k * 256;
-                if (i >= n) break;
-                const int r = i / wc, cx = wx0 + i - r * wc;
-                bool in = false;
-                for (int q = s_roff[r]; q < s_roff[r + 1]; q += 2) in = in || (cx >= s_span[q] && cx < s_span[q + 1]);
-                s_grey[i] = in ? g[k] : -0.5f;
+            for (int k = 0; k < IPT; k++) {
+                const int j = j0 + k * 256 + tid;
+                if (j >= n) break;
+                const int r = j / nq, c = 4 * (j - r * nq);
+                float g[4];
+                if (fast[k]) {
+                    const unsigned s = unsigned(off[k]);
+                    const unsigned b[3] = {__builtin_amdgcn_alignbyte(raw[k].y, raw[k].x, s),
+                                           __builtin_amdgcn_alignbyte(raw[k].z, raw[k].y, s),
+                                           __builtin_amdgcn_alignbyte(raw[k].w, raw[k].z, s)};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int m0 = 3 * e, m1 = m0 + 1, m2 = m0 + 2;
+                        const float cr = float((b[m0 >> 2] >> (8 * (m0 & 3))) & 255u);
+                        const float cg = float((b[m1 >> 2] >> (8 * (m1 & 3))) & 255u);
+                        const float cb = float((b[m2 >> 2] >> (8 * (m2 & 3))) & 255u);
+                        float v = -0.5f + cr * (0.299f / 255.f);  // as grey_px, term by term
+                        v = v + cg * (0.587f / 255.f);
+                        g[e] = v + cb * (0.114f / 255.f);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        g[e] = grey_px(L.rgb, L.pw, L.ph, L.left + wx0 + c + e, L.top + wy0 + r);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (c + e >= wc) break;
+                    const int cx = wx0 + c + e;
+                    bool in = false;
+                    for (int q = s_roff[r]; q < s_roff[r + 1]; q += 2) in = in || (cx >= s_span[q] && cx < s_span[q + 1]);
+                    s_grey[r * wc + c + e] = in ? g[e] : -0.5f;
+                }
             }
         }
         __syncthreads();
