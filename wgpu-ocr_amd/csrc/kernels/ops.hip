@@ -275,15 +275,35 @@ __global__ void grey_resize_kernel(const GreyParams p) {
     g.y[i] = mixf(top, bot, wy);
 }
 
-// ---- mask_up (gpu.rs:563-593): a wavefront per 64 columns of MR rows (two bit words a row,
-// assembled with a ballot); a thread walks its column down the rows, so a wavefront's loads of
-// neighbouring rows (which share source rows) are in flight together.
-constexpr int MR = 8;
+// ---- mask_up (gpu.rs:563-593): a wavefront per MJ blocks of 64 columns (2*MJ bit words, one
+// 64-byte store a row) of MR rows; a lane takes column 64*j + lane of block j, and block j's
+// ballot gives words 2j and 2j+1. The map rows the MR output rows read are interpolated across
+// once per block and lane (two taps a map row instead of four an output row).
+constexpr int MR = 8, MJ = 8;
 struct MaskParams {
     MaskPage pg[GPMAX];
     int stride;
     float thr;
 };
+// Source coordinate of output index o (monotone in o, so a run of output rows reads a run of map
+// rows).
+__device__ inline float mask_src(float s, int o, int n) {
+#pragma clang fp contract(off)
+    return fminf(fmaxf(s * (float(o) + 0.5f) - 0.5f, 0.f), float(n) - 1.f);
+}
+// The bit word of one output row that lane 2j (low half) or 2j + 1 (high half) stores: block j's
+// pixels thresholded after the vertical step of the bilinear interpolation.
+__device__ __forceinline__ uint32_t mask_word(const float (&top)[MJ], const float (&bot)[MJ], const bool (&col)[MJ],
+                                              float fy, float thr, int lane) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < MJ; j++) {
+        const unsigned long long b = __ballot(col[j] && mixf(top[j], bot[j], fy) > thr);
+        if (lane == 2 * j) word = uint32_t(b);
+        if (lane == 2 * j + 1) word = uint32_t(b >> 32);
+    }
+    return word;
+}
 __global__ void mask_up_kernel(const MaskParams p) {
 #pragma clang fp contract(off)
     const MaskPage &g = p.pg[blockIdx.y];
@@ -292,32 +312,68 @@ __global__ void mask_up_kernel(const MaskParams p) {
     const float sx = g.sx, sy = g.sy, thr = p.thr;
     uint32_t *bits = g.bits;
     const int lane = threadIdx.x & 63;
-    const long wv = (long(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-    const int pairs = (words + 1) / 2, groups = (h + MR - 1) / MR;
-    if (wv >= long(pairs) * groups) return;  // the whole wavefront
-    const int rg = int(wv / pairs), wp = int(wv - long(rg) * pairs);
-    const int ox = wp * 64 + lane;
-    const bool col = ox < w;
-    const float ix = fminf(fmaxf(sx * (float(ox) + 0.5f) - 0.5f, 0.f), float(mw) - 1.f);
-    const int x1 = int(ix), x2 = min(x1 + 1, mw - 1);
-    const float fx = ix - float(x1);
+    // The wavefront's index, uniform (read from lane 0) so that everything derived from it is too.
+    const long wv = long(blockIdx.x) * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int chunks = (words + 2 * MJ - 1) / (2 * MJ), groups = (h + MR - 1) / MR;
+    if (wv >= long(chunks) * groups) return;  // the whole wavefront
+    const int rg = int(wv / chunks), wc = int(wv - long(rg) * chunks);
+    int x1[MJ], x2[MJ];
+    float fx[MJ];
+    bool col[MJ];
 #pragma unroll
-    for (int k = 0; k < MR; k++) {
-        const int oy = rg * MR + k;
-        if (oy >= h) break;
-        bool on = false;
-        if (col) {
-            const float iy = fminf(fmaxf(sy * (float(oy) + 0.5f) - 0.5f, 0.f), float(mh) - 1.f);
-            const int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
-            const float fy = iy - float(y1);
-            const float top = mixf(m[size_t(y1) * stride + x1], m[size_t(y1) * stride + x2], fx);
-            const float bot = mixf(m[size_t(y2) * stride + x1], m[size_t(y2) * stride + x2], fx);
-            on = mixf(top, bot, fy) > thr;
+    for (int j = 0; j < MJ; j++) {
+        const int ox = (wc * MJ + j) * 64 + lane;
+        col[j] = ox < w;
+        const float ix = mask_src(sx, ox, mw);
+        x1[j] = int(ix), x2[j] = min(x1[j] + 1, mw - 1);
+        fx[j] = ix - float(x1[j]);
+    }
+    // Output row oy reads map rows y1 = int(iy) and min(y1 + 1, mh - 1), iy its source coordinate
+    // (monotone in oy); ya and yl are the group's first and last y1 (uniform). When
+    // yl - ya + 2 <= HR (a page larger than the map), the rows ya .. ya + HR - 1, clamped to the
+    // map, are interpolated across once per block and lane, and the output rows are walked pair
+    // by pair: pair q (rows ya + q and ya + q + 1, which the clamp makes the same row at the
+    // map's last) takes the output rows whose y1 is ya + q in a uniform loop, so its registers
+    // are fixed. Every tap address is inside the map, so the loads are unconditional and in
+    // flight together; a lane past the page width only has its result dropped.
+    constexpr int HR = 5;
+    const int k1 = min(MR, h - rg * MR);  // output rows of the group
+    const int ya = int(mask_src(sy, rg * MR, mh)), yl = int(mask_src(sy, rg * MR + k1 - 1, mh));
+    const int wi = wc * 2 * MJ + lane;  // the word lane < 2*MJ stores
+    if (yl - ya + 2 <= HR) {
+        float hrow[HR][MJ];
+#pragma unroll
+        for (int q = 0; q < HR; q++) {
+            const float *r = m + size_t(min(ya + q, mh - 1)) * stride;
+#pragma unroll
+            for (int j = 0; j < MJ; j++) hrow[q][j] = mixf(r[x1[j]], r[x2[j]], fx[j]);
         }
-        const unsigned long long b = __ballot(on);
-        uint32_t *row = bits + size_t(oy) * words;
-        if (lane == 0) row[2 * wp] = uint32_t(b);
-        if (lane == 1 && 2 * wp + 1 < words) row[2 * wp + 1] = uint32_t(b >> 32);
+        int k = 0;
+#pragma unroll
+        for (int q = 0; q + 1 < HR; q++)
+            for (; k < k1; k++) {
+                const int oy = rg * MR + k;
+                const float iy = mask_src(sy, oy, mh);
+                const int y1 = int(iy);
+                if (y1 != ya + q) break;
+                const uint32_t word = mask_word(hrow[q], hrow[q + 1], col, iy - float(y1), thr, lane);
+                if (lane < 2 * MJ && wi < words) bits[size_t(oy) * words + wi] = word;
+            }
+    } else {
+        for (int k = 0; k < k1; k++) {
+            const int oy = rg * MR + k;
+            const float iy = mask_src(sy, oy, mh);
+            const int y1 = int(iy), y2 = min(y1 + 1, mh - 1);
+            const float *r1 = m + size_t(y1) * stride, *r2 = m + size_t(y2) * stride;
+            float top[MJ], bot[MJ];
+#pragma unroll
+            for (int j = 0; j < MJ; j++) {
+                top[j] = mixf(r1[x1[j]], r1[x2[j]], fx[j]);
+                bot[j] = mixf(r2[x1[j]], r2[x2[j]], fx[j]);
+            }
+            const uint32_t word = mask_word(top, bot, col, iy - float(y1), thr, lane);
+            if (lane < 2 * MJ && wi < words) bits[size_t(oy) * words + wi] = word;
+        }
     }
 }
 
@@ -505,7 +561,7 @@ void mask_up(const MaskPage *pages, int count, int stride, float thr, hipStream_
     for (int k = 0; k < count; k++) {
         const int words = (pages[k].w + 31) / 32;
         bytes += 4.0 * double(pages[k].mw) * pages[k].mh + 4.0 * double(words) * pages[k].h;
-        waves = std::max(waves, size_t((words + 1) / 2) * ((pages[k].h + MR - 1) / MR));
+        waves = std::max(waves, size_t((words + 2 * MJ - 1) / (2 * MJ)) * ((pages[k].h + MR - 1) / MR));
     }
     ProbeScope probe("mask_up", s, 0, bytes);
     for (int k0 = 0; k0 < count; k0 += GPMAX) {
