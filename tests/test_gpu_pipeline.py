@@ -144,6 +144,13 @@ def test_word_rects_gpu_labelling_identical(detector, ctx):
     masks.append((_pack_bits(np.zeros((10, 40), bool)), 40))
     diag = np.eye(120, 130, dtype=bool) | np.eye(120, 130, k=7, dtype=bool)[:, ::-1]
     masks.append((_pack_bits(diag), 130))
+    # 5000 runs a row on both sides of a 32-row band edge (more than a row's runs staged in LDS),
+    # joined diagonally into one component, over sparse noise.
+    wide = rng.random((40, 10000)) < 0.05
+    wide[31], wide[32] = False, False
+    wide[31, 0::2] = True
+    wide[32, 1::2] = True
+    masks.append((_pack_bits(wide), 10000))
     for bits, w in masks:
         print(f"word rects of a {bits.shape[0]} x {w} mask", flush=True)
         want = ol.word_rects(bits, w)
