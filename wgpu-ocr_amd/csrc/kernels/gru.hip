@@ -117,6 +117,14 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
     };
     float2 gcur[3][RT];
     load_g(0, gcur);
+    // The recurrent bias of the lane's units, the same every step.
+    float rbv[3][RT][2];
+#pragma unroll
+    for (int q = 0; q < 3; q++)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) rbv[q][rt][i] = s_rb[q * 256 + wave * UPW + rt * 16 + 4 * g + usub + i];
 
     typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     for (int s = 0; s < maxlen; s++) {
@@ -128,11 +136,15 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
                 acc[q][rt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        // R h for row tile rt of the three gates (8 k-slices).
+        // R h for row tile rt of the three gates (8 k-slices); the B fragment of k-slice kt + 1
+        // is read from LDS before k-slice kt's MFMAs, so its latency hides behind them.
         auto mfmas = [&](int rt) __attribute__((always_inline)) {
+            half8 bb[2];
+            bb[0] = *reinterpret_cast<const half8 *>(&hbuf[cur][r][8 * g]);
 #pragma unroll
             for (int kt = 0; kt < 8; kt++) {
-                const half8 b = *reinterpret_cast<const half8 *>(&hbuf[cur][r][kt * 32 + 8 * g]);
+                if (kt < 7) bb[(kt + 1) & 1] = *reinterpret_cast<const half8 *>(&hbuf[cur][r][(kt + 1) * 32 + 8 * g]);
+                const half8 b = bb[kt & 1];
 #pragma unroll
                 for (int q = 0; q < 3; q++) {
                     const half8 a = (q >= 3 - KLQ && kt >= 8 - KL)
@@ -168,9 +180,9 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
                 const float gz = i ? gcur[0][rt].y : gcur[0][rt].x;
                 const float gr = i ? gcur[1][rt].y : gcur[1][rt].x;
                 const float gh = i ? gcur[2][rt].y : gcur[2][rt].x;
-                const float z = sigm(gz + (rh[0][i] + s_rb[u0 + i]));
-                const float rr = sigm(gr + (rh[1][i] + s_rb[256 + u0 + i]));
-                const float c = tanh_f(gh + rr * (rh[2][i] + s_rb[512 + u0 + i]));
+                const float z = sigm(gz + (rh[0][i] + rbv[0][rt][i]));
+                const float rr = sigm(gr + (rh[1][i] + rbv[1][rt][i]));
+                const float c = tanh_f(gh + rr * (rh[2][i] + rbv[2][rt][i]));
                 hn[rt][i] = (1.f - z) * c + z * h[rt][i];
                 h[rt][i] = on ? hn[rt][i] : h[rt][i];
                 hi2[i] = (_Float16)h[rt][i];
