@@ -314,7 +314,7 @@ def config_figures(ctx, det, rec, reps=20):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=160, help="timed steps (160 host-page steps take about 2 s)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--pages", type=int, default=12)
     ap.add_argument("--merge", type=int, default=6)
@@ -327,6 +327,10 @@ def main():
     ap.add_argument("--conv-layer", metavar="CIN,COUT,N,H,W[,PHxPW]",
                     help="only time one 3x3 convolution layer (+ ReLU, optional max pool)")
     ap.add_argument("--gru-lines", type=int, metavar="N", help="only time the GRU on N recognised lines")
+    ap.add_argument("--trace", action="store_true",
+                    help="after the warm-up, run one step from host memory with the pipeline's trace "
+                         "(OCR_PIPE_TRACE: upload, detection and recognition spans on the GPU, host "
+                         "steps) printed to stderr, and stop")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
@@ -356,6 +360,11 @@ def main():
     for _ in range(args.warmup):
         pipe.run(pages)
     ctx.synchronize()
+    if args.trace:
+        os.environ["OCR_PIPE_TRACE"] = "1"
+        pipe.run(pages)
+        del os.environ["OCR_PIPE_TRACE"]
+        return
 
     # The timed region probes only the dominant kernel family (two events around each of its
     # launches, for the roofline); the per-family breakdown comes from one more step outside the

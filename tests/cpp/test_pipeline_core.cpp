@@ -167,6 +167,11 @@ struct Hooks final : PipelineHooks {
                 const int after = int(std::count_if(detected_at.begin(), detected_at.end(), [](int t) { return t >= 0; }));
                 if (f.detect < 0) CHECK(any == (after > before), "recognize(%d): poll result %d, %d -> %d groups", r, int(any), before, after);
                 polled_groups += after - before;
+                CHECK(bool(detections_pending), "recognize(%d): no detections_pending", r);
+                if (!detections_pending())
+                    for (int g = 0; g < P.groups(); g++)
+                        CHECK(detected_at[size_t(g)] >= 0 || g == f.stage || g == f.detect,
+                              "recognize(%d): nothing pending but group %d not queued", r, g);
                 nap();
             }
         }
@@ -230,6 +235,7 @@ int run_case(const char *name, int npages, int merge, int det_batch, int workers
     for (int p = 0; p < npages; p++)
         if (!bad[size_t(p)]) CHECK(H.laid_at[size_t(p)] >= 0, "%s: page %d not laid out", name, p);
     CHECK(!H.poll_detections, "%s: poll_detections left set after the run", name);
+    CHECK(!H.detections_pending, "%s: detections_pending left set after the run", name);
     return H.polled_groups;
 }
 

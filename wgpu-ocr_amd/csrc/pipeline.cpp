@@ -601,8 +601,12 @@ struct PipelineRun final : PipelineHooks {
             OCR_HIP(hipEventRecord(e, st));
             stage_ev.push_back(e);
             if (poll_detections) poll_detections();
-            if (stage_ev.size() < 2) return;
-            const hipEvent_t prev = stage_ev[stage_ev.size() - 2];
+            // With a detection group still to come, wait for the stage just queued (a group
+            // staged meanwhile then runs right after it); otherwise for the one before it, so the
+            // stage just queued keeps the GPU busy while the next one is queued.
+            const bool pending = detections_pending && detections_pending();
+            if (!pending && stage_ev.size() < 2) return;
+            const hipEvent_t prev = pending ? stage_ev.back() : stage_ev[stage_ev.size() - 2];
             for (;;) {
                 const hipError_t q = hipEventQuery(prev);
                 if (q == hipSuccess) break;

@@ -83,6 +83,10 @@ class PipelineHooks {
     // between its stages, so that pages which reach the device meanwhile are detected after the
     // stage in flight rather than after the whole pass.
     std::function<bool()> poll_detections;
+    // Set with poll_detections: whether some detection group is not queued yet (staged or not).
+    // A pass that knows one is still to come can wait on its stage in flight, polling, so the
+    // group goes right behind that stage.
+    std::function<bool()> detections_pending;
 };
 
 // Runs fn on a worker thread (the caller's pool); must not block the calling thread.
@@ -244,6 +248,10 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
             any = true;
         }
     };
+    H.detections_pending = [&]() -> bool {
+        std::lock_guard<std::mutex> lk(mu);
+        return next_det < ng;
+    };
     while (next_rec < nr) {
         int do_det = -1, do_rec = -1;
         std::vector<char> pass_ok;
@@ -315,6 +323,7 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
         });
     }
     H.poll_detections = nullptr;
+    H.detections_pending = nullptr;
     // Detections queued after the last pass (none in a valid plan), then every task and thread.
     {
         std::unique_lock<std::mutex> lk(mu);
