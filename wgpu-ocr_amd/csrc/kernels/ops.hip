@@ -168,13 +168,20 @@ __global__ __launch_bounds__(256) void convt_k2s2_kernel(const float *x, int h, 
         }
         const float4 *wp = reinterpret_cast<const float4 *>(sw + size_t(((oy & 1) * 2 + px) * cin) * cout) + q;
         float acc[4][4] = {};
+        // The next block of 4 input channels is loaded before this block's FMAs.
+        float4 nx[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) nx[k] = *reinterpret_cast<const float4 *>(xp[k]);
         for (int ci = 0; ci < cin; ci += 4) {
             float xs[4][4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const float4 v = *reinterpret_cast<const float4 *>(xp[k] + ci);
+                const float4 v = nx[k];
                 xs[k][0] = v.x, xs[k][1] = v.y, xs[k][2] = v.z, xs[k][3] = v.w;
             }
+            if (ci + 4 < cin)
+#pragma unroll
+                for (int k = 0; k < 4; k++) nx[k] = *reinterpret_cast<const float4 *>(xp[k] + ci + 4);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float4 wv = wp[size_t(ci + e) * cq];
