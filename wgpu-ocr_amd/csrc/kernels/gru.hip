@@ -138,7 +138,7 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
                 acc[q][rt] = floatx4{0.f, 0.f, 0.f, 0.f};
         // R h for row tile rt of the three gates (8 k-slices); the B fragment of k-slice kt + 1
         // is read from LDS before k-slice kt's MFMAs, so its latency hides behind them.
-        auto mfmas = [&](int rt) __attribute__((always_inline)) {
+        auto mfmas = [&](int rt, int q0 = 0, int q1 = 3) __attribute__((always_inline)) {
             half8 bb[2];
             bb[0] = *reinterpret_cast<const half8 *>(&hbuf[cur][r][8 * g]);
 #pragma unroll
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
                 if (kt < 7) bb[(kt + 1) & 1] = *reinterpret_cast<const half8 *>(&hbuf[cur][r][(kt + 1) * 32 + 8 * g]);
                 const half8 b = bb[kt & 1];
 #pragma unroll
-                for (int q = 0; q < 3; q++) {
+                for (int q = q0; q < q1; q++) {
                     const half8 a = (q >= 3 - KLQ && kt >= 8 - KL)
                                         ? s_rf[wave][((q - (3 - KLQ)) * RT + rt) * KL + kt - (8 - KL)][lane]
                                         : rf[q][rt][kt];
@@ -154,35 +154,48 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
                 }
             }
         };
-        // The gates of row tile rt, branch-free (a line past its end keeps its state), and the
-        // next step's B operand: units u0 and u0 + 1 as one 32-bit word of hi parts and one of
-        // lo parts. hi + lo of R h: lane r < 8 keeps rows 0, 1 and sends rows 2, 3 to lane r + 8
-        // (and the reverse).
+        // The new state of row tile rt's units (also the step's Y).
         float hn[RT][2];
-        auto gates = [&](int rt) __attribute__((always_inline)) {
-            float rh[3][2];
-#pragma unroll
-            for (int q = 0; q < 3; q++) {
-                // The lane's choice between rows 0, 1 and 2, 3 as bit selects on the upper-lane
-                // mask (one bitfield insert each; a ternary on `upper` is compiled as a dynamic
-                // index into the accumulator, a chain of compares and selects).
-                const float send0 = sel_bits(umask, acc[q][rt][0], acc[q][rt][2]);
-                const float send1 = sel_bits(umask, acc[q][rt][1], acc[q][rt][3]);
-                const float keep0 = sel_bits(umask, acc[q][rt][2], acc[q][rt][0]);
-                const float keep1 = sel_bits(umask, acc[q][rt][3], acc[q][rt][1]);
-                rh[q][0] = keep0 + ror8(send0);
-                rh[q][1] = keep1 + ror8(send1);
-            }
-            const int u0 = wave * UPW + rt * 16 + 4 * g + usub;
-            half2_t hi2, lo2;
+        float zv[RT][2], rv[RT][2];
+        // hi + lo of R h for gate q of row tile rt: lane r < 8 keeps rows 0, 1 and sends rows 2, 3
+        // to lane r + 8 (and the reverse).
+        auto rh_of = [&](int q, int rt, float (&o)[2]) __attribute__((always_inline)) {
+            // The lane's choice between rows 0, 1 and 2, 3 as bit selects on the upper-lane
+            // mask (one bitfield insert each; a ternary on `upper` is compiled as a dynamic
+            // index into the accumulator, a chain of compares and selects).
+            const float send0 = sel_bits(umask, acc[q][rt][0], acc[q][rt][2]);
+            const float send1 = sel_bits(umask, acc[q][rt][1], acc[q][rt][3]);
+            const float keep0 = sel_bits(umask, acc[q][rt][2], acc[q][rt][0]);
+            const float keep1 = sel_bits(umask, acc[q][rt][3], acc[q][rt][1]);
+            o[0] = keep0 + ror8(send0);
+            o[1] = keep1 + ror8(send1);
+        };
+        // The update and reset gates of row tile rt (they need only their own rows' MFMAs).
+        auto gates_zr = [&](int rt) __attribute__((always_inline)) {
+            float rz[2], rr2[2];
+            rh_of(0, rt, rz);
+            rh_of(1, rt, rr2);
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const float gz = i ? gcur[0][rt].y : gcur[0][rt].x;
                 const float gr = i ? gcur[1][rt].y : gcur[1][rt].x;
+                zv[rt][i] = sigm(gz + (rz[i] + rbv[0][rt][i]));
+                rv[rt][i] = sigm(gr + (rr2[i] + rbv[1][rt][i]));
+            }
+        };
+        // The candidate and the new state of row tile rt, branch-free (a line past its end keeps
+        // its state), and the next step's B operand: units u0 and u0 + 1 as one 32-bit word of
+        // hi parts and one of lo parts.
+        auto gates_h = [&](int rt) __attribute__((always_inline)) {
+            float rhh[2];
+            rh_of(2, rt, rhh);
+            const int u0 = wave * UPW + rt * 16 + 4 * g + usub;
+            half2_t hi2, lo2;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
                 const float gh = i ? gcur[2][rt].y : gcur[2][rt].x;
-                const float z = sigm(gz + (rh[0][i] + rbv[0][rt][i]));
-                const float rr = sigm(gr + (rh[1][i] + rbv[1][rt][i]));
-                const float c = tanh_f(gh + rr * (rh[2][i] + rbv[2][rt][i]));
+                const float z = zv[rt][i], rr = rv[rt][i];
+                const float c = tanh_f(gh + rr * (rhh[i] + rbv[2][rt][i]));
                 hn[rt][i] = (1.f - z) * c + z * h[rt][i];
                 h[rt][i] = on ? hn[rt][i] : h[rt][i];
                 hi2[i] = (_Float16)h[rt][i];
@@ -191,14 +204,19 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
             *reinterpret_cast<half2_t *>(&hbuf[cur ^ 1][lr][u0]) = hi2;
             *reinterpret_cast<half2_t *>(&hbuf[cur ^ 1][lr + LINES][u0]) = lo2;
         };
+        auto gates = [&](int rt) __attribute__((always_inline)) {
+            gates_zr(rt);
+            gates_h(rt);
+        };
         // Two row tiles: row tile 0's MFMAs; then row tile 1's MFMAs with row tile 0's gate
         // arithmetic between them (the vector ALU works while the matrix core does); then row
-        // tile 1's gates. One row tile: its MFMAs, then its gates (the other wavefronts on the
-        // SIMD keep the matrix core busy meanwhile).
+        // tile 1's gates. One row tile: the update and reset rows' MFMAs, then the candidate
+        // rows' MFMAs with the update and reset gates between them, then the candidate and the
+        // new state.
         static_assert(RT == 1 || RT == 2, "one or two row tiles a wavefront");
-        mfmas(0);
-        __builtin_amdgcn_sched_barrier(0);
         if constexpr (RT == 2) {
+            mfmas(0);
+            __builtin_amdgcn_sched_barrier(0);
             mfmas(1);
             gates(0);
 #pragma unroll
@@ -208,7 +226,21 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        gates(RT - 1);
+        if constexpr (RT == 1) {
+            mfmas(0, 0, 2);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(0, 2, 3);
+            gates_zr(0);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            gates_h(0);
+        } else {
+            gates(RT - 1);
+        }
         if (on) {
             const int t = dir == 0 ? s : len - 1 - s;
 #pragma unroll
