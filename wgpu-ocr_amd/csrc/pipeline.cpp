@@ -496,7 +496,10 @@ struct PipelineRun final : PipelineHooks {
 
     void detect_wait(int g) override {
         ctx.bind();
-        OCR_HIP(hipEventSynchronize(det_ev[size_t(g)]));
+        // The last group's result is on the run's critical path and the layouts before it are
+        // done by then: poll it (yielding) rather than sleep in the blocking wait.
+        if (g + 1 == P.groups()) wait_event(det_ev[size_t(g)], true);
+        else OCR_HIP(hipEventSynchronize(det_ev[size_t(g)]));
         mark("det group " + std::to_string(g) + " done");
     }
 
