@@ -1,1 +1,1 @@
-"""ORACLE: the CPU checker for the HIP path. Test infrastructure only; the product never imports it."""
+"""ORACLE: the CPU restatement the HIP path is tested against. Test infrastructure only; the product never imports it."""

@@ -1,6 +1,6 @@
 """ORACLE (test infrastructure only): runs an ONNX graph on the CPU in float32 with the C
 restatement in oracle.c for the heavy operators and numpy for the shape operators. Only tests,
-the smoke check and bench.py's cpu_baseline leg use it, always as the checker.
+the smoke check and bench.py's cpu_baseline leg use it, always as the oracle results are compared with.
 
 ONNX operator semantics as rten (the reference's CPU engine, rten 0.26.0) implements them; the
 ocrs front and back ends follow the reference's GPU code where ocrs itself is not available:

@@ -1,5 +1,5 @@
 """ORACLE (test infrastructure only): the page layout before recognition, restated apart from the
-product's host code, for the checker of the page pipeline.
+product's host code, as the oracle of the page pipeline.
 
 - Words: src/bin/ocr-bench.rs:40-60 (ocrs' find_connected_component_rects) through contours.c:
   external contours (Suzuki-Abe), Douglas-Peucker with epsilon 2, minimum-area rectangle, grown by

@@ -1,6 +1,6 @@
 /*
  * ORACLE - test infrastructure only. A plain-C, float32 CPU restatement of the reference's
- * GPU path (huppiflupp/wgpu-ocr, src/gpu.rs), used as the checker for the HIP kernels and, timed,
+ * GPU path (huppiflupp/wgpu-ocr, src/gpu.rs): the oracle the tests compare the HIP kernels with and, timed,
  * as the CPU baseline. Nothing in the product links or calls this file.
  *
  * Layout is ONNX's: NCHW float32. Each function cites the reference code it restates.

@@ -1,4 +1,4 @@
-"""ORACLE (test infrastructure only): PNG pages to 8-bit RGB, the checker of the page decode
+"""ORACLE (test infrastructure only): PNG pages to 8-bit RGB, the oracle of the page decode
 image::open(p)?.into_rgb8() (src/bin/ocr-bench.rs:424, src/bin/stages.rs:94,
 src/bin/ppocr-bench.rs:69; image 0.25.10 over png 0.18.1 in the reference's Cargo.lock).
 

@@ -119,7 +119,7 @@ def test_det_prep_golden():
 
 
 def test_det_input_size_rule():
-    # nd.rs:1356-1358 on the BASELINE page: 2550 x 3300 with long side 960 -> 736 x 960.
+    # nd.rs:1356-1358 on a 300-dpi US Letter page: 2550 x 3300 with long side 960 -> 736 x 960.
     assert graph.det_input_size(2550, 3300, 960) == (736, 960)
     assert graph.det_input_size(100, 50, 960) == (96, 64)   # no down-scaling; 50 / 32 rounds to 2
     assert graph.det_input_size(10, 10, 960) == (32, 32)    # at least 32

@@ -7,13 +7,13 @@ residual Add, squeeze-excitation (HardSigmoid gate Mul read by a dense Conv), th
 LayerNorm chain, MatMul + bias + SiLU (Sigmoid, Mul), ConvTranspose + bias + Relu / Sigmoid,
 nearest Resize, and shape arithmetic kept on the host (Shape, Gather, Concat of integers).
 
-Recogniser: [n, 3, 48, W] -> a CNN backbone (stride-2 stem, depthwise +
+Recogniser (the PP-OCR text-line configuration): [n, 3, 48, W] -> a CNN backbone (stride-2 stem, depthwise +
 pointwise blocks, one SE block, one GELU residual block, AveragePool (3, 1)) to [n, 256, 1, W/8]
 -> an SVTR neck (3x3 and 1x1 convs to dim 120, 2 transformer blocks with 8 heads and MLP ratio
 2, LayerNorm, then back to channels, concat with the shortcut, 3x3 and 1x1 convs) -> a linear
 CTC head over 18 708 classes -> Softmax.
 
-Detector: [1, 3, H, W] (multiples of 32) -> stem + 4 depthwise/pointwise
+Detector (the PP-OCR page configuration): [1, 3, H, W] (multiples of 32) -> stem + 4 depthwise/pointwise
 stages (strides 4, 8, 16, 32; 32-256 channels) -> a DB FPN (1x1 laterals to 64, nearest x2
 top-down adds, 3x3 convs to 16, nearest upsampling to H/4, Concat) -> the DB head (3x3 conv,
 BatchNormalization, Relu, ConvTranspose x2 with Relu, ConvTranspose x2 with Sigmoid) -> the
