@@ -99,6 +99,21 @@ def test_detection_config2(detector, det_oracle):
     assert np.array_equal((got > 0.5)[~band], (want > 0.5)[~band])
 
 
+@pytest.mark.parametrize("h,w", [(3300, 2550), (1000, 700), (500, 420), (1100, 97)])
+def test_mask_up_bit_exact_on_the_gpu_map(detector, h, w):
+    # The page mask from the GPU's own probability map: detect() on the oracle's grey resize
+    # (gpu.rs:530-561, bit-exact) runs the same graph on the same input as detect_page() does,
+    # so detect_page()'s bits must equal the oracle's upsampling and threshold of that map
+    # (gpu.rs:563-593) bit for bit: for a page larger than the map (rows interpolated once per
+    # wavefront) and for smaller ones (taps read per output row).
+    page = np.ascontiguousarray(synth.page(1)[:h, :w])
+    print(f"mask_up {h}x{w}", flush=True)
+    bits = detector.detect_page(page, 0.5)
+    m = detector.detect(og.grey_resize(page, w, h))
+    want = og.pack_bits(og.mask_up_prob(m, w, h), 0.5)
+    np.testing.assert_array_equal(bits, want)
+
+
 @pytest.mark.parametrize("h,w", [(3300, 2550), (1000, 700), (500, 420)])
 def test_detect_page_mask(detector, det_oracle, h, w):
     page = synth.page(1)
