@@ -152,6 +152,30 @@ def gru_lines(nlines, reps=5):
     print(json.dumps({"lines": nlines, "steps": tmax, "gru_us_per_launch": us, "gru_us_per_step": us / tmax}))
 
 
+def host_cpu():
+    """The host CPU the baseline runs on: model name from /proc/cpuinfo, the cores this process
+    may run on (its affinity mask) and the logical CPUs the system shows."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"model": model, "affinity_cores": affinity, "logical_cpus": os.cpu_count()}
+
+
+def baseline_threads():
+    """Threads for a CPU baseline: OMP_NUM_THREADS when set (the GPU box sets it to its CPU
+    share), else every core of the affinity mask, never more than the mask holds."""
+    cpu = host_cpu()
+    want = int(os.environ.get("OMP_NUM_THREADS", cpu["affinity_cores"]))
+    return max(1, min(want, cpu["affinity_cores"])), cpu
+
+
 def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
     """The oracle (C restatement, OpenMP on all host cores) page by page, as the reference's CPU
     baseline loop runs (src/bin/ocr-bench.rs:431-444): oracle detection, the oracle's layout,
@@ -161,6 +185,8 @@ def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
     from oracle import layout as ol
     from oracle import onnx_read
 
+    cores, cpu = baseline_threads()
+    os.environ["OMP_NUM_THREADS"] = str(cores)
     det, rec = onnx_read.load(det_path), onnx_read.load(rec_path)
     og.lib()
     layout = ol.Layout
@@ -170,10 +196,9 @@ def cpu_baseline(det_path, rec_path, pages, min_secs=10.0):
         og.page_pipeline(det, rec, pages[n % len(pages)], 0.5, layout)
         n += 1
     secs = time.perf_counter() - t
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": n / secs, "unit": "pages/s", "cores": cores, "kind": "port",
+    return {"value": n / secs, "unit": "pages/s", "cores": cores, "kind": "port", "cpu": cpu,
             "sample": f"{n} of the synthetic 2550x3300 pages, whole pipeline page by page, {secs:.1f} s "
-                      f"(oracle: C restatement with OpenMP, float32)"}
+                      f"on {cores} threads of {cpu['model']} (oracle: C restatement with OpenMP, float32)"}
 
 
 def cpu_baseline_torch(det_path, rec_path, pages, min_secs=10.0):
@@ -186,8 +211,9 @@ def cpu_baseline_torch(det_path, rec_path, pages, min_secs=10.0):
     from oracle import onnx_read
     from oracle import torch_cpu
 
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    cores, cpu = baseline_threads()
     torch.set_num_threads(cores)
+    cores = torch.get_num_threads()
     det = torch_cpu.TorchGraph(onnx_read.load(det_path))
     rec = torch_cpu.TorchGraph(onnx_read.load(rec_path))
     torch_cpu.page_pipeline(det, rec, pages[0], 0.5, ol.Layout)
@@ -196,8 +222,9 @@ def cpu_baseline_torch(det_path, rec_path, pages, min_secs=10.0):
         torch_cpu.page_pipeline(det, rec, pages[n % len(pages)], 0.5, ol.Layout)
         n += 1
     secs = time.perf_counter() - t
-    return {"value": n / secs, "unit": "pages/s", "cores": cores, "kind": "port",
+    return {"value": n / secs, "unit": "pages/s", "cores": cores, "kind": "port", "cpu": cpu,
             "sample": f"{n} of the synthetic 2550x3300 pages, whole pipeline page by page, {secs:.1f} s "
+                      f"on {cores} threads of {cpu['model']} "
                       f"(torch {torch.__version__} CPU for the detection and recognition graphs, float32; "
                       f"the stand-in for rten)"}
 

@@ -59,6 +59,13 @@ int ocr_memcpy_d2h(ocr_ctx *ctx, void *dst, const void *src, size_t bytes);
  * stream first. */
 void *ocr_host_alloc(ocr_ctx *ctx, size_t bytes);
 int ocr_host_free(ocr_ctx *ctx, void *p);
+/* Memory accounting, no counterpart in the reference: device_allocs and host_allocs count every
+ * device (hipMalloc) and page-locked host (hipHostMalloc) allocation the library has made in
+ * this process; pool_live and pool_held are the bytes of ctx's scratch pool handed out and kept
+ * for reuse (src/gpu.rs:938-966 keeps the same pool without reporting it). Any pointer may be
+ * NULL. */
+int ocr_memory_stats(ocr_ctx *ctx, uint64_t *device_allocs, uint64_t *host_allocs, uint64_t *pool_live,
+                     uint64_t *pool_held);
 
 /* ---- Page images ------------------------------------------------------------------------------
  * The reference's page decode, image::open(p)?.into_rgb8() (src/bin/ocr-bench.rs:424, also

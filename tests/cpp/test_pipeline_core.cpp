@@ -6,6 +6,7 @@
 // ThreadSanitizer.
 #include <algorithm>
 #include "pipeline_core.h"
+#include "wait.h"
 
 #include <atomic>
 #include <cstdio>
@@ -75,6 +76,7 @@ class Pool {
 
 struct Faults {
     int stage = -1, detect = -1, detect_wait = -1, layout = -1, recognize = -1, decode = -1;
+    int detect_stall = -1;  // this group's wait never sees its event: the bounded wait gives up
 };
 
 // Records what ran and checks the ordering rules as it goes.
@@ -125,6 +127,9 @@ struct Hooks final : PipelineHooks {
         CHECK(detected_at[size_t(g)] >= 0, "detect_wait(%d) before detect", g);
         nap();
         if (g == f.detect_wait) throw std::runtime_error("detect_wait fault");
+        if (g == f.detect_stall)
+            wait_until([] { return false; }, [&] { return "detection group " + std::to_string(g) + " (stall fault)"; },
+                       false, 20.0);
         waited_at[size_t(g)] = tick();
     }
     void layout(int p) override {
@@ -134,7 +139,8 @@ struct Hooks final : PipelineHooks {
             std::lock_guard<std::mutex> lk(mu);
             for (int q = 0; q < P.pass_p0[size_t(P.pass_of[size_t(p)])]; q++)
                 CHECK(laid_at[size_t(q)] >= 0 || q == f.layout || P.group_of[size_t(q)] == f.stage ||
-                          P.group_of[size_t(q)] == f.detect || P.group_of[size_t(q)] == f.detect_wait,
+                          P.group_of[size_t(q)] == f.detect || P.group_of[size_t(q)] == f.detect_wait ||
+                          P.group_of[size_t(q)] == f.detect_stall,
                       "layout(%d) before page %d of an earlier pass", p, q);
         }
         nap();
@@ -192,8 +198,8 @@ std::vector<char> expected_failed(const PipelinePlan &P, const Faults &f) {
     std::vector<char> bad(size_t(P.npages), 0);
     for (int p = 0; p < P.npages; p++) {
         const int g = P.group_of[size_t(p)], r = P.pass_of[size_t(p)];
-        bad[size_t(p)] = g == f.stage || g == f.detect || g == f.detect_wait || p == f.layout || r == f.recognize ||
-                         r == f.decode;
+        bad[size_t(p)] = g == f.stage || g == f.detect || g == f.detect_wait || g == f.detect_stall ||
+                         p == f.layout || r == f.recognize || r == f.decode;
     }
     return bad;
 }
@@ -219,6 +225,10 @@ int run_case(const char *name, int npages, int merge, int det_batch, int workers
         if (bad[size_t(p)] && !err[size_t(p)].empty())
             CHECK(err[size_t(p)].find("fault") != std::string::npos, "%s: page %d message '%s'", name, p,
                   err[size_t(p)].c_str());
+        if (P.group_of[size_t(p)] == f.detect_stall && p < int(err.size()))
+            CHECK(err[size_t(p)].find("did not finish within 20 ms") != std::string::npos &&
+                      err[size_t(p)].find("detection group") != std::string::npos,
+                  "%s: page %d stall message '%s'", name, p, err[size_t(p)].c_str());
     }
     // Every pass with a page that reached recognition was recognised and (unless it failed
     // there) decoded; every page without a failure was laid out.
@@ -226,7 +236,7 @@ int run_case(const char *name, int npages, int merge, int det_batch, int workers
         bool any_ok = false;
         for (int p = P.pass_p0[size_t(r)]; p < P.pass_p0[size_t(r) + 1]; p++) {
             const int g = P.group_of[size_t(p)];
-            any_ok |= !(g == f.stage || g == f.detect || g == f.detect_wait || p == f.layout);
+            any_ok |= !(g == f.stage || g == f.detect || g == f.detect_wait || g == f.detect_stall || p == f.layout);
         }
         if (any_ok && r != f.recognize) CHECK(H.rec_at[size_t(r)] >= 0, "%s: pass %d not recognised", name, r);
         if (any_ok && r != f.recognize && r != f.decode) CHECK(H.dec_at[size_t(r)] >= 0, "%s: pass %d not decoded", name, r);
@@ -256,6 +266,33 @@ int main() {
         }
         CHECK(plan_pipeline(0, 2, 4).passes() == 0, "plan: no pages");
     }
+    // The bounded wait itself: it returns once ready() holds, passes ready()'s own errors through,
+    // and gives up past its deadline with the description of what it waited for.
+    {
+        int polls = 0;
+        wait_until([&] { return ++polls == 5; }, [] { return std::string("five polls"); }, false, 1000.0);
+        CHECK(polls == 5, "wait_until: %d polls", polls);
+        bool passed = false;
+        try {
+            wait_until([]() -> bool { throw std::runtime_error("gpu error"); }, [] { return std::string("x"); });
+        } catch (const WaitTimeout &) {
+        } catch (const std::runtime_error &e) {
+            passed = std::string(e.what()) == "gpu error";
+        }
+        CHECK(passed, "wait_until: ready()'s error not passed through");
+        const auto t0 = std::chrono::steady_clock::now();
+        std::string msg;
+        try {
+            wait_until([] { return false; }, [] { return std::string("stage 2 of recognition pass 1"); }, false, 30.0);
+        } catch (const WaitTimeout &e) {
+            msg = e.what();
+        }
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        CHECK(msg.find("within 30 ms") != std::string::npos && msg.find("stage 2 of recognition pass 1") != std::string::npos,
+              "wait_until: timeout message '%s'", msg.c_str());
+        CHECK(ms >= 30.0 && ms < 5000.0, "wait_until: gave up after %.1f ms", ms);
+        CHECK(wait_timeout_ms() == 25.0, "wait_timeout_ms: %.1f (OCR_WAIT_TIMEOUT_MS=25 expected)", wait_timeout_ms());
+    }
     const Faults none;
     run_case("clean", 12, 6, 6, 4, none, 1, true);
     run_case("one worker", 9, 2, 3, 1, none, 2, true);
@@ -275,6 +312,9 @@ int main() {
         Faults w;
         w.detect_wait = g;
         run_case("detect_wait fault", 12, 6, 6, 3, w, 40u + unsigned(g), true);
+        Faults sl;
+        sl.detect_stall = g;
+        run_case("detect stall", 12, 6, 6, 3, sl, 45u + unsigned(g), true);
     }
     for (int r : {0, 1}) {
         Faults f;

@@ -45,19 +45,25 @@ def test_pipeline_text_matches_cpu(pipeline, detector, det_oracle, rec_oracle):
 
 
 def test_bench_configuration_text_matches_cpu(detector, recognizer, det_oracle, rec_oracle):
-    # The benchmark's workload: 12 pages from host memory, 6 pages a recognition pass, 2 a
-    # detection pass. Every page's text equals the CPU pipeline's (oracle detection, layout,
-    # line images, recognition, CTC) on the same mask; a pass of 6 detection pages gives the same.
+    # The benchmark's workload and plan (bench.py's defaults): 12 pages from host memory, 6 pages
+    # a recognition pass, 4 a detection group. Every page's text equals the CPU pipeline's (oracle
+    # detection, layout, line images, recognition, CTC) on the same mask; detection groups of 2
+    # and 6 give the same text.
     pages = [synth.page(i) for i in range(12)]
-    p = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=2)
-    print("bench configuration: 12 pages", flush=True)
+    p = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=4)
+    print("bench configuration: 12 pages, merge 6, detection groups of 4", flush=True)
     p.run(pages)
-    q = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=6)
-    q.run(pages)
+    others = []
+    for db in (2, 6):
+        q = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=db)
+        print(f"bench configuration: detection groups of {db}", flush=True)
+        q.run(pages)
+        others.append(q)
     for k, page in enumerate(pages):
         print(f"bench configuration: page {k} against the oracle", flush=True)
         texts, words = p.texts(k)
-        assert q.texts(k) == (texts, words)
+        for q in others:
+            assert q.texts(k) == (texts, words)
         bits = detector.detect_page(page, 0.5)
         want_bits, prob, _ = og.detect_page(det_oracle, page, 0.5)
         diff = np.unpackbits((bits ^ want_bits).view(np.uint8), bitorder="little").reshape(bits.shape[0], -1)

@@ -2,7 +2,9 @@
 (tests/cpp/test_pipeline_core.cpp): a failing stage, detection, layout, recognition or decode
 fails exactly the pages it covers and every other page finishes, as the reference reports errors
 per page (src/bin/ocr-bench.rs:277-281, 303-307). Built with g++ under AddressSanitizer +
-UndefinedBehaviorSanitizer, and under ThreadSanitizer."""
+UndefinedBehaviorSanitizer, and under ThreadSanitizer. The bounded host wait (csrc/wait.h) is
+forced past its deadline there: a stalled detection group fails its own pages with an error
+naming it, and the other pages finish."""
 import os
 import shutil
 import subprocess
@@ -22,7 +24,7 @@ def _build_and_run(tmp_path, sanitize):
            SRC, "-o", exe, "-pthread"]
     subprocess.run(cmd, check=True, capture_output=True, text=True)
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1", UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1",
-               TSAN_OPTIONS="halt_on_error=1")
+               TSAN_OPTIONS="halt_on_error=1", OCR_WAIT_TIMEOUT_MS="25")
     r = subprocess.run([exe], capture_output=True, text=True, env=env, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "all checks passed" in r.stdout

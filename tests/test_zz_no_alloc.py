@@ -45,6 +45,25 @@ def test_noalloc_word_rects_match_pooled_entry(detector, ctx):
     _same(ctx, full, page.shape[1], "full page mask again")
 
 
+def test_noalloc_word_rects_allocate_nothing():
+    # A context of its own, used by nothing else: its pool starts empty. The allocation-free
+    # entry, called on masks of decreasing size, must leave the library's device and page-locked
+    # allocation counts and the pool untouched; the pooled entry afterwards does allocate.
+    ctx = ocrhip.Context(pool_mb=64)
+    rng = np.random.Generator(np.random.PCG64(11))
+    masks = [(_pack(rng.random((1200, 2000)) < 0.3), 2000), (_pack(rng.random((300, 700)) < 0.3), 700)]
+    print("noalloc word rects: allocation counts", flush=True)
+    before = ctx.memory_stats()
+    for bits, w in masks:
+        ocrhip.word_rects_gpu_noalloc(ctx, bits, w)
+    after = ctx.memory_stats()
+    assert after == before, (before, after)
+    ocrhip.word_rects_gpu(ctx, *masks[1])
+    pooled = ctx.memory_stats()
+    assert pooled["device_allocs"] > after["device_allocs"] or pooled["pool_held"] > after["pool_held"]
+    ctx.close()
+
+
 def test_noalloc_word_rects_reject_oversize(ctx):
     print("noalloc word rects: oversize masks", flush=True)
     with pytest.raises(ocrhip.OcrError, match="exceed"):

@@ -108,7 +108,9 @@ Onnx onnx_of(const ocr_onnx *g) {
         std::vector<int64_t> dims(t.dims, t.dims + t.rank);
         for (int64_t d : dims) {
             if (d < 0) fail("graph: tensor " + name + " has a negative dimension");
-            n *= uint64_t(d);
+            // Refuse dims whose product overflows (it could wrap round to the value count).
+            if (__builtin_mul_overflow(n, uint64_t(d), &n) || n > (uint64_t(1) << 40))
+                fail("graph: tensor " + name + " has more elements than a model tensor can hold");
         }
         if ((t.data != nullptr) == (t.ints != nullptr)) fail("graph: tensor " + name + " needs exactly one of data, ints");
         if (t.data) {
@@ -189,7 +191,7 @@ void *ocr_device_alloc(ocr_ctx *ctx, size_t bytes) {
         need(ctx, "ctx");
         ctx->ctx->bind();
         void *p = nullptr;
-        OCR_HIP(hipMalloc(&p, bytes ? bytes : 16));
+        device_malloc(&p, bytes ? bytes : 16);
         return p;
     });
 }
@@ -203,12 +205,23 @@ int ocr_device_free(ocr_ctx *ctx, void *p) {
     });
 }
 
+int ocr_memory_stats(ocr_ctx *ctx, uint64_t *device_allocs, uint64_t *host_allocs, uint64_t *pool_live,
+                     uint64_t *pool_held) {
+    return guard([&] {
+        need(ctx, "ctx");
+        if (device_allocs) *device_allocs = device_allocations();
+        if (host_allocs) *host_allocs = host_allocations();
+        if (pool_live) *pool_live = ctx->ctx->pool().live();
+        if (pool_held) *pool_held = ctx->ctx->pool().held();
+    });
+}
+
 void *ocr_host_alloc(ocr_ctx *ctx, size_t bytes) {
     return guard_ptr<void>([&]() -> void * {
         need(ctx, "ctx");
         ctx->ctx->bind();
         void *p = nullptr;
-        OCR_HIP(hipHostMalloc(&p, bytes ? bytes : 16, hipHostMallocDefault));
+        host_malloc(&p, bytes ? bytes : 16);
         return p;
     });
 }

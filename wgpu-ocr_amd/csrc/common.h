@@ -17,6 +17,11 @@ struct Error : std::runtime_error {
 
 [[noreturn]] void fail(const std::string &msg);
 
+// Every device and page-locked host allocation the library makes goes through these two, so
+// they can be counted (ocr_memory_stats): callers that must not allocate can check a path.
+void device_malloc(void **p, size_t bytes);
+void host_malloc(void **p, size_t bytes);
+
 #define OCR_HIP(call)                                                                              \
     do {                                                                                           \
         hipError_t e_ = (call);                                                                    \

@@ -171,7 +171,7 @@ struct Pinned {
         if (n <= bytes) return;
         if (p) (void)hipHostFree(p);
         p = nullptr;
-        OCR_HIP(hipHostMalloc(&p, n, hipHostMallocDefault));
+        host_malloc(&p, n);
         // Touch every page now: the first CPU access to a page of it faults it in (about 2 GB/s
         // where later accesses run at memory speed), which would otherwise land on a run.
         std::memset(p, 0, n);

@@ -12,6 +12,7 @@
 // calls and a call never sees the previous call's contents.
 #include <hip/hip_runtime.h>
 
+#include <exception>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -49,6 +50,20 @@ std::mutex g_init_mu;
 void *g_scratch[MAX_DEVICES];       // the array's device address on each device (null: not set up)
 std::mutex g_call_mu[MAX_DEVICES];  // one call at a time per device
 
+// Leaving a call by an exception after its kernels were queued: wait for the stream before the
+// device's lock is released, or the next call would overwrite the array under those kernels.
+struct SyncOnUnwind {
+    hipStream_t st;
+    int uncaught = std::uncaught_exceptions();
+    ~SyncOnUnwind() {
+        if (std::uncaught_exceptions() <= uncaught) return;
+        try {
+            wait_stream(st, "the labelling kernels of a failed allocation-free call");
+        } catch (...) {
+        }
+    }
+};
+
 }  // namespace
 
 void noalloc_init(int device) {
@@ -85,6 +100,7 @@ std::vector<RRect> word_rects_gpu_noalloc(Ctx &c, const uint32_t *bits, int w, i
     c.bind();
     unsigned char *s = static_cast<unsigned char *>(base);
     const hipStream_t st = c.stream();
+    SyncOnUnwind drain{st};
     OCR_HIP(hipMemcpyAsync(s + OFF_BITS, bits, words * 4, hipMemcpyHostToDevice, st));
     CclPage pg{};
     pg.bits = reinterpret_cast<const uint32_t *>(s + OFF_BITS), pg.w = w, pg.h = h;
@@ -99,7 +115,7 @@ std::vector<RRect> word_rects_gpu_noalloc(Ctx &c, const uint32_t *bits, int w, i
     ccl_runs(&pg, 1, st);
     int32_t tot[4] = {0, 0, 0, 0};
     OCR_HIP(hipMemcpyAsync(tot, pg.total, 16, hipMemcpyDeviceToHost, st));
-    OCR_HIP(hipStreamSynchronize(st));
+    wait_stream(st, "the allocation-free labelling of a " + std::to_string(w) + " x " + std::to_string(h) + " mask");
     // More runs, components or row slots than the array holds: the host labels the mask from
     // the bits (the same rectangles; see word_rects_from_rows).
     if (tot[0] > NOALLOC_RUNS || tot[1] > NOALLOC_COMPS || tot[2] > NOALLOC_SLOTS) return word_rects(bits, w, h);
@@ -110,7 +126,7 @@ std::vector<RRect> word_rects_gpu_noalloc(Ctx &c, const uint32_t *bits, int w, i
         OCR_HIP(hipMemcpyAsync(comps.data(), pg.comps, nc * 16, hipMemcpyDeviceToHost, st));
         OCR_HIP(hipMemcpyAsync(xmin.data(), pg.xmin, ns * 4, hipMemcpyDeviceToHost, st));
         OCR_HIP(hipMemcpyAsync(xmax.data(), pg.xmax, ns * 4, hipMemcpyDeviceToHost, st));
-        OCR_HIP(hipStreamSynchronize(st));
+        wait_stream(st, "the copies of the allocation-free labelling's records");
     }
     return word_rects_from_rows(bits, w, h, comps.data(), int(nc), xmin.data(), xmax.data(), int(ns));
 }

@@ -508,14 +508,7 @@ int cu_count3() {
     return n;
 }
 
-const float4 *zero_block() {
-    static float4 *z = nullptr;
-    if (!z) {
-        OCR_HIP(hipMalloc(&z, 64));
-        OCR_HIP(hipMemset(z, 0, 64));
-    }
-    return z;
-}
+const float4 *zero_block() { return static_cast<const float4 *>(zero_block64()); }
 
 }  // namespace
 

@@ -323,14 +323,7 @@ int gcu_count() {
     return n;
 }
 
-const float *gzero() {
-    static float *z = nullptr;
-    if (!z) {
-        OCR_HIP(hipMalloc(&z, 64));
-        OCR_HIP(hipMemset(z, 0, 64));
-    }
-    return z;
-}
+const float *gzero() { return static_cast<const float *>(zero_block64()); }
 
 }  // namespace
 

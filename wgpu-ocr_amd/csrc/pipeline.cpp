@@ -22,19 +22,9 @@
 
 namespace ocr {
 
-// Waits for a GPU event by polling every 20 microseconds: the worker threads waiting for
-// detection or recognition results sleep instead of spinning, so the host cores go to the
-// layouts; spin: yield between polls instead (the last pass, when no layout is left to run and
-// a sleep's wake-up latency would add to the run).
-static void wait_event(hipEvent_t ev, bool spin = false) {
-    for (;;) {
-        const hipError_t e = hipEventQuery(ev);
-        if (e == hipSuccess) return;
-        if (e != hipErrorNotReady) OCR_HIP(e);
-        if (spin) std::this_thread::yield();
-        else std::this_thread::sleep_for(std::chrono::microseconds(20));
-    }
-}
+// Worker threads wait for detection and recognition results with wait_event (runtime.h): after a
+// short yielding phase they sleep between polls, so the host cores go to the layouts; the last
+// pass's wait keeps yielding (a sleep's wake-up would add to the run). Every wait is bounded.
 
 PageLayout layout_page(const uint32_t *bits, int w, int h, float relv, float relend, int threads, int page_prio,
                        const MaskRows *rows) {
@@ -217,7 +207,7 @@ struct Pipeline::Impl {
     ~Impl() {
         for (hipStream_t s : {copy, up})
             if (s) {
-                (void)hipStreamSynchronize(s);
+                drain_stream(s, s == up ? "the pipeline's upload stream" : "the pipeline's copy stream");
                 ctx.pool().retire_stream(s);
                 (void)hipStreamDestroy(s);
             }
@@ -236,7 +226,7 @@ struct Pipeline::Impl {
             const int k = next_slot;
             next_slot = (next_slot + 1) % SLOTS;
             slot[k].ensure(SLOT_BYTES);
-            if (slot_used[k]) OCR_HIP(hipEventSynchronize(slot_ev[k]));
+            if (slot_used[k]) wait_event(slot_ev[k], "the upload reading staging slot " + std::to_string(k), true);
             uint8_t *stage = static_cast<uint8_t *>(slot[k].p);
             crew.copy(stage, src + off, n);
             OCR_HIP(hipMemcpyAsync(dst + off, stage, n, hipMemcpyHostToDevice, up));
@@ -382,9 +372,9 @@ struct PipelineRun final : PipelineHooks {
     }
     ~PipelineRun() override {
         // Nothing may still use the run's buffers once they go back to the pool.
-        (void)hipStreamSynchronize(I.up);
-        (void)hipStreamSynchronize(I.copy);
-        (void)hipStreamSynchronize(st);
+        drain_stream(I.up, "a finished run's uploads");
+        drain_stream(I.copy, "a finished run's copies to the host");
+        drain_stream(st, "a finished run's kernels");
         for (hipEvent_t e : up_ev)
             if (e) (void)hipEventDestroy(e);
         for (hipEvent_t e : det_ev)
@@ -498,8 +488,8 @@ struct PipelineRun final : PipelineHooks {
         ctx.bind();
         // The last group's result is on the run's critical path and the layouts before it are
         // done by then: poll it (yielding) rather than sleep in the blocking wait.
-        if (g + 1 == P.groups()) wait_event(det_ev[size_t(g)], true);
-        else OCR_HIP(hipEventSynchronize(det_ev[size_t(g)]));
+        wait_event(det_ev[size_t(g)], "detection group " + std::to_string(g) + " of " + std::to_string(P.groups()),
+                   g + 1 == P.groups());
         mark("det group " + std::to_string(g) + " done");
     }
 
@@ -609,14 +599,20 @@ struct PipelineRun final : PipelineHooks {
             // stage just queued keeps the GPU busy while the next one is queued.
             const bool pending = detections_pending && detections_pending();
             if (!pending && stage_ev.size() < 2) return;
-            const hipEvent_t prev = pending ? stage_ev.back() : stage_ev[stage_ev.size() - 2];
-            for (;;) {
-                const hipError_t q = hipEventQuery(prev);
-                if (q == hipSuccess) break;
-                if (q != hipErrorNotReady) OCR_HIP(q);
-                if (poll_detections) poll_detections();
-                std::this_thread::sleep_for(std::chrono::microseconds(20));
-            }
+            const size_t k = pending ? stage_ev.size() - 1 : stage_ev.size() - 2;
+            const hipEvent_t prev = stage_ev[k];
+            wait_until(
+                [&] {
+                    const hipError_t q = hipEventQuery(prev);
+                    if (q == hipSuccess) return true;
+                    if (q != hipErrorNotReady) OCR_HIP(q);
+                    if (poll_detections) poll_detections();
+                    return false;
+                },
+                [&] {
+                    return "stage " + std::to_string(k) + " of recognition pass " + std::to_string(r) +
+                           " on the compute stream";
+                });
         };
         I.rec.recognize_device(rb.data(), int(rb.size()), logits.as<float>(), R.best.as<uint32_t>(), R.lens.data(),
                                between);
@@ -643,7 +639,7 @@ struct PipelineRun final : PipelineHooks {
         ctx.bind();
         const RecPass &R = passes[size_t(r)];
         if (!R.done) return;
-        wait_event(R.done, last);
+        wait_event(R.done, "recognition pass " + std::to_string(r) + " and its arg-max copy", last);
         mark("ctc " + std::to_string(r) + " start");
         const uint32_t *bh = static_cast<const uint32_t *>(I.best_host[size_t(r)].p);
         // Lines in chunks on the loop pool (each line's text has a slot of its own).

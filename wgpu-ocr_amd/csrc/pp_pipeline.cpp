@@ -131,7 +131,7 @@ void PpPipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, in
                     double busy = 0;
                     try {
                         (void)hipSetDevice(dev);
-                        OCR_HIP(hipEventSynchronize(ev));
+                        wait_event(ev, "the probability map and mask of page " + std::to_string(k));
                         const auto tc = Clock::now();
                         PageBoxes B;
                         for (const RRect &r : db_boxes(bt, pr, mw, mh, float(pw) / float(mw), float(ph) / float(mh), I.opts.db))
@@ -226,7 +226,7 @@ void PpPipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, in
                 double busy = 0;
                 try {
                     (void)hipSetDevice(dev);
-                    OCR_HIP(hipEventSynchronize(ev));
+                    wait_event(ev, "the arg-max of recognition pass " + std::to_string(r));
                     const auto tc = Clock::now();
                     for (const Row &row : rows[size_t(r)])
                         pages_[size_t(row.page)].lines[size_t(row.line)] = pp_ctc_decode(bh + row.off, row.steps);

@@ -5,6 +5,86 @@
 
 namespace ocr {
 
+namespace {
+std::atomic<uint64_t> g_device_allocs{0}, g_host_allocs{0};
+}  // namespace
+
+hipError_t try_device_malloc(void **p, size_t bytes) {
+    g_device_allocs.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(p, bytes);
+}
+
+void device_malloc(void **p, size_t bytes) { OCR_HIP(try_device_malloc(p, bytes)); }
+
+void host_malloc(void **p, size_t bytes) {
+    g_host_allocs.fetch_add(1, std::memory_order_relaxed);
+    OCR_HIP(hipHostMalloc(p, bytes, hipHostMallocDefault));
+}
+
+uint64_t device_allocations() { return g_device_allocs.load(std::memory_order_relaxed); }
+uint64_t host_allocations() { return g_host_allocs.load(std::memory_order_relaxed); }
+
+void wait_event(hipEvent_t ev, const std::string &what, bool spin) {
+    wait_until(
+        [&] {
+            const hipError_t e = hipEventQuery(ev);
+            if (e == hipSuccess) return true;
+            if (e != hipErrorNotReady) OCR_HIP(e);
+            return false;
+        },
+        [&] {
+            char b[48];
+            std::snprintf(b, sizeof b, " (event %p)", static_cast<void *>(ev));
+            return what + b;
+        },
+        spin);
+}
+
+void wait_stream(hipStream_t s, const std::string &what, bool spin) {
+    wait_until(
+        [&] {
+            const hipError_t e = hipStreamQuery(s);
+            if (e == hipSuccess) return true;
+            if (e != hipErrorNotReady) OCR_HIP(e);
+            return false;
+        },
+        [&] {
+            char b[48];
+            std::snprintf(b, sizeof b, " (stream %p)", static_cast<void *>(s));
+            return what + b;
+        },
+        spin);
+}
+
+void drain_stream(hipStream_t s, const std::string &what) noexcept {
+    try {
+        wait_stream(s, what);
+        return;
+    } catch (const WaitTimeout &e) {
+        std::fprintf(stderr, "ocrhip: %s; still waiting\n", e.what());
+        std::fflush(stderr);
+    } catch (...) {
+    }
+    (void)hipStreamSynchronize(s);
+}
+
+const void *zero_block64() {
+    constexpr int MAX_DEV = 64;
+    static std::mutex mu;
+    static void *blocks[MAX_DEV] = {};
+    int dev = 0;
+    OCR_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEV) fail("zero block: device index " + std::to_string(dev));
+    std::lock_guard<std::mutex> lk(mu);
+    if (!blocks[dev]) {
+        void *z = nullptr;
+        device_malloc(&z, 64);
+        OCR_HIP(hipMemset(z, 0, 64));
+        blocks[dev] = z;
+    }
+    return blocks[dev];
+}
+
 void fail(const std::string &msg) { throw Error(msg); }
 
 Probe &Probe::get() {
@@ -61,7 +141,7 @@ bool Probe::stop(const std::string &family, uint32_t *calls, double *ms, double 
     Fam &f = it->second;
     double total = 0;
     for (auto &pr : f.ev) {
-        OCR_HIP(hipEventSynchronize(pr.second));
+        wait_event(pr.second, "the end of a probed " + family + " launch", true);
         float t = 0;
         OCR_HIP(hipEventElapsedTime(&t, pr.first, pr.second));
         total += t;
@@ -139,12 +219,12 @@ void *Pool::get(size_t bytes, hipStream_t s) {
         }
     }
     void *p = nullptr;
-    hipError_t e = hipMalloc(&p, sz);
+    hipError_t e = try_device_malloc(&p, sz);
     if (e != hipSuccess) {
         // Out of memory: give back what the pool holds and try once more.
         (void)hipGetLastError();
         trim();
-        OCR_HIP(hipMalloc(&p, sz));
+        device_malloc(&p, sz);
     }
     std::lock_guard<std::mutex> lk(mu_);
     size_of_[p] = sz;
@@ -249,7 +329,7 @@ Ctx::Ctx(int device, uint32_t lines, size_t pool_mb) : device_(device), lines_(l
 
 Ctx::~Ctx() {
     (void)hipSetDevice(device_);
-    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (stream_) drain_stream(stream_, "the context's stream before it is destroyed");
     for (const Staged &st : staged_) (void)hipEventDestroy(st.done);
     for (hipEvent_t e : spare_events_) (void)hipEventDestroy(e);
     if (ring_) (void)hipHostFree(ring_);
@@ -277,11 +357,11 @@ StreamScope::~StreamScope() {
 
 void Ctx::bind() const { OCR_HIP(hipSetDevice(device_)); }
 
-void Ctx::sync() { OCR_HIP(hipStreamSynchronize(stream())); }
+void Ctx::sync() { wait_stream(stream(), "the context's work on device " + std::to_string(device_)); }
 
 const void *Ctx::upload_raw(const void *data, size_t bytes) {
     void *p = nullptr;
-    OCR_HIP(hipMalloc(&p, bytes ? bytes : 16));
+    device_malloc(&p, bytes ? bytes : 16);
     weights_.push_back(p);
     if (bytes) OCR_HIP(hipMemcpy(p, data, bytes, hipMemcpyHostToDevice));
     return p;
@@ -300,7 +380,9 @@ void Ctx::h2d(void *dst, const void *src, size_t bytes) {
     }
     std::lock_guard<std::mutex> lk(ring_mu_);
     if (!ring_) {
-        OCR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ring_), RING_BYTES, hipHostMallocDefault));
+        void *ring = nullptr;
+        host_malloc(&ring, RING_BYTES);
+        ring_ = static_cast<char *>(ring);
         // Fault every page in now (a page's first CPU write runs at about 2 GB/s, later ones at
         // memory speed), not while a run stages its tables.
         std::memset(ring_, 0, RING_BYTES);
@@ -320,7 +402,7 @@ void Ctx::h2d(void *dst, const void *src, size_t bytes) {
         return false;
     };
     while (overlaps()) {
-        OCR_HIP(hipEventSynchronize(staged_.front().done));
+        wait_event(staged_.front().done, "an upload still reading the staging ring", true);
         spare_events_.push_back(staged_.front().done);
         staged_.pop_front();
     }
@@ -342,7 +424,7 @@ void Ctx::h2d(void *dst, const void *src, size_t bytes) {
 void Ctx::d2h(void *dst, const void *src, size_t bytes) {
     const hipStream_t st = stream();
     if (bytes) OCR_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st));
-    OCR_HIP(hipStreamSynchronize(st));
+    wait_stream(st, "a device-to-host copy of " + std::to_string(bytes) + " bytes");
 }
 
 }  // namespace ocr

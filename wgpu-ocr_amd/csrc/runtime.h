@@ -14,8 +14,26 @@
 #include <vector>
 
 #include "common.h"
+#include "wait.h"
 
 namespace ocr {
+
+// As device_malloc (common.h), but returns the error instead of failing (the pool retries after a trim).
+hipError_t try_device_malloc(void **p, size_t bytes);
+uint64_t device_allocations();
+uint64_t host_allocations();
+// Bounded waits (wait.h) for an event or for all work of a stream; `what` names it, with the
+// event or stream, in the error a deadline raises.
+void wait_event(hipEvent_t ev, const std::string &what, bool spin = false);
+void wait_stream(hipStream_t s, const std::string &what, bool spin = true);
+// For destructors, which cannot fail: a bounded wait as above; past the deadline the stall is
+// reported on stderr and the wait goes on (the buffers the stream uses must not be reused before
+// it ends). GPU errors are ignored here.
+void drain_stream(hipStream_t s, const std::string &what) noexcept;
+
+// 64 zero bytes on the current device (allocated once per device, kept until the process ends):
+// the kernels' source for out-of-range taps.
+const void *zero_block64();
 
 // Size-classed, stream-ordered pool of device buffers (gpu.rs:938-966). hipMalloc is slow and
 // synchronising, so scratch buffers are reused. Every buffer has a home stream, the stream its

@@ -44,6 +44,8 @@ SIGNATURES = {
     "ocr_memcpy_d2h": (ctypes.c_int, [P, P, P, SZ]),
     "ocr_host_alloc": (P, [P, SZ]),
     "ocr_host_free": (ctypes.c_int, [P, P]),
+    "ocr_memory_stats": (ctypes.c_int, [P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                                        ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "ocr_png_dims": (ctypes.c_int, [P, SZ, PU32, PU32]),
     "ocr_png_decode": (ctypes.c_int, [P, SZ, P, SZ, PU32, PU32]),
     "ocr_detector_new": (P, [P, ctypes.c_char_p]),
@@ -309,6 +311,12 @@ class Context:
     def host_array(self, shape, dtype=np.uint8) -> "HostArray":
         """A numpy array in page-locked host memory (ocr_host_alloc)."""
         return HostArray(self, shape, dtype)
+
+    def memory_stats(self) -> dict:
+        """The library's allocation counts (process-wide) and this context's pool bytes."""
+        v = [ctypes.c_uint64() for _ in range(4)]
+        _check(lib().ocr_memory_stats(self.handle, *[ctypes.byref(x) for x in v]))
+        return dict(zip(("device_allocs", "host_allocs", "pool_live", "pool_held"), (x.value for x in v)))
 
     def close(self):
         if self.handle:
@@ -596,7 +604,7 @@ def decode_pngs(srcs, threads: int = 8) -> list:
 def word_rects(bits: np.ndarray, w: int, threads: int = 1):
     """Words of a page mask (ocr-bench.rs:40-60) as an [n, 6] array (cx, cy, ux, uy, w, h),
     computed on `threads` host threads."""
-    bits = np.ascontiguousarray(bits, np.uint32)
+    bits = _mask_bits(bits, w)
     h = bits.shape[0]
     count = ctypes.c_uint32()
     _check(lib().ocr_word_rects_mt(_ptr(bits), w, h, threads, None, 0, ctypes.byref(count)))
@@ -605,9 +613,17 @@ def word_rects(bits: np.ndarray, w: int, threads: int = 1):
     return out
 
 
+def _mask_bits(bits: np.ndarray, w: int) -> np.ndarray:
+    """A page mask as the C ABI reads it: h rows of ceil(w / 32) 32-bit words."""
+    bits = np.ascontiguousarray(bits, np.uint32)
+    if bits.ndim != 2 or bits.shape[1] != (w + 31) // 32:
+        raise OcrError(f"mask of shape {bits.shape} is not rows of ceil({w} / 32) = {(w + 31) // 32} words")
+    return bits
+
+
 def word_rects_gpu(ctx: "Context", bits: np.ndarray, w: int):
     """The same words with the mask's runs labelled on the GPU (the page pipeline's path)."""
-    bits = np.ascontiguousarray(bits, np.uint32)
+    bits = _mask_bits(bits, w)
     h = bits.shape[0]
     count = ctypes.c_uint32()
     _check(lib().ocr_word_rects_gpu(ctx.handle, _ptr(bits), w, h, None, 0, ctypes.byref(count)))
@@ -618,7 +634,7 @@ def word_rects_gpu(ctx: "Context", bits: np.ndarray, w: int):
 
 def word_rects_gpu_noalloc(ctx: "Context", bits: np.ndarray, w: int):
     """word_rects_gpu with the labelling in the library's fixed device array (no allocation)."""
-    bits = np.ascontiguousarray(bits, np.uint32)
+    bits = _mask_bits(bits, w)
     h = bits.shape[0]
     count = ctypes.c_uint32()
     _check(lib().ocr_word_rects_gpu_noalloc(ctx.handle, _ptr(bits), w, h, None, 0, ctypes.byref(count)))
