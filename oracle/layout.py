@@ -13,8 +13,10 @@ product's host code, as the oracle of the page pipeline.
   rule for them (a word joins the line whose last word ends nearest before it when they overlap
   vertically by half the smaller height and the gap is at most twice the taller height; the line
   polygon of the words' top and bottom edges, floored, filled by the even-odd rule at pixel
-  centres, resized to height 64 keeping the aspect ratio, width clamped to [10, 800]). Parity
-  with ocrs itself is unpinned for these two.
+  centres, resized to height 64 keeping the aspect ratio, width clamped to [10, 800]). The lines
+  are pinned against ocrs's own lines on the reference's four 300-dpi pages
+  (results/texts-245k/ocrs_0..3.txt; tests/test_ocrs_lines.py): the same line counts, reading
+  order and line extents. The rule's word-level decisions beyond those pages stay unpinned.
 
 Arithmetic is float32 in the order the restated steps give it, so results are comparable bit for
 bit.
