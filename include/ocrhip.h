@@ -309,6 +309,12 @@ ocr_nd *ocr_nd_new(ocr_ctx *ctx, const char *onnx_path, int stop_before_softmax)
 /* NdGraph::new(&Gpu, &Onnx, stop_before_softmax) (src/nd.rs:505) from a graph the host has parsed. */
 ocr_nd *ocr_nd_new_onnx(ocr_ctx *ctx, const ocr_onnx *graph, int stop_before_softmax);
 void ocr_nd_free(ocr_nd *g);
+/* The fusion plan NdGraph::new makes for an ONNX file (the operator contract of src/nd.rs:505-817),
+ * as text, without a GPU: one line a launch, "<kind> <op>@<node> [<nodes>] [act=<a>] [bias=<n>]
+ * [bn@<node>] [residual=<value>] [in_scale=<value>] -> <output>", in the order they run (node
+ * indices after Identity nodes and unused nodes are dropped). Writes at most cap bytes, NUL
+ * included, into buf (which may be NULL); *len receives the length without the NUL. */
+int ocr_nd_plan(const char *onnx_path, int stop_before_softmax, char *buf, uint32_t cap, uint32_t *len);
 /* Output shape (rank <= 6) for an input shape, without running the graph. */
 int ocr_nd_dims(ocr_nd *g, const int64_t *in_shape, uint32_t rank, int64_t *out_shape, uint32_t *out_rank);
 /* NdGraph::run (src/nd.rs:834-1195) on a row-major float input (host); out receives the output

@@ -171,6 +171,36 @@ def test_binary_broadcast_and_shape_ops(ctx, tmp_path):
     check(ctx, p, RNG.standard_normal((2, 5, 6)).astype(np.float32))
 
 
+def test_fusions_across_unrelated_nodes_and_operand_orders(ctx, tmp_path):
+    # Chains the plan matches over def-use edges rather than node order: a bias Add given first
+    # and placed after an unrelated node, a residual produced after the conv, the LayerNorm's
+    # gamma Mul with its operands swapped and an unrelated node inside the chain, GELU with its
+    # constants first. Each runs fused and must equal the unfused oracle.
+    def fn(g, x):
+        c = conv(g, x, 8, 16, bias=False)
+        side = g.add("Relu", [x])
+        y = g.add("Add", [g.init("b0", (RNG.standard_normal((1, 16, 1, 1)) * 0.1).astype(np.float32)), c])
+        h = g.add("Erf", [g.add("Div", [y, const(g, 1.4142135)])])
+        y = g.add("Mul", [const(g, 0.5), g.add("Mul", [g.add("Add", [const(g, 1.0), h]), y])])
+        y = g.add("Add", [conv(g, side, 8, 16), y])
+        t = g.add("Reshape", [y, ints(g, [2, 16, -1])])
+        m = g.add("ReduceMean", [t], axes=[-1])
+        d = g.add("Sub", [t, m])
+        v = g.add("ReduceMean", [g.add("Pow", [d, const(g, 2.0)])], axes=[-1])
+        other = g.add("Sigmoid", [t])
+        n = g.add("Div", [d, g.add("Sqrt", [g.add("Add", [const(g, 1e-5), v])])])
+        width = 11 * 13
+        n = g.add("Mul", [g.init("gm", RNG.uniform(0.5, 1.5, width).astype(np.float32)), n])
+        n = g.add("Add", [n, g.init("bt", RNG.uniform(-.1, .1, width).astype(np.float32))])
+        return g.add("Add", [n, other])
+    p = build(tmp_path, "defuse", fn, (2, 8, 11, 13))
+    import ocrhip
+    kinds = [line.split()[0] for line in ocrhip.nd_plan(p)]
+    assert kinds.count("layer_norm") == 1 and any("act=gelu" in line and "residual" in line
+                                                  for line in ocrhip.nd_plan(p))
+    check(ctx, p, RNG.standard_normal((2, 8, 11, 13)).astype(np.float32))
+
+
 def test_unsupported_and_bad_shapes_raise(ctx, tmp_path):
     import ocrhip
     p = build(tmp_path, "bad", lambda g, x: g.add("Tanh", [x]), (1, 4))

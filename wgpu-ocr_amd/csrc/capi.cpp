@@ -1,6 +1,7 @@
 // The C ABI (include/ocrhip.h): status codes and a thread-local message, nothing thrown across.
 #include "../../include/ocrhip.h"
 
+#include <cstring>
 #include <memory>
 #include <string>
 #include <vector>
@@ -787,6 +788,19 @@ void det_input_size(uint32_t w, uint32_t h, uint32_t max_side, int *ow, int *oh)
 }  // namespace
 
 extern "C" {
+
+int ocr_nd_plan(const char *onnx_path, int stop_before_softmax, char *buf, uint32_t cap, uint32_t *len) {
+    return guard([&] {
+        need(onnx_path, "onnx_path");
+        const std::string text = describe(plan_nd(Onnx::load(onnx_path), stop_before_softmax != 0));
+        if (len) *len = uint32_t(text.size());
+        if (buf && cap) {
+            const size_t n = std::min<size_t>(text.size(), cap - 1);
+            std::memcpy(buf, text.data(), n);
+            buf[n] = 0;
+        }
+    });
+}
 
 ocr_nd *ocr_nd_new(ocr_ctx *ctx, const char *onnx_path, int stop_before_softmax) {
     return guard_ptr<ocr_nd>([&] {

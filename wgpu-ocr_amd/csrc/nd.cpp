@@ -1,7 +1,7 @@
-// NdGraph: load-time fusions as the reference's NdGraph::new (src/nd.rs:505-817) decides them,
-// plus one of this library's own (a BatchNormalization right after a Conv becomes the conv's
-// epilogue affine), and a run loop over the ops of NdGraph::run (nd.rs:834-1195). Buffers come
-// from the context's stream-ordered pool and go back after their last reader.
+// NdGraph: the fusion plan of nd_plan.cpp (the operator contract of the reference's
+// NdGraph::new, src/nd.rs:505-817) with each step's weights laid out for its kernel, and a run
+// loop over the steps (NdGraph::run, nd.rs:834-1195). Buffers come from the context's
+// stream-ordered pool and go back after their last reader.
 #include "nd.h"
 
 #include <algorithm>
@@ -38,363 +38,171 @@ std::string shape_str(const std::vector<int64_t> &s) {
     return o + "]";
 }
 
-bool env_set(const char *n) { return std::getenv(n) != nullptr; }
-
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
 // Build
 // ---------------------------------------------------------------------------------------------
-NdGraph NdGraph::build(Ctx &ctx, const Onnx &onnx, bool stop_before_softmax) {
-    NdGraph g;
-    // Identity nodes: readers read their input instead (nd.rs:506-524).
-    std::map<std::string, std::string> alias;
-    for (const Node &n : onnx.nodes)
-        if (n.op == "Identity") {
-            auto it = alias.find(n.inputs.at(0));
-            alias[n.outputs.at(0)] = it != alias.end() ? it->second : n.inputs.at(0);
-        }
-    auto resolve = [&](const std::string &s) {
-        auto it = alias.find(s);
-        return it == alias.end() ? s : it->second;
-    };
-    std::vector<Node> nodes;
-    for (const Node &n : onnx.nodes) {
-        if (n.op == "Identity") continue;
-        Node c = n;
-        for (auto &i : c.inputs) i = resolve(i);
-        nodes.push_back(std::move(c));
-    }
-    std::string output = resolve(onnx.output);
-    // Drop a final Softmax (nd.rs:526-532).
-    if (stop_before_softmax) {
-        for (size_t i = nodes.size(); i-- > 0;)
-            if (!nodes[i].outputs.empty() && nodes[i].outputs[0] == output) {
-                if (nodes[i].op == "Softmax") {
-                    output = nodes[i].inputs.at(0);
-                    nodes.resize(i);
-                }
-                break;
-            }
-    }
-    auto has_weight = [&](const std::string &nm) { return onnx.weights.count(nm) > 0; };
-    auto scalar = [&](const std::string &nm) -> std::optional<float> {
-        auto it = onnx.weights.find(nm);
-        if (it == onnx.weights.end() || it->second.data.size() != 1) return std::nullopt;
-        return it->second.data[0];
-    };
-    std::vector<bool> skip(nodes.size(), false);
-    auto count_readers = [&]() {
-        std::map<std::string, int> c;
-        for (size_t k = 0; k < nodes.size(); k++)
-            if (!skip[k])
-                for (const auto &i : nodes[k].inputs) c[i]++;
-        return c;
-    };
-    // Squeeze-excitation: Mul(x, HardSigmoid gate) read only by a dense Conv becomes that conv's
-    // input scale (nd.rs:552-571).
-    std::map<size_t, std::string> in_scale;
-    {
-        auto first = count_readers();
-        auto readers = [&](const std::string &nm) { return first[nm] + (nm == output ? 1 : 0); };
-        std::vector<std::tuple<size_t, size_t, std::string, std::string>> se;
-        for (size_t mi = 0; mi < nodes.size(); mi++) {
-            const Node &m = nodes[mi];
-            if (m.op != "Mul" || readers(m.outputs[0]) != 1) continue;
-            size_t ci = nodes.size();
-            for (size_t c = 0; c < nodes.size(); c++)
-                if (nodes[c].op == "Conv" && nodes[c].inputs.at(0) == m.outputs[0] && nodes[c].int_("group").value_or(1) == 1) {
-                    ci = c;
-                    break;
-                }
-            if (ci == nodes.size()) continue;
-            auto gate = [&](const std::string &nm) {
-                return std::any_of(nodes.begin(), nodes.end(),
-                                   [&](const Node &x) { return x.op == "HardSigmoid" && x.outputs[0] == nm; });
-            };
-            if (gate(m.inputs.at(1))) se.emplace_back(mi, ci, m.inputs[0], m.inputs[1]);
-            else if (gate(m.inputs.at(0))) se.emplace_back(mi, ci, m.inputs[1], m.inputs[0]);
-        }
-        if (!env_set("NOSE"))
-            for (auto &[mi, ci, x, sc] : se) {
-                in_scale[ci] = sc;
-                skip[mi] = true;
-                nodes[ci].inputs[0] = x;
-            }
-    }
-    auto counts = count_readers();
-    auto readers = [&](const std::string &nm) {
-        auto it = counts.find(nm);
-        return (it == counts.end() ? 0 : it->second) + (nm == output ? 1 : 0);
-    };
-    // A following Add of a constant `want`-element bias with at most one non-1 dimension.
-    auto takes_bias = [&](const Node &next, const std::string &out, size_t want) -> std::optional<std::string> {
-        if (next.op != "Add" || readers(out) != 1) return std::nullopt;
-        std::string other;
-        if (next.inputs.at(0) == out) other = next.inputs.at(1);
-        else if (next.inputs.at(1) == out) other = next.inputs.at(0);
-        else return std::nullopt;
-        auto it = onnx.weights.find(other);
-        if (it == onnx.weights.end() || it->second.data.size() != want) return std::nullopt;
-        int non1 = 0;
-        for (int64_t d : it->second.dims) non1 += d != 1;
-        if (non1 > 1) return std::nullopt;
-        return other;
-    };
+namespace {
 
-    size_t i = 0;
-    while (i < nodes.size()) {
-        if (skip[i]) {
-            i++;
-            continue;
-        }
-        const Node &n = nodes[i];
+// Scale and shift of an inference BatchNormalization node: y = s x + t per channel, with
+// s = gamma / sqrt(var + eps) and t = beta - mean s. Returned as [s..., t...].
+std::vector<float> batch_norm_affine(const Onnx &onnx, const Node &bn, size_t channels) {
+    const float eps = bn.f32("epsilon").value_or(1e-5f);
+    const Weight &gamma = onnx.weight(bn.inputs.at(1)), &beta = onnx.weight(bn.inputs.at(2)),
+                 &mean = onnx.weight(bn.inputs.at(3)), &var = onnx.weight(bn.inputs.at(4));
+    for (const Weight *w : {&gamma, &beta, &mean, &var})
+        if (w->data.size() != channels)
+            fail("BatchNormalization parameters of " + std::to_string(w->data.size()) + " values for " +
+                 std::to_string(channels) + " channels");
+    std::vector<float> st(2 * channels);
+    for (size_t c = 0; c < channels; c++) {
+        st[c] = gamma.data[c] / std::sqrt(var.data[c] + eps);
+        st[channels + c] = beta.data[c] - mean.data[c] * st[c];
+    }
+    return st;
+}
+
+// Packs [rows][k] float weights into the matrix-core layout as float16 hi (+ lo when some value
+// is not a float16 value) and uploads them.
+void pack_upload(Ctx &ctx, NdOp &op, const float *w, int cin, int cout, int kh, int kw) {
+    op.pk = plan_conv_pack(cin, cout, kh, kw);
+    std::vector<uint16_t> hi(op.pk.halves()), lo(op.pk.halves());
+    bool exact = true;
+    pack_conv_weights(op.pk, w, hi.data(), lo.data(), &exact);
+    op.pk.exact = exact;
+    op.whi = ctx.upload_weights(hi.data(), hi.size());
+    if (!exact) op.wlo = ctx.upload_weights(lo.data(), lo.size());
+}
+
+// The epilogue bias of a step: the anchor's own bias input (if any) plus every bias Add taken.
+std::vector<float> step_bias(const Onnx &onnx, const NdStep &s, const Node &anchor, size_t channels) {
+    std::vector<float> b(channels, 0.f);
+    auto add = [&](const std::string &name, const char *what) {
+        const Weight &w = onnx.weight(name);
+        if (w.data.size() != channels)
+            fail(std::string(what) + " of " + std::to_string(w.data.size()) + " values for " + std::to_string(channels) +
+                 " output channels");
+        for (size_t c = 0; c < channels; c++) b[c] += w.data[c];
+    };
+    if (anchor.inputs.size() > 2 && !anchor.inputs[2].empty()) add(anchor.inputs[2], (anchor.op + " bias").c_str());
+    for (const auto &name : s.bias) add(name, "added bias");
+    return b;
+}
+
+}  // namespace
+
+// The plan (nd_plan.cpp) decides which nodes run together; here each step's weights are laid out
+// for its kernel and uploaded once.
+NdGraph NdGraph::build(Ctx &ctx, const Onnx &onnx, bool stop_before_softmax) {
+    NdPlan plan = plan_nd(onnx, stop_before_softmax);
+    NdGraph g;
+    for (const NdStep &s : plan.steps) {
+        const Node &n = plan.nodes[size_t(s.anchor)];
         NdOp op;
-        op.node = int(i);
+        op.kind = s.kind;
+        op.node = s.anchor;
         op.inputs = n.inputs;
-        op.output = n.outputs.at(0);
-        size_t j = i + 1;
-        std::string out = n.outputs[0];
-        // LayerNorm chain (nd.rs:583-611).
-        if (n.op == "ReduceMean" && i + 9 <= nodes.size()) {
-            const Node &mean = nodes[i], &sub = nodes[i + 1], &pw = nodes[i + 2], &var = nodes[i + 3],
-                       &add = nodes[i + 4], &sq = nodes[i + 5], &div = nodes[i + 6], &mul = nodes[i + 7],
-                       &beta = nodes[i + 8];
-            auto last_axis = [](const Node &x) {
-                auto a = x.ints("axes");
-                return a && a->size() == 1 && (*a)[0] == -1;
-            };
-            const bool chain =
-                last_axis(mean) && sub.op == "Sub" && sub.inputs[0] == mean.inputs[0] && sub.inputs[1] == mean.outputs[0] &&
-                pw.op == "Pow" && pw.inputs[0] == sub.outputs[0] && scalar(pw.inputs[1]) == std::optional<float>(2.f) &&
-                var.op == "ReduceMean" && var.inputs[0] == pw.outputs[0] && last_axis(var) && add.op == "Add" &&
-                add.inputs[0] == var.outputs[0] && scalar(add.inputs[1]).has_value() && sq.op == "Sqrt" &&
-                sq.inputs[0] == add.outputs[0] && div.op == "Div" && div.inputs[0] == sub.outputs[0] &&
-                div.inputs[1] == sq.outputs[0] && mul.op == "Mul" && mul.inputs[0] == div.outputs[0] &&
-                has_weight(mul.inputs[1]) && beta.op == "Add" && beta.inputs[0] == mul.outputs[0] &&
-                has_weight(beta.inputs[1]) && readers(mean.outputs[0]) == 1 && readers(sub.outputs[0]) == 2 &&
-                readers(pw.outputs[0]) == 1 && readers(var.outputs[0]) == 1 && readers(add.outputs[0]) == 1 &&
-                readers(sq.outputs[0]) == 1 && readers(div.outputs[0]) == 1 && readers(mul.outputs[0]) == 1;
-            if (chain) {
-                const Weight &gm = onnx.weight(mul.inputs[1]), &bt = onnx.weight(beta.inputs[1]);
-                if (gm.data.size() != bt.data.size()) fail("LayerNorm gamma and beta sizes differ");
-                std::vector<float> gb = gm.data;
-                gb.insert(gb.end(), bt.data.begin(), bt.data.end());
-                op.kind = NdKind::LayerNorm;
-                op.gb = ctx.upload_weights(gb.data(), gb.size());
-                op.len = int(gm.data.size());
-                op.eps = *scalar(add.inputs[1]);
-                op.inputs = {mean.inputs[0]};
-                op.output = beta.outputs[0];
-                for (size_t k = i + 1; k < i + 9; k++) skip[k] = true;
-                g.ops.push_back(std::move(op));
-                i += 9;
-                continue;
-            }
+        op.output = s.output;
+        op.act = s.act;
+        switch (s.kind) {
+        case NdKind::Generic:
+            break;
+        case NdKind::LayerNorm: {
+            const Weight &gm = onnx.weight(s.gamma), &bt = onnx.weight(s.beta);
+            if (gm.data.size() != bt.data.size()) fail("LayerNorm: " + std::to_string(gm.data.size()) + " scales and " +
+                                                       std::to_string(bt.data.size()) + " shifts");
+            std::vector<float> gb = gm.data;
+            gb.insert(gb.end(), bt.data.begin(), bt.data.end());
+            op.gb = ctx.upload_weights(gb.data(), gb.size());
+            op.len = int(gm.data.size());
+            op.eps = s.eps;
+            op.inputs = {n.inputs.at(0)};
+            break;
         }
-        if (n.op == "Conv") {
+        case NdKind::Affine: {
+            const size_t c = onnx.weight(n.inputs.at(1)).data.size();
+            const std::vector<float> st = batch_norm_affine(onnx, n, c);
+            op.st = ctx.upload_weights(st.data(), st.size());
+            op.cout = int(c);
+            op.inputs = {n.inputs.at(0)};
+            break;
+        }
+        case NdKind::Conv: {
             const Weight &w = onnx.weight(n.inputs.at(1));
-            if (w.dims.size() != 4) fail("conv weight not 4D");
-            op.kind = NdKind::Conv;
+            if (w.dims.size() != 4) fail("Conv weight of rank " + std::to_string(w.dims.size()) + ", not 4");
+            if (auto d = n.ints("dilations"))
+                for (int64_t v : *d)
+                    if (v != 1) fail("Conv dilation " + std::to_string(v) + " (only 1 is supported)");
             op.cout = int(w.dims[0]);
             op.cin_g = int(w.dims[1]);
             op.kh = int(w.dims[2]);
             op.kw = int(w.dims[3]);
             op.group = int(n.int_("group").value_or(1));
             op.cin = op.cin_g * op.group;
-            std::vector<float> b(size_t(op.cout), 0.f);
-            if (n.inputs.size() > 2 && !n.inputs[2].empty()) {
-                const Weight &bw = onnx.weight(n.inputs[2]);
-                if (bw.data.size() != size_t(op.cout)) fail("Conv bias size");
-                b = bw.data;
-            }
-            if (j < nodes.size())
-                if (auto bn = takes_bias(nodes[j], out, size_t(op.cout))) {
-                    const Weight &bw = onnx.weight(*bn);
-                    for (int c = 0; c < op.cout; c++) b[size_t(c)] += bw.data[size_t(c)];
-                    out = nodes[j].outputs[0];
-                    j++;
-                }
-            // This library's fusion: BatchNormalization right after, as the epilogue affine.
-            if (j < nodes.size() && nodes[j].op == "BatchNormalization" && nodes[j].inputs.at(0) == out &&
-                readers(out) == 1 && !env_set("NOBNFUSE")) {
-                const Node &bn = nodes[j];
-                const float eps = bn.f32("epsilon").value_or(1e-5f);
-                const Weight &sc = onnx.weight(bn.inputs.at(1)), &sf = onnx.weight(bn.inputs.at(2)),
-                             &mn = onnx.weight(bn.inputs.at(3)), &vr = onnx.weight(bn.inputs.at(4));
-                std::vector<float> st(size_t(2 * op.cout));
-                for (int c = 0; c < op.cout; c++) {
-                    const float s = sc.data.at(size_t(c)) / std::sqrt(vr.data.at(size_t(c)) + eps);
-                    st[size_t(c)] = s;
-                    st[size_t(op.cout + c)] = sf.data.at(size_t(c)) - mn.data.at(size_t(c)) * s;
-                }
-                op.affine = ctx.upload_weights(st.data(), st.size());
-                out = bn.outputs[0];
-                j++;
-            }
-            if (j < nodes.size() && nodes[j].op == "Relu" && nodes[j].inputs.at(0) == out && readers(out) == 1) {
-                op.act = ACT_RELU;
-                out = nodes[j].outputs[0];
-                j++;
-            }
-            // GELU as the exporter writes it: x * (erf(x / sqrt 2) + 1) * 0.5 (nd.rs:650-676).
-            if (op.act == ACT_NONE && j + 5 <= nodes.size()) {
-                const Node &dv = nodes[j], &ef = nodes[j + 1], &ad = nodes[j + 2], &ml = nodes[j + 3], &hf = nodes[j + 4];
-                auto contains = [](const std::vector<std::string> &v, const std::string &x) {
-                    return std::find(v.begin(), v.end(), x) != v.end();
-                };
-                auto any_scalar = [&](const std::vector<std::string> &v, float want, float tol) {
-                    return std::any_of(v.begin(), v.end(), [&](const std::string &x) {
-                        auto s = scalar(x);
-                        return s && std::fabs(*s - want) < tol;
-                    });
-                };
-                auto sq2 = scalar(dv.inputs.size() > 1 ? dv.inputs[1] : "");
-                if (dv.op == "Div" && dv.inputs[0] == out && sq2 && std::fabs(*sq2 - 1.41421356f) < 1e-4f &&
-                    ef.op == "Erf" && ef.inputs[0] == dv.outputs[0] && ad.op == "Add" && contains(ad.inputs, ef.outputs[0]) &&
-                    any_scalar(ad.inputs, 1.f, 1e-6f) && ml.op == "Mul" && contains(ml.inputs, out) &&
-                    contains(ml.inputs, ad.outputs[0]) && hf.op == "Mul" && contains(hf.inputs, ml.outputs[0]) &&
-                    any_scalar(hf.inputs, 0.5f, 1e-6f) && readers(out) == 2 && readers(dv.outputs[0]) == 1 &&
-                    readers(ef.outputs[0]) == 1 && readers(ad.outputs[0]) == 1 && readers(ml.outputs[0]) == 1) {
-                    op.act = ACT_GELU;
-                    out = hf.outputs[0];
-                    j += 5;
-                }
-            }
-            // A residual Add of another computed tensor (nd.rs:678-690).
-            if (j < nodes.size() && nodes[j].op == "Add" && readers(out) == 1) {
-                const Node &ad = nodes[j];
-                const std::string *other = nullptr;
-                if (ad.inputs.at(0) == out) other = &ad.inputs.at(1);
-                else if (ad.inputs.at(1) == out) other = &ad.inputs.at(0);
-                if (other && !onnx.weights.count(*other) && !onnx.ints.count(*other)) {
-                    op.residual = *other;
-                    out = ad.outputs[0];
-                    j++;
-                }
-            }
-            if (auto d = n.ints("dilations"))
-                for (int64_t v : *d)
-                    if (v != 1) fail("dilated conv");
-            auto st = n.ints("strides").value_or(std::vector<int64_t>{1, 1});
-            op.sh = int(st.at(0));
-            op.sw = int(st.at(1));
-            const auto ap = n.str("auto_pad").value_or("NOTSET");
-            op.same_upper = ap == "SAME_UPPER";
-            if (ap != "NOTSET" && ap != "SAME_UPPER") fail("Conv auto_pad " + ap);
+            const auto strides = n.ints("strides").value_or(std::vector<int64_t>{1, 1});
+            if (strides.size() != 2) fail("Conv strides of rank " + std::to_string(strides.size()));
+            op.sh = int(strides[0]);
+            op.sw = int(strides[1]);
+            const std::string pad_mode = n.str("auto_pad").value_or("NOTSET");
+            if (pad_mode != "NOTSET" && pad_mode != "SAME_UPPER") fail("Conv auto_pad " + pad_mode + " is not supported");
+            op.same_upper = pad_mode == "SAME_UPPER";
             if (auto p = n.ints("pads")) {
-                if (p->size() != 4) fail("Conv pads");
+                if (p->size() != 4) fail("Conv pads of length " + std::to_string(p->size()));
                 for (int k = 0; k < 4; k++) op.pads[k] = int((*p)[size_t(k)]);
             }
-            auto isc = in_scale.find(i);
-            if (isc != in_scale.end()) op.in_scale = isc->second;
-            if ((op.group != 1) && (!op.residual.empty() || !op.in_scale.empty()))
-                fail("residual or input scale after a grouped conv");
+            std::vector<float> b = step_bias(onnx, s, n, size_t(op.cout));
+            if (s.batch_norm >= 0) {
+                const std::vector<float> st = batch_norm_affine(onnx, plan.nodes[size_t(s.batch_norm)], size_t(op.cout));
+                op.affine = ctx.upload_weights(st.data(), st.size());
+            }
+            op.residual = s.residual;
+            op.in_scale = s.in_scale;
+            if (op.group != 1 && (!op.residual.empty() || !op.in_scale.empty()))
+                fail("a grouped Conv cannot take a residual or an input scale");
             op.b = ctx.upload_weights(b.data(), b.size());
             op.mfma = op.group == 1 && conv_mfma_supported(op.kh, op.kw, op.sh, op.sw);
-            if (op.mfma) {
-                op.pk = plan_conv_pack(op.cin, op.cout, op.kh, op.kw);
-                std::vector<uint16_t> hi(op.pk.halves()), lo(op.pk.halves());
-                bool exact = true;
-                pack_conv_weights(op.pk, w.data.data(), hi.data(), lo.data(), &exact);
-                op.pk.exact = exact;
-                op.whi = ctx.upload_weights(hi.data(), hi.size());
-                if (!exact) op.wlo = ctx.upload_weights(lo.data(), lo.size());
-            } else {
-                op.w = ctx.upload_weights(w.data.data(), w.data.size());
-            }
-            op.inputs = {nodes[i].inputs[0]};
-        } else if (n.op == "MatMul" && onnx.weights.count(n.inputs.at(1)) &&
-                   onnx.weight(n.inputs[1]).dims.size() == 2) {
-            const Weight &w = onnx.weight(n.inputs[1]);
-            op.kind = NdKind::Linear;
-            op.k = int(w.dims[0]);
-            op.n = int(w.dims[1]);
-            std::vector<float> b(size_t(op.n), 0.f);
-            if (j < nodes.size())
-                if (auto bn = takes_bias(nodes[j], out, size_t(op.n))) {
-                    b = onnx.weight(*bn).data;
-                    out = nodes[j].outputs[0];
-                    j++;
-                }
-            // SiLU: x * sigmoid(x) (nd.rs:738-752).
-            if (j + 2 <= nodes.size()) {
-                const Node &sg = nodes[j], &ml = nodes[j + 1];
-                if (sg.op == "Sigmoid" && sg.inputs.at(0) == out && ml.op == "Mul" &&
-                    std::find(ml.inputs.begin(), ml.inputs.end(), out) != ml.inputs.end() &&
-                    std::find(ml.inputs.begin(), ml.inputs.end(), sg.outputs[0]) != ml.inputs.end() &&
-                    readers(out) == 2 && readers(sg.outputs[0]) == 1) {
-                    op.act = ACT_SILU;
-                    out = ml.outputs[0];
-                    j += 2;
-                }
-            }
-            // [k][n] -> rows [n][k] for the GEMM's packed layout.
-            std::vector<float> t(size_t(op.n) * op.k);
-            for (int kk = 0; kk < op.k; kk++)
-                for (int c = 0; c < op.n; c++) t[size_t(c) * op.k + kk] = w.data[size_t(kk) * op.n + c];
-            op.pk = plan_conv_pack(op.k, op.n, 1, 1);
-            std::vector<uint16_t> hi(op.pk.halves()), lo(op.pk.halves());
-            bool exact = true;
-            pack_conv_weights(op.pk, t.data(), hi.data(), lo.data(), &exact);
-            op.pk.exact = exact;
-            op.whi = ctx.upload_weights(hi.data(), hi.size());
-            if (!exact) op.wlo = ctx.upload_weights(lo.data(), lo.size());
-            op.b = ctx.upload_weights(b.data(), b.size());
-            op.inputs = {n.inputs[0]};
-        } else if (n.op == "ConvTranspose") {
+            if (op.mfma) pack_upload(ctx, op, w.data.data(), op.cin, op.cout, op.kh, op.kw);
+            else op.w = ctx.upload_weights(w.data.data(), w.data.size());
+            op.inputs = {s.conv_input};
+            break;
+        }
+        case NdKind::Linear: {
             const Weight &w = onnx.weight(n.inputs.at(1));
-            if (w.dims.size() != 4) fail("ConvTranspose weight not 4D");
-            auto st = n.ints("strides").value_or(std::vector<int64_t>{1, 1});
-            bool bad = n.int_("group").value_or(1) != 1 || st.size() != 2 || st[0] != st[1];
-            for (const char *a : {"pads", "output_padding"})
+            op.k = int(w.dims.at(0));
+            op.n = int(w.dims.at(1));
+            const std::vector<float> b = step_bias(onnx, s, n, size_t(op.n));
+            // The weight [k][n] is packed as n rows of k (a 1 x 1 conv from k to n channels).
+            std::vector<float> rows(size_t(op.n) * op.k);
+            for (int kk = 0; kk < op.k; kk++)
+                for (int c = 0; c < op.n; c++) rows[size_t(c) * op.k + kk] = w.data[size_t(kk) * op.n + c];
+            pack_upload(ctx, op, rows.data(), op.k, op.n, 1, 1);
+            op.b = ctx.upload_weights(b.data(), b.size());
+            op.inputs = {n.inputs.at(0)};
+            break;
+        }
+        case NdKind::ConvT: {
+            const Weight &w = onnx.weight(n.inputs.at(1));
+            if (w.dims.size() != 4) fail("ConvTranspose weight of rank " + std::to_string(w.dims.size()) + ", not 4");
+            const auto strides = n.ints("strides").value_or(std::vector<int64_t>{1, 1});
+            bool ok = n.int_("group").value_or(1) == 1 && strides.size() == 2 && strides[0] == strides[1];
+            for (const char *a : {"pads", "output_padding", "dilations"})
                 if (auto p = n.ints(a))
-                    for (int64_t v : *p) bad |= v != 0;
-            if (bad) fail("unsupported ConvTranspose attributes");
-            op.kind = NdKind::ConvT;
+                    for (int64_t v : *p) ok &= v == (std::string(a) == "dilations" ? 1 : 0);
+            if (!ok) fail("ConvTranspose: only group 1, equal strides, no padding and no dilation are supported");
             op.cin = int(w.dims[0]);
             op.cout = int(w.dims[1]);
             op.kh = int(w.dims[2]);
             op.kw = int(w.dims[3]);
-            op.sh = op.sw = int(st[0]);
-            std::vector<float> b(size_t(op.cout), 0.f);
-            if (n.inputs.size() > 2 && !n.inputs[2].empty()) b = onnx.weight(n.inputs[2]).data;
-            if (j < nodes.size())
-                if (auto bn = takes_bias(nodes[j], out, size_t(op.cout))) {
-                    const Weight &bw = onnx.weight(*bn);
-                    for (int c = 0; c < op.cout; c++) b[size_t(c)] += bw.data[size_t(c)];
-                    out = nodes[j].outputs[0];
-                    j++;
-                }
-            if (j < nodes.size() && (nodes[j].op == "Relu" || nodes[j].op == "Sigmoid") &&
-                nodes[j].inputs.at(0) == out && readers(out) == 1) {
-                op.act = nodes[j].op == "Relu" ? ACT_RELU : ACT_SIGMOID;
-                out = nodes[j].outputs[0];
-                j++;
-            }
+            op.sh = op.sw = int(strides[0]);
+            const std::vector<float> b = step_bias(onnx, s, n, size_t(op.cout));
             op.w = ctx.upload_weights(w.data.data(), w.data.size());
             op.b = ctx.upload_weights(b.data(), b.size());
-            op.inputs = {n.inputs[0]};
-        } else if (n.op == "BatchNormalization") {
-            const float eps = n.f32("epsilon").value_or(1e-5f);
-            const Weight &sc = onnx.weight(n.inputs.at(1)), &sf = onnx.weight(n.inputs.at(2)),
-                         &mn = onnx.weight(n.inputs.at(3)), &vr = onnx.weight(n.inputs.at(4));
-            const size_t c = sc.data.size();
-            std::vector<float> st(2 * c);
-            for (size_t ch = 0; ch < c; ch++) {
-                const float s = sc.data[ch] / std::sqrt(vr.data.at(ch) + eps);
-                st[ch] = s;
-                st[c + ch] = sf.data.at(ch) - mn.data.at(ch) * s;
-            }
-            op.kind = NdKind::Affine;
-            op.st = ctx.upload_weights(st.data(), st.size());
-            op.cout = int(c);
-            op.inputs = {n.inputs[0]};
+            op.inputs = {n.inputs.at(0)};
+            break;
         }
-        for (size_t k = i + 1; k < j; k++) skip[k] = true;
-        op.output = out;
+        }
         g.ops.push_back(std::move(op));
-        i = j;
     }
     // Weights every generic op may read, and small constants kept on the host too.
     for (const auto &kv : onnx.weights) {
@@ -405,9 +213,9 @@ NdGraph NdGraph::build(Ctx &ctx, const Onnx &onnx, bool stop_before_softmax) {
         g.weights_[kv.first] = std::move(w);
     }
     g.ints_ = onnx.ints;
-    g.nodes_ = std::move(nodes);
-    g.input = onnx.input;
-    g.output = output;
+    g.nodes_ = std::move(plan.nodes);
+    g.input = plan.input;
+    g.output = plan.output;
     for (size_t k = 0; k < g.ops.size(); k++) {
         for (const auto &nm : g.ops[k].inputs) g.last_use_[nm] = k;
         if (!g.ops[k].residual.empty()) g.last_use_[g.ops[k].residual] = k;

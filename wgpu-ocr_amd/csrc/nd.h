@@ -9,6 +9,7 @@
 
 #include "kernels.h"
 #include "nd_kernels.h"
+#include "nd_plan.h"
 #include "onnx.h"
 #include "runtime.h"
 
@@ -27,9 +28,8 @@ struct NdValue {
     std::vector<int64_t> iv, ishape;
 };
 
-enum class NdKind { Generic, Conv, ConvT, Linear, LayerNorm, Affine };
-
-// One step of the plan: a node, or a node with the ones fused into it (nd.rs:505-817).
+// One step of the plan (nd_plan.h) with its weights on the device: a node, or a node with the
+// ones fused into it.
 struct NdOp {
     NdKind kind = NdKind::Generic;
     int node = 0;  // the first node's index

@@ -86,6 +86,7 @@ SIGNATURES = {
     "ocr_pipeline_line_text": (ctypes.c_int, [P, U32, U32, ctypes.c_char_p, U32, PU32]),
     "ocr_pipeline_page_error": (ctypes.c_int, [P, U32, ctypes.c_char_p, U32, PU32]),
     "ocr_nd_new": (P, [P, ctypes.c_char_p, ctypes.c_int]),
+    "ocr_nd_plan": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.c_char_p, U32, PU32]),
     "ocr_nd_free": (None, [P]),
     "ocr_nd_dims": (ctypes.c_int, [P, P, U32, P, PU32]),
     "ocr_nd_run": (ctypes.c_int, [P, P, P, U32, P]),
@@ -407,6 +408,15 @@ class Graph:
                 self.handle = None
         except Exception:
             pass
+
+
+def nd_plan(onnx_path: str, stop_before_softmax: bool = False) -> list:
+    """The N-D executor's fusion plan for an ONNX file (no GPU needed): one text line a launch."""
+    n = ctypes.c_uint32()
+    _check(lib().ocr_nd_plan(onnx_path.encode(), int(bool(stop_before_softmax)), None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    _check(lib().ocr_nd_plan(onnx_path.encode(), int(bool(stop_before_softmax)), buf, n.value + 1, ctypes.byref(n)))
+    return buf.value.decode().splitlines()
 
 
 class NdGraph:
