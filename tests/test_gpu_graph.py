@@ -72,6 +72,47 @@ def test_conv_inexact_weights_third_pass(ctx, tmp_path):
     check(ctx, p, RNG.standard_normal((1, 24, 10, 19)).astype(np.float32))
 
 
+def _ran(families, fn):
+    """Runs fn with the kernel families probed; returns {family: launches}."""
+    import ocrhip
+    for f in families:
+        ocrhip.probe_start(f)
+    out = fn()
+    calls = {f: ocrhip.probe_stop(f)["calls"] for f in families}
+    return out, calls
+
+
+FAST = ("conv3x3_dma", "gemm_dma", "conv_igemm", "conv_mfma")
+
+
+@pytest.mark.parametrize("cin,cout,h,w,pool", [(128, 128, 8, 61, (2, 1)), (128, 256, 4, 37, (2, 1)),
+                                               (64, 128, 16, 45, (2, 1)), (32, 64, 32, 41, (2, 2)),
+                                               (32, 16, 33, 17, None), (16, 32, 20, 33, None)])
+def test_conv3x3_dma_inexact_weights(ctx, tmp_path, cin, cout, h, w, pool):
+    # Float32 weights that are not float16 values (as a trained model's are) on the DMA-fed 3 x 3
+    # kernel: the remainder slices are a second walk over the input; float32-class results.
+    def fn(g, x):
+        y = conv(g, x, cin, cout, exact=False, act="Relu")
+        return g.add("MaxPool", [y], kernel_shape=list(pool), strides=list(pool)) if pool else y
+    p = build(tmp_path, "c3i", fn, (2, cin, h, w))
+    x = RNG.standard_normal((2, cin, h, w)).astype(np.float32)
+    _, calls = _ran(FAST, lambda: check(ctx, p, x))
+    assert calls["conv3x3_dma"] >= 1 and calls["conv_mfma"] == 0, calls
+
+
+@pytest.mark.parametrize("cin,cout,h,w,fam", [(512, 1536, 1, 700, "gemm_dma"), (256, 97, 3, 301, "gemm_dma"),
+                                              (40, 24, 7, 53, "gemm_dma"), (20, 24, 7, 53, "conv_igemm")])
+def test_conv1x1_inexact_weights(ctx, tmp_path, cin, cout, h, w, fam):
+    # The GRU input projection's shape (512 -> 1536), the output layer's (-> 97) and narrow 1 x 1
+    # convs (K of 40 is 4 weight slices with its remainders: the DMA GEMM; K of 20 only 2: the
+    # implicit GEMM), all with float32 weights that are not float16 values.
+    p = build(tmp_path, "g1i", lambda g, x: conv(g, x, cin, cout, k=(1, 1), pads=(0, 0, 0, 0), exact=False),
+              (1, cin, h, w))
+    x = RNG.standard_normal((1, cin, h, w)).astype(np.float32)
+    _, calls = _ran(FAST, lambda: check(ctx, p, x))
+    assert calls[fam] >= 1 and calls["conv_mfma"] == 0, calls
+
+
 def test_conv_asymmetric_pads(ctx, tmp_path):
     p = build(tmp_path, "ca", lambda g, x: conv(g, x, 8, 12, k=(3, 2), pads=(0, 1, 2, 0)), (1, 8, 9, 10))
     check(ctx, p, RNG.standard_normal((1, 8, 9, 10)).astype(np.float32))

@@ -52,6 +52,37 @@ def test_recognition_config1(recognizer, rec_oracle):
     assert check_recognition(recognizer, rec_oracle, batches, widths) > 36 * 50
 
 
+@pytest.mark.parametrize("f16", ["0", None])
+def test_recognition_config1_float32_weights(ctx, f16):
+    """Config 1 with float32 weights that are not float16 values (a trained model's). The trunk,
+    projections and output layer run the fast kernels with remainder slices. With F16=0 the
+    recurrence keeps R in float32 (gru_recurrence_f32), as the reference does with F16 off
+    (gpu.rs:858, 1476-1486); by default R is rounded to float16, as the reference does with F16 on.
+    Both must meet the bar against the float32 oracle."""
+    import os
+
+    import ocrhip
+    from oracle import onnx_read
+    path = synth.model_path("rec_f32")
+    old = os.environ.pop("F16", None)
+    try:
+        if f16 is not None:
+            os.environ["F16"] = f16
+        rec = ocrhip.Recognizer(ctx, path)
+    finally:
+        os.environ.pop("F16", None)
+        if old is not None:
+            os.environ["F16"] = old
+    lines = synth.rec_lines(36, seed=0, wmin=200, wmax=800)
+    batches, _, widths = synth.batch_lines(lines)
+    fams = ("conv3x3_dma", "gemm_dma", "conv_igemm", "conv_mfma", "gru")
+    for f in fams:
+        ocrhip.probe_start(f)
+    check_recognition(rec, onnx_read.load(path), batches, widths)
+    calls = {f: ocrhip.probe_stop(f)["calls"] for f in fams}
+    assert calls["conv3x3_dma"] >= 1 and calls["gemm_dma"] >= 1 and calls["conv_mfma"] == 0, calls
+
+
 def test_recognition_edge_shapes(recognizer, rec_oracle):
     # one narrow line (T = 2), a width not a multiple of 4, and a single-line batch
     rng = np.random.Generator(np.random.PCG64(9))

@@ -158,8 +158,8 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     s.pk.exact = exact;
                     s.whi = ctx.upload_weights(hi.data(), hi.size());
                     if (!exact) s.wlo = ctx.upload_weights(lo.data(), lo.size());
-                    std::vector<uint16_t> frag(s.pk.halves());
-                    pack_conv_frags(s.pk, hi.data(), frag.data());
+                    std::vector<uint16_t> frag(s.pk.frag_halves());
+                    pack_conv_frags(s.pk, hi.data(), lo.data(), frag.data());
                     s.wfrag = ctx.upload_weights(frag.data(), frag.size());
                     // A 1 x 1 conv to a few channels (a head) also keeps float32 weights for the
                     // bandwidth-bound kernel.
@@ -229,8 +229,8 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                     ph.pk.exact = exact;
                     ph.whi = ctx.upload_weights(hi.data(), hi.size());
                     if (!exact) ph.wlo = ctx.upload_weights(lo.data(), lo.size());
-                    std::vector<uint16_t> frag(ph.pk.halves());
-                    pack_conv_frags(ph.pk, hi.data(), frag.data());
+                    std::vector<uint16_t> frag(ph.pk.frag_halves());
+                    pack_conv_frags(ph.pk, hi.data(), lo.data(), frag.data());
                     ph.wfrag = ctx.upload_weights(frag.data(), frag.size());
                     s.phases.push_back(std::move(ph));
                 }
@@ -260,12 +260,11 @@ Graph Graph::build(Ctx &ctx, const Onnx &onnx, const char *stop, Node *stop_node
                 bool exact = true;
                 pack_conv_weights(ap.pk, cw.data(), hi.data(), lo.data(), &exact);
                 ap.pk.exact = exact;
-                if (exact) {
-                    ap.whi = ctx.upload_weights(hi.data(), hi.size());
-                    std::vector<uint16_t> frag(ap.pk.halves());
-                    pack_conv_frags(ap.pk, hi.data(), frag.data());
-                    ap.wfrag = ctx.upload_weights(frag.data(), frag.size());
-                }
+                ap.whi = ctx.upload_weights(hi.data(), hi.size());
+                if (!exact) ap.wlo = ctx.upload_weights(lo.data(), lo.size());
+                std::vector<uint16_t> frag(ap.pk.frag_halves());
+                pack_conv_frags(ap.pk, hi.data(), lo.data(), frag.data());
+                ap.wfrag = ctx.upload_weights(frag.data(), frag.size());
             }
         } else if (n.op == "MaxPool") {
             auto k = n.ints("kernel_shape");
@@ -596,6 +595,7 @@ void Graph::Exec::step(size_t i) {
             ca.x = a;
             ca.y = y;
             ca.wt_hi = s.allph.whi;
+            ca.wt_lo = s.allph.wlo;
             ca.wt_frag = s.allph.wfrag;
             ca.bias = s.b;
             ca.act = s.act;

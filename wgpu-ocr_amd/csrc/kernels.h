@@ -19,15 +19,21 @@ struct ConvPack {
     int nblocks = 0;  // ceil(cout / bn)
     bool exact = true;
     size_t halves() const { return size_t(nblocks) * chunks * kh * kw * bn * 32; }
+    // Weight slices of the fragment layout (pack_conv_frags): the float16 values, then, for
+    // weights that are not all float16 values, their float16 remainders as further slices.
+    int frag_chunks() const { return exact ? chunks : 2 * chunks; }
+    size_t frag_halves() const { return halves() * (exact ? 1 : 2); }
 };
 
 // Layout of a packed weight set: [nblock][chunk][tap][bn][32 input channels], float16.
 // w is ONNX's [cout][cin][kh][kw]. Returns the pack description; hi/lo (host) are filled.
 ConvPack plan_conv_pack(int cin, int cout, int kh, int kw);
 void pack_conv_weights(const ConvPack &pk, const float *w, uint16_t *hi, uint16_t *lo, bool *exact);
-// The same float16 weights as MFMA B fragments for conv_igemm: [16-channel tile][slice][tap]
-// [lane][8], lane 16 g + r holding inputs 8g..8g+7 of channel 16 * tile + r (pk.halves() halves).
-void pack_conv_frags(const ConvPack &pk, const uint16_t *hi, uint16_t *frag);
+// The same weights as MFMA fragments for the DMA-fed kernels: [16-channel tile][slice][tap]
+// [lane][8], lane 16 g + r holding inputs 8g..8g+7 of channel 16 * tile + r. Slices 0 .. chunks-1
+// hold hi; when the pack is not exact, slices chunks .. 2 chunks-1 hold lo (the kernels run the
+// input's slices twice, so sum x (hi + lo) gives float32-class products). pk.frag_halves() halves.
+void pack_conv_frags(const ConvPack &pk, const uint16_t *hi, const uint16_t *lo, uint16_t *frag);
 
 struct ConvArgs {
     Act x, y;                       // input and output views (NHWC, or NCHW with nchw set)
@@ -175,5 +181,9 @@ void argmax_rows(const float *x, int rows, int classes, uint32_t *best, hipStrea
 // steps: the sum of lens (for the probe's work count only).
 void gru_recurrence(const float *G, const uint16_t *R, const float *Rb, float *Y, const uint32_t *lens, int ntot,
                     int tmax, long long steps, hipStream_t s);
+// The same with float32 recurrent weights, given transposed: Rt [2][256 k][768 rows] (for R
+// that is not float16-valued when rounding it is not allowed; R streams from L2 every step).
+void gru_recurrence_f32(const float *G, const float *Rt, const float *Rb, float *Y, const uint32_t *lens, int ntot,
+                        long long steps, hipStream_t s);
 
 }  // namespace ocr

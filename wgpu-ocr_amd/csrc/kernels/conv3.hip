@@ -1,12 +1,14 @@
-// 3 x 3 stride-1 convolution (NHWC float32 activations, float16-exact weights) on the gfx950
+// 3 x 3 stride-1 convolution (NHWC float32 activations, float32 weights) on the gfx950
 // matrix cores with the operands fed by the LDS DMA path: the hot
 // path of the recogniser trunk and the detector's deeper layers. Semantics of the reference's
 // conv / conv_fast / conv128 programs (src/gpu.rs:37-350): y = act(sum x * w + b[c]), then an
 // optional 2 x 2 or 2 x 1 MaxPool of the activated output (gpu.rs:462-482).
 //
 // Precision: each float32 activation is split into float16 hi and the float16 remainder lo
-// (x = hi + lo to about 2^-22) and both go through v_mfma_f32_16x16x32_f16 against the exact
-// float16 weights with float32 accumulation.
+// (x = hi + lo to about 2^-22) and both go through v_mfma_f32_16x16x32_f16 against the float16
+// weights with float32 accumulation. Weights that are not all float16 values are packed as
+// further slices of their float16 remainders, and the input's slices are walked a second time
+// against them: sum (hi + lo)(w_hi + w_lo), float32-class products at twice the matrix work.
 //
 // Data movement: nothing is staged through registers. global_load_lds_dwordx4 writes 16 bytes a
 // lane straight into LDS (lane l at base + 16 l), so
@@ -78,7 +80,8 @@ struct C3Params {
     float *tm;
     int tm_ntot;
     const half8 *wt;  // fragments [n-tile][slice][tap][64 lanes] of 8 halves
-    int ntiles, cout, chunks;
+    int ntiles, cout, chunks;  // chunks: weight slices (twice the input's for inexact weights)
+    int xchunks;               // input slices of 32 channels
     const float *bias;
     int th, tw, mx, hw, hh, rs, npx, hblocks;
     int tiles_y, tiles, nblocks, runs, nseg;
@@ -226,10 +229,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void conv3_dma_kernel(C3Params p) 
         const float *base;
         int iy0, ix0, w, cleft;
     };
+    // Weight slice c reads input slice c, or c - xchunks for the remainder slices of inexact
+    // weights (the input is walked a second time against them).
     auto halo_of = [&](const Seq &s) __attribute__((always_inline)) {
         const C3Seg &sd = p.seg[s.sg];
-        return Halo{sd.x + size_t(s.img) * p.h * sd.w * p.xcs + s.c * 32, s.ty * p.th - 1, s.tx * p.tw - 1, sd.w,
-                    p.cin - s.c * 32};
+        const int ci = s.c >= p.xchunks ? s.c - p.xchunks : s.c;
+        return Halo{sd.x + size_t(s.img) * p.h * sd.w * p.xcs + ci * 32, s.ty * p.th - 1, s.tx * p.tw - 1, sd.w,
+                    p.cin - ci * 32};
     };
     auto dma_h = [&](const Halo &hl, int i) __attribute__((always_inline)) {
         const int b = min(i * NW + wave, p.hblocks - 1);
@@ -517,7 +523,7 @@ namespace {
 // The checks of one segment; pool mode out (0 none, 1 = 2 x 2, 2 = 2 x 1), -1 when not taken.
 int c3_accepts(const ConvArgs &a) {
     const ConvPack &pk = a.pk;
-    if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res || a.rows || !pk.exact) return -1;
+    if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res || a.rows) return -1;
     if (pk.kh != 3 || pk.kw != 3 || a.pt != 1 || a.pl != 1 || pk.cin != a.x.c || pk.cout != a.y.c) return -1;
     if (a.y.n != a.x.n || a.y.h != a.x.h || a.y.w != a.x.w || a.y_px || a.y_row || a.y_img) return -1;
     if (a.x.c % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15)) return -1;
@@ -560,7 +566,8 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     p.wt = reinterpret_cast<const half8 *>(a.wt_frag);
     p.ntiles = pk.nblocks * pk.bn / 16;
     p.cout = cout;
-    p.chunks = pk.chunks;
+    p.chunks = pk.frag_chunks();
+    p.xchunks = pk.chunks;
     p.bias = a.bias;
     // Tile shape (16 blocks of 2 x 8 pixels) and channel block (32 nt channels) chosen
     // together. A workgroup walks ceil(tiles / runs) tiles, runs = CUs / blocks, so the launch
@@ -597,7 +604,7 @@ void c3_launch(const ConvArgs *args, int count, int pool, hipStream_t s) {
     p.npx = p.hh * p.hw;
     p.hblocks = (p.npx + 7) / 8;
     p.tiles_y = (p.oh + p.th - 1) / p.th;
-    double tiles = 0, flops = 0, bytes = 2.0 * double(pk.halves());
+    double tiles = 0, flops = 0, bytes = 2.0 * double(pk.frag_halves());
     for (int k = 0; k < count; k++) {
         const ConvArgs &b = args[k];
         C3Seg &sg = p.seg[k];
@@ -668,7 +675,7 @@ bool conv3x3_dma_multi(const ConvArgs *args, int count, hipStream_t s) {
             b.bias != a.bias || b.act != a.act ||
             b.x.h != a.x.h || b.x.c != a.x.c || b.x.cs != a.x.cs || b.y.c != a.y.c || b.y.cs != a.y.cs ||
             b.ypool.cs != a.ypool.cs || (b.ypool.p && !b.keep_full) != (a.ypool.p && !a.keep_full) ||
-            b.pk.chunks != a.pk.chunks)
+            b.pk.chunks != a.pk.chunks || b.pk.exact != a.pk.exact)
             return false;
     }
     for (int k = 0; k < count; k += C3MAXSEG) c3_launch(args + k, std::min(C3MAXSEG, count - k), pool, s);

@@ -1,12 +1,13 @@
 // Dense 1 x 1 convolution / GEMM on the gfx950 matrix cores: y[m][n] = act(sum_k x[m][k] w[k][n]
-// + b[n]) with float32 x (NHWC pixels, or GEMM rows picked by a row map) and float16-exact w.
+// + b[n]) with float32 x (NHWC pixels, or GEMM rows picked by a row map) and float32 w.
 // The recogniser's GRU input projections (src/gpu.rs:1538-1566: [rows][256 or 512] x
 // [.][1536]) and its output layer run here, as does any NHWC 1 x 1 convolution of the executor
 // with at least 128 input channels.
 //
 // Precision: each float32 activation is split into float16 hi and the float16 remainder lo
-// (x = hi + lo to about 2^-22); both go through v_mfma_f32_16x16x32_f16 against the exact float16
-// weights with float32 accumulation.
+// (x = hi + lo to about 2^-22); both go through v_mfma_f32_16x16x32_f16 against the float16
+// weights with float32 accumulation. Weights that are not all float16 values come as further K
+// slices of their float16 remainders, against which the activations' K slices are read again.
 //
 // Roles: the weights are the MFMA's A operand and the activations its B operand, so a lane's four
 // accumulators are four neighbouring output channels of one row and leave as one 16-byte store.
@@ -45,7 +46,8 @@ constexpr int ASU = GBM * RSU;  // activation stage size in units
 struct GParams {
     const float *x;
     long xcs;
-    int K, chunks;
+    int K, chunks;  // chunks: weight slices of 32 (twice K's for inexact weights)
+    int xchunks;    // slices of K
     const int *rows;  // row map (row i of the GEMM reads x row rows[i], writes y row rows[i]) or null
     int M;
     float *y;
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GParams p) {
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const int k0 = c * 32 + 8 * lq + 4 * e;
+                const int k0 = (c >= p.xchunks ? c - p.xchunks : c) * 32 + 8 * lq + 4 * e;
                 const float4 *src = reinterpret_cast<const float4 *>(p.zero);
                 if (live && ld_row[h] >= 0 && k0 < p.K) src = reinterpret_cast<const float4 *>(p.x + size_t(ld_row[h]) * p.xcs + k0);
                 R[2 * h + e] = *src;
@@ -329,7 +331,7 @@ const float *gzero() { return static_cast<const float *>(zero_block64()); }
 
 bool gemm_dma(const ConvArgs &a, hipStream_t s) {
     const ConvPack &pk = a.pk;
-    if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res || !pk.exact) return false;
+    if (!a.wt_frag || a.nchw || a.in_scale || a.affine || a.amax_part || a.res) return false;
     if (pk.kh != 1 || pk.kw != 1 || a.pt || a.pl || a.ypool.p || a.y_px || a.y_row || a.y_img) return false;
     if (pk.cin != a.x.c || pk.cout != a.y.c) return false;
     if (a.x.n != a.y.n || a.x.h != a.y.h || a.x.w != a.y.w) return false;
@@ -337,14 +339,15 @@ bool gemm_dma(const ConvArgs &a, hipStream_t s) {
     if (a.rows && (a.x.n != 1 || a.x.h != 1)) return false;
     const int K = a.x.c, N = a.y.c;
     // Four or more K chunks: the row map of a tile stays in LDS until its epilogue.
-    if (K % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15) || pk.chunks < 4 || N < 1) return false;
+    if (K % 4 || a.x.cs % 4 || (reinterpret_cast<uintptr_t>(a.x.p) & 15) || pk.frag_chunks() < 4 || N < 1) return false;
     const double m = double(a.x.n) * a.x.h * a.x.w;
     if (m >= 2147483647.0 - GBM) return false;
     GParams p{};
     p.x = a.x.p;
     p.xcs = a.x.cs;
     p.K = K;
-    p.chunks = pk.chunks;
+    p.chunks = pk.frag_chunks();
+    p.xchunks = pk.chunks;
     p.rows = a.rows;
     p.M = int(m);
     p.y = a.y.p;
@@ -363,7 +366,7 @@ bool gemm_dma(const ConvArgs &a, hipStream_t s) {
     if (p.M == 0) return true;
     const int grid = p.runs * p.nblocks;
     const double flops = 2.0 * p.M * double(N) * K;
-    const double bytes = 4.0 * (double(p.M) * K + double(p.M) * N) + 2.0 * double(pk.halves());
+    const double bytes = 4.0 * (double(p.M) * K + double(p.M) * N) + 2.0 * double(pk.frag_halves());
     ProbeScope probe("gemm_dma", s, flops, bytes);
     auto launch = [&](auto ACTc) {
         constexpr int A = decltype(ACTc)::value;

@@ -257,6 +257,64 @@ __global__ __launch_bounds__(H / UPW * 64) void gru_kernel(const float *__restri
     }
 }
 
+// Float32 recurrent weights (the reference's recurrence with F16 off, gpu.rs:858, 1476-1486):
+// for R that is not float16-valued when rounding it is not allowed. R is too large to stay on
+// chip next to its remainders, so this kernel streams it from L2 every step: one workgroup per
+// (direction, 8 lines), thread u owns hidden unit u of all 8 lines, and R^T [dir][k][768] makes
+// the 256 threads' reads of one (k, gate) row one coalesced 1 KiB access. h lives in LDS
+// (double-buffered, one barrier a step); the gates use expf and a true division.
+constexpr int FL = 8;  // lines per workgroup
+
+__global__ __launch_bounds__(256) void gru_f32_kernel(const float *__restrict__ G, const float *__restrict__ Rt,
+                                                      const float *__restrict__ Rb, float *__restrict__ Y,
+                                                      const uint32_t *__restrict__ lens, int ntot) {
+    __shared__ float hs[2][FL][H];
+    const int u = threadIdx.x, dir = blockIdx.y, n0 = blockIdx.x * FL;
+    const float *rt = Rt + size_t(dir) * H * 768;
+    int len[FL], maxlen = 0;
+#pragma unroll
+    for (int l = 0; l < FL; l++) {
+        len[l] = n0 + l < ntot ? int(lens[n0 + l]) : 0;
+        maxlen = max(maxlen, len[l]);
+        hs[0][l][u] = 0.f;
+    }
+    const float rbz = Rb[dir * 768 + u], rbr = Rb[dir * 768 + 256 + u], rbh = Rb[dir * 768 + 512 + u];
+    float h[FL];
+#pragma unroll
+    for (int l = 0; l < FL; l++) h[l] = 0.f;
+    __syncthreads();
+    for (int s = 0; s < maxlen; s++) {
+        const int cur = s & 1;
+        float az[FL], ar[FL], ah[FL];
+#pragma unroll
+        for (int l = 0; l < FL; l++) az[l] = ar[l] = ah[l] = 0.f;
+        for (int k = 0; k < H; k++) {
+            const float wz = rt[size_t(k) * 768 + u], wr = rt[size_t(k) * 768 + 256 + u], wh = rt[size_t(k) * 768 + 512 + u];
+#pragma unroll
+            for (int l = 0; l < FL; l++) {
+                const float hk = hs[cur][l][k];
+                az[l] = fmaf(wz, hk, az[l]);
+                ar[l] = fmaf(wr, hk, ar[l]);
+                ah[l] = fmaf(wh, hk, ah[l]);
+            }
+        }
+#pragma unroll
+        for (int l = 0; l < FL; l++) {
+            if (s < len[l]) {
+                const int t = dir == 0 ? s : len[l] - 1 - s;
+                const float *gr = G + (size_t(t) * ntot + n0 + l) * 1536 + dir * 768;
+                const float z = 1.f / (1.f + expf(-(gr[u] + az[l] + rbz)));
+                const float r = 1.f / (1.f + expf(-(gr[256 + u] + ar[l] + rbr)));
+                const float c = tanhf(gr[512 + u] + r * (ah[l] + rbh));
+                h[l] = (1.f - z) * c + z * h[l];
+                Y[(size_t(t) * ntot + n0 + l) * 512 + dir * 256 + u] = h[l];
+            }
+            hs[cur ^ 1][l][u] = h[l];
+        }
+        __syncthreads();
+    }
+}
+
 }  // namespace
 
 void gru_recurrence(const float *G, const uint16_t *R, const float *Rb, float *Y, const uint32_t *lens, int ntot,
@@ -272,6 +330,16 @@ void gru_recurrence(const float *G, const uint16_t *R, const float *Rb, float *Y
     constexpr int UPW = 16;
     hipLaunchKernelGGL((gru_kernel<UPW>), grid, dim3(H / UPW * 64), 0, s, G, reinterpret_cast<const half8 *>(R), Rb,
                        Y, lens, ntot);
+    OCR_HIP(hipGetLastError());
+}
+
+void gru_recurrence_f32(const float *G, const float *Rt, const float *Rb, float *Y, const uint32_t *lens, int ntot,
+                        long long steps, hipStream_t s) {
+    if (ntot <= 0) return;
+    dim3 grid(unsigned((ntot + FL - 1) / FL), 2);
+    ProbeScope probe("gru", s, 2.0 * 2.0 * double(steps) * 768 * 256,
+                     2.0 * double(steps) * (768 + 256) * 4 + 2.0 * 768 * 256 * 4);
+    hipLaunchKernelGGL(gru_f32_kernel, grid, dim3(H), 0, s, G, Rt, Rb, Y, lens, ntot);
     OCR_HIP(hipGetLastError());
 }
 

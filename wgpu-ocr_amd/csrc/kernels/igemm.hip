@@ -1,5 +1,5 @@
 // Stride-1 convolution (kernel up to 3 x 3) and 1 x 1 GEMM on the gfx950 matrix cores, for NHWC
-// float32 activations and float16-exact weights: the hot path of the ocrs detector, recogniser
+// float32 activations and float32 weights: the hot path of the ocrs detector, recogniser
 // trunk and GRU projections. Semantics of the reference's conv / conv_fast / conv128 and gemm
 // programs (src/gpu.rs:37-350, 616-678): y = act(sum_k x * w + b[c]), then an optional MaxPool
 // (gpu.rs:462-482) of the activated output.
@@ -53,13 +53,15 @@ struct IgParams {
     long yn, yy, yx;  // output pixel strides: image, row, column
     float *yp;        // pooled output, or null
     int poh, pow_, ypcs, pool;  // pool: 0 none, 1 = 2 x 2, 2 = 2 x 1 (rows)
-    const half8 *wt;  // packed [cout block of pbn][slice][tap][pbn][32] float16
-    int pbn, cpad;    // the pack's block width and padded channel count
+    const half8 *wt;     // packed [cout block of pbn][slice][tap][pbn][32] float16
+    const half8 *wt_lo;  // the same layout of the float16 remainders (inexact weights), or null
+    int pbn, cpad;       // the pack's block width and padded channel count
     int cout;
     const float *bias;
     const int *rows;  // GEMM row map (gather x rows, scatter y rows), or null
     int phc, phs, phh, phw;  // ConvTranspose phases: channels a phase, stride, y's size (0: off)
     int kw, pt, pl, act, chunks, taps;
+    int slices;  // passes over the input's chunks: chunks, or 2 chunks with remainders
     int th, tw, mx;   // tile rows and columns; row tiles per tile row of blocks
     int hw, hwp, halo_px;  // halo columns, padded row length, halo pixels
     int tiles_x, tiles_y, tiles;
@@ -115,13 +117,13 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
         for (int j = 0; j < NT; j++) acc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // B fragment of n-tile j for (slice, tap): lane (g, r) takes channel co + r, inputs 8g..8g+7.
-    auto load_b = [&](half8 (&b)[NT], int c, int tap) {
+    auto load_b = [&](half8 (&b)[NT], const half8 *wt, int c, int tap) {
 #pragma unroll
         for (int j = 0; j < NT; j++) {
             const int co = co_w + 16 * j;
             if (co < p.cpad) {
                 const int nbp = co / p.pbn, off = co - nbp * p.pbn;
-                b[j] = p.wt[((size_t(nbp * p.chunks + c) * p.taps + tap) * p.pbn + off + r) * 4 + g];
+                b[j] = wt[((size_t(nbp * p.chunks + c) * p.taps + tap) * p.pbn + off + r) * 4 + g];
             } else {
                 b[j] = half8{};
             }
@@ -129,7 +131,11 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
     };
 
     const int iy0 = oy0 - p.pt, ix0 = ox0 - p.pl;
-    for (int c = 0; c < p.chunks; c++) {
+    // Slice sl: input chunk c against the float16 weights, then (inexact weights) every chunk
+    // again against the remainders.
+    for (int sl = 0; sl < p.slices; sl++) {
+        const int c = sl < p.chunks ? sl : sl - p.chunks;
+        const half8 *wt = sl < p.chunks ? p.wt : p.wt_lo;
         const int ci0 = c * 32;
         // Stage the halo: 8 threads per pixel, 4 channels each; zero outside the image.
         float4 st[SI];
@@ -148,8 +154,8 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
             st[s] = v;
         }
         half8 bcur[NT];
-        load_b(bcur, c, 0);
-        if (c > 0) __syncthreads();  // every wavefront is done with the previous slice
+        load_b(bcur, wt, c, 0);
+        if (sl > 0) __syncthreads();  // every wavefront is done with the previous slice
 #pragma unroll
         for (int s = 0; s < SI; s++) {
             const int i = tid + s * 256, hp = i >> 3, q = i & 7;
@@ -167,7 +173,7 @@ __global__ __launch_bounds__(256) void conv_igemm_kernel(IgParams p) {
         __syncthreads();
         for (int tap = 0; tap < p.taps; tap++) {
             half8 bnext[NT];
-            if (tap + 1 < p.taps) load_b(bnext, c, tap + 1);
+            if (tap + 1 < p.taps) load_b(bnext, wt, c, tap + 1);
             const int ky = tap / p.kw, kx = tap - ky * p.kw, toff = ky * p.hwp + kx;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
@@ -267,25 +273,30 @@ void launch_si(const IgParams &p, dim3 grid, size_t lds, hipStream_t s) {
 
 }  // namespace
 
-void pack_conv_frags(const ConvPack &pk, const uint16_t *hi, uint16_t *frag) {
-    // hi: [nblock][chunk][tap][bn][32]; frag: [n-tile][chunk][tap][lane = 16 g + r][8], lane
-    // (g, r) holding inputs 8g..8g+7 of channel 16 * tile + r.
-    const int taps = pk.kh * pk.kw, ntiles = pk.nblocks * pk.bn / 16;
+void pack_conv_frags(const ConvPack &pk, const uint16_t *hi, const uint16_t *lo, uint16_t *frag) {
+    // hi, lo: [nblock][chunk][tap][bn][32]; frag: [n-tile][slice][tap][lane = 16 g + r][8], lane
+    // (g, r) holding inputs 8g..8g+7 of channel 16 * tile + r; slice c >= chunks is lo's c - chunks.
+    if (!pk.exact && !lo) fail("pack_conv_frags: inexact weights need their remainders");
+    const int taps = pk.kh * pk.kw, ntiles = pk.nblocks * pk.bn / 16, slices = pk.frag_chunks();
     size_t o = 0;
     for (int nt = 0; nt < ntiles; nt++)
-        for (int c = 0; c < pk.chunks; c++)
+        for (int sl = 0; sl < slices; sl++) {
+            const uint16_t *src_w = sl < pk.chunks ? hi : lo;
+            const int c = sl < pk.chunks ? sl : sl - pk.chunks;
             for (int tap = 0; tap < taps; tap++)
                 for (int l = 0; l < 64; l++, o += 8) {
                     const int g = l >> 4, r = l & 15, co = nt * 16 + r;
                     const int nb = co / pk.bn, off = co - nb * pk.bn;
                     const size_t src = (((size_t(nb) * pk.chunks + c) * taps + tap) * pk.bn + off) * 32 + 8 * g;
-                    std::memcpy(frag + o, hi + src, 8 * sizeof(uint16_t));
+                    std::memcpy(frag + o, src_w + src, 8 * sizeof(uint16_t));
                 }
+        }
 }
 
 bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     const ConvPack &pk = a.pk;
-    if (a.nchw || a.in_scale || a.affine || a.amax_part || a.res || !pk.exact) return false;
+    if (a.nchw || a.in_scale || a.affine || a.amax_part || a.res) return false;
+    if (!pk.exact && !a.wt_lo) return false;
     const bool phm = a.ph_cout > 0;
     if (phm) {
         // All s x s phases of a ConvTranspose: one conv over x (taps (a, b) read x[i - a][j - b],
@@ -351,6 +362,7 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     p.ypcs = a.ypool.cs;
     p.pool = pool;
     p.wt = reinterpret_cast<const half8 *>(a.wt_hi);
+    p.wt_lo = pk.exact ? nullptr : reinterpret_cast<const half8 *>(a.wt_lo);
     p.pbn = pk.bn;
     p.cpad = pk.nblocks * pk.bn;
     p.cout = cout;
@@ -361,6 +373,7 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     p.pl = a.pl;
     p.act = a.act;
     p.chunks = pk.chunks;
+    p.slices = pk.exact ? pk.chunks : 2 * pk.chunks;
     p.taps = pk.kh * pk.kw;
 
     // Tile shape: one row of bm pixels for a one-row input (GEMM rows); otherwise 2 x 8 blocks,
@@ -400,7 +413,7 @@ bool conv_igemm(const ConvArgs &a, hipStream_t s) {
     dim3 grid(unsigned(p.tiles), unsigned(nblocks));
     const double flops = 2.0 * p.n * p.oh * p.ow * cout * p.cin * pk.kh * pk.kw;
     const double bytes = 4.0 * (double(p.n) * p.h * p.w * p.cin + double(p.n) * p.oh * p.ow * cout) +
-                         2.0 * double(pk.halves());
+                         2.0 * double(pk.frag_halves());
     ProbeScope probe("conv_igemm", s, flops, bytes);
     if (WM == 4 && NT == 1) launch_si<4, 1, 1>(p, grid, lds, s);
     else if (WM == 4 && NT == 2) launch_si<4, 1, 2>(p, grid, lds, s);

@@ -77,8 +77,8 @@ void pack_linear(Ctx &ctx, const std::vector<float> &w_rows, int rows, int cols,
     pk.exact = exact;
     hi = ctx.upload_weights(h.data(), h.size());
     lo = exact ? nullptr : ctx.upload_weights(l.data(), l.size());
-    std::vector<uint16_t> f(pk.halves());
-    pack_conv_frags(pk, h.data(), f.data());
+    std::vector<uint16_t> f(pk.frag_halves());
+    pack_conv_frags(pk, h.data(), l.data(), f.data());
     frag = ctx.upload_weights(f.data(), f.size());
 }
 
@@ -118,17 +118,27 @@ Recognizer::Recognizer(Ctx &ctx, const Onnx &onnx, uint32_t lines) : ctx_(ctx), 
         }
         L.wb = ctx.upload_weights(wb.data(), wb.size());
         L.rb = ctx.upload_weights(rb.data(), rb.size());
-        // R in float16 (gpu.rs:1478-1484). Exact for float16-valued weights; otherwise rounded,
-        // as the reference does with F16 (F16=0 refuses such a model here).
+        // R in float16 (gpu.rs:1478-1484): exact for float16-valued weights; otherwise rounded,
+        // as the reference does with F16 on (its default). With F16=0 the reference keeps R in
+        // float32, and so does this library for R that is not float16-valued: the recurrence
+        // then streams R^T in float32 (gru_recurrence_f32).
         std::vector<uint16_t> rh(r.data.size());
+        bool exact = true;
         for (size_t i = 0; i < r.data.size(); i++) {
             _Float16 v = (_Float16)r.data[i];
-            if ((float)v != r.data[i]) r_exact_ = false;
+            if ((float)v != r.data[i]) exact = false;
             std::memcpy(&rh[i], &v, 2);
         }
+        r_exact_ = r_exact_ && exact;
         const char *f16 = std::getenv("F16");
-        if (!r_exact_ && f16 && std::string(f16) == "0")
-            fail("GRU recurrent weights are not float16 values and F16=0 forbids rounding them");
+        if (!exact && f16 && std::string(f16) == "0") {
+            std::vector<float> rt(r.data.size());
+            for (int d = 0; d < 2; d++)
+                for (int row = 0; row < 768; row++)
+                    for (int k = 0; k < 256; k++)
+                        rt[(size_t(d) * 256 + k) * 768 + row] = r.data[(size_t(d) * 768 + row) * 256 + k];
+            L.r32 = ctx.upload_weights(rt.data(), rt.size());
+        }
         L.r = ctx.upload_weights(rh.data(), rh.size());
     }
     if (nl != 2) fail(std::to_string(nl) + " GRU layers");
@@ -258,7 +268,8 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         ca.bias = L.wb;
         ca.pk = L.pk;
         conv_mfma(ca, st);
-        gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd, ntot, tmax, steps, st);
+        if (L.r32) gru_recurrence_f32(G.as<float>(), L.r32, L.rb, Y[l].as<float>(), lensd, ntot, steps, st);
+        else gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd, ntot, tmax, steps, st);
         in = Y[l].as<float>();
         in_c = 512;
         if (between) between();

@@ -60,6 +60,7 @@ class Recognizer {
         const uint16_t *w_hi = nullptr, *w_lo = nullptr, *w_frag = nullptr;
         const float *wb = nullptr;  // [2][768]
         const uint16_t *r = nullptr;  // [2][768][256] float16
+        const float *r32 = nullptr;   // [2][256][768] float32 (R transposed), when R stays float32
         const float *rb = nullptr;    // [2][768]
         int input = 0;
     };

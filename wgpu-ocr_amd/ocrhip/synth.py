@@ -37,14 +37,16 @@ def _f16_exact(a: np.ndarray) -> np.ndarray:
     return a.astype(np.float16).astype(np.float32)
 
 
-def kaiming(rng: np.random.Generator, shape, fan_in: int) -> np.ndarray:
+def kaiming(rng: np.random.Generator, shape, fan_in: int, exact: bool = True) -> np.ndarray:
     std = np.float32(np.sqrt(2.0 / fan_in))
-    return _f16_exact(rng.standard_normal(shape, dtype=np.float32) * std)
+    w = rng.standard_normal(shape, dtype=np.float32) * std
+    return _f16_exact(w) if exact else w
 
 
-def uniform_bias(rng: np.random.Generator, n: int, fan_in: int) -> np.ndarray:
+def uniform_bias(rng: np.random.Generator, n: int, fan_in: int, exact: bool = True) -> np.ndarray:
     b = np.float32(1.0 / np.sqrt(fan_in))
-    return _f16_exact(rng.uniform(-b, b, n).astype(np.float32))
+    v = rng.uniform(-b, b, n).astype(np.float32)
+    return _f16_exact(v) if exact else v
 
 
 # ---------------------------------------------------------------------------------------------
@@ -53,13 +55,17 @@ def uniform_bias(rng: np.random.Generator, n: int, fan_in: int) -> np.ndarray:
 REC_CONVS = [(1, 32, (2, 2)), (32, 64, (2, 2)), (64, 128, (2, 1)), (128, 128, (2, 1)), (128, 256, (2, 1))]
 
 
-def rec_model(seed: int = 0) -> bytes:
+def rec_model(seed: int = 0, exact: bool = True) -> bytes:
+    """The recogniser with Kaiming-normal weights; exact=False keeps them float32 (not rounded to
+    float16 values), as a trained model's are."""
     rng = np.random.Generator(np.random.PCG64(seed))
+    kaiming_ = lambda *a: kaiming(*a, exact=exact)  # noqa: E731
+    bias_ = lambda *a: uniform_bias(*a, exact=exact)  # noqa: E731
     g = ow.Graph("ocrs_rec_synth")
     x = "line_images"
     for i, (cin, cout, pool) in enumerate(REC_CONVS):
-        w = g.init(f"conv{i}.w", kaiming(rng, (cout, cin, 3, 3), cin * 9))
-        b = g.init(f"conv{i}.b", uniform_bias(rng, cout, cin * 9))
+        w = g.init(f"conv{i}.w", kaiming_(rng, (cout, cin, 3, 3), cin * 9))
+        b = g.init(f"conv{i}.b", bias_(rng, cout, cin * 9))
         x = g.add("Conv", [x, w, b], kernel_shape=[3, 3], pads=[1, 1, 1, 1], strides=[1, 1])
         x = g.add("Relu", [x])
         x = g.add("MaxPool", [x], kernel_shape=list(pool), strides=list(pool))
@@ -69,17 +75,17 @@ def rec_model(seed: int = 0) -> bytes:
     shape512 = g.init("shape_t_n_512", np.array([0, 0, 2 * HIDDEN], np.int64))
     inp = HIDDEN
     for layer in range(2):
-        w = g.init(f"gru{layer}.W", kaiming(rng, (2, 3 * HIDDEN, inp), inp))
-        r = g.init(f"gru{layer}.R", kaiming(rng, (2, 3 * HIDDEN, HIDDEN), HIDDEN))
-        bb = np.concatenate([uniform_bias(rng, 6 * HIDDEN, HIDDEN) for _ in range(2)]).reshape(2, 6 * HIDDEN)
+        w = g.init(f"gru{layer}.W", kaiming_(rng, (2, 3 * HIDDEN, inp), inp))
+        r = g.init(f"gru{layer}.R", kaiming_(rng, (2, 3 * HIDDEN, HIDDEN), HIDDEN))
+        bb = np.concatenate([bias_(rng, 6 * HIDDEN, HIDDEN) for _ in range(2)]).reshape(2, 6 * HIDDEN)
         b = g.init(f"gru{layer}.B", bb)
         y, _ = g.add("GRU", [x, w, r, b], n_out=2, hidden_size=HIDDEN, direction="bidirectional",
                      linear_before_reset=1)
         y = g.add("Transpose", [y], perm=[0, 2, 1, 3])  # [T, N, 2, 256]
         x = g.add("Reshape", [y, shape512])
         inp = 2 * HIDDEN
-    lw = g.init("output.w", kaiming(rng, (2 * HIDDEN, CLASSES), 2 * HIDDEN))
-    lb = g.init("output.b", uniform_bias(rng, CLASSES, 2 * HIDDEN))
+    lw = g.init("output.w", kaiming_(rng, (2 * HIDDEN, CLASSES), 2 * HIDDEN))
+    lb = g.init("output.b", bias_(rng, CLASSES, 2 * HIDDEN))
     x = g.add("MatMul", [x, lw])
     x = g.add("Add", [x, lb])
     out = g.add("LogSoftmax", [x], axis=2)
@@ -215,7 +221,8 @@ def det_model(seed: int = 0) -> bytes:
 
 
 def model_path(kind: str, seed: int = 0, directory: str | None = None) -> str:
-    """Write (once) and return the path of a synthetic model: kind 'rec' or 'det'."""
+    """Write (once) and return the path of a synthetic model: kind 'rec', 'det', or 'rec_f32'
+    (the recogniser with float32 weights that are not float16 values)."""
     directory = directory or os.environ.get("OCRHIP_MODELS") or os.path.join(
         os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), ".models")
     os.makedirs(directory, exist_ok=True)
@@ -223,7 +230,9 @@ def model_path(kind: str, seed: int = 0, directory: str | None = None) -> str:
     tag = hashlib.sha256(src + kind.encode() + str(seed).encode()).hexdigest()[:12]
     path = os.path.join(directory, f"{kind}_s{seed}_{tag}.onnx")
     if not os.path.exists(path):
-        data = rec_model(seed) if kind == "rec" else det_model(seed)
+        if kind not in ("rec", "det", "rec_f32"):
+            raise ValueError(f"unknown synthetic model kind {kind!r}")
+        data = rec_model(seed) if kind == "rec" else rec_model(seed, exact=False) if kind == "rec_f32" else det_model(seed)
         tmp = f"{path}.{os.getpid()}.tmp"
         with open(tmp, "wb") as f:
             f.write(data)
