@@ -201,6 +201,98 @@ def test_fusions_across_unrelated_nodes_and_operand_orders(ctx, tmp_path):
     check(ctx, p, RNG.standard_normal((2, 8, 11, 13)).astype(np.float32))
 
 
+# ---- the N-D convolution and row-GEMM kernels at the PP-OCR shapes --------------------------------
+@pytest.mark.parametrize("shape,stride,k", [((2, 32, 24, 70), (1, 1), 3), ((2, 64, 24, 70), (2, 2), 3),
+                                            ((3, 128, 12, 37), (2, 1), 3), ((1, 16, 9, 8), (1, 2), 3),
+                                            ((2, 24, 13, 29), (2, 2), 5)])
+def test_depthwise_shapes(ctx, tmp_path, shape, stride, k):
+    c = shape[1]
+    p = build(tmp_path, "dw", lambda g, x: g.add("Relu", [bn(g, conv(g, x, c, c, k=k, stride=stride, group=c,
+                                                                       bias=False), c)]), shape)
+    check(ctx, p, RNG.standard_normal(shape).astype(np.float32))
+
+
+@pytest.mark.parametrize("cin,cout,h,wd,exact", [(32, 64, 24, 73, True), (64, 128, 12, 37, False),
+                                                  (256, 256, 3, 109, True), (120, 256, 1, 61, True),
+                                                  (30, 20, 5, 7, True), (128, 32, 1, 1, False)])
+def test_1x1_nchw_shapes(ctx, tmp_path, cin, cout, h, wd, exact):
+    shape = (3, cin, h, wd)
+    p = build(tmp_path, "pw", lambda g, x: g.add("Relu", [bn(g, conv(g, x, cin, cout, k=1, bias=False, exact=exact),
+                                                               cout)]), shape)
+    check(ctx, p, RNG.standard_normal(shape).astype(np.float32))
+
+
+@pytest.mark.parametrize("n,cin,cout,h,wd,exact", [(4, 256, 32, 1, 109, True), (3, 512, 32, 1, 61, False),
+                                                    (2, 64, 16, 20, 45, True), (2, 40, 24, 7, 130, False),
+                                                    (16, 64, 64, 1, 9, True)])
+def test_3x3_nchw_shapes(ctx, tmp_path, n, cin, cout, h, wd, exact):
+    # One-row inputs (the SVTR neck's convs: two of the three kernel rows read padding only, and
+    # few tiles make the wavefronts of a workgroup share the K steps) and two-dimensional ones.
+    shape = (n, cin, h, wd)
+    p = build(tmp_path, "c3", lambda g, x: g.add("Relu", [conv(g, x, cin, cout, k=3, exact=exact)]), shape)
+    check(ctx, p, RNG.standard_normal(shape).astype(np.float32))
+
+
+def test_se_gate_and_gelu_residual_at_pp_shapes(ctx, tmp_path):
+    def fn(g, x):
+        se = g.add("GlobalAveragePool", [x])
+        se = g.add("Relu", [conv(g, se, 128, 32, k=1)])
+        se = g.add("HardSigmoid", [conv(g, se, 32, 128, k=1)], alpha=0.2, beta=0.5)
+        y = g.add("Relu", [conv(g, g.add("Mul", [x, se]), 128, 256, k=1)])
+        z = conv(g, y, 256, 256, k=1)
+        d = g.add("Div", [z, const(g, np.float32(np.sqrt(2.0)))])
+        m = g.add("Mul", [z, g.add("Add", [g.add("Erf", [d]), const(g, 1.0)])])
+        return g.add("Add", [g.add("Mul", [m, const(g, 0.5)]), y])
+    p = build(tmp_path, "se2", fn, (3, 128, 6, 45))
+    check(ctx, p, RNG.standard_normal((3, 128, 6, 45)).astype(np.float32))
+
+
+@pytest.mark.parametrize("cin,cout,shape,stride", [(3, 32, (2, 3, 48, 97), (2, 2)), (1, 16, (3, 1, 21, 40), (1, 1)),
+                                                    (3, 48, (1, 3, 33, 35), (2, 1))])
+def test_stem_convs(ctx, tmp_path, cin, cout, shape, stride):
+    p = build(tmp_path, "stem", lambda g, x: g.add("Relu", [bn(g, conv(g, x, cin, cout, stride=stride, bias=False),
+                                                                 cout)]), shape)
+    check(ctx, p, RNG.standard_normal(shape).astype(np.float32))
+
+
+@pytest.mark.parametrize("shape,k,n,exact", [((16, 109, 120), 120, 360, True), ((64, 200, 120), 120, 240, False),
+                                             ((2, 21, 30), 30, 7, True), ((5, 33, 240), 240, 120, True)])
+def test_linear_row_gemm_shapes(ctx, tmp_path, shape, k, n, exact):
+    def fn(g, x):
+        y = g.add("MatMul", [x, w(g, (k, n), k, exact=exact)])
+        return g.add("Add", [y, g.init("lb", (RNG.standard_normal(n) * 0.1).astype(np.float32))])
+    p = build(tmp_path, "rows", fn, shape)
+    check(ctx, p, RNG.standard_normal(shape).astype(np.float32))
+
+
+@pytest.mark.parametrize("k,n,exact", [(120, 200, True), (256, 300, False), (64, 1000, True)])
+def test_head_argmax_first_index_on_ties(ctx, tmp_path, k, n, exact):
+    """The fused head: classes come in pairs with the same weights and bias, so every row's
+    maximum is a tie; the first index of the pair must win (nd.rs:383), as in the oracle's
+    logits."""
+    import ocrhip
+
+    def fn(g, x):
+        a = RNG.standard_normal((k, n // 2)).astype(np.float32) * np.float32(np.sqrt(2 / k))
+        a = f16x(a) if exact else a
+        wt = np.repeat(a, 2, axis=1)
+        bias = np.repeat((RNG.standard_normal(n // 2) * 0.1).astype(np.float32), 2)
+        y = g.add("MatMul", [x, g.init("hw", wt)])
+        y = g.add("Add", [y, g.init("hb", bias)])
+        return g.add("Softmax", [y], axis=-1)
+    shape = (3, 41, k)
+    p = build(tmp_path, "head", fn, shape)
+    x = RNG.standard_normal(shape).astype(np.float32)
+    head = ocrhip.NdGraph(ctx, p, stop_before_softmax=True)
+    got = head.argmax(x)
+    probs, _ = og.run(onnx_read.load(p), x)
+    want = np.argmax(probs, axis=-1)  # equal logits give equal probabilities: the first index
+    assert np.all(want % 2 == 0)
+    assert np.all(got % 2 == 0), "a tie went to the second index"
+    assert np.array_equal(got, want)
+    assert np.array_equal(got, np.argmax(head.run(x), axis=-1))
+
+
 def test_unsupported_and_bad_shapes_raise(ctx, tmp_path):
     import ocrhip
     p = build(tmp_path, "bad", lambda g, x: g.add("Tanh", [x]), (1, 4))

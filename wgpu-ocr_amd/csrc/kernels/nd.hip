@@ -196,18 +196,26 @@ __global__ __launch_bounds__(256) void argmax_first_kernel(const float *x, uint3
     }
 }
 
-// Partial arg-max results (value, index) of the fused head GEMM, reduced per row.
-__global__ void argmax_partials_kernel(const float2 *part, int parts, size_t rows, uint32_t *best) {
-    size_t row = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+// Partial arg-max results (value, index) of the fused head GEMM, reduced per row: a wavefront
+// per row, its lanes reading neighbouring partials (coalesced), then a butterfly over the lanes.
+__global__ __launch_bounds__(256) void argmax_partials_kernel(const float2 *part, int parts, size_t rows,
+                                                              uint32_t *best) {
+    const size_t row = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int k = 0; k < parts; k++) {
+    for (int k = lane; k < parts; k += 64) {
         const float2 p = part[row * parts + k];
         const int idx = __float_as_int(p.y);
         if (p.x > bv || (p.x == bv && idx < bi)) { bv = p.x; bi = idx; }
     }
-    best[row] = uint32_t(bi == 0x7fffffff ? 0 : bi);
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) best[row] = uint32_t(bi == 0x7fffffff ? 0 : bi);
 }
 
 // ---- pooling (nd.rs nd_pool): stride, leading padding; the average never counts padding -------
@@ -411,7 +419,8 @@ void nd_argmax(const float *x, uint32_t *best, size_t rows, int len, hipStream_t
 
 void nd_argmax_partials(const float *part, int parts, size_t rows, uint32_t *best, hipStream_t s) {
     if (!rows) return;
-    hipLaunchKernelGGL(argmax_partials_kernel, dim3(grid_for(rows)), dim3(256), 0, s,
+    ProbeScope probe("nd_argmax", s, 0, 8.0 * double(rows) * parts + 4.0 * double(rows));
+    hipLaunchKernelGGL(argmax_partials_kernel, dim3(grid_for(rows, 4)), dim3(256), 0, s,
                        reinterpret_cast<const float2 *>(part), parts, rows, best);
     OCR_HIP(hipGetLastError());
 }

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <functional>
 #include <numeric>
 
@@ -30,6 +31,16 @@ std::vector<size_t> strides_of(const std::vector<int64_t> &shape) {
     std::vector<size_t> s(shape.size(), 1);
     for (size_t d = shape.size(); d-- > 1;) s[d - 1] = s[d] * size_t(shape[d]);
     return s;
+}
+
+// OCR_NO_NDCONV=1 keeps the N-D convs and MatMuls on the general kernels (for side-by-side
+// timing of the two paths on one GPU).
+bool no_ndconv() {
+    static const bool off = [] {
+        const char *e = std::getenv("OCR_NO_NDCONV");
+        return e && *e && *e != '0';
+    }();
+    return off;
 }
 
 std::string shape_str(const std::vector<int64_t> &s) {
@@ -307,6 +318,27 @@ NdTensor NdGraph::run_ops(Ctx *ctx, const NdTensor &x, size_t nops, std::map<std
             }
             if (shapes_only) break;
             if (op.mfma) {
+                NdMfmaConvArgs ma;
+                ma.x = a.p;
+                ma.n = nb;
+                ma.cin = cin;
+                ma.h = h;
+                ma.w = w;
+                ma.y = out.t.p;
+                ma.cout = op.cout;
+                ma.oh = oh;
+                ma.ow = ow;
+                ma.wt_hi = op.whi;
+                ma.wt_lo = op.wlo;
+                ma.pk = op.pk;
+                ma.bias = op.b;
+                ma.affine = op.affine;
+                ma.res = res.p;
+                ma.in_scale = sc.p;
+                ma.pt = pt;
+                ma.pl = pl;
+                ma.act = op.act;
+                if (!no_ndconv() && nd_conv_nchw_mfma(ma, st)) break;
                 ConvArgs ca;
                 ca.x = Act{a.p, nb, h, w, cin, cin};
                 ca.y = Act{out.t.p, nb, oh, ow, op.cout, op.cout};
@@ -346,6 +378,7 @@ NdTensor NdGraph::run_ops(Ctx *ctx, const NdTensor &x, size_t nops, std::map<std
                 ca.pl = pl;
                 ca.group = op.group;
                 ca.act = op.act;
+                if (!no_ndconv() && (nd_conv_dw(ca, st) || nd_conv_small(ca, st))) break;
                 nd_conv_generic(ca, st);
             }
             break;
@@ -370,6 +403,18 @@ NdTensor NdGraph::run_ops(Ctx *ctx, const NdTensor &x, size_t nops, std::map<std
             out.t = alloc(shape);
             if (shapes_only || m == 0) break;
             if (m > 0x7fffffff) fail("MatMul: too many rows");
+            NdRowsArgs ra;
+            ra.x = a.p;
+            ra.m = int(m);
+            ra.k = op.k;
+            ra.n = op.n;
+            ra.wt_hi = op.whi;
+            ra.wt_lo = op.wlo;
+            ra.pk = op.pk;
+            ra.bias = op.b;
+            ra.y = out.t.p;
+            ra.act = op.act;
+            if (!no_ndconv() && nd_gemm_rows(ra, st)) break;
             ConvArgs ca;
             ca.x = Act{a.p, 1, 1, int(m), op.k, op.k};
             ca.y = Act{out.t.p, 1, 1, int(m), op.n, op.n};
@@ -772,6 +817,23 @@ void NdGraph::run_argmax(Ctx &ctx, const NdTensor &x, uint32_t *d_best, std::vec
         }
         if (m == 0) return;
         if (m > 0x7fffffff) fail("head: too many rows");
+        if (!no_ndconv() && op.pk.bn == 64 && op.pk.chunks <= 8) {
+            const int parts = nd_head_parts(int(m), op.pk);
+            DBuf hp(&ctx, m * size_t(parts) * 2 * sizeof(float));
+            NdRowsArgs ra;
+            ra.x = a.p;
+            ra.m = int(m);
+            ra.k = op.k;
+            ra.n = op.n;
+            ra.wt_hi = op.whi;
+            ra.wt_lo = op.wlo;
+            ra.pk = op.pk;
+            ra.bias = op.b;
+            if (nd_head_argmax(ra, hp.as<float>(), parts, st)) {
+                nd_argmax_partials(hp.as<float>(), parts, m, d_best, st);
+                return;
+            }
+        }
         DBuf part(&ctx, m * size_t(op.pk.nblocks) * 2 * sizeof(float));
         ConvArgs ca;
         ca.x = Act{a.p, 1, 1, int(m), op.k, op.k};

@@ -8,6 +8,7 @@
 #include <cstdint>
 
 #include "common.h"
+#include "kernels.h"
 
 namespace ocr {
 
@@ -58,6 +59,46 @@ struct NdConvArgs {
     int cout = 0, oh = 0, ow = 0, kh = 0, kw = 0, sh = 1, sw = 1, pt = 0, pl = 0, group = 1, act = 0;
 };
 void nd_conv_generic(const NdConvArgs &a, hipStream_t s);
+// Depthwise (group = cin = cout, 3 x 3 or 5 x 5, strides 1 or 2 per axis; no residual or input
+// scale), the taps summed as nd_conv_generic sums them. False (nothing launched) otherwise.
+bool nd_conv_dw(const NdConvArgs &a, hipStream_t s);
+// Group 1, 3 x 3, one or three input channels, at most 64 output channels, any stride (the
+// stems): one thread an output pixel. False (nothing launched) otherwise.
+bool nd_conv_small(const NdConvArgs &a, hipStream_t s);
+
+// A group-1, stride-1 conv up to 3 x 3 in NCHW on the matrix cores (kernels/ndconv.hip), with
+// the weights packed by pack_conv_weights: act(affine(acc + b)) + res, in_scale[n][cin] applied to
+// the input first. False (nothing launched) for shapes it does not take.
+struct NdMfmaConvArgs {
+    const float *x = nullptr;
+    int n = 0, cin = 0, h = 0, w = 0;
+    float *y = nullptr;
+    int cout = 0, oh = 0, ow = 0;
+    const uint16_t *wt_hi = nullptr, *wt_lo = nullptr;
+    ConvPack pk;
+    const float *bias = nullptr, *affine = nullptr, *res = nullptr, *in_scale = nullptr;
+    int pt = 0, pl = 0, act = ACT_NONE;
+};
+bool nd_conv_nchw_mfma(const NdMfmaConvArgs &a, hipStream_t s);
+
+// y [m][n] = act(x [m][k] W + b) (+ res [m][n]) with W packed as n rows of k (pack_conv_weights,
+// 1 x 1), on the matrix cores. False (nothing launched) for packs it does not take.
+struct NdRowsArgs {
+    const float *x = nullptr;
+    int m = 0, k = 0, n = 0;
+    const uint16_t *wt_hi = nullptr, *wt_lo = nullptr;
+    ConvPack pk;
+    const float *bias = nullptr, *res = nullptr;
+    float *y = nullptr;
+    int act = ACT_NONE;
+};
+bool nd_gemm_rows(const NdRowsArgs &a, hipStream_t s);
+// The CTC head without its logits: per row of x, nd_head_parts partial (max, index bits) pairs of
+// x W + b (first index on ties) at part[row * parts + j], for nd_argmax_partials. Needs 64-column
+// blocks and k <= 256. False (nothing launched) otherwise.
+int nd_head_parts(int m, const ConvPack &pk);
+bool nd_head_argmax(const NdRowsArgs &a, float *part, int parts, hipStream_t s);
+
 // ConvTranspose, group 1, no pads; wt is ONNX's [cin][cout][kh][kw].
 void nd_conv_transpose(const float *x, int n, int cin, int h, int w, const float *wt, const float *b, float *y,
                        int cout, int kh, int kw, int stride, int act, hipStream_t s);
