@@ -293,6 +293,29 @@ def test_head_argmax_first_index_on_ties(ctx, tmp_path, k, n, exact):
     assert np.array_equal(got, np.argmax(head.run(x), axis=-1))
 
 
+def _attention(g, x, dim, heads):
+    hd = dim // heads
+    qkv = g.add("MatMul", [x, w(g, (dim, 3 * dim), dim)])
+    t5 = g.add("Transpose", [g.add("Reshape", [qkv, ints(g, [0, 0, 3, heads, hd])])], perm=[2, 0, 3, 1, 4])
+    parts = [g.add("Squeeze", [g.add("Slice", [t5, ints(g, [i]), ints(g, [i + 1]), ints(g, [0])]), ints(g, [0])])
+             for i in range(3)]
+    q = g.add("Mul", [parts[0], const(g, np.float32(hd ** -0.5))])
+    att = g.add("Softmax", [g.add("MatMul", [q, g.add("Transpose", [parts[1]], perm=[0, 1, 3, 2])])], axis=-1)
+    o = g.add("Transpose", [g.add("MatMul", [att, parts[2]])], perm=[0, 2, 1, 3])
+    return g.add("Reshape", [o, ints(g, [0, 0, dim])])
+
+
+@pytest.mark.parametrize("n,t,dim,heads", [(3, 37, 120, 8), (2, 300, 120, 8), (2, 77, 64, 2), (1, 150, 128, 2),
+                                           (4, 1, 48, 4)])
+def test_fused_attention_shapes(ctx, tmp_path, n, t, dim, heads):
+    # Heads of 15, 32 and 64 values; 300 and 150 keys take several LDS tiles (the running softmax
+    # rescaled between them); one query alone.
+    import ocrhip
+    p = build(tmp_path, "attn", lambda g, x: _attention(g, x, dim, heads), (n, t, dim))
+    assert any(line.startswith("attention") for line in ocrhip.nd_plan(p))
+    check(ctx, p, RNG.standard_normal((n, t, dim)).astype(np.float32))
+
+
 def test_unsupported_and_bad_shapes_raise(ctx, tmp_path):
     import ocrhip
     p = build(tmp_path, "bad", lambda g, x: g.add("Tanh", [x]), (1, 4))

@@ -2,8 +2,8 @@
 run as one launch, against the operator contract of the reference's NdGraph::new
 (src/nd.rs:505-817): Identity nodes dropped, a final Softmax cut on request, the squeeze-excitation
 gate as a conv's input scale, the exporter's LayerNorm chain as one op, Conv + bias + BN + ReLU or
-GELU + residual, MatMul + bias + SiLU, ConvTranspose + bias + ReLU or Sigmoid, a lone BN as a
-channel affine. Chains are matched over def-use edges, so operand order (Add, Mul) and unrelated
+GELU + residual, MatMul + bias + SiLU (+ a residual Add), ConvTranspose + bias + ReLU or Sigmoid, a
+lone BN as a channel affine, and the exporter's multi-head self-attention chain as one step. Chains are matched over def-use edges, so operand order (Add, Mul) and unrelated
 nodes in between do not matter, and a value some other node still reads is never fused away.
 The numerics of every fused launch are checked on the GPU (tests/test_gpu_nd.py)."""
 import re
@@ -64,6 +64,54 @@ def test_pp_recognizer_plan():
     assert nodes == list(range(len(nodes)))
     full = steps(ocrhip.nd_plan(synth_pp.model_path("rec"), False))
     assert full[-1][1] == "Softmax" and len(full) == len(s) + 1
+
+
+def test_pp_recognizer_attention_and_linear_residuals():
+    s = steps(ocrhip.nd_plan(synth_pp.model_path("rec"), True))
+    att = [(nodes, out) for k, _, nodes, _, out in s if k == "attention"]
+    assert len(att) == 2 and all(len(nodes) == 15 for nodes, _ in att)
+    # attention projection and second MLP layer of each block take the block's residual Add
+    assert sum(1 for k, _, _, a, _ in s if k == "linear" and "residual" in a) == 4
+    assert not any(op in ("Softmax", "Slice") for k, op, *_ in s if k == "node")
+
+
+def _attention_graph(g, x, perm=(2, 0, 3, 1, 4), k_first=False, scale_first=False):
+    qkv = g.add("MatMul", [x, w(g, (24, 72))])
+    s5 = g.init(g.fresh("s"), np.array([0, 0, 3, 4, 6], np.int64))
+    t5 = g.add("Transpose", [g.add("Reshape", [qkv, s5])], perm=list(perm))
+    parts = {}
+    for i in ((1, 0, 2) if k_first else (0, 1, 2)):
+        ii = lambda v: g.init(g.fresh("i"), np.array(v, np.int64))  # noqa: E731
+        sl = g.add("Slice", [t5, ii([i]), ii([i + 1]), ii([0])])
+        parts[i] = g.add("Squeeze", [sl, ii([0])])
+    sc = const(g, 6 ** -0.5)
+    q = g.add("Mul", [sc, parts[0]] if scale_first else [parts[0], sc])
+    att = g.add("Softmax", [g.add("MatMul", [q, g.add("Transpose", [parts[1]], perm=[0, 1, 3, 2])])], axis=-1)
+    o = g.add("Transpose", [g.add("MatMul", [att, parts[2]])], perm=[0, 2, 1, 3])
+    return g.add("Reshape", [o, g.init(g.fresh("r"), np.array([0, 0, 24], np.int64))]), att
+
+
+def test_attention_chain_in_any_slice_order(tmp_path):
+    for k_first, scale_first in ((False, False), (True, True)):
+        lines, _ = plan(tmp_path, "att", lambda g, x: _attention_graph(g, x, k_first=k_first,
+                                                                       scale_first=scale_first)[0], (2, 5, 24))
+        s = steps(lines)
+        assert [k for k, *_ in s] == ["linear", "attention"], lines
+
+
+def test_attention_chain_with_another_layout_is_not_fused(tmp_path):
+    lines, _ = plan(tmp_path, "att2", lambda g, x: _attention_graph(g, x, perm=(2, 0, 1, 3, 4))[0], (2, 5, 24))
+    assert not any(k == "attention" for k, *_ in steps(lines))
+
+
+def test_attention_chain_with_a_value_read_elsewhere_is_not_fused(tmp_path):
+    def fn(g, x):
+        y, sm = _attention_graph(g, x)
+        # the softmax probabilities also leave the chain: nothing may be fused away
+        return g.add("Add", [y, g.add("ReduceMean", [g.add("Reshape", [sm, g.init("r2", np.array([2, 5, -1], np.int64))])],
+                                     axes=[-1], keepdims=1)])
+    lines, _ = plan(tmp_path, "att3", fn, (2, 5, 24))
+    assert not any(k == "attention" for k, *_ in steps(lines))
 
 
 def test_pp_detector_plan():

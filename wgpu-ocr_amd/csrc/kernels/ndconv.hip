@@ -100,25 +100,35 @@ __global__ __launch_bounds__(256) void conv_nchw_kernel(NchwParams p) {
             oy = line - img * p.oh;
         }
         const int taps = p.kh * p.kw, steps = p.chunks * taps;
-        for (int s = kpart; s < steps; s += p.ksplit) {
+        const float *xim = p.x + size_t(img) * p.cin * plane;
+        // K step s is (chunk, tap); steps whose kernel row reads only padding are skipped (the
+        // same for the whole wavefront).
+        auto valid_from = [&](int s) {
+            for (; s < steps; s += p.ksplit) {
+                if (p.flat) return s;
+                const int tap = s % taps, iy = oy + tap / p.kw - p.pt;
+                if (iy >= 0 && iy < p.h) return s;
+            }
+            return steps;
+        };
+        // Operands of one K step: the weight fragments and the float32 inputs (split at use).
+        half8 a[NT], al[NT];
+        float v[MT][8];
+        auto load = [&](int s, half8 (&wa)[NT], half8 (&wl)[NT], float (&xv)[MT][8]) {
             const int chunk = s / taps, tap = s - chunk * taps;
             const int ky = tap / p.kw, kx = tap - ky * p.kw;
-            const int iy = p.flat ? 0 : oy + ky - p.pt;
-            if (iy < 0 || iy >= p.h) continue;  // the whole kernel row reads padding (uniform)
-            const half8 *wp = p.wt + (size_t(nb * p.chunks + chunk) * taps + tap) * (p.bn * 4) + size_t(r) * 4 + g;
-            half8 a[NT], al[NT];
+            const size_t wo = (size_t(nb * p.chunks + chunk) * taps + tap) * (p.bn * 4) + size_t(r) * 4 + g;
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                a[t] = wp[t * 64];
-                if constexpr (LO) al[t] = p.wt_lo[(wp - p.wt) + t * 64];
+                wa[t] = p.wt[wo + t * 64];
+                if constexpr (LO) wl[t] = p.wt_lo[wo + t * 64];
             }
             const int c0 = chunk * 32 + 8 * g;
-            const float *xrow = p.x + size_t(img) * p.cin * plane + (p.flat ? 0 : size_t(iy) * p.w);
+            const float *xrow = xim + (p.flat ? 0 : size_t(oy + ky - p.pt) * p.w);
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 const int px = x0 + 16 * m + r + (p.flat ? 0 : kx - p.pl);
                 const bool in = px >= 0 && px < lim;
-                float v[8];
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int ci = c0 + j;
@@ -127,10 +137,22 @@ __global__ __launch_bounds__(256) void conv_nchw_kernel(NchwParams p) {
                         t = xrow[size_t(ci) * plane + px];
                         if (p.in_scale) t *= p.in_scale[size_t(img) * p.cin + ci];
                     }
-                    v[j] = t;
+                    xv[m][j] = t;
                 }
+            }
+        };
+        int s = valid_from(kpart);
+        if (s < steps) load(s, a, al, v);
+        while (s < steps) {
+            // The next step's loads go out before this step's matrix work.
+            const int sn = valid_from(s + p.ksplit);
+            half8 na[NT], nal[NT];
+            float nv[MT][8];
+            if (sn < steps) load(sn, na, nal, nv);
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
                 half8 hi, lo;
-                split8(v, hi, lo);
+                split8(v[m], hi, lo);
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], hi, acc[m][t], 0, 0, 0);
@@ -138,6 +160,17 @@ __global__ __launch_bounds__(256) void conv_nchw_kernel(NchwParams p) {
                     if constexpr (LO) acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], hi, acc[m][t], 0, 0, 0);
                 }
             }
+            if (sn >= steps) break;
+            s = sn;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                a[t] = na[t];
+                if constexpr (LO) al[t] = nal[t];
+            }
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[m][j] = nv[m][j];
         }
     }
     if (p.ksplit > 1) {
@@ -206,33 +239,54 @@ struct DwParams {
     const float *x;
     float *y;
     const float *wt, *bias, *affine;  // wt [c][1][k][k]
-    int c, h, w, oh, ow, pt, pl, act, tiles_plane;
+    int c, h, w, oh, ow, pt, pl, act, quads, tiles_plane;
 };
 
+// A thread makes four neighbouring outputs of one row: each input row segment is read once for
+// the four (the taps of one output still summed in the general kernel's order).
 template <int K, int SH, int SW>
 __global__ __launch_bounds__(256) void conv_dw_kernel(DwParams p) {
+    constexpr int SEG = 3 * SW + K;  // input columns under four outputs
     const int plane = blockIdx.x / p.tiles_plane;
-    const int i = (blockIdx.x - plane * p.tiles_plane) * 256 + threadIdx.x;
-    if (i >= p.oh * p.ow) return;
+    const int item = (blockIdx.x - plane * p.tiles_plane) * 256 + threadIdx.x;
+    if (item >= p.oh * p.quads) return;
     const int ch = plane % p.c;
-    const int oy = i / p.ow, ox = i - oy * p.ow;
+    const int oy = item / p.quads, ox0 = (item - oy * p.quads) * 4;
     const float *xp = p.x + size_t(plane) * p.h * p.w;
     const float *wp = p.wt + size_t(ch) * K * K;
-    float acc = 0.f;
+    float wk[K * K];
+#pragma unroll
+    for (int k = 0; k < K * K; k++) wk[k] = wp[k];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const int ix0 = ox0 * SW - p.pl;
 #pragma unroll
     for (int ky = 0; ky < K; ky++) {
         const int iy = oy * SH - p.pt + ky;
         if (iy < 0 || iy >= p.h) continue;
+        const float *row = xp + size_t(iy) * p.w;
+        float seg[SEG];
 #pragma unroll
-        for (int kx = 0; kx < K; kx++) {
-            const int ix = ox * SW - p.pl + kx;
-            if (ix < 0 || ix >= p.w) continue;
-            acc = __fmaf_rn(xp[size_t(iy) * p.w + ix], wp[ky * K + kx], acc);
+        for (int j = 0; j < SEG; j++) {
+            const int ix = ix0 + j;
+            seg[j] = (ix >= 0 && ix < p.w) ? row[ix] : 0.f;
         }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int kx = 0; kx < K; kx++) {
+                const int ix = ix0 + q * SW + kx;
+                if (ix >= 0 && ix < p.w) acc[q] = __fmaf_rn(seg[q * SW + kx], wk[ky * K + kx], acc[q]);
+            }
     }
-    float v = acc + (p.bias ? p.bias[ch] : 0.f);
-    if (p.affine) v = v * p.affine[ch] + p.affine[p.c + ch];
-    p.y[size_t(plane) * p.oh * p.ow + i] = act_dev(v, p.act);
+    const float b = p.bias ? p.bias[ch] : 0.f;
+    float *yr = p.y + size_t(plane) * p.oh * p.ow + size_t(oy) * p.ow;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (ox0 + q >= p.ow) break;
+        float v = acc[q] + b;
+        if (p.affine) v = v * p.affine[ch] + p.affine[p.c + ch];
+        yr[ox0 + q] = act_dev(v, p.act);
+    }
 }
 
 template <int K>
@@ -253,11 +307,17 @@ struct SmallParams {
     int n, h, w, cout, oh, ow, sh, sw, pt, pl, act;
 };
 
+// blockIdx.y picks 16 output channels; a thread keeps 8 accumulators at a time (8 independent
+// chains, the weights of 8 channels read from LDS as two 16-byte reads a tap).
 template <int CIN, int KH, int KW>
 __global__ __launch_bounds__(256) void conv_small_kernel(SmallParams p) {
     constexpr int T = CIN * KH * KW;
-    __shared__ float s_w[64 * T];
-    for (int i = threadIdx.x; i < p.cout * T; i += 256) s_w[i] = p.wt[i];
+    __shared__ __align__(16) float s_w[T][16];  // this block's channels, [tap][channel]
+    const int cb = blockIdx.y * 16;
+    for (int i = threadIdx.x; i < T * 16; i += 256) {
+        const int t = i / 16, c = i % 16;
+        s_w[t][c] = cb + c < p.cout ? p.wt[size_t(cb + c) * T + t] : 0.f;
+    }
     __syncthreads();
     const size_t opl = size_t(p.oh) * p.ow;
     const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
@@ -285,17 +345,30 @@ __global__ __launch_bounds__(256) void conv_small_kernel(SmallParams p) {
             }
         }
     }
-    for (int co = 0; co < p.cout; co++) {
-        float acc = 0.f;
 #pragma unroll
-        for (int t = 0; t < T; t++)
-            if (ok[t]) acc = __fmaf_rn(xv[t], s_w[co * T + t], acc);
-        float v = acc + (p.bias ? p.bias[co] : 0.f);
-        if (p.affine) v = v * p.affine[co] + p.affine[p.cout + co];
-        v = act_dev(v, p.act);
-        const size_t o = (size_t(img) * p.cout + co) * opl + rem;
-        if (p.res) v += p.res[o];
-        p.y[o] = v;
+    for (int half = 0; half < 2; half++) {
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const float4 w0 = *reinterpret_cast<const float4 *>(&s_w[t][8 * half]);
+            const float4 w1 = *reinterpret_cast<const float4 *>(&s_w[t][8 * half + 4]);
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            if (ok[t]) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc[j] = __fmaf_rn(xv[t], wv[j], acc[j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int co = cb + 8 * half + j;
+            if (co >= p.cout) break;
+            float v = acc[j] + (p.bias ? p.bias[co] : 0.f);
+            if (p.affine) v = v * p.affine[co] + p.affine[p.cout + co];
+            v = act_dev(v, p.act);
+            const size_t o = (size_t(img) * p.cout + co) * opl + rem;
+            if (p.res) v += p.res[o];
+            p.y[o] = v;
+        }
     }
 }
 
@@ -309,6 +382,7 @@ struct RowsParams {
     int m, k, n, bn, chunks, nblocks, act;
     int rtiles;      // ceil(m / (16 RT))
     int parts, nb_per_wave;
+    int tsplit;      // wavefronts a 64-column block is split between (1, 2 or 4)
     int vec;         // k % 4 == 0 and x 16-byte aligned: 16-byte loads
 };
 
@@ -326,36 +400,47 @@ __device__ inline void rows_frag(const RowsParams &p, int row, int c0, half8 &hi
     split8(v, hi, lo);
 }
 
-template <int RT, int NT, bool LO>
+// A wavefront: RT 16-row tiles by NT 16-column tiles (part `tpart` of its 64-column block). The
+// operands of KC input chunks are read at once, then the matrix work of those chunks.
+template <int RT, int NT, int KC, bool LO>
 __global__ __launch_bounds__(256) void gemm_rows_kernel(RowsParams p) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rt = blockIdx.x * 4 + wave, nb = blockIdx.y;
+    const int wid = blockIdx.x * 4 + wave, nb = blockIdx.y;
+    const int rt = wid / p.tsplit, tpart = wid - rt * p.tsplit;
     if (rt >= p.rtiles) return;
     const int r = lane & 15, g = lane >> 4;
-    const int r0 = rt * 16 * RT;
+    const int r0 = rt * 16 * RT, t0 = tpart * NT;
     floatx4 acc[RT][NT];
 #pragma unroll
     for (int m = 0; m < RT; m++)
 #pragma unroll
         for (int t = 0; t < NT; t++) acc[m][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int chunk = 0; chunk < p.chunks; chunk++) {
-        const size_t wo = size_t(nb * p.chunks + chunk) * (p.bn * 4) + size_t(r) * 4 + g;
-        half8 a[NT], al[NT];
+    for (int cg = 0; cg < p.chunks; cg += KC) {
+        half8 bh[RT][KC], bl[RT][KC], a[KC][NT], al[KC][NT];
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            a[t] = p.wt[wo + t * 64];
-            if constexpr (LO) al[t] = p.wt_lo[wo + t * 64];
-        }
-#pragma unroll
-        for (int m = 0; m < RT; m++) {
-            half8 hi, lo;
-            rows_frag(p, r0 + 16 * m + r, chunk * 32 + 8 * g, hi, lo);
+        for (int c = 0; c < KC; c++) {
+            if (cg + c >= p.chunks) break;
+            const size_t wo = size_t(nb * p.chunks + cg + c) * (p.bn * 4) + size_t(r) * 4 + g;
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], hi, acc[m][t], 0, 0, 0);
-                acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], lo, acc[m][t], 0, 0, 0);
-                if constexpr (LO) acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], hi, acc[m][t], 0, 0, 0);
+                a[c][t] = p.wt[wo + (t0 + t) * 64];
+                if constexpr (LO) al[c][t] = p.wt_lo[wo + (t0 + t) * 64];
             }
+#pragma unroll
+            for (int m = 0; m < RT; m++) rows_frag(p, r0 + 16 * m + r, (cg + c) * 32 + 8 * g, bh[m][c], bl[m][c]);
+        }
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            if (cg + c >= p.chunks) break;
+#pragma unroll
+            for (int m = 0; m < RT; m++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][t], bh[m][c], acc[m][t], 0, 0, 0);
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][t], bl[m][c], acc[m][t], 0, 0, 0);
+                    if constexpr (LO)
+                        acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[c][t], bh[m][c], acc[m][t], 0, 0, 0);
+                }
         }
     }
     // Lane (r, g) holds columns 4g..4g+3 of n-tile t for row 16m + r.
@@ -365,7 +450,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(RowsParams p) {
         if (row >= p.m) continue;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            const int c = nb * p.bn + 16 * t + 4 * g;
+            const int c = nb * p.bn + 16 * (t0 + t) + 4 * g;
             float v[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -507,31 +592,24 @@ bool nd_conv_nchw_mfma(const NdMfmaConvArgs &a, hipStream_t s) {
     const double lim = p.flat ? double(a.h) * a.w : double(a.ow);
     const double lines = p.flat ? double(a.n) : double(a.n) * a.oh;
     if (lim > 0x7fffffff || lines > 0x7fffffff) return false;
-    // Pixels a wavefront: the widest of 64 / 32 / 16 that wastes at most a quarter of its tiles.
+    // Pixels a wavefront: the widest of 64 / 32 / 16 that wastes at most a quarter of its tiles
+    // and still gives 2048 wavefronts (8 a CU, to keep loads in flight); else 16.
+    const int nt = pk.bn / 16;
+    auto tiles_of = [&](int m) { return lines * std::ceil(lim / (16.0 * m)); };
     int mt = 1;
     for (int cand : {4, 2}) {
         const double tl = std::ceil(lim / (16.0 * cand));
-        if ((tl * 16 * cand - lim) * 4 <= lim) { mt = cand; break; }
+        if ((tl * 16 * cand - lim) * 4 <= lim && tiles_of(cand) * pk.nblocks >= 2048) { mt = cand; break; }
     }
-    const int nt = pk.bn / 16;
-    p.tiles_line = int(std::ceil(lim / (16.0 * mt)));
-    const double tiles = lines * p.tiles_line;
-    if (tiles > 0x3fffffff) return false;
-    p.tiles = int(tiles);
     const int steps = pk.chunks * (p.flat ? 1 : std::min(pk.kh, a.h) * pk.kw);
-    const double waves = tiles * pk.nblocks;
+    const double waves = tiles_of(mt) * pk.nblocks;
     int ks = 1;
     if (waves < 1024 && steps >= 8) ks = 4;
     else if (waves < 2048 && steps >= 4) ks = 2;
-    while (ks > 1 && mt * nt > 8) {
-        if (mt > 1) {
-            mt /= 2;
-            p.tiles_line = int(std::ceil(lim / (16.0 * mt)));
-            p.tiles = int(lines * p.tiles_line);
-        } else {
-            ks = 1;
-        }
-    }
+    if (ks > 1 && mt * nt > 8) mt = std::max(1, 8 / nt);
+    p.tiles_line = int(std::ceil(lim / (16.0 * mt)));
+    if (tiles_of(mt) > 0x3fffffff) return false;
+    p.tiles = int(tiles_of(mt));
     p.ksplit = ks;
     const size_t lds = ks > 1 ? size_t(4) * mt * nt * 4 * 64 * sizeof(float) : 0;
     const int per_block = 4 / ks;
@@ -569,7 +647,8 @@ bool nd_conv_dw(const NdConvArgs &a, hipStream_t s) {
     p.pt = a.pt;
     p.pl = a.pl;
     p.act = a.act;
-    p.tiles_plane = int((opl + 255) / 256);
+    p.quads = (a.ow + 3) / 4;
+    p.tiles_plane = int((size_t(a.oh) * p.quads + 255) / 256);
     const double blocks = double(p.tiles_plane) * planes;
     if (blocks > 0x7fffffff) return false;
     const dim3 grid{unsigned(blocks)};
@@ -606,7 +685,7 @@ bool nd_conv_small(const NdConvArgs &a, hipStream_t s) {
     p.pt = a.pt;
     p.pl = a.pl;
     p.act = a.act;
-    const dim3 grid{unsigned((total + 255) / 256)};
+    const dim3 grid{unsigned((total + 255) / 256), unsigned((a.cout + 15) / 16)};
     ProbeScope probe("nd_conv_small", s, 2.0 * double(total) * a.cout * a.cin * 9,
                      4.0 * (double(a.n) * a.cin * a.h * a.w + double(total) * a.cout));
     if (a.cin == 3) hipLaunchKernelGGL((conv_small_kernel<3, 3, 3>), grid, dim3(256), 0, s, p);
@@ -646,18 +725,28 @@ bool nd_gemm_rows(const NdRowsArgs &a, hipStream_t s) {
     if (a.m <= 0) return true;
     if (pk.nblocks > 65535) return false;
     RowsParams p = rows_params(a);
-    const int nt = pk.bn / 16;
-    // Rows a wavefront: 32 unless that leaves fewer than about 4 wavefronts a CU.
-    const int rt = (double((a.m + 31) / 32) * pk.nblocks >= 1024) ? 2 : 1;
+    // 32 rows a wavefront, then 16, then a part of the column block, until there are 2048
+    // wavefronts (8 a CU) or no smaller split.
+    const int ntf = pk.bn / 16;
+    auto waves = [&](int rt, int ts) { return double((a.m + 16 * rt - 1) / (16 * rt)) * ts * pk.nblocks; };
+    int rt = 2, ts = 1;
+    if (waves(rt, ts) < 2048) rt = 1;
+    while (waves(rt, ts) < 2048 && ts < ntf) ts *= 2;
+    const int nt = ntf / ts;
     p.rtiles = (a.m + 16 * rt - 1) / (16 * rt);
-    dim3 grid(unsigned((p.rtiles + 3) / 4), unsigned(pk.nblocks));
+    p.tsplit = ts;
+    const double blocks = std::ceil(double(p.rtiles) * ts / 4);
+    if (blocks > 0x7fffffff) return false;
+    const dim3 grid{unsigned(blocks), unsigned(pk.nblocks)};
     ProbeScope probe("nd_gemm_rows", s, 2.0 * a.m * double(a.k) * a.n,
                      4.0 * (double(a.m) * a.k + double(a.m) * a.n) + 2.0 * double(pk.halves()) * (pk.exact ? 1 : 2));
-    const bool lo = !pk.exact;
-#define ROWS_LAUNCH(RT, NT)                                                                  \
-    do {                                                                                     \
-        if (lo) hipLaunchKernelGGL((gemm_rows_kernel<RT, NT, true>), grid, dim3(256), 0, s, p);  \
-        else hipLaunchKernelGGL((gemm_rows_kernel<RT, NT, false>), grid, dim3(256), 0, s, p);    \
+    const bool lo = !pk.exact, k8 = pk.chunks > 4;
+#define ROWS_LAUNCH(RT, NT)                                                                          \
+    do {                                                                                             \
+        if (lo && k8) hipLaunchKernelGGL((gemm_rows_kernel<RT, NT, 8, true>), grid, dim3(256), 0, s, p);   \
+        else if (lo) hipLaunchKernelGGL((gemm_rows_kernel<RT, NT, 4, true>), grid, dim3(256), 0, s, p);    \
+        else if (k8) hipLaunchKernelGGL((gemm_rows_kernel<RT, NT, 8, false>), grid, dim3(256), 0, s, p);   \
+        else hipLaunchKernelGGL((gemm_rows_kernel<RT, NT, 4, false>), grid, dim3(256), 0, s, p);           \
     } while (0)
     if (rt == 2) {
         if (nt == 1) ROWS_LAUNCH(2, 1);

@@ -178,6 +178,10 @@ NdGraph NdGraph::build(Ctx &ctx, const Onnx &onnx, bool stop_before_softmax) {
             op.inputs = {s.conv_input};
             break;
         }
+        case NdKind::Attention:
+            op.inputs = {s.conv_input, s.attn_shape, s.attn_out_shape};
+            op.scale = s.attn_scale;
+            break;
         case NdKind::Linear: {
             const Weight &w = onnx.weight(n.inputs.at(1));
             op.k = int(w.dims.at(0));
@@ -190,6 +194,7 @@ NdGraph NdGraph::build(Ctx &ctx, const Onnx &onnx, bool stop_before_softmax) {
             pack_upload(ctx, op, rows.data(), op.k, op.n, 1, 1);
             op.b = ctx.upload_weights(b.data(), b.size());
             op.inputs = {n.inputs.at(0)};
+            op.residual = s.residual;
             break;
         }
         case NdKind::ConvT: {
@@ -403,7 +408,14 @@ NdTensor NdGraph::run_ops(Ctx *ctx, const NdTensor &x, size_t nops, std::map<std
             out.t = alloc(shape);
             if (shapes_only || m == 0) break;
             if (m > 0x7fffffff) fail("MatMul: too many rows");
+            NdTensor res;
+            if (!op.residual.empty()) {
+                res = get(vals, op.residual).t;
+                if (res.shape != out.t.shape)
+                    fail("residual " + shape_str(res.shape) + " for a MatMul giving " + shape_str(out.t.shape));
+            }
             NdRowsArgs ra;
+            ra.res = res.p;
             ra.x = a.p;
             ra.m = int(m);
             ra.k = op.k;
@@ -423,7 +435,47 @@ NdTensor NdGraph::run_ops(Ctx *ctx, const NdTensor &x, size_t nops, std::map<std
             ca.bias = op.b;
             ca.act = op.act;
             ca.pk = op.pk;
+            ca.res = res.p;
+            ca.res_cs = op.n;
             conv_mfma(ca, st);
+            break;
+        }
+        case NdKind::Attention: {
+            const NdTensor qkv = flt(0);
+            if (qkv.shape.size() != 3) fail("attention input " + shape_str(qkv.shape) + ", expects [n, T, 3 H d]");
+            const int64_t nb = qkv.shape[0], tt = qkv.shape[1], c3 = qkv.shape[2];
+            // The first Reshape's shape [n, T, 3, H, d] (0 copies a dimension, one -1 is inferred).
+            std::vector<int64_t> s5 = ints(1);
+            if (s5.size() != 5) fail("attention: a reshape to " + std::to_string(s5.size()) + " dimensions");
+            const int64_t in_dims[3] = {nb, tt, c3};
+            int64_t known = 1;
+            int infer = -1;
+            for (int d = 0; d < 5; d++) {
+                if (s5[size_t(d)] == 0 && d < 3) s5[size_t(d)] = in_dims[d];
+                if (s5[size_t(d)] == -1) {
+                    if (infer >= 0) fail("attention: two inferred dimensions");
+                    infer = d;
+                } else {
+                    known *= s5[size_t(d)];
+                }
+            }
+            if (infer >= 0 && known > 0) s5[size_t(infer)] = nb * tt * c3 / known;
+            const int64_t heads = s5[3], hd = s5[4];
+            if (s5[0] != nb || s5[1] != tt || s5[2] != 3 || heads <= 0 || hd <= 0 || 3 * heads * hd != c3)
+                fail("attention: reshape of " + shape_str(qkv.shape) + " to " + shape_str(s5));
+            // The last Reshape must give [n, T, H d].
+            std::vector<int64_t> s3 = ints(2);
+            const int64_t od[3] = {nb, tt, heads * hd};
+            for (size_t d = 0; d < s3.size() && d < 3; d++)
+                if (s3[d] == 0) s3[d] = od[d];
+            if (s3.size() == 3)
+                for (size_t d = 0; d < 3; d++)
+                    if (s3[d] == -1) s3[d] = od[d];
+            if (s3 != std::vector<int64_t>(od, od + 3)) fail("attention: output reshape to " + shape_str(s3));
+            out.t = alloc({nb, tt, heads * hd});
+            if (shapes_only || nb * tt == 0) break;
+            if (hd > 64 || nb > 65535 || heads > 65535) fail("attention: heads of " + std::to_string(hd) + " values");
+            nd_attention(qkv.p, int(nb), int(tt), int(heads), int(hd), op.scale, out.t.p, st);
             break;
         }
         case NdKind::LayerNorm: {

@@ -52,6 +52,8 @@ struct NdOp {
     float eps = 1e-5f;
     // Affine
     const float *st = nullptr;
+    // Attention: inputs are the QKV projection, the first and the last Reshape's shapes
+    float scale = 1.f;
 };
 
 class NdGraph {

@@ -108,6 +108,10 @@ void nd_det_prep(const uint8_t *rgb, int w, int h, float *y, int ow, int oh, hip
 // prob > thr as bit rows: h rows of ceil(w / 32) words, bit x % 32 of word x / 32.
 void nd_threshold_bits(const float *prob, int w, int h, float thr, uint32_t *bits, hipStream_t s);
 
+// Multi-head self-attention from a fused QKV projection: x [n][t][3 heads d] (q, k, v blocks of
+// heads x d), y[i][j][h d + c] = sum_k softmax_k(scale q_j . k_k) v_k[c] (kernels/attn.hip).
+void nd_attention(const float *x, int n, int t, int heads, int d, float scale, float *y, hipStream_t s);
+
 // Batched C[b] = A[b] (M x K) * B[b] (K x N) on the matrix cores, both operands float32 split
 // into float16 hi + lo (three passes: hi*hi, hi*lo, lo*hi), float32 accumulation. Element
 // (m, k) of batch b of A is at a[b * sab + m * sam + k * sak]; likewise B and C.

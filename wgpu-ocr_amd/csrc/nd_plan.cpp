@@ -16,11 +16,12 @@ namespace {
 // An operand of a pattern node: the value the pattern starts from (X), the output of an earlier
 // node of the pattern, a scalar initializer within `tol` of `value`, any scalar initializer, any
 // float initializer, or any computed value other than X (a tensor some other step produces).
-enum class Arg { X, Out, Near, Scalar, Weight, Value };
+enum class Arg { X, Out, Near, Scalar, Weight, Value, Any, Ints };
 struct Operand {
     Arg kind;
     int ref = -1;
     float value = 0.f, tol = 0.f;
+    std::vector<int64_t> ints;  // Ints: an integer initializer holding exactly these values
 };
 Operand X() { return {Arg::X}; }
 Operand Out(int k) { return {Arg::Out, k}; }
@@ -28,6 +29,8 @@ Operand Near(float v, float tol) { return {Arg::Near, -1, v, tol}; }
 Operand AnyScalar() { return {Arg::Scalar}; }
 Operand AnyWeight() { return {Arg::Weight}; }
 Operand AnyValue() { return {Arg::Value}; }
+Operand AnyInput() { return {Arg::Any}; }
+Operand Ints(std::vector<int64_t> v) { return {Arg::Ints, -1, 0.f, 0.f, std::move(v)}; }
 
 struct PNode {
     const char *op;
@@ -76,6 +79,36 @@ const Pattern kBatchNorm{
     "batch_norm", {{"BatchNormalization", {X(), AnyWeight(), AnyWeight(), AnyWeight(), AnyWeight()}}}, true};
 const Pattern kResidual{"residual", {{"Add", {X(), AnyValue()}}}, true};
 
+bool perm_is(const Node &n, std::vector<int64_t> want) { return n.ints("perm").value_or(std::vector<int64_t>{}) == want; }
+bool perm_20314(const Node &n) { return perm_is(n, {2, 0, 3, 1, 4}); }
+bool perm_0132(const Node &n) { return perm_is(n, {0, 1, 3, 2}); }
+bool perm_0213(const Node &n) { return perm_is(n, {0, 2, 1, 3}); }
+bool last_axis_softmax(const Node &n) {
+    const int64_t a = n.int_("axis").value_or(-1);
+    return a == -1 || a == 3;
+}
+// Multi-head self-attention as the exporter writes it from a fused QKV projection x [n, T, 3 H d]:
+// reshape to [n, T, 3, H, d], transpose to [3, n, H, T, d], slice and squeeze q, k, v, scale q,
+// softmax(q k^T) v, back to [n, T, H d]. Captured: the first reshape's shape, the scale, the last
+// reshape's shape.
+const Pattern kAttention{"attention",
+                         {{"Reshape", {X(), AnyInput()}},
+                          {"Transpose", {Out(0)}, perm_20314},
+                          {"Slice", {Out(1), Ints({0}), Ints({1}), Ints({0})}},
+                          {"Squeeze", {Out(2), Ints({0})}},
+                          {"Slice", {Out(1), Ints({1}), Ints({2}), Ints({0})}},
+                          {"Squeeze", {Out(4), Ints({0})}},
+                          {"Slice", {Out(1), Ints({2}), Ints({3}), Ints({0})}},
+                          {"Squeeze", {Out(6), Ints({0})}},
+                          {"Mul", {Out(3), AnyScalar()}},
+                          {"Transpose", {Out(5)}, perm_0132},
+                          {"MatMul", {Out(8), Out(9)}},
+                          {"Softmax", {Out(10)}, last_axis_softmax},
+                          {"MatMul", {Out(11), Out(7)}},
+                          {"Transpose", {Out(12)}, perm_0213},
+                          {"Reshape", {Out(13), AnyInput()}}},
+                         false};
+
 // Epilogue slots of each anchor kind, in order; a slot takes the first of its options that
 // matches, or none.
 enum class Effect { Bias, BatchNorm, Act, Residual };
@@ -89,7 +122,7 @@ const Slots kConvSlots{{{&kBiasAdd, Effect::Bias}},
                        {{&kBatchNorm, Effect::BatchNorm}},
                        {{&kRelu, Effect::Act, ACT_RELU}, {&kGelu, Effect::Act, ACT_GELU}},
                        {{&kResidual, Effect::Residual}}};
-const Slots kLinearSlots{{{&kBiasAdd, Effect::Bias}}, {{&kSilu, Effect::Act, ACT_SILU}}};
+const Slots kLinearSlots{{{&kBiasAdd, Effect::Bias}}, {{&kSilu, Effect::Act, ACT_SILU}}, {{&kResidual, Effect::Residual}}};
 const Slots kConvTSlots{{{&kBiasAdd, Effect::Bias}},
                         {{&kRelu, Effect::Act, ACT_RELU}, {&kSigmoid, Effect::Act, ACT_SIGMOID}}};
 
@@ -185,6 +218,14 @@ bool Planner::operand_ok(const Operand &o, const std::string &name, const std::s
         if (name == x || name.empty() || is_const(name)) return false;
         caps.push_back(name);
         return true;
+    case Arg::Any:
+        if (name.empty()) return false;
+        caps.push_back(name);
+        return true;
+    case Arg::Ints: {
+        auto it = onnx_.ints.find(name);
+        return it != onnx_.ints.end() && it->second == o.ints;
+    }
     }
     return false;
 }
@@ -328,6 +369,20 @@ void Planner::run() {
                 continue;
             }
         }
+        if (n.op == "Reshape" && !n.inputs.empty()) {
+            auto m = match(kAttention, n.inputs[0]);
+            if (m && m->nodes[0] == i) {
+                s.kind = NdKind::Attention;
+                take(s, *m);
+                s.conv_input = n.inputs[0];
+                s.attn_shape = m->captured.at(0);
+                s.attn_scale = *scalar(m->captured.at(1));
+                s.attn_out_shape = m->captured.at(2);
+                s.output = nodes()[size_t(s.last)].outputs[0];
+                plan_.steps.push_back(std::move(s));
+                continue;
+            }
+        }
         taken_[size_t(i)] = 1;
         s.nodes.push_back(i);
         std::string v = n.outputs.at(0);
@@ -364,6 +419,7 @@ const char *kind_name(NdKind k) {
     case NdKind::Linear: return "linear";
     case NdKind::LayerNorm: return "layer_norm";
     case NdKind::Affine: return "affine";
+    case NdKind::Attention: return "attention";
     default: return "node";
     }
 }

@@ -17,8 +17,10 @@
 // scale, the exporter's LayerNorm chain becomes one op, Conv takes a constant bias Add, a ReLU or
 // the exporter's GELU chain and a residual Add, a MatMul by a weight takes a bias Add and SiLU,
 // a ConvTranspose takes a bias Add and ReLU or Sigmoid, and a lone BatchNormalization becomes a
-// channel affine. This library adds one: a BatchNormalization right after a Conv's bias becomes
-// the conv's epilogue affine.
+// channel affine. This library adds three: a BatchNormalization right after a Conv's bias becomes
+// the conv's epilogue affine, a MatMul by a weight takes a residual Add after its bias and
+// activation, and the exporter's multi-head self-attention chain (from the QKV projection's
+// reshape to the output's reshape) becomes one step.
 #pragma once
 
 #include <string>
@@ -29,7 +31,7 @@
 
 namespace ocr {
 
-enum class NdKind { Generic, Conv, ConvT, Linear, LayerNorm, Affine };
+enum class NdKind { Generic, Conv, ConvT, Linear, LayerNorm, Affine, Attention };
 
 struct NdStep {
     NdKind kind = NdKind::Generic;
@@ -46,6 +48,9 @@ struct NdStep {
     // LayerNorm
     std::string gamma, beta;
     float eps = 1e-5f;
+    // Attention (its input is conv_input: the fused QKV projection [n, T, 3 H d])
+    std::string attn_shape, attn_out_shape;  // the first and the last Reshape's shape operands
+    float attn_scale = 1.f;
 };
 
 struct NdPlan {

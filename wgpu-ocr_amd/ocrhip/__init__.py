@@ -556,7 +556,7 @@ class Recognizer:
 FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_narrow", "conv_igemm", "conv_mfma", "gru", "conv_transpose", "conv_direct", "conv_generic", "maxpool", "mask_up",
             "grey_resize", "line_crop", "avgpool_t", "argmax", "copy", "ccl")
 ND_FAMILIES = ("conv3x3_dma", "gemm_dma", "conv_narrow", "conv_igemm", "conv_mfma", "nd_conv_nchw", "nd_conv_dw", "nd_conv_small",
-               "nd_gemm_rows", "nd_head", "nd_bgemm", "nd_conv_generic", "nd_conv_transpose", "nd_elementwise", "nd_copy",
+               "nd_gemm_rows", "nd_head", "nd_attention", "nd_bgemm", "nd_conv_generic", "nd_conv_transpose", "nd_elementwise", "nd_copy",
                "nd_reduce", "nd_layer_norm", "nd_softmax", "nd_argmax", "nd_pool", "nd_resize", "nd_det_prep",
                "nd_threshold")
 
