@@ -4,13 +4,12 @@
 //
 // conv_nchw: group-1, stride-1 convolutions up to 3 x 3 on the matrix cores
 // (v_mfma_f32_16x16x32_f16). No LDS staging: every wavefront loads its own operands. The A
-// operand is 16 output channels x 32 input channels of the packed float16 weights, one 16-byte
-// read a lane; the B operand is 32 input channels x 16 neighbouring output pixels of one row,
-// eight reads a lane of one channel plane each (16 lanes read 64 neighbouring bytes). The float32
+// operand is 16 neighbouring output pixels of one row x 32 input channels, eight reads a lane of
+// one channel plane each (16 lanes read 64 neighbouring bytes); the B operand is 32 input channels
+// x 16 output channels of the packed float16 weights, one 16-byte read a lane. The float32
 // inputs are split into float16 hi + lo (x = hi + lo to about 2^-22) and both go through the
 // matrix core, accumulating in float32: float32-class results. A lane's four accumulators are
-// four output channels of one pixel, so a store instruction writes 64 neighbouring bytes of four
-// channel planes. A wavefront owns 16 MT pixels of one output row (of the flattened plane for a
+// four neighbouring pixels of one output channel, stored with one 16-byte write. A wavefront owns 16 MT pixels of one output row (of the flattened plane for a
 // 1 x 1 conv) and 16 NT output channels; when there are too few such tiles to fill the GPU, up
 // to four wavefronts of a workgroup share one tile's K steps and add their accumulators through
 // LDS in a fixed order. Kernel rows that fall wholly into the padding are skipped (a 3 x 3 conv
@@ -155,9 +154,9 @@ __global__ __launch_bounds__(256) void conv_nchw_kernel(NchwParams p) {
                 split8(v[m], hi, lo);
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
-                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], hi, acc[m][t], 0, 0, 0);
-                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], lo, acc[m][t], 0, 0, 0);
-                    if constexpr (LO) acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], hi, acc[m][t], 0, 0, 0);
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, a[t], acc[m][t], 0, 0, 0);
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, a[t], acc[m][t], 0, 0, 0);
+                    if constexpr (LO) acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, al[t], acc[m][t], 0, 0, 0);
                 }
             }
             if (sn >= steps) break;
@@ -198,26 +197,43 @@ __global__ __launch_bounds__(256) void conv_nchw_kernel(NchwParams p) {
         }
     }
     if (!live) return;
-    // Lane (r, g) holds output channels 4g..4g+3 of n-tile t for pixel 16m + r of its tile.
+    // Lane (r, g) holds pixels 16m + 4g .. 16m + 4g + 3 of its tile for output channel 16t + r:
+    // one 16-byte store where the four are whole and aligned.
     const int olim = p.flat ? p.oh * p.ow : p.ow;
     const size_t oplane = size_t(p.oh) * p.ow;
+    const bool vec = (p.flat ? (oplane & 3) == 0 : (p.ow & 3) == 0) && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 &&
+                     (!p.res || (reinterpret_cast<uintptr_t>(p.res) & 15) == 0);
 #pragma unroll
-    for (int m = 0; m < MT; m++) {
-        const int px = x0 + 16 * m + r;
-        if (px >= olim) continue;
+    for (int t = 0; t < NT; t++) {
+        const int co = nb * p.bn + 16 * t + r;
+        if (co >= p.cout) continue;
+        const float b = p.bias ? p.bias[co] : 0.f;
+        const float as = p.affine ? p.affine[co] : 1.f, at = p.affine ? p.affine[p.cout + co] : 0.f;
+        const size_t o0 = (size_t(img) * p.cout + co) * oplane + (p.flat ? 0 : size_t(oy) * p.ow);
 #pragma unroll
-        for (int t = 0; t < NT; t++)
+        for (int m = 0; m < MT; m++) {
+            const int px = x0 + 16 * m + 4 * g;
+            if (px >= olim) continue;
+            float v[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int co = nb * p.bn + 16 * t + 4 * g + k;
-                if (co >= p.cout) continue;
-                float v = acc[m][t][k] + (p.bias ? p.bias[co] : 0.f);
-                if (p.affine) v = v * p.affine[co] + p.affine[p.cout + co];
-                v = act_dev(v, p.act);
-                const size_t o = (size_t(img) * p.cout + co) * oplane + (p.flat ? 0 : size_t(oy) * p.ow) + px;
-                if (p.res) v += p.res[o];
-                p.y[o] = v;
+                float u = acc[m][t][k] + b;
+                if (p.affine) u = u * as + at;
+                v[k] = act_dev(u, p.act);
             }
+            float *dst = p.y + o0 + px;
+            if (vec && px + 4 <= olim) {
+                if (p.res) {
+                    const float4 q = *reinterpret_cast<const float4 *>(p.res + o0 + px);
+                    v[0] += q.x, v[1] += q.y, v[2] += q.z, v[3] += q.w;
+                }
+                *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (px + k < olim) dst[k] = v[k] + (p.res ? p.res[o0 + px + k] : 0.f);
+            }
+        }
     }
 }
 
@@ -240,6 +256,7 @@ struct DwParams {
     float *y;
     const float *wt, *bias, *affine;  // wt [c][1][k][k]
     int c, h, w, oh, ow, pt, pl, act, quads, tiles_plane;
+    int vec;  // ow % 4 == 0 and y 16-byte aligned: 16-byte stores
 };
 
 // A thread makes four neighbouring outputs of one row: each input row segment is read once for
@@ -280,12 +297,19 @@ __global__ __launch_bounds__(256) void conv_dw_kernel(DwParams p) {
     }
     const float b = p.bias ? p.bias[ch] : 0.f;
     float *yr = p.y + size_t(plane) * p.oh * p.ow + size_t(oy) * p.ow;
+    float v[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        if (ox0 + q >= p.ow) break;
-        float v = acc[q] + b;
-        if (p.affine) v = v * p.affine[ch] + p.affine[p.c + ch];
-        yr[ox0 + q] = act_dev(v, p.act);
+        v[q] = acc[q] + b;
+        if (p.affine) v[q] = v[q] * p.affine[ch] + p.affine[p.c + ch];
+        v[q] = act_dev(v[q], p.act);
+    }
+    if (p.vec && ox0 + 4 <= p.ow) {
+        *reinterpret_cast<float4 *>(yr + ox0) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (ox0 + q < p.ow) yr[ox0 + q] = v[q];
     }
 }
 
@@ -648,6 +672,7 @@ bool nd_conv_dw(const NdConvArgs &a, hipStream_t s) {
     p.pl = a.pl;
     p.act = a.act;
     p.quads = (a.ow + 3) / 4;
+    p.vec = (a.ow % 4 == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) ? 1 : 0;
     p.tiles_plane = int((size_t(a.oh) * p.quads + 255) / 256);
     const double blocks = double(p.tiles_plane) * planes;
     if (blocks > 0x7fffffff) return false;
