@@ -86,6 +86,13 @@ def test_pp_pipeline_merge_batching_and_device_entry(ctx, pp_models):
         assert one.texts(k) == two.texts(k)
     st = two.stats()
     assert st["pages"] == 3 and st["rec_passes"] == 2 and st["lines"] > 60
+    # From host memory with uploads between the detection passes (one page a pass), twice in a
+    # row on one pipeline (its uploader and staging slots reused): the same text.
+    three = ocrhip.PpPipeline(det, rec, merge=2, det_batch=1)
+    for _ in range(2):
+        three.run(pages)
+        for k in range(3):
+            assert three.texts(k) == one.texts(k)
 
 
 def test_pp_pipeline_blank_small_and_empty_pages(ctx, pp_models):

@@ -1020,20 +1020,13 @@ int ocr_pp_pipeline_run(ocr_pp_pipeline *pipe, const uint8_t *const *rgb, const 
             need(w, "w");
             need(h, "h");
         }
-        Ctx &c = *pipe->owner->ctx;
-        c.bind();
-        std::vector<DBuf> bufs;
-        std::vector<const uint8_t *> ptrs;
         std::vector<int> wi(npages), hi(npages);
         for (uint32_t k = 0; k < npages; k++) {
             need(rgb[k], "page");
+            if (w[k] > 0x7fffffffu || h[k] > 0x7fffffffu) fail("pp pipeline: page size");
             wi[k] = int(w[k]), hi[k] = int(h[k]);
-            const size_t bytes = size_t(w[k]) * h[k] * 3;
-            bufs.emplace_back(&c, std::max<size_t>(bytes, 1));
-            c.h2d(bufs.back().get(), rgb[k], bytes);
-            ptrs.push_back(bufs.back().as<uint8_t>());
         }
-        pipe->pipe->run(ptrs.data(), wi.data(), hi.data(), int(npages));
+        pipe->pipe->run_host(rgb, wi.data(), hi.data(), int(npages));
     });
 }
 

@@ -2,10 +2,12 @@
 
 #include <algorithm>
 #include <cmath>
+#include <memory>
 #include <mutex>
 
 #include "crop.h"
 #include "host_util.h"
+#include "upload.h"
 
 namespace ocr {
 
@@ -32,6 +34,7 @@ struct PpPipeline::Impl {
     PpPipelineOpts opts;
     Workers workers;
     std::vector<Pinned> prob_host, bits_host, best_host;
+    std::unique_ptr<PageUploader> upl;  // made by the first run from host memory
     Impl(Ctx &c, NdGraph &d, NdGraph &r, const PpPipelineOpts &o)
         : ctx(c), det(d), rec(r), opts(o), workers(worker_count(o.threads)) {}
 };
@@ -45,6 +48,54 @@ PpPipeline::PpPipeline(Ctx &ctx, NdGraph &det, NdGraph &rec, const PpPipelineOpt
 PpPipeline::~PpPipeline() { delete impl_; }
 
 void PpPipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages) {
+    run_pages(d_rgb, w, h, npages, [](int, int) {});
+}
+
+void PpPipeline::run_host(const uint8_t *const *rgb, const int *w, const int *h, int npages) {
+    Impl &I = *impl_;
+    Ctx &ctx = I.ctx;
+    ctx.bind();
+    if (!I.upl) I.upl.reset(new PageUploader(ctx));
+    const hipStream_t up = I.upl->stream(), st = ctx.stream();
+    std::vector<DBuf> dpages;
+    std::vector<const uint8_t *> ptrs;
+    std::vector<char> pinned(size_t(std::max(npages, 0)));
+    for (int p = 0; p < npages; p++) {
+        if (!rgb[p]) fail("pp pipeline: page " + std::to_string(p) + " has no pixels");
+        if (w[p] <= 0 || h[p] <= 0) fail("pp pipeline: empty page " + std::to_string(p));
+        dpages.emplace_back(&ctx, size_t(w[p]) * h[p] * 3);
+        dpages.back().used_on(up);
+        ptrs.push_back(dpages.back().as<uint8_t>());
+        pinned[size_t(p)] = host_pinned(rgb[p]);
+    }
+    // The page buffers come from the pool in the compute stream's order: the uploads wait for it.
+    hipEvent_t ready, done;
+    OCR_HIP(hipEventCreateWithFlags(&ready, hipEventDisableTiming));
+    OCR_HIP(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+    struct Events {
+        hipEvent_t a, b;
+        ~Events() {
+            (void)hipEventDestroy(a);
+            (void)hipEventDestroy(b);
+        }
+    } guard{ready, done};
+    OCR_HIP(hipEventRecord(ready, st));
+    OCR_HIP(hipStreamWaitEvent(up, ready, 0));
+    try {
+        run_pages(ptrs.data(), w, h, npages, [&](int p, int q) {
+            for (int k = p; k < q; k++)
+                I.upl->upload(dpages[size_t(k)].as<uint8_t>(), rgb[k], size_t(w[k]) * h[k] * 3, pinned[size_t(k)] != 0);
+            OCR_HIP(hipEventRecord(done, up));
+            OCR_HIP(hipStreamWaitEvent(st, done, 0));
+        });
+    } catch (...) {
+        drain_stream(up, "the uploads of a failed run");
+        throw;
+    }
+}
+
+void PpPipeline::run_pages(const uint8_t *const *d_rgb, const int *w, const int *h, int npages,
+                           const std::function<void(int, int)> &before_pass) {
     Impl &I = *impl_;
     Ctx &ctx = I.ctx;
     const hipStream_t st = ctx.stream();
@@ -96,6 +147,7 @@ void PpPipeline::run(const uint8_t *const *d_rgb, const int *w, const int *h, in
                 q++;
             const int n = q - p, W = ow[size_t(p)], H = oh[size_t(p)];
             const size_t plane = size_t(W) * H, words = size_t((W + 31) / 32) * H;
+            before_pass(p, q);
             NdTensor in;
             in.shape = {n, 3, H, W};
             in.buf = std::make_shared<DBuf>(&ctx, size_t(n) * 3 * plane * sizeof(float));

@@ -4,6 +4,7 @@
 // host CTC. Pages overlap: the host works on one page's boxes while the GPU detects the next.
 #pragma once
 
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -30,12 +31,19 @@ class PpPipeline {
     ~PpPipeline();
     // All pages' RGB bytes already in device memory.
     void run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages);
+    // Pages in host memory (page-locked or pageable): each detection pass's pages go up on the
+    // uploader's stream right before the pass, so later pages upload while earlier ones are
+    // detected (the reference uploads each page in its detection path, src/nd.rs:1353-1369).
+    void run_host(const uint8_t *const *rgb, const int *w, const int *h, int npages);
     const std::vector<PageText> &pages() const { return pages_; }
     const PipelineStats &stats() const { return stats_; }
 
   private:
     struct Impl;
     Impl *impl_;
+    // before_pass(p, q): called before the detection pass of pages [p, q) is queued.
+    void run_pages(const uint8_t *const *d_rgb, const int *w, const int *h, int npages,
+                   const std::function<void(int, int)> &before_pass);
     std::vector<PageText> pages_;
     PipelineStats stats_;
 };
