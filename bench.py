@@ -328,8 +328,15 @@ def config_figures(ctx, det, rec, reps=20):
     out["det_800x600"] = {"workload": "ocrs-architecture U-Net 16-256 on [1, 1, 800, 600] (host in and out)",
                           "ms_per_page": 1e3 * secs, "gflop_per_page": sum(k["flops"] for k in kern.values()) / 1e9,
                           **_kernel_summary(kern, 1)}
-    # PP-OCRv6-architecture recognition: 36 RGB lines 3 x 48 x [160, 960], 16 a batch, SVTR neck,
-    # 18 708-class CTC head (arg-max fused: the logits are never written).
+    out["pp_rec_36_lines"] = pp_rec_figure(ctx, reps)
+    return out
+
+
+def pp_rec_figure(ctx, reps=20):
+    """PP-OCRv6-architecture recognition: 36 RGB lines 3 x 48 x [160, 960], 16 a batch, SVTR
+    neck, 18 708-class CTC head (arg-max fused: the logits are never written), inputs resident."""
+    import ocrhip
+    from ocrhip import synth_pp
     prec = ocrhip.NdGraph(ctx, synth_pp.model_path("rec"), stop_before_softmax=True)
     pb, _ = synth_pp.batch_lines(synth_pp.rec_lines(36, seed=0))
     pdev = []
@@ -344,11 +351,27 @@ def config_figures(ctx, det, rec, reps=20):
             prec.argmax_device(b, shape, bb)
     secs = _timed(ctx, pp_rec, reps)
     kern = _probed(ocrhip.ND_FAMILIES, lambda: (pp_rec(), ctx.synchronize()))
-    out["pp_rec_36_lines"] = {"workload": "PP-OCRv6-architecture rec, 36 RGB lines 3 x 48 x [160, 960], 16 a batch",
-                              "ms_per_batch": 1e3 * secs, "lines_per_sec": 36 / secs,
-                              "gflop_per_batch": sum(k["flops"] for k in kern.values()) / 1e9,
-                              **_kernel_summary(kern, 1)}
-    return out
+    return {"workload": "PP-OCRv6-architecture rec, 36 RGB lines 3 x 48 x [160, 960], 16 a batch",
+            "ms_per_batch": 1e3 * secs, "lines_per_sec": 36 / secs,
+            "gflop_per_batch": sum(k["flops"] for k in kern.values()) / 1e9, **_kernel_summary(kern, 1)}
+
+
+def pp_only(npages, merge):
+    """Only the PP-OCR figures: the whole-page pipeline on `npages` synthetic pages (resident and
+    from host memory) and the 36-line recogniser batch (for kernel and counter profiles)."""
+    import ocrhip
+    from ocrhip import synth
+    ctx = ocrhip.Context()
+    pages = [synth.page(i) for i in range(npages)]
+    d_pages = []
+    for p in pages:
+        b = ctx.alloc(p.nbytes)
+        b.upload(p)
+        d_pages.append(b)
+    ws, hs = [p.shape[1] for p in pages], [p.shape[0] for p in pages]
+    out = {"pp_pipeline": pp_pipeline(ctx, d_pages, ws, hs, merge, host_pages=pages),
+           "pp_rec_36_lines": pp_rec_figure(ctx, reps=5)}
+    print(json.dumps(out))
 
 
 def main():
@@ -367,6 +390,9 @@ def main():
     ap.add_argument("--conv-layer", metavar="CIN,COUT,N,H,W[,PHxPW]",
                     help="only time one 3x3 convolution layer (+ ReLU, optional max pool)")
     ap.add_argument("--gru-lines", type=int, metavar="N", help="only time the GRU on N recognised lines")
+    ap.add_argument("--pp-only", action="store_true",
+                    help="only the PP-OCR figures: page pipeline (resident and host pages) and the 36-line "
+                         "recogniser batch")
     ap.add_argument("--trace", action="store_true",
                     help="after the warm-up, run one step from host memory with the pipeline's trace "
                          "(OCR_PIPE_TRACE: upload, detection and recognition spans on the GPU, host "
@@ -380,6 +406,9 @@ def main():
         return
     if args.gru_lines:
         gru_lines(args.gru_lines)
+        return
+    if args.pp_only:
+        pp_only(args.pages, args.merge)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the pipeline shards by page with no exchange, so N GPUs run N "

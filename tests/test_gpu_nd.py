@@ -293,6 +293,20 @@ def test_head_argmax_first_index_on_ties(ctx, tmp_path, k, n, exact):
     assert np.array_equal(got, np.argmax(head.run(x), axis=-1))
 
 
+@pytest.mark.parametrize("cin,cout,k,s,act", [(16, 16, 2, 2, "Relu"), (16, 1, 2, 2, "Sigmoid"), (8, 5, 3, 3, "Relu"),
+                                             (6, 4, 3, 2, "Sigmoid"), (5, 7, 4, 4, None)])
+def test_conv_transpose_nchw_shapes(ctx, tmp_path, cin, cout, k, s, act):
+    # kernel = stride (each input pixel alone makes its s x s outputs) and an overlapping one
+    def fn(g, x):
+        y = g.add("ConvTranspose", [x, w(g, (cin, cout, k, k), cin), g.init("tb", (RNG.standard_normal(cout) * 0.1)
+                                                                          .astype(np.float32))],
+                  kernel_shape=[k, k], strides=[s, s])
+        return g.add(act, [y]) if act else y
+    shape = (2, cin, 23, 37)
+    p = build(tmp_path, "convt", fn, shape)
+    check(ctx, p, RNG.standard_normal(shape).astype(np.float32))
+
+
 def _attention(g, x, dim, heads):
     hd = dim // heads
     qkv = g.add("MatMul", [x, w(g, (dim, 3 * dim), dim)])

@@ -312,6 +312,41 @@ __global__ void convt_nchw_kernel(const float *x, int n, int cin, int h, int w, 
     y[i] = act_nd(acc + (b ? b[co] : 0.f), act);
 }
 
+// ConvTranspose with kernel = stride S (no overlap: input pixel (iy, ix) alone makes the S x S
+// outputs (S iy + a, S ix + b)): a thread per input pixel and output channel, the channel sum in
+// the order convt_nchw_kernel takes it, the S x S results stored as S rows of S neighbours.
+template <int S>
+__global__ void convt_ks_nchw_kernel(const float *x, int n, int cin, int h, int w, const float *wt, const float *b,
+                                     float *y, int cout, int act) {
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(n) * cout * h * w) return;
+    const int ix = int(i % w), iy = int((i / w) % h);
+    const int co = int((i / (size_t(w) * h)) % cout);
+    const int img = int(i / (size_t(w) * h * cout));
+    float acc[S][S];
+#pragma unroll
+    for (int a = 0; a < S; a++)
+#pragma unroll
+        for (int c = 0; c < S; c++) acc[a][c] = 0.f;
+    const float *xp = x + (size_t(img) * cin * h + iy) * w + ix;
+    const float *wp = wt + size_t(co) * S * S;  // [cin][cout][S][S]
+    for (int ci = 0; ci < cin; ci++) {
+        const float xv = xp[size_t(ci) * h * w];
+        const float *wc = wp + size_t(ci) * cout * S * S;
+#pragma unroll
+        for (int a = 0; a < S; a++)
+#pragma unroll
+            for (int c = 0; c < S; c++) acc[a][c] = __fmaf_rn(xv, wc[a * S + c], acc[a][c]);
+    }
+    const float bv = b ? b[co] : 0.f;
+    const int ow = w * S;
+    float *yp = y + ((size_t(img) * cout + co) * h * S + size_t(iy) * S) * ow + size_t(ix) * S;
+#pragma unroll
+    for (int a = 0; a < S; a++)
+#pragma unroll
+        for (int c = 0; c < S; c++) yp[size_t(a) * ow + c] = act_nd(acc[a][c] + bv, act);
+}
+
 // ---- PP-OCR detection input (nd.rs nd_det_prep, src/nd.rs:1353-1369) -------------------------
 // WGSL mix(a, b, t) = a (1 - t) + b t, each operation rounded on its own: contraction into
 // fused multiply-adds is off in the front-end kernels so they follow the stated arithmetic.
@@ -460,8 +495,24 @@ void nd_conv_transpose(const float *x, int n, int cin, int h, int w, const float
     if (!total) return;
     ProbeScope probe("nd_conv_transpose", s, 2.0 * double(n) * h * w * cin * cout * kh * kw,
                      4.0 * (double(n) * cin * h * w + double(total)));
-    hipLaunchKernelGGL(convt_nchw_kernel, dim3(grid_for(total)), dim3(256), 0, s, x, n, cin, h, w, wt, b, y, cout, oh,
-                       ow, kh, kw, stride, act);
+    const size_t inputs = size_t(n) * cout * h * w;
+    if (kh == stride && kw == stride && stride >= 1 && stride <= 4) {
+        if (stride == 2)
+            hipLaunchKernelGGL(convt_ks_nchw_kernel<2>, dim3(grid_for(inputs)), dim3(256), 0, s, x, n, cin, h, w, wt, b, y,
+                               cout, act);
+        else if (stride == 1)
+            hipLaunchKernelGGL(convt_ks_nchw_kernel<1>, dim3(grid_for(inputs)), dim3(256), 0, s, x, n, cin, h, w, wt, b, y,
+                               cout, act);
+        else if (stride == 3)
+            hipLaunchKernelGGL(convt_ks_nchw_kernel<3>, dim3(grid_for(inputs)), dim3(256), 0, s, x, n, cin, h, w, wt, b, y,
+                               cout, act);
+        else
+            hipLaunchKernelGGL(convt_ks_nchw_kernel<4>, dim3(grid_for(inputs)), dim3(256), 0, s, x, n, cin, h, w, wt, b, y,
+                               cout, act);
+    } else {
+        hipLaunchKernelGGL(convt_nchw_kernel, dim3(grid_for(total)), dim3(256), 0, s, x, n, cin, h, w, wt, b, y, cout, oh,
+                           ow, kh, kw, stride, act);
+    }
     OCR_HIP(hipGetLastError());
 }
 
