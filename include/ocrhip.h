@@ -28,7 +28,8 @@ typedef struct ocr_recognizer ocr_recognizer;
 typedef struct ocr_pipeline ocr_pipeline;
 
 /* Options of a context. lines: lines per GRU workgroup (LINES, src/bin/ocr-bench.rs:135; this
- * build's recurrence always groups 8). pool_mb: the scratch pool's cap (POOLMB, src/gpu.rs:919).
+ * build's recurrence always groups 8, the lines whose hi and lo parts fill one MFMA operand's 16
+ * columns; any value is taken). pool_mb: the scratch pool's cap (POOLMB, src/gpu.rs:919).
  * device: the HIP device index. */
 typedef struct ocr_opts {
     uint32_t lines;
