@@ -152,6 +152,52 @@ def gru_lines(nlines, reps=5):
     print(json.dumps({"lines": nlines, "steps": tmax, "gru_us_per_launch": us, "gru_us_per_step": us / tmax}))
 
 
+def bandwidth(npages=16, nlines=540, reps=5):
+    """The bandwidth-bound families at multi-page launch sizes (a single page's tensors are launch-
+    dominated): detection of `npages` resident pages as one pass (grey_resize, the U-Net, mask_up)
+    and recognition of `nlines` resident lines as one pass (conv_direct, argmax and the rest);
+    prints each family's launches, average time, algorithmic bytes a launch and GB/s."""
+    import ocrhip
+    from ocrhip import synth
+    ctx = ocrhip.Context()
+    det = ocrhip.Detector(ctx, synth.model_path("det"))
+    rec = ocrhip.Recognizer(ctx, synth.model_path("rec"))
+    pages = [synth.page(i % 12) for i in range(npages)]
+    d_pages, d_bits = [], []
+    for p in pages:
+        b = ctx.alloc(p.nbytes)
+        b.upload(p)
+        d_pages.append(b)
+        d_bits.append(ctx.alloc(p.shape[0] * ((p.shape[1] + 31) // 32) * 4))
+    ws, hs = [p.shape[1] for p in pages], [p.shape[0] for p in pages]
+    batches, _, _ = synth.batch_lines(synth.rec_lines(nlines, seed=0, wmin=200, wmax=800))
+    dev = []
+    for data, n, w in batches:
+        buf = ctx.alloc(data.nbytes)
+        buf.upload(np.ascontiguousarray(data))
+        dev.append((buf, n, w))
+    tmax, ntot, _ = rec.dims(dev)
+    d_best = ctx.alloc(tmax * ntot * 4)
+
+    def step():
+        det.detect_pages_device(d_pages, ws, hs, 0.5, d_bits)
+        rec.recognize_device(dev, d_best=d_best)
+    step()
+    ctx.synchronize()
+    kern = _probed(ocrhip.FAMILIES, lambda: ([step() for _ in range(reps)], ctx.synchronize()))
+    out = {"workload": f"detection of {npages} resident 2550x3300 pages as one pass and recognition of {nlines} "
+                       f"resident lines as one pass, {reps} times", "families": {}}
+    for f, k in sorted(kern.items(), key=lambda kv: -kv[1]["ms"]):
+        calls = max(k["calls"], 1)
+        secs = k["ms"] / 1e3
+        out["families"][f] = {"calls": k["calls"], "avg_us": 1e3 * k["ms"] / calls,
+                              "algorithmic_mb_per_launch": k["bytes"] / calls / 1e6,
+                              "gbps": k["bytes"] / max(secs, 1e-12) / 1e9,
+                              "frac_hbm": k["bytes"] / max(secs, 1e-12) / (HBM_PEAK_GBS * 1e9),
+                              "tflops": k["flops"] / max(secs, 1e-12) / 1e12}
+    print(json.dumps(out))
+
+
 def host_cpu():
     """The host CPU the baseline runs on: model name from /proc/cpuinfo, the cores this process
     may run on (its affinity mask) and the logical CPUs the system shows."""
@@ -390,6 +436,9 @@ def main():
     ap.add_argument("--conv-layer", metavar="CIN,COUT,N,H,W[,PHxPW]",
                     help="only time one 3x3 convolution layer (+ ReLU, optional max pool)")
     ap.add_argument("--gru-lines", type=int, metavar="N", help="only time the GRU on N recognised lines")
+    ap.add_argument("--bandwidth", action="store_true",
+                    help="only the bandwidth-bound families at multi-page sizes: detection of 16 pages and "
+                         "recognition of 540 lines, each as one pass")
     ap.add_argument("--pp-only", action="store_true",
                     help="only the PP-OCR figures: page pipeline (resident and host pages) and the 36-line "
                          "recogniser batch")
@@ -409,6 +458,9 @@ def main():
         return
     if args.pp_only:
         pp_only(args.pages, args.merge)
+        return
+    if args.bandwidth:
+        bandwidth()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the pipeline shards by page with no exchange, so N GPUs run N "

@@ -222,6 +222,29 @@ def test_conv_transpose_phases(ctx, tmp_path, k, stride, cin, cout, hw, exact):
     check(ctx, p, RNG.standard_normal((2, cin, *hw)).astype(np.float32))
 
 
+@pytest.mark.parametrize("cin,cout,hw,stride,act,exact", [(32, 16, (37, 29), 2, "Relu", True),
+                                                          (64, 48, (11, 13), 2, "Sigmoid", False),
+                                                          (24, 32, (7, 9), 3, "Relu", True),
+                                                          (16, 8, (9, 10), 2, "Relu", True)])
+def test_conv_transpose_into_concat_slice(ctx, tmp_path, cin, cout, hw, stride, act, exact):
+    """Kernel = stride ConvTranspose writing its phases into a channel slice of a Concat (the
+    U-Net's skip joins), as one matrix-core GEMM over the input pixels when the phases are packed
+    (output channels a multiple of 16), else the float32 or general paths."""
+    def net(g, x):
+        wt = RNG.standard_normal((cin, cout, stride, stride)).astype(np.float32) * 0.3
+        if exact:
+            wt = f16x(wt)
+        up = g.add("ConvTranspose", [x, g.init("w", wt), g.init("b", RNG.standard_normal(cout).astype(np.float32))],
+                   kernel_shape=[stride, stride], strides=[stride, stride])
+        up = g.add(act, [up])
+        side = g.add("Relu", [g.add("ConvTranspose", [x, g.init("w2", f16x(RNG.standard_normal(
+            (cin, 16, stride, stride)).astype(np.float32) * 0.3))], kernel_shape=[stride, stride],
+            strides=[stride, stride])])
+        return g.add("Concat", [side, up], axis=1)
+    p = build(tmp_path, "tcat", net, (2, cin, *hw))
+    check(ctx, p, RNG.standard_normal((2, cin, *hw)).astype(np.float32))
+
+
 def test_conv_pool_fusion_single_and_dual(ctx, tmp_path):
     """A MaxPool after a 3 x 3 conv runs in its epilogue: alone, and next to the full output
     when a Concat also reads the conv."""

@@ -586,8 +586,12 @@ void Graph::Exec::step(size_t i) {
             conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
             break;
         }
-        // Kernel = stride = 2 with few channels: the GEMM over the input pixels would be one
-        // 32-wide K chunk deep, so a float32 pass at HBM speed does better.
+        // Kernel = stride: one GEMM over the input pixels whose epilogue writes the phases
+        // (operands read straight into the matrix cores, no staging set-up to pay back).
+        if (s.allph.whi && s.kh == s.sh && s.kw == s.sw && !env_set("NOCONVTROWS") &&
+            convt_rows(a, y, s.allph.whi, s.allph.wlo, s.allph.pk, s.b, s.sh, s.act, st))
+            break;
+        // Kernel = stride = 2 with few channels: a float32 pass with the weights in LDS.
         if (convt_k2s2(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st)) break;
         if (s.allph.whi) {
             // All phases as one GEMM over the input pixels.

@@ -124,6 +124,12 @@ void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, 
 // (the weights in LDS): one float32 pass at HBM speed. False (nothing launched) otherwise.
 bool convt_k2s2(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride, int act,
                 hipStream_t s);
+// ConvTranspose with kernel = stride (s <= 4) as one matrix-core GEMM over the input pixels
+// (kernels/convt_rows.hip): pk packs the cin -> s s cout weights as a 1 x 1 conv (output column
+// k cout + c is channel c of phase k = py s + px), b the cout biases, act none / ReLU / Sigmoid.
+// False (nothing launched) for anything else.
+bool convt_rows(const Act &x, const Act &y, const uint16_t *whi, const uint16_t *wlo, const ConvPack &pk,
+                const float *b, int stride, int act, hipStream_t st);
 void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s);
 void copy_act(const Act &x, const Act &y, int y0, int x0, hipStream_t s);  // Slice / Concat copies
 void activate(const Act &x, const Act &y, int act, hipStream_t s);

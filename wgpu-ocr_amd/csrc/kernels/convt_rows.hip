@@ -1,0 +1,213 @@
+// ConvTranspose with kernel = stride s (the U-Net's upsamplers, src/gpu.rs:424-460) in NHWC as one
+// GEMM over the input pixels on the gfx950 matrix cores (v_mfma_f32_16x16x32_f16): output column
+// k cout + c of input pixel (i, j) is channel c of y's pixel (s i + k / s, s j + k % s), written
+// when that pixel lies inside y. No LDS: a wavefront loads its own operands, the packed float16
+// weights as the A operand (one 16-byte read a lane) and 16 input pixels' channels as the B
+// operand (two 16-byte reads a lane), split into float16 hi + lo (x = hi + lo to about 2^-22) and
+// both multiplied, accumulating in float32 (float32-class results). A lane's four accumulators are
+// four neighbouring channels of one output pixel: one 16-byte store. A wavefront owns 16 RT input
+// pixels x 16 NT output columns; every chunk's operands of a group of KC chunks are loaded before
+// the group's MFMAs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "../kernels.h"
+#include "../runtime.h"
+
+namespace ocr {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+namespace {
+
+struct CtParams {
+    const float *x;
+    long xcs;
+    int npx, hw, w, cin;       // input pixels (n h w), h w, w, channels
+    const half8 *wt, *wt_lo;   // [nblock][chunk][1][bn][32]: cin -> s s cout
+    int bn, chunks;
+    float *y;
+    long ycs;
+    int oh, ow, cout, s, ncol;  // ncol = s s cout
+    const float *bias;
+    int act;
+    int rtiles, tsplit, vecx, vecy;
+};
+
+__device__ inline float ct_act(float v, int act) {
+    if (act == ACT_RELU) return fmaxf(v, 0.f);
+    if (act == ACT_SIGMOID) return 1.f / (1.f + expf(-v));
+    return v;
+}
+
+template <int RT, int NT, int KC, bool LO>
+__global__ __launch_bounds__(256) void convt_rows_kernel(CtParams p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wid = blockIdx.x * 4 + wave, nb = blockIdx.y;
+    const int rt = wid / p.tsplit, tpart = wid - rt * p.tsplit;
+    if (rt >= p.rtiles) return;
+    const int r = lane & 15, g = lane >> 4;
+    const int r0 = rt * 16 * RT, t0 = tpart * NT;
+    floatx4 acc[RT][NT];
+#pragma unroll
+    for (int m = 0; m < RT; m++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[m][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int cg = 0; cg < p.chunks; cg += KC) {
+        half8 bh[RT][KC], bl[RT][KC], a[KC][NT], al[KC][NT];
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            if (cg + c >= p.chunks) break;
+            const size_t wo = size_t(nb * p.chunks + cg + c) * (p.bn * 4) + size_t(r) * 4 + g;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                a[c][t] = p.wt[wo + (t0 + t) * 64];
+                if constexpr (LO) al[c][t] = p.wt_lo[wo + (t0 + t) * 64];
+            }
+            const int c0 = (cg + c) * 32 + 8 * g;
+#pragma unroll
+            for (int m = 0; m < RT; m++) {
+                const int px = r0 + 16 * m + r;
+                float v[8];
+                if (px < p.npx && p.vecx && c0 + 8 <= p.cin) {
+                    const float4 *src = reinterpret_cast<const float4 *>(p.x + size_t(px) * p.xcs + c0);
+                    const float4 q0 = src[0], q1 = src[1];
+                    v[0] = q0.x, v[1] = q0.y, v[2] = q0.z, v[3] = q0.w, v[4] = q1.x, v[5] = q1.y, v[6] = q1.z, v[7] = q1.w;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) v[j] = (px < p.npx && c0 + j < p.cin) ? p.x[size_t(px) * p.xcs + c0 + j] : 0.f;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const _Float16 hv = (_Float16)v[j];
+                    bh[m][c][j] = hv;
+                    bl[m][c][j] = (_Float16)(v[j] - (float)hv);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            if (cg + c >= p.chunks) break;
+#pragma unroll
+            for (int m = 0; m < RT; m++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][t], bh[m][c], acc[m][t], 0, 0, 0);
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][t], bl[m][c], acc[m][t], 0, 0, 0);
+                    if constexpr (LO)
+                        acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[c][t], bh[m][c], acc[m][t], 0, 0, 0);
+                }
+        }
+    }
+    // Lane (r, g) holds columns 4g..4g+3 of n-tile t for input pixel 16m + r.
+#pragma unroll
+    for (int m = 0; m < RT; m++) {
+        const int px = r0 + 16 * m + r;
+        if (px >= p.npx) continue;
+        const int img = px / p.hw, rem = px - img * p.hw;
+        const int iy = rem / p.w, ix = rem - iy * p.w;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int col0 = nb * p.bn + 16 * (t0 + t) + 4 * g;
+            if (col0 >= p.ncol) continue;
+            if (p.vecy) {
+                // cout % 4 == 0: the four columns are neighbouring channels of one phase.
+                const int ph = col0 / p.cout, c = col0 - ph * p.cout;
+                const int oy = p.s * iy + ph / p.s, ox = p.s * ix + ph % p.s;
+                if (oy >= p.oh || ox >= p.ow) continue;
+                float4 o;
+                o.x = ct_act(acc[m][t][0] + p.bias[c], p.act);
+                o.y = ct_act(acc[m][t][1] + p.bias[c + 1], p.act);
+                o.z = ct_act(acc[m][t][2] + p.bias[c + 2], p.act);
+                o.w = ct_act(acc[m][t][3] + p.bias[c + 3], p.act);
+                *reinterpret_cast<float4 *>(p.y + ((size_t(img) * p.oh + oy) * p.ow + ox) * p.ycs + c) = o;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int col = col0 + k;
+                    if (col >= p.ncol) break;
+                    const int ph = col / p.cout, c = col - ph * p.cout;
+                    const int oy = p.s * iy + ph / p.s, ox = p.s * ix + ph % p.s;
+                    if (oy < p.oh && ox < p.ow)
+                        p.y[((size_t(img) * p.oh + oy) * p.ow + ox) * p.ycs + c] = ct_act(acc[m][t][k] + p.bias[c], p.act);
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool convt_rows(const Act &x, const Act &y, const uint16_t *whi, const uint16_t *wlo, const ConvPack &pk,
+                const float *b, int stride, int act, hipStream_t st) {
+    if (stride < 1 || stride > 4 || !whi || !b || (!pk.exact && !wlo)) return false;
+    if (pk.kh != 1 || pk.kw != 1 || pk.cin != x.c || pk.cout != stride * stride * y.c) return false;
+    if (pk.bn != 16 && pk.bn != 32 && pk.bn != 64) return false;
+    if (act != ACT_NONE && act != ACT_RELU && act != ACT_SIGMOID) return false;
+    if (x.n != y.n || y.h > stride * x.h || y.w > stride * x.w || y.h < 1 || y.w < 1) return false;
+    const double npx = double(x.n) * x.h * x.w;
+    if (npx >= 2147483647.0 - 64 || pk.nblocks > 65535 || double(y.n) * y.h * y.w * y.cs >= 9.0e18) return false;
+    CtParams p{};
+    p.x = x.p;
+    p.xcs = x.cs;
+    p.npx = int(npx);
+    p.hw = x.h * x.w;
+    p.w = x.w;
+    p.cin = x.c;
+    p.wt = reinterpret_cast<const half8 *>(whi);
+    p.wt_lo = reinterpret_cast<const half8 *>(wlo);
+    p.bn = pk.bn;
+    p.chunks = pk.chunks;
+    p.y = y.p;
+    p.ycs = y.cs;
+    p.oh = y.h;
+    p.ow = y.w;
+    p.cout = y.c;
+    p.s = stride;
+    p.ncol = pk.cout;
+    p.bias = b;
+    p.act = act;
+    p.vecx = (x.c % 4 == 0 && x.cs % 4 == 0 && (reinterpret_cast<uintptr_t>(x.p) & 15) == 0) ? 1 : 0;
+    p.vecy = (y.c % 4 == 0 && y.cs % 4 == 0 && (reinterpret_cast<uintptr_t>(y.p) & 15) == 0) ? 1 : 0;
+    if (p.npx == 0) return true;
+    // 32 pixels a wavefront, then 16, then a part of the column block, until there are 2048
+    // wavefronts (8 a CU) or no smaller split.
+    const int ntf = pk.bn / 16;
+    auto waves = [&](int rt, int ts) { return std::ceil(npx / (16.0 * rt)) * ts * pk.nblocks; };
+    int rt = 2, ts = 1;
+    if (waves(rt, ts) < 2048) rt = 1;
+    while (waves(rt, ts) < 2048 && ts < ntf) ts *= 2;
+    const int nt = ntf / ts;
+    p.rtiles = int((npx + 16 * rt - 1) / (16 * rt));
+    p.tsplit = ts;
+    const double blocks = std::ceil(double(p.rtiles) * ts / 4);
+    if (blocks > 2147483647.0) return false;
+    const dim3 grid{unsigned(blocks), unsigned(pk.nblocks)};
+    ProbeScope probe("conv_transpose", st, 2.0 * npx * double(x.c) * pk.cout,
+                     4.0 * (npx * x.c + double(y.n) * y.h * y.w * y.c) + 2.0 * double(pk.halves()) * (pk.exact ? 1 : 2));
+    const bool lo = !pk.exact, k8 = pk.chunks > 4;
+#define CT_LAUNCH(RT, NT)                                                                                   \
+    do {                                                                                                    \
+        if (lo && k8) hipLaunchKernelGGL((convt_rows_kernel<RT, NT, 8, true>), grid, dim3(256), 0, st, p);  \
+        else if (lo) hipLaunchKernelGGL((convt_rows_kernel<RT, NT, 4, true>), grid, dim3(256), 0, st, p);   \
+        else if (k8) hipLaunchKernelGGL((convt_rows_kernel<RT, NT, 8, false>), grid, dim3(256), 0, st, p);  \
+        else hipLaunchKernelGGL((convt_rows_kernel<RT, NT, 4, false>), grid, dim3(256), 0, st, p);          \
+    } while (0)
+    if (rt == 2) {
+        if (nt == 1) CT_LAUNCH(2, 1);
+        else if (nt == 2) CT_LAUNCH(2, 2);
+        else CT_LAUNCH(2, 4);
+    } else {
+        if (nt == 1) CT_LAUNCH(1, 1);
+        else if (nt == 2) CT_LAUNCH(1, 2);
+        else CT_LAUNCH(1, 4);
+    }
+#undef CT_LAUNCH
+    OCR_HIP(hipGetLastError());
+    return true;
+}
+
+}  // namespace ocr
