@@ -617,13 +617,15 @@ bool nd_conv_nchw_mfma(const NdMfmaConvArgs &a, hipStream_t s) {
     const double lines = p.flat ? double(a.n) : double(a.n) * a.oh;
     if (lim > 0x7fffffff || lines > 0x7fffffff) return false;
     // Pixels a wavefront: the widest of 64 / 32 / 16 that wastes at most a quarter of its tiles
-    // and still gives 2048 wavefronts (8 a CU, to keep loads in flight); else 16.
+    // and still gives 8192 wavefronts (32 a CU, so that other wavefronts' loads cover each one's
+    // load latency: the PP-OCR recogniser's convs take 1.12 ms a batch at this target, 1.18 at
+    // 2048, 1.12 at 32768); else 16.
     const int nt = pk.bn / 16;
     auto tiles_of = [&](int m) { return lines * std::ceil(lim / (16.0 * m)); };
     int mt = 1;
     for (int cand : {4, 2}) {
         const double tl = std::ceil(lim / (16.0 * cand));
-        if ((tl * 16 * cand - lim) * 4 <= lim && tiles_of(cand) * pk.nblocks >= 2048) { mt = cand; break; }
+        if ((tl * 16 * cand - lim) * 4 <= lim && tiles_of(cand) * pk.nblocks >= 8192) { mt = cand; break; }
     }
     const int steps = pk.chunks * (p.flat ? 1 : std::min(pk.kh, a.h) * pk.kw);
     const double waves = tiles_of(mt) * pk.nblocks;
