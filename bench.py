@@ -37,8 +37,9 @@ F16_PEAK_TFLOPS = 2500.0
 DOMINANT = "conv3x3_dma"
 
 
-def roofline(kernels):
-    """The kernel family with the most time in the timed region, against its bound."""
+def roofline(kernels, traffic=True):
+    """The kernel family with the most time in the timed region, against its bound. `traffic`:
+    attach the rocprofv3-measured bytes a launch, which are measured on the page pipeline only."""
     fam, k = max(kernels.items(), key=lambda kv: kv[1]["ms"])
     secs = k["ms"] / 1e3
     intensity = k["flops"] / max(k["bytes"], 1.0)
@@ -53,7 +54,7 @@ def roofline(kernels):
                "frac": achieved / HBM_PEAK_GBS}
     calls = max(k["calls"], 1)
     out.update({"kernel": fam, "calls": k["calls"], "avg_us": 1e3 * k["ms"] / calls,
-                "traffic": measured_traffic(fam),
+                "traffic": measured_traffic(fam) if traffic else None,
                 "algorithmic_bytes_per_launch": k["bytes"] / calls, "algorithmic_flops_per_launch": k["flops"] / calls,
                 # both views of the same launches: algorithmic bytes over HBM peak, algorithmic FLOPs
                 # over the dense f16 matrix-core peak
@@ -334,12 +335,29 @@ def _timed(ctx, fn, reps, warmup=3):
     return (time.perf_counter() - t) / reps
 
 
-def _kernel_summary(kernels, units):
+# The recurrence's floor a time step: a SIMD issues the 96 v_mfma_f32_16x16x32_f16 of its four
+# wavefronts (16 cycles each) at 2.4 GHz; the gate arithmetic and the step's barrier come on top.
+GRU_FLOOR_US = 96 * 16 / 2400.0
+
+
+def _gru_latency(k, steps):
+    """The recurrence as what bounds it, the latency of a time step's dependent chain, against
+    the matrix-core floor of a step (a bytes- or FLOP-rate fraction says nothing for it)."""
+    us = 1e3 * k["ms"] / max(k["calls"] * steps, 1)
+    secs = k["ms"] / 1e3
+    return {"bound": "latency", "achieved": us, "peak": GRU_FLOOR_US, "unit": "us/step", "frac": GRU_FLOOR_US / us,
+            "kernel": "gru", "calls": k["calls"], "avg_us": 1e3 * k["ms"] / max(k["calls"], 1), "steps_per_launch": steps,
+            "traffic": None, "frac_hbm": k["bytes"] / secs / (HBM_PEAK_GBS * 1e9),
+            "frac_mfma_f16": k["flops"] / secs / (F16_PEAK_TFLOPS * 1e12)}
+
+
+def _kernel_summary(kernels, units, gru_steps=0):
     """Per-family ms per unit, the dominant family, and its roofline (algorithmic work over its
-    summed launch time)."""
+    summed launch time; for the recurrence, time a step against its floor)."""
     top = max(kernels, key=lambda f: kernels[f]["ms"])
+    dom = _gru_latency(kernels[top], gru_steps) if top == "gru" and gru_steps else roofline({top: kernels[top]}, traffic=False)
     return {"kernels_ms": {f: round(k["ms"] / units, 4) for f, k in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])},
-            "dominant": roofline({top: kernels[top]})}
+            "dominant": dom}
 
 
 def config_figures(ctx, det, rec, reps=20):
@@ -366,7 +384,7 @@ def config_figures(ctx, det, rec, reps=20):
         "workload": "36 grey lines 64 x [200, 800], ocrs batching, CNN trunk + 2 x BiGRU(256) + 97-class head",
         "ms_per_batch": 1e3 * secs, "lines_per_sec": 36 / secs, "gru_steps": 2 * tmax,
         "us_per_gru_step": 1e3 * gru["ms"] / max(gru["calls"] * tmax, 1),
-        "gflop_per_batch": sum(k["flops"] for k in kern.values()) / 1e9, **_kernel_summary(kern, 1)}
+        "gflop_per_batch": sum(k["flops"] for k in kern.values()) / 1e9, **_kernel_summary(kern, 1, tmax)}
     # The detection U-Net on one [1, 1, 800, 600] grey image (host in, probabilities out).
     img = synth.det_input(0)
     secs = _timed(ctx, lambda: det.detect(img), reps)
