@@ -114,6 +114,35 @@ def test_recognition_batches_together_match_separate(recognizer):
         k0 += n
 
 
+@pytest.mark.parametrize("tied", [(7, 40, 96), (3, 60), (0, 1)])
+def test_recognition_argmax_ties(ctx, tied):
+    """Tied maxima at every step: output-layer columns made identical, with a bias well above
+    the others, give bit-identical logits, and the arg-max is the last tied index (the
+    reference's rule, ocr-bench.rs:67), also where the last class (96) is one of them and where
+    the tie sits in the first lanes of a row."""
+    import ocrhip
+    from oracle import onnx_read
+    m = onnx_read.load(synth.model_path("rec"))
+    weights = dict(m.weights)
+    w, b = weights["output.w"].copy(), weights["output.b"].copy()
+    for c in tied:
+        w[:, c] = w[:, tied[0]]
+        b[c] = 50.0
+    weights["output.w"], weights["output.b"] = w, b
+    nodes = [(n.op, n.inputs, n.outputs, n.attrs) for n in m.nodes]
+    rec = ocrhip.Recognizer(ctx, ocrhip.ParsedGraph(nodes, weights, m.ints, m.input, m.output))
+    batches, _, _ = synth.batch_lines(synth.rec_lines(12, seed=4, wmin=120, wmax=700))
+    print(f"arg-max ties {tied}: {[(n, wd) for _, n, wd in batches]}", flush=True)
+    logits, lens, best = rec.recognize(batches)
+    k0 = 0
+    for _, n, _ in batches:
+        for j in range(k0, k0 + n):
+            T = int(lens[j])
+            assert np.all(logits[:T, j][:, list(tied)] == logits[:T, j, tied[0]][:, None])
+            assert np.all(best[:T, j] == max(tied)), (tied, j)
+        k0 += n
+
+
 def test_recognition_empty_batch_is_an_error(recognizer):
     import ocrhip
     with pytest.raises(ocrhip.OcrError):
