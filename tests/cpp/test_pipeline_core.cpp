@@ -252,11 +252,23 @@ int run_case(const char *name, int npages, int merge, int det_batch, int workers
 }  // namespace
 
 int main() {
-    // The plan itself: passes of `merge` pages, groups inside passes, the first group smaller.
+    // The plan itself: passes of `merge` pages, groups inside passes, the first group smaller and
+    // the last pass's last group half of det_batch.
     {
         const PipelinePlan P = plan_pipeline(12, 6, 6);
         CHECK(P.passes() == 2 && P.pass_p0[1] == 6, "plan: passes");
-        CHECK(P.groups() == 3 && P.group_p0[0] == 0 && P.group_p0[1] == 2 && P.group_p0[2] == 6, "plan: groups");
+        CHECK(P.groups() == 4 && P.group_p0[0] == 0 && P.group_p0[1] == 2 && P.group_p0[2] == 6 &&
+                  P.group_p0[3] == 9 && P.group_p0[4] == 12,
+              "plan: groups");
+        // The bench's plan (merge 6, det_batch 4): [0], [1, 2], [3, 4, 5], [6 .. 9], [10, 11].
+        const PipelinePlan B = plan_pipeline(12, 6, 4);
+        const int bg[] = {0, 1, 3, 6, 10, 12};
+        CHECK(B.groups() == 5, "plan: bench groups %d", B.groups());
+        for (int g = 0; g <= 5 && g <= B.groups(); g++) CHECK(B.group_p0[size_t(g)] == bg[g], "plan: bench group %d", g);
+        // One pass: the first and the last rules both apply; two pages split one and one.
+        const PipelinePlan O = plan_pipeline(6, 6, 4);
+        CHECK(O.groups() == 3 && O.group_p0[1] == 1 && O.group_p0[2] == 4, "plan: one pass");
+        CHECK(plan_pipeline(2, 6, 4).groups() == 2 && plan_pipeline(1, 6, 4).groups() == 1, "plan: small runs");
         const PipelinePlan Q = plan_pipeline(7, 3, 2);
         for (int p = 0; p < 7; p++) {
             const int g = Q.group_of[size_t(p)];

@@ -32,7 +32,9 @@ namespace ocr {
 
 // Recognition passes of `merge` pages and detection groups of at most det_batch pages that
 // never straddle a pass. The first group is a third of det_batch (at least one page), so the
-// host starts on layouts while the GPU detects the rest of the first pass.
+// host starts on layouts while the GPU detects the rest of the first pass; the last pass's last
+// group is half of det_batch (at least one page), so that its other pages are detected and laid
+// out while those last pages still upload, and less detection and layout follows the last upload.
 struct PipelinePlan {
     int npages = 0;
     std::vector<int> pass_p0;   // pass r covers pages [pass_p0[r], pass_p0[r + 1])
@@ -59,8 +61,12 @@ inline PipelinePlan plan_pipeline(int npages, int merge, int det_batch) {
             P.group_p0.push_back(q0);
             q0 += first;
         }
-        const int ng = (r1 - q0 + det_batch - 1) / det_batch;
-        for (int k = 0; k < ng; k++) P.group_p0.push_back(q0 + int(long(r1 - q0) * k / ng));
+        const int last = std::max(1, det_batch / 2);
+        const int tail = (r + 1 == P.passes() && r1 - q0 > last) ? last : 0;
+        const int b1 = r1 - tail;
+        const int ng = (b1 - q0 + det_batch - 1) / det_batch;
+        for (int k = 0; k < ng; k++) P.group_p0.push_back(q0 + int(long(b1 - q0) * k / ng));
+        if (tail) P.group_p0.push_back(b1);
     }
     P.group_p0.push_back(P.npages);
     for (int g = 0; g < P.groups(); g++)
