@@ -224,13 +224,28 @@ def test_1x1_nchw_shapes(ctx, tmp_path, cin, cout, h, wd, exact):
 
 @pytest.mark.parametrize("n,cin,cout,h,wd,exact", [(4, 256, 32, 1, 109, True), (3, 512, 32, 1, 61, False),
                                                     (2, 64, 16, 20, 45, True), (2, 40, 24, 7, 130, False),
-                                                    (16, 64, 64, 1, 9, True)])
+                                                    (16, 64, 64, 1, 9, True), (2, 960, 64, 1, 49, True),
+                                                    (1, 480, 60, 1, 120, False), (5, 960, 48, 1, 37, False)])
 def test_3x3_nchw_shapes(ctx, tmp_path, n, cin, cout, h, wd, exact):
     # One-row inputs (the SVTR neck's convs: two of the three kernel rows read padding only, and
-    # few tiles make the wavefronts of a workgroup share the K steps) and two-dimensional ones.
+    # few tiles make the wavefronts of a workgroup share the K steps, up to 16 of them for a long
+    # K: 960 -> 64 and 960 -> 48) and two-dimensional ones.
     shape = (n, cin, h, wd)
     p = build(tmp_path, "c3", lambda g, x: g.add("Relu", [conv(g, x, cin, cout, k=3, exact=exact)]), shape)
     check(ctx, p, RNG.standard_normal(shape).astype(np.float32))
+
+
+@pytest.mark.parametrize("n,cin,cout,wd,exact", [(2, 1024, 64, 40, True), (3, 1024, 32, 21, False),
+                                                 (1, 1200, 16, 300, True)])
+def test_1x1_nchw_long_k(ctx, tmp_path, n, cin, cout, wd, exact):
+    # 1 x 1 convs with a long K over few pixels: the K steps shared by up to 16 wavefronts of a
+    # workgroup, their partial sums added in a fixed order.
+    import ocrhip
+    shape = (n, cin, 1, wd)
+    p = build(tmp_path, "c1k", lambda g, x: conv(g, x, cin, cout, k=1, exact=exact), shape)
+    x = RNG.standard_normal(shape).astype(np.float32)
+    got, _ = check(ctx, p, x)
+    np.testing.assert_array_equal(ocrhip.NdGraph(ctx, p).run(x), got)  # the same bits on a rerun
 
 
 def test_se_gate_and_gelu_residual_at_pp_shapes(ctx, tmp_path):

@@ -67,14 +67,16 @@ struct NchwParams {
     int flat;        // 1 x 1: pixels run over the flattened plane (h * w of them)
     int tiles_line;  // wavefront tiles along an output row (flat: along a plane)
     int tiles;       // all tiles of one channel block: lines x tiles_line
-    int ksplit;      // wavefronts sharing one tile's K steps (1, 2 or 4)
+    int ksplit;      // wavefronts sharing one tile's K steps (1, 2 or 4 of 4; 8 or 16 of 16)
 };
 
-template <int MT, int NT, bool LO>
-__global__ __launch_bounds__(256) void conv_nchw_kernel(NchwParams p) {
+// WPB wavefronts a workgroup: 4, or 16 for launches of few tiles and long K (up to 16 wavefronts
+// share one tile's K steps).
+template <int MT, int NT, bool LO, int WPB>
+__global__ __launch_bounds__(64 * WPB) void conv_nchw_kernel(NchwParams p) {
     extern __shared__ float s_red[];  // ksplit > 1: [wave][MT * NT * 4][64 lanes]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tile = blockIdx.x * (4 / p.ksplit) + wave / p.ksplit;
+    const int tile = blockIdx.x * (WPB / p.ksplit) + wave / p.ksplit;
     const int kpart = wave % p.ksplit;
     const int nb = blockIdx.y;
     const int r = lane & 15, g = lane >> 4;
@@ -237,17 +239,17 @@ __global__ __launch_bounds__(256) void conv_nchw_kernel(NchwParams p) {
     }
 }
 
-template <int MT, int NT>
+template <int MT, int NT, int WPB>
 void launch_nchw(const NchwParams &p, bool lo, dim3 grid, size_t lds, hipStream_t s) {
-    if (lo) hipLaunchKernelGGL((conv_nchw_kernel<MT, NT, true>), grid, dim3(256), lds, s, p);
-    else hipLaunchKernelGGL((conv_nchw_kernel<MT, NT, false>), grid, dim3(256), lds, s, p);
+    if (lo) hipLaunchKernelGGL((conv_nchw_kernel<MT, NT, true, WPB>), grid, dim3(64 * WPB), lds, s, p);
+    else hipLaunchKernelGGL((conv_nchw_kernel<MT, NT, false, WPB>), grid, dim3(64 * WPB), lds, s, p);
 }
 
-template <int MT>
+template <int MT, int WPB = 4>
 void launch_nchw_nt(const NchwParams &p, int nt, bool lo, dim3 grid, size_t lds, hipStream_t s) {
-    if (nt == 1) launch_nchw<MT, 1>(p, lo, grid, lds, s);
-    else if (nt == 2) launch_nchw<MT, 2>(p, lo, grid, lds, s);
-    else launch_nchw<MT, 4>(p, lo, grid, lds, s);
+    if (nt == 1) launch_nchw<MT, 1, WPB>(p, lo, grid, lds, s);
+    else if (nt == 2) launch_nchw<MT, 2, WPB>(p, lo, grid, lds, s);
+    else launch_nchw<MT, 4, WPB>(p, lo, grid, lds, s);
 }
 
 // ---- conv_dw ---------------------------------------------------------------------------------
@@ -629,16 +631,24 @@ bool nd_conv_nchw_mfma(const NdMfmaConvArgs &a, hipStream_t s) {
     }
     const int steps = pk.chunks * (p.flat ? 1 : std::min(pk.kh, a.h) * pk.kw);
     const double waves = tiles_of(mt) * pk.nblocks;
-    int ks = 1;
-    if (waves < 1024 && steps >= 8) ks = 4;
+    // K split across a workgroup's wavefronts when the launch has few tiles: each wavefront walks
+    // every ks-th K step, and the partial sums meet in LDS in a fixed order. A launch of under
+    // 1024 wavefronts with 16 or more K steps (the SVTR neck's 3 x 3 convs over one-row tensors,
+    // 90 steps, and its 1 x 1 convs) takes 16-wavefront workgroups and 8 or 16 parts (not for four
+    // n-tiles of inexact weights, whose operands do not fit 128 VGPRs): the PP-OCR recogniser's
+    // batch 1.12 -> 1.08 ms; with at most 4 parts the neck's 3 x 3 convs took 14-23 us each on a
+    // few hundred wavefronts, each walking 22 dependent steps. 8 steps as the bar measured 1.10 ms.
+    int ks = 1, wpb = 4;
+    if (waves < 1024 && steps >= 16 && (nt <= 2 || pk.exact)) ks = waves < 512 ? 16 : 8, wpb = 16, mt = 1;
+    else if (waves < 1024 && steps >= 8) ks = 4;
     else if (waves < 2048 && steps >= 4) ks = 2;
     if (ks > 1 && mt * nt > 8) mt = std::max(1, 8 / nt);
     p.tiles_line = int(std::ceil(lim / (16.0 * mt)));
     if (tiles_of(mt) > 0x3fffffff) return false;
     p.tiles = int(tiles_of(mt));
     p.ksplit = ks;
-    const size_t lds = ks > 1 ? size_t(4) * mt * nt * 4 * 64 * sizeof(float) : 0;
-    const int per_block = 4 / ks;
+    const size_t lds = ks > 1 ? size_t(wpb) * mt * nt * 4 * 64 * sizeof(float) : 0;
+    const int per_block = wpb / ks;
     dim3 grid(unsigned((p.tiles + per_block - 1) / per_block), unsigned(pk.nblocks));
     if (pk.nblocks > 65535) return false;
     const double flops = 2.0 * a.n * a.oh * a.ow * a.cout * a.cin * pk.kh * pk.kw;
@@ -646,7 +656,8 @@ bool nd_conv_nchw_mfma(const NdMfmaConvArgs &a, hipStream_t s) {
                          2.0 * double(pk.halves()) * (pk.exact ? 1 : 2);
     ProbeScope probe("nd_conv_nchw", s, flops, bytes);
     const bool lo = !pk.exact;
-    if (mt == 4) launch_nchw_nt<4>(p, nt, lo, grid, lds, s);
+    if (wpb == 16) launch_nchw_nt<1, 16>(p, nt, lo, grid, lds, s);
+    else if (mt == 4) launch_nchw_nt<4>(p, nt, lo, grid, lds, s);
     else if (mt == 2) launch_nchw_nt<2>(p, nt, lo, grid, lds, s);
     else launch_nchw_nt<1>(p, nt, lo, grid, lds, s);
     OCR_HIP(hipGetLastError());
