@@ -47,7 +47,7 @@ __device__ inline float ct_act(float v, int act) {
 
 template <int RT, int NT, bool LO>
 __global__ __launch_bounds__(256) void convt_rows_kernel(CtParams p) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wid = blockIdx.x * 4 + wave, nb = blockIdx.y;
     const int rt = wid / p.tsplit, tpart = wid - rt * p.tsplit;
     if (rt >= p.rtiles) return;

@@ -100,7 +100,7 @@ __global__ void affine_kernel(const float *x, const float *st, float *y, size_t 
 
 // ---- mean over a row (ReduceMean over trailing axes, GlobalAveragePool) -----------------------
 __global__ void reduce_mean_kernel(const float *x, float *y, size_t rows, int len) {
-    const size_t row = size_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
+    const size_t row = size_t(blockIdx.x) * (blockDim.x / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *r = x + row * size_t(len);
@@ -113,7 +113,7 @@ __global__ void reduce_mean_kernel(const float *x, float *y, size_t rows, int le
 // ---- LayerNorm over the last axis (the exporter's 9-node chain, fused as nd.rs:583-611) -------
 // (x - mean) / sqrt(var + eps) * gamma + beta, var the mean of squared deviations.
 __global__ void layer_norm_kernel(const float *x, const float *gb, float *y, size_t rows, int len, float eps) {
-    const size_t row = size_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
+    const size_t row = size_t(blockIdx.x) * (blockDim.x / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *r = x + row * size_t(len);
@@ -132,7 +132,7 @@ __global__ void layer_norm_kernel(const float *x, const float *gb, float *y, siz
 
 // ---- softmax over the last axis (nd.rs nd_softmax): one wavefront per row ---------------------
 __global__ void softmax_wave_kernel(const float *x, float *y, size_t rows, int len) {
-    const size_t row = size_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
+    const size_t row = size_t(blockIdx.x) * (blockDim.x / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *r = x + row * size_t(len);
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void argmax_first_kernel(const float *x, uint3
 // per row, its lanes reading neighbouring partials (coalesced), then a butterfly over the lanes.
 __global__ __launch_bounds__(256) void argmax_partials_kernel(const float2 *part, int parts, size_t rows,
                                                               uint32_t *best) {
-    const size_t row = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const size_t row = size_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     float bv = -INFINITY;

@@ -75,7 +75,7 @@ struct NchwParams {
 template <int MT, int NT, bool LO, int WPB>
 __global__ __launch_bounds__(64 * WPB) void conv_nchw_kernel(NchwParams p) {
     extern __shared__ float s_red[];  // ksplit > 1: [wave][MT * NT * 4][64 lanes]
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tile = blockIdx.x * (WPB / p.ksplit) + wave / p.ksplit;
     const int kpart = wave % p.ksplit;
     const int nb = blockIdx.y;
@@ -83,6 +83,7 @@ __global__ __launch_bounds__(64 * WPB) void conv_nchw_kernel(NchwParams p) {
     const bool live = tile < p.tiles;
     const int lim = p.flat ? p.h * p.w : p.w;  // input pixels along a tile's line
     const size_t plane = size_t(p.h) * p.w;
+    const unsigned planeu = unsigned(plane);
 
     floatx4 acc[MT][NT];
 #pragma unroll
@@ -125,20 +126,24 @@ __global__ __launch_bounds__(64 * WPB) void conv_nchw_kernel(NchwParams p) {
                 if constexpr (LO) wl[t] = p.wt_lo[wo + t * 64];
             }
             const int c0 = chunk * 32 + 8 * g;
+            // The row base is the same for the whole wavefront; a lane's inputs are 32-bit byte
+            // offsets from it (an image holds fewer than 2^30 values, checked by the host). The
+            // reads are unconditional, from a position inside the image (channel clamped to the
+            // last, pixel to the row's first), and the values outside are zeroed after.
             const float *xrow = xim + (p.flat ? 0 : size_t(oy + ky - p.pt) * p.w);
+            const bool full = c0 + 8 <= p.cin;
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 const int px = x0 + 16 * m + r + (p.flat ? 0 : kx - p.pl);
                 const bool in = px >= 0 && px < lim;
+                const unsigned pxc = in ? unsigned(px) : 0u;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const int ci = c0 + j;
-                    float t = 0.f;
-                    if (in && ci < p.cin) {
-                        t = xrow[size_t(ci) * plane + px];
-                        if (p.in_scale) t *= p.in_scale[size_t(img) * p.cin + ci];
-                    }
-                    xv[m][j] = t;
+                    const int ci = full ? c0 + j : min(c0 + j, p.cin - 1);
+                    const unsigned boff = (unsigned(ci) * planeu + pxc) * 4u;
+                    float t = *reinterpret_cast<const float *>(reinterpret_cast<const char *>(xrow) + boff);
+                    if (p.in_scale) t *= p.in_scale[size_t(img) * p.cin + ci];
+                    xv[m][j] = (in && (full || c0 + j < p.cin)) ? t : 0.f;
                 }
             }
         };
@@ -430,7 +435,7 @@ __device__ inline void rows_frag(const RowsParams &p, int row, int c0, half8 &hi
 // operands of KC input chunks are read at once, then the matrix work of those chunks.
 template <int RT, int NT, int KC, bool LO>
 __global__ __launch_bounds__(256) void gemm_rows_kernel(RowsParams p) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wid = blockIdx.x * 4 + wave, nb = blockIdx.y;
     const int rt = wid / p.tsplit, tpart = wid - rt * p.tsplit;
     if (rt >= p.rtiles) return;
@@ -505,7 +510,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(RowsParams p) {
 template <int RT, int KC, bool LO>
 __global__ __launch_bounds__(256) void gemm_rows_amax_kernel(RowsParams p) {
     constexpr int NT = 4;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wid = blockIdx.x * 4 + wave;
     const int rt = wid / p.parts, part = wid - rt * p.parts;
     if (rt >= p.rtiles) return;
@@ -615,6 +620,7 @@ bool nd_conv_nchw_mfma(const NdMfmaConvArgs &a, hipStream_t s) {
     p.act = a.act;
     // Stride 1: the output is the input size plus the pads less the kernel, checked by the caller.
     p.flat = (pk.kh == 1 && pk.kw == 1 && a.pt == 0 && a.pl == 0 && a.oh == a.h && a.ow == a.w) ? 1 : 0;
+    if (double(a.cin) * a.h * a.w >= 1073741824.0) return false;  // 32-bit byte offsets within an image
     const double lim = p.flat ? double(a.h) * a.w : double(a.ow);
     const double lines = p.flat ? double(a.n) : double(a.n) * a.oh;
     if (lim > 0x7fffffff || lines > 0x7fffffff) return false;
