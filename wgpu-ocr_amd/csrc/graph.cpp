@@ -586,9 +586,10 @@ void Graph::Exec::step(size_t i) {
             conv_transpose(a, y, s.w, s.b, s.kh, s.kw, s.sh, s.act, st);
             break;
         }
-        // Kernel = stride: one GEMM over the input pixels whose epilogue writes the phases
-        // (operands read straight into the matrix cores, no staging set-up to pay back).
-        if (s.allph.whi && s.kh == s.sh && s.kw == s.sw && !env_set("NOCONVTROWS") &&
+        // All phases as one GEMM over the output's s x s blocks whose epilogue writes the phases
+        // (operands read straight into the matrix cores, no staging set-up to pay back); a
+        // kernel past the stride adds taps (the detector's 2 x 3 upsampler: a 1 x 2 window).
+        if (s.allph.whi && s.sh == s.sw && !env_set("NOCONVTROWS") &&
             convt_rows(a, y, s.allph.whi, s.allph.wlo, s.allph.pk, s.b, s.sh, s.act, st))
             break;
         // Kernel = stride = 2 with few channels: a float32 pass with the weights in LDS.

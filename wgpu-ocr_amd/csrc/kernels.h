@@ -124,10 +124,11 @@ void conv_transpose(const Act &x, const Act &y, const float *w, const float *b, 
 // (the weights in LDS): one float32 pass at HBM speed. False (nothing launched) otherwise.
 bool convt_k2s2(const Act &x, const Act &y, const float *w, const float *b, int kh, int kw, int stride, int act,
                 hipStream_t s);
-// ConvTranspose with kernel = stride (s <= 4) as one matrix-core GEMM over the input pixels
-// (kernels/convt_rows.hip): pk packs the cin -> s s cout weights as a 1 x 1 conv (output column
-// k cout + c is channel c of phase k = py s + px), b the cout biases, act none / ReLU / Sigmoid.
-// False (nothing launched) for anything else.
+// ConvTranspose (stride s <= 4, kernel at least the stride) as one matrix-core GEMM over the
+// output's s x s blocks (kernels/convt_rows.hip): pk packs the cin -> s s cout weights as a
+// pk.kh x pk.kw conv over the input (tap (a, b) reads x[i - (kh - 1 - a)][j - (kw - 1 - b)];
+// output column k cout + c is channel c of phase k = py s + px; 1 x 1 when kernel = stride), b
+// the cout biases, act none / ReLU / Sigmoid. False (nothing launched) for anything else.
 bool convt_rows(const Act &x, const Act &y, const uint16_t *whi, const uint16_t *wlo, const ConvPack &pk,
                 const float *b, int stride, int act, hipStream_t st);
 void maxpool(const Act &x, const Act &y, int kh, int kw, hipStream_t s);
