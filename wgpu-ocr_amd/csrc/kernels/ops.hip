@@ -320,7 +320,11 @@ __global__ void mask_up_kernel(const MaskParams p) {
     uint32_t *bits = g.bits;
     const int lane = threadIdx.x & 63;
     // The wavefront's index, uniform (read from lane 0) so that everything derived from it is too.
-    const long wv = long(blockIdx.x) * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Blocks are renumbered so that each XCD takes a contiguous run (neighbouring row groups share
+    // map rows, which that XCD's L2 then serves once).
+    const int G = gridDim.x, q8 = G >> 3, r8 = G & 7, xb = blockIdx.x & 7;
+    const int blk = xb * q8 + min(xb, r8) + (blockIdx.x >> 3);
+    const long wv = long(blk) * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int chunks = (words + 2 * MJ - 1) / (2 * MJ), groups = (h + MR - 1) / MR;
     if (wv >= long(chunks) * groups) return;  // the whole wavefront
     const int rg = int(wv / chunks), wc = int(wv - long(rg) * chunks);
