@@ -90,8 +90,13 @@ struct Hooks final : PipelineHooks {
     int clock = 0;
     bool jitter, lookahead = false, interleave = false;
     int polled_groups = 0;  // groups a recognition pass queued between its stages
+    // Copies in flight: landed(g) holds land_us after stage(g) returned (at once when negative),
+    // never for group never_lands.
+    int land_us = -1, never_lands = -1;
+    std::vector<std::chrono::steady_clock::time_point> staged_time;
     Hooks(const PipelinePlan &plan, Faults faults, unsigned seed, bool jit)
         : P(plan), f(faults), rng(seed), jitter(jit) {
+        staged_time.resize(size_t(P.groups()));
         staged_at.assign(size_t(P.groups()), -1);
         detected_at = waited_at = staged_at;
         laid_at.assign(size_t(P.npages), -1);
@@ -115,10 +120,23 @@ struct Hooks final : PipelineHooks {
     void stage(int g) override {
         nap();
         if (g == f.stage) throw std::runtime_error("stage fault");
+        staged_time[size_t(g)] = std::chrono::steady_clock::now();
         staged_at[size_t(g)] = tick();
+    }
+    bool landed(int g) override {
+        if (g == never_lands) return false;
+        return land_us < 0 ||
+               std::chrono::steady_clock::now() - staged_time[size_t(g)] >= std::chrono::microseconds(land_us);
     }
     void detect(int g) override {
         CHECK(staged_at[size_t(g)] >= 0, "detect(%d) before its stage", g);
+        if (g == never_lands) {
+            const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() -
+                                                                        staged_time[size_t(g)]).count();
+            CHECK(ms >= 100.0, "detect(%d) %.1f ms after its stage, before its copy landed", g, ms);
+        } else {
+            CHECK(landed(g), "detect(%d) before its copy landed", g);
+        }
         nap();
         if (g == f.detect) throw std::runtime_error("detect fault");
         detected_at[size_t(g)] = tick();
@@ -205,9 +223,11 @@ std::vector<char> expected_failed(const PipelinePlan &P, const Faults &f) {
 }
 
 int run_case(const char *name, int npages, int merge, int det_batch, int workers, Faults f, unsigned seed,
-             bool jitter, bool lookahead = false, bool interleave = false) {
+             bool jitter, bool lookahead = false, bool interleave = false, int land_us = -1,
+             int never_lands = -1) {
     const PipelinePlan P = plan_pipeline(npages, merge, det_batch);
     Hooks H(P, f, seed, jitter);
+    H.land_us = land_us, H.never_lands = never_lands;
     H.lookahead = lookahead;
     H.interleave = interleave;
     std::vector<std::string> err;
@@ -370,6 +390,11 @@ int main() {
         st.stage = 5;
         run_case("interleave stage fault", 12, 3, 2, 2, st, 331, true, false, true);
     }
+    // Copies still in flight after stage() returns: a group is detected only once it has landed,
+    // and one that never lands is queued after 100 ms anyway (its bounded waits then report it).
+    for (unsigned seed = 400; seed < 410; seed++)
+        run_case("in flight", 12, 6, 4, 1 + int(seed % 3), none, seed, true, false, seed % 2 == 0, 400);
+    run_case("never lands", 12, 6, 4, 2, none, 410, true, false, true, 200, 3);
     if (failures) {
         std::fprintf(stderr, "%d check(s) failed\n", failures);
         return 1;

@@ -89,12 +89,14 @@ constexpr uint32_t block_ring(uint32_t b) {
            ((b >> 6) & 1u) << 5 | ((b >> 7) & 1u) << 6 | ((b >> 8) & 1u) << 7;
 }
 
-// Step (3.3) of the border following as a table: for a pixel's 3 x 3 block and the direction
-// dprev of the pixel it came from, the first set neighbour counter-clockwise after dprev (the
-// ring always holds dprev; entries where it does not are never read).
-struct NextDir {
+// Steps (3.3)-(3.4) of the border following as one table lookup: for a pixel's 3 x 3 block and
+// the direction dprev of the pixel it came from, the first set neighbour counter-clockwise after
+// dprev, given as the move there (dx + 1 in bits 0-1, dy + 1 in bits 2-3) and the direction from
+// that neighbour back to the pixel (bits 4-6), the next step's dprev. The ring always holds dprev;
+// entries where it does not are never read.
+struct BorderStep {
     uint8_t t[512 * 8];
-    NextDir() {
+    BorderStep() {
         for (uint32_t b = 0; b < 512; b++) {
             const uint32_t r = block_ring(b);
             for (int d = 0; d < 8; d++) {
@@ -104,69 +106,125 @@ struct NextDir {
                         n = (d + k) & 7;
                         break;
                     }
-                t[b * 8 + uint32_t(d)] = uint8_t(n);
+                t[b * 8 + uint32_t(d)] = uint8_t((DIR_X[n] + 1) | (DIR_Y[n] + 1) << 2 | ((n + 4) & 7) << 4);
             }
         }
     }
 };
-const NextDir NEXT_DIR;
+const BorderStep BORDER_STEP;
 
-// The outer border of the 8-connected component whose raster-first pixel is (x0, y0), as the
-// pixels Suzuki-Abe border following visits (steps 3.1-3.5: from the west neighbour clockwise to
-// the first set pixel, then from each pixel counter-clockwise after the one it came from), x, y
-// pairs in visiting order, starting at (x0, y0). A lone pixel is its own border.
-void trace_outer(const PaddedMask &m, int x0, int y0, std::vector<int32_t> &xy) {
-    xy.clear();
-    xy.push_back(x0), xy.push_back(y0);
-    const uint32_t b0 = m.block(x0, y0), r0 = block_ring(b0);
-    if (!r0) return;
-    int d1 = 4;
-    while (!((r0 >> d1) & 1u)) d1 = (d1 + 7) & 7;  // clockwise from the west
-    const int x1 = x0 + DIR_X[d1], y1 = y0 + DIR_Y[d1];
-    int x3 = x0, y3 = y0, dprev = d1;
-    uint32_t b = b0;
-    for (;;) {
-        const int d4 = NEXT_DIR.t[b * 8 + uint32_t(dprev)];
-        const int x4 = x3 + DIR_X[d4], y4 = y3 + DIR_Y[d4];
-        if (x4 == x0 && y4 == y0 && x3 == x1 && y3 == y1) return;
-        dprev = (d4 + 4) & 7;
-        x3 = x4, y3 = y4;
-        xy.push_back(x3), xy.push_back(y3);
-        b = m.block(x3, y3);
+// The outer borders of the 8-connected components seeds[lo, hi), each given by its raster-first
+// pixel (fx, fy): the pixels Suzuki-Abe border following visits (steps 3.1-3.5: from the west
+// neighbour clockwise to the first set pixel, then from each pixel counter-clockwise after the
+// one it came from), x, y pairs in visiting order, starting at the first pixel; a lone pixel is
+// its own border. done(i, xy) gets component i's border as it closes (in no fixed order; xy is
+// reused afterwards). TRACE_LANES borders are followed side by side on the calling thread: each
+// is a chain of dependent loads, and independent chains interleaved keep the core busy.
+constexpr int TRACE_LANES = 4;
+template <class Seeds, class F>
+void trace_outer_many(const PaddedMask &m, const Seeds &seeds, int lo, int hi,
+                      std::vector<int32_t> (&buf)[TRACE_LANES], F &&done) {
+    struct Lane {
+        int i, x0, y0, x1, y1, x, y;
+        uint32_t dprev, b;
+        std::vector<int32_t> *xy;
+    };
+    Lane lane[TRACE_LANES];
+    int nl = 0, next = lo;
+    // Puts the next component with more than one border pixel on l (the others are done at
+    // once); false when none is left.
+    auto start = [&](Lane &l, std::vector<int32_t> *xy) {
+        while (next < hi) {
+            const int i = next++;
+            const int x0 = seeds[size_t(i)].fx, y0 = seeds[size_t(i)].fy;
+            xy->clear();
+            xy->push_back(x0), xy->push_back(y0);
+            const uint32_t b0 = m.block(x0, y0), r0 = block_ring(b0);
+            if (!r0) {
+                done(i, *xy);
+                continue;
+            }
+            int d1 = 4;
+            while (!((r0 >> d1) & 1u)) d1 = (d1 + 7) & 7;  // clockwise from the west
+            l = Lane{i, x0, y0, x0 + DIR_X[d1], y0 + DIR_Y[d1], x0, y0, uint32_t(d1), b0, xy};
+            return true;
+        }
+        return false;
+    };
+    for (int k = 0; k < TRACE_LANES; k++)
+        if (start(lane[nl], &buf[k])) nl++;
+    while (nl > 0) {
+        for (int k = 0; k < nl; k++) {
+            Lane &l = lane[k];
+            const uint32_t e = BORDER_STEP.t[l.b * 8 + l.dprev];
+            const int x = l.x + int(e & 3u) - 1, y = l.y + int((e >> 2) & 3u) - 1;
+            if (x == l.x0 && y == l.y0 && l.x == l.x1 && l.y == l.y1) {
+                // Back at the start, about to take the first step again: the border is closed.
+                done(l.i, *l.xy);
+                if (!start(l, l.xy)) lane[k--] = lane[--nl];
+                continue;
+            }
+            l.dprev = e >> 4, l.x = x, l.y = y;
+            l.xy->push_back(x), l.xy->push_back(y);
+            l.b = m.block(x, y);
+        }
     }
 }
 
 // Squared distances from the points k in (s, e) (coordinates px, py) to the segment between
 // points s and e (from point s when the segment is a point), into d2[k]: the float operations of
-// the distance itself up to its square root, so sqrt(d2[k]) is that distance bit for bit.
-// Built for AVX2 and for the baseline ISA (the loader picks one); the same IEEE operations either
-// way, no fused multiply-adds. (Host code only: the device pass of this file compiles nothing.)
+// the distance itself up to its square root, so sqrt(d2[k]) is that distance bit for bit. Eight
+// points at a time, the last block running up to 7 points past e (px, py and d2 hold them; their
+// lanes are left out of the maximum). Returns the largest d2 of (s, e), 0 when it is empty (max is
+// exact in any order). Built for AVX2 and for the baseline ISA (the loader picks one); the same
+// IEEE operations either way, no fused multiply-adds. (Host code only: the device pass of this
+// file compiles nothing.)
 #if defined(__HIP_DEVICE_COMPILE__)
 #define OCR_HOST_CLONES
 #else
 #define OCR_HOST_CLONES __attribute__((target_clones("avx2", "default")))
 #endif
+typedef float F8 __attribute__((vector_size(32)));
+typedef int I8 __attribute__((vector_size(32)));
+constexpr int SEG_PAD = 8;  // readable floats past the last point of px, py and d2
+
 OCR_HOST_CLONES
-void seg_dist2(const float *__restrict px, const float *__restrict py, int s, int e, float *__restrict d2) {
+float seg_dist2_max(const float *__restrict px, const float *__restrict py, int s, int e, float *__restrict d2) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
     const float ax = px[s], ay = py[s], bx = px[e], by = py[e];
-    if (ax == bx && ay == by) {
-        for (int k = s + 1; k < e; k++) {
-            const float dx = px[k] - ax, dy = py[k] - ay;
-            d2[k] = dx * dx + dy * dy;
-        }
-        return;
-    }
+    const int k0 = s + 1, cnt = e - s - 1;
+    const F8 zero = {}, vax = ax + zero, vay = ay + zero, vbx = bx + zero, vby = by + zero;
+    const I8 lane = {0, 1, 2, 3, 4, 5, 6, 7};
+    const bool point = ax == bx && ay == by;
     const float abx = bx - ax, aby = by - ay, den = abx * abx + aby * aby;
-    // Branch-free (both ends and the projection computed, then selected) so it vectorises.
-    for (int k = s + 1; k < e; k++) {
-        const float acx = px[k] - ax, acy = py[k] - ay;
-        const float t = (acx * abx + acy * aby) / den;
-        float qx = ax + abx * t, qy = ay + aby * t;
-        qx = t >= 1.f ? bx : qx, qy = t >= 1.f ? by : qy;
-        qx = t <= 0.f ? ax : qx, qy = t <= 0.f ? ay : qy;
-        const float dx = px[k] - qx, dy = py[k] - qy;
-        d2[k] = dx * dx + dy * dy;
+    const F8 vabx = abx + zero, vaby = aby + zero, vden = den + zero;
+    F8 mx = zero;
+    for (int i = 0; i < cnt; i += 8) {
+        F8 x, y, d;
+        std::memcpy(&x, px + k0 + i, sizeof x);
+        std::memcpy(&y, py + k0 + i, sizeof y);
+        if (point) {
+            const F8 dx = x - vax, dy = y - vay;
+            d = dx * dx + dy * dy;
+        } else {
+            // Both ends and the projection computed, then selected.
+            const F8 acx = x - vax, acy = y - vay;
+            const F8 t = (acx * vabx + acy * vaby) / vden;
+            F8 qx = vax + vabx * t, qy = vay + vaby * t;
+            qx = t >= 1.f ? vbx : qx, qy = t >= 1.f ? vby : qy;
+            qx = t <= 0.f ? vax : qx, qy = t <= 0.f ? vay : qy;
+            const F8 dx = x - qx, dy = y - qy;
+            d = dx * dx + dy * dy;
+        }
+        std::memcpy(d2 + k0 + i, &d, sizeof d);
+        const F8 dm = lane < cnt - i ? d : zero;
+        mx = dm > mx ? dm : mx;
     }
+    float m = mx[0];
+    for (int j = 1; j < 8; j++) m = mx[j] > m ? mx[j] : m;
+    return m;
 }
 
 // Scratch of simplify_closed, kept per thread.
@@ -179,17 +237,19 @@ struct SimplifyScratch {
 // simplify_polygon(points, eps): Ramer-Douglas-Peucker on the closed polygon (the first point
 // appended, then dropped): a run splits at its farthest inner point from the segment between its
 // ends (distance to the segment, from its first point when it is a point; the last of equally
-// far points) when that is farther than eps. The farthest point is found on squared distances,
-// then the last point whose distance equals the largest one is picked by the distances
-// themselves (squared distances a few ulps apart can share a square root).
+// far points) when that is farther than eps. The largest distance is the root of the largest
+// squared one; the points as far as it are those whose squared distance has that same root,
+// which (sqrt being monotonic and correctly rounded) are the ones at or above the smallest float
+// with that root: the split is the last of them.
 void simplify_closed(const std::vector<int32_t> &xy, float eps, std::vector<Pt> &out, SimplifyScratch &S) {
     const int n = int(xy.size() / 2);
     out.clear();
     if (n == 0) return;
-    S.px.resize(size_t(n) + 1), S.py.resize(size_t(n) + 1), S.d2.resize(size_t(n) + 1);
+    const size_t len = size_t(n) + 1 + SEG_PAD;
+    S.px.resize(len), S.py.resize(len), S.d2.resize(len);
     float *px = S.px.data(), *py = S.py.data(), *d2 = S.d2.data();
     for (int k = 0; k < n; k++) px[k] = float(xy[size_t(2 * k)]), py[k] = float(xy[size_t(2 * k + 1)]);
-    px[n] = px[0], py[n] = py[0];
+    for (size_t k = size_t(n); k < len; k++) px[k] = px[0], py[k] = py[0];
     S.keep.assign(size_t(n) + 1, 0);
     S.stack.assign(1, {0, n});
     while (!S.stack.empty()) {
@@ -197,26 +257,36 @@ void simplify_closed(const std::vector<int32_t> &xy, float eps, std::vector<Pt> 
         S.stack.pop_back();
         S.keep[size_t(s)] = S.keep[size_t(e)] = 1;
         if (e - s < 2) continue;
-        seg_dist2(px, py, s, e, d2);
-        // The largest squared distance: 8 running maxima (max is exact in any order).
-        float mx[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        int k = s + 1;
-        for (; k + 8 <= e; k += 8)
-            for (int j = 0; j < 8; j++) mx[j] = d2[k + j] > mx[j] ? d2[k + j] : mx[j];
-        for (; k < e; k++) mx[0] = d2[k] > mx[0] ? d2[k] : mx[0];
-        float m2 = mx[0];
-        for (int j = 1; j < 8; j++) m2 = mx[j] > m2 ? mx[j] : m2;
-        const float dmax = std::sqrt(m2), near = m2 - m2 * 1e-5f;
-        int best = e - 1;
-        for (int q = e - 1; q > s; q--)
-            if (d2[q] >= near && std::sqrt(d2[q]) == dmax) {
-                best = q;
-                break;
-            }
-        if (dmax > eps) {
-            S.stack.push_back({best, e});
-            S.stack.push_back({s, best});
+        const float m2 = seg_dist2_max(px, py, s, e, d2);
+        const float dmax = std::sqrt(m2);
+        if (!(dmax > eps)) continue;
+        // The smallest float whose root is dmax: step down one ulp at a time (a root's preimage
+        // spans a few floats); below a positive float lies its bit pattern less one.
+        float lo = m2;
+        while (lo > 0.f) {
+            uint32_t u;
+            std::memcpy(&u, &lo, 4);
+            float below;
+            u -= 1;
+            std::memcpy(&below, &u, 4);
+            if (std::sqrt(below) != dmax) break;
+            lo = below;
         }
+        // The last point at or above lo: eight at a time from the end while every lane is below.
+        // One exists (the largest), so the scan stops inside (s, e).
+        int best = e - 1;
+        while (best - 7 > s) {
+            F8 v;
+            std::memcpy(&v, d2 + best - 7, sizeof v);
+            const I8 hit = v >= lo;
+            int any = 0;
+            for (int j = 0; j < 8; j++) any |= hit[j];
+            if (any) break;
+            best -= 8;
+        }
+        while (d2[best] < lo) best--;
+        S.stack.push_back({best, e});
+        S.stack.push_back({s, best});
     }
     for (int k = 0; k < n; k++)
         if (S.keep[size_t(k)]) out.push_back({px[k], py[k]});
@@ -437,22 +507,25 @@ std::vector<Pt> merge_rows(std::vector<Pt> all) {
 
 thread_local int t_loop_prio = 0;
 
-// fn(i) for i in [0, n): on the calling thread alone when threads is 1, else in contiguous
-// chunks (up to 4 per thread, for balance) on the caller and the shared loop pool, at this
-// thread's loop priority.
-template <class F> void parallel_for(int n, int threads, F fn) {
+// fn(lo, hi) over contiguous ranges covering [0, n): the whole range on the calling thread when
+// threads is 1, else up to 4 ranges a thread (for balance) on the caller and the shared loop pool,
+// at this thread's loop priority.
+template <class F> void parallel_ranges(int n, int threads, F fn) {
     threads = std::max(1, std::min(threads, n));
     if (threads == 1) {
-        for (int i = 0; i < n; i++) fn(i);
+        if (n > 0) fn(0, n);
         return;
     }
     const int chunks = std::min(n, 4 * threads);
     LoopPool::get().run(
-        chunks,
-        [&](int t) {
-            for (int i = int(long(n) * t / chunks); i < int(long(n) * (t + 1) / chunks); i++) fn(i);
-        },
-        t_loop_prio);
+        chunks, [&](int t) { fn(int(long(n) * t / chunks), int(long(n) * (t + 1) / chunks)); }, t_loop_prio);
+}
+
+// fn(i) for i in [0, n), as parallel_ranges cuts it.
+template <class F> void parallel_for(int n, int threads, F fn) {
+    parallel_ranges(n, threads, [&](int lo, int hi) {
+        for (int i = lo; i < hi; i++) fn(i);
+    });
 }
 
 }  // namespace
@@ -585,14 +658,15 @@ void external_rects(const uint32_t *bits, int w, int h, const std::vector<Seed> 
     std::vector<std::vector<int32_t>> chains(static_cast<size_t>(n));
     rects.assign(size_t(n), RRect{});
     ok.assign(size_t(n), 1);
-    parallel_for(n, threads, [&](int i) {
-        thread_local std::vector<int32_t> chain;
+    parallel_ranges(n, threads, [&](int lo, int hi) {
+        thread_local std::vector<int32_t> buf[TRACE_LANES];
         thread_local std::vector<Pt> simp, hull;
         thread_local SimplifyScratch scratch;
-        std::vector<int32_t> &xy = encloser[size_t(i)] ? chains[size_t(i)] : chain;
-        trace_outer(m, seeds[size_t(i)].fx, seeds[size_t(i)].fy, xy);
-        simplify_closed(xy, 2.f, simp, scratch);
-        if (!min_area_rect(simp, hull, rects[size_t(i)])) ok[size_t(i)] = 0;
+        trace_outer_many(m, seeds, lo, hi, buf, [&](int i, const std::vector<int32_t> &xy) {
+            if (encloser[size_t(i)]) chains[size_t(i)] = xy;
+            simplify_closed(xy, 2.f, simp, scratch);
+            if (!min_area_rect(simp, hull, rects[size_t(i)])) ok[size_t(i)] = 0;
+        });
     });
     // A component inside a hole of another one is left out (an outer border winds around the
     // background pixel west of its first pixel).

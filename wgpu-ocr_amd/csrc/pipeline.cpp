@@ -284,6 +284,11 @@ struct PipelineRun final : PipelineHooks {
         mark("stage " + std::to_string(g) + " queued");
     }
 
+    bool landed(int g) override {
+        const hipEvent_t e = up_ev[size_t(g)];
+        return !e || hipEventQuery(e) != hipErrorNotReady;
+    }
+
     // Detection of a group's pages, the labelling of their masks, and the copies of masks and
     // labels to the host (on the copy stream).
     void detect(int g) override {

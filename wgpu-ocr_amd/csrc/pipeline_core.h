@@ -78,14 +78,18 @@ class PipelineHooks {
   public:
     virtual ~PipelineHooks() = default;
     virtual void stage(int g) = 0;
+    // Whether staged group g's pages have reached the device (stage() may return with the copy
+    // still in flight). A recognition pass that is ready goes ahead of a group that has not: the
+    // group would only hold the stream until it lands.
+    virtual bool landed(int) { return true; }
     virtual void detect(int g) = 0;
     virtual void detect_wait(int g) = 0;
     virtual void layout(int p) = 0;
     // ok[p - first page of r]: page p has a layout (pages without one are left out).
     virtual void recognize(int r, const std::vector<char> &ok) = 0;
     virtual void decode(int r, bool last) = 0;
-    // Set by run_schedule while it runs (main thread only): queues every detection group that is
-    // staged and not yet queued, returns whether it queued any. A recognition pass may call it
+    // Set by run_schedule while it runs (main thread only): queues, in order, the detection groups
+    // that are staged, landed and not yet queued, returns whether it queued any. A recognition pass may call it
     // between its stages, so that pages which reach the device meanwhile are detected after the
     // stage in flight rather than after the whole pass.
     std::function<bool()> poll_detections;
@@ -242,7 +246,7 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
             int g;
             {
                 std::lock_guard<std::mutex> lk(mu);
-                if (next_det >= ng || staged <= next_det) return any;
+                if (next_det >= ng || staged <= next_det || !H.landed(next_det)) return any;
                 g = next_det++;
                 if (group_failed[size_t(g)]) {
                     queued = next_det;
@@ -273,11 +277,31 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
                 const int q = P.pass_p0[size_t(std::min(r + (lookahead ? 2 : 1), nr))];
                 return q >= np ? ng : P.group_of[size_t(q)];
             };
-            cv.wait(lk, [&] {
-                return (next_det < ng && staged > next_det) ||
-                       (pass_ready(next_rec) && next_det >= groups_before(next_rec));
-            });
-            if (next_det < ng && staged > next_det) {
+            // A staged group goes first once it has landed; a ready pass goes ahead of a group
+            // still in flight. While a group is in flight and no pass is ready, look again every
+            // 20 us, for at most 100 ms (then the group is queued anyway, and the stream's own
+            // bounded waits report a copy that never ends).
+            auto staged_next = [&] { return next_det < ng && staged > next_det; };
+            auto rec_now = [&] { return pass_ready(next_rec) && next_det >= groups_before(next_rec); };
+            bool take_det = false;
+            const auto t_in = clk::now();
+            for (;;) {
+                if (staged_next() && (H.landed(next_det) || clk::now() - t_in > std::chrono::milliseconds(100))) {
+                    take_det = true;
+                    break;
+                }
+                if (rec_now()) break;
+                if (staged_next()) {
+                    // A plain sleep (a timed condition wait on the steady clock is a call that
+                    // thread checkers do not follow).
+                    lk.unlock();
+                    std::this_thread::sleep_for(std::chrono::microseconds(20));
+                    lk.lock();
+                } else {
+                    cv.wait(lk, [&] { return staged_next() || rec_now(); });
+                }
+            }
+            if (take_det) {
                 do_det = next_det++;
                 if (group_failed[size_t(do_det)]) {
                     queued = next_det;  // nothing to queue, nothing to wait for
