@@ -445,7 +445,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--pages", type=int, default=12)
     ap.add_argument("--merge", type=int, default=6)
-    ap.add_argument("--det-batch", type=int, default=4, help="pages per detection pass")
+    ap.add_argument("--det-batch", type=int, default=3, help="pages per detection pass")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-pp", action="store_true", help="skip the PP-OCR pipeline measurement")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration figures")

@@ -250,7 +250,7 @@ int ocr_layout_batch(ocr_layout *lay, uint32_t i, uint32_t *width, uint32_t *lin
 
 /* merge: pages per recognition pass (MERGE); relv / relend: line padding (RELV, RELEND);
  * thr: detection threshold; threads: host worker threads (0 = up to 16); det_batch: pages per
- * detection pass. Zeros take the defaults 2, 0.15, 0.1, 0.5, 0, 4.
+ * detection pass. Zeros take the defaults 2, 0.15, 0.1, 0.5, 0, 3.
  * label_runs / label_comps / label_slots: capacities of the GPU labelling of a page's mask
  * (0 = 131072 runs, 16384 components, 65536 component rows). A page that needs more, or is
  * wider or taller than 65536 pixels, is labelled on the host from its mask bits instead, with

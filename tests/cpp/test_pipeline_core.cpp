@@ -272,30 +272,50 @@ int run_case(const char *name, int npages, int merge, int det_batch, int workers
 }  // namespace
 
 int main() {
-    // The plan itself: passes of `merge` pages, groups inside passes, the first group smaller and
-    // the last pass's last group half of det_batch.
+    // The plan itself: passes of at most `merge` pages, the first of ceil(merge / 2) when there
+    // are more, groups inside passes, the first group smaller and the last pass's last group half
+    // of det_batch rounded up.
     {
         const PipelinePlan P = plan_pipeline(12, 6, 6);
-        CHECK(P.passes() == 2 && P.pass_p0[1] == 6, "plan: passes");
-        CHECK(P.groups() == 4 && P.group_p0[0] == 0 && P.group_p0[1] == 2 && P.group_p0[2] == 6 &&
-                  P.group_p0[3] == 9 && P.group_p0[4] == 12,
+        CHECK(P.passes() == 3 && P.pass_p0[1] == 3 && P.pass_p0[2] == 7 && P.pass_p0[3] == 12, "plan: passes");
+        CHECK(P.groups() == 5 && P.group_p0[0] == 0 && P.group_p0[1] == 2 && P.group_p0[2] == 3 &&
+                  P.group_p0[3] == 7 && P.group_p0[4] == 9 && P.group_p0[5] == 12,
               "plan: groups");
-        // The bench's plan (merge 6, det_batch 4): [0], [1, 2], [3, 4, 5], [6 .. 9], [10, 11].
-        const PipelinePlan B = plan_pipeline(12, 6, 4);
-        const int bg[] = {0, 1, 3, 6, 10, 12};
-        CHECK(B.groups() == 5, "plan: bench groups %d", B.groups());
-        for (int g = 0; g <= 5 && g <= B.groups(); g++) CHECK(B.group_p0[size_t(g)] == bg[g], "plan: bench group %d", g);
-        // One pass: the first and the last rules both apply; two pages split one and one.
+        // The bench's plan (merge 6, det_batch 3): passes [0, 3), [3, 7), [7, 12); groups [0],
+        // [1, 2], [3, 4], [5, 6], [7 .. 9], [10, 11].
+        const PipelinePlan B = plan_pipeline(12, 6, 3);
+        const int bg[] = {0, 1, 3, 5, 7, 10, 12};
+        CHECK(B.groups() == 6, "plan: bench groups %d", B.groups());
+        for (int g = 0; g <= 6 && g <= B.groups(); g++) CHECK(B.group_p0[size_t(g)] == bg[g], "plan: bench group %d", g);
+        // Passes share the pages after the first evenly: 3, then 5, 5, 5, 6 for 24 pages.
+        const PipelinePlan L = plan_pipeline(24, 6, 3);
+        const int lp[] = {0, 3, 8, 13, 18, 24};
+        CHECK(L.passes() == 5, "plan: 24 pages, %d passes", L.passes());
+        for (int r = 0; r <= 5 && r <= L.passes(); r++) CHECK(L.pass_p0[size_t(r)] == lp[r], "plan: 24 pages, pass %d", r);
+        // One pass (no more pages than merge): the first and the last rules both apply; two pages
+        // split one and one.
         const PipelinePlan O = plan_pipeline(6, 6, 4);
-        CHECK(O.groups() == 3 && O.group_p0[1] == 1 && O.group_p0[2] == 4, "plan: one pass");
+        CHECK(O.passes() == 1 && O.groups() == 3 && O.group_p0[1] == 1 && O.group_p0[2] == 4, "plan: one pass");
         CHECK(plan_pipeline(2, 6, 4).groups() == 2 && plan_pipeline(1, 6, 4).groups() == 1, "plan: small runs");
-        const PipelinePlan Q = plan_pipeline(7, 3, 2);
-        for (int p = 0; p < 7; p++) {
-            const int g = Q.group_of[size_t(p)];
-            CHECK(Q.pass_of[size_t(Q.group_p0[size_t(g)])] == Q.pass_of[size_t(Q.group_p0[size_t(g) + 1] - 1)],
-                  "plan: group %d straddles a pass", g);
-            CHECK(Q.group_p0[size_t(g) + 1] - Q.group_p0[size_t(g)] <= 2, "plan: group %d larger than det_batch", g);
-        }
+        CHECK(plan_pipeline(5, 1, 4).passes() == 5, "plan: merge 1");
+        for (int n = 1; n <= 40; n++)
+            for (int merge = 1; merge <= 8; merge++)
+                for (int db = 1; db <= 6; db++) {
+                    const PipelinePlan Q = plan_pipeline(n, merge, db);
+                    CHECK(Q.pass_p0.front() == 0 && Q.pass_p0.back() == n && Q.group_p0.front() == 0 &&
+                              Q.group_p0.back() == n,
+                          "plan (%d, %d, %d): ends", n, merge, db);
+                    for (int r = 0; r < Q.passes(); r++) {
+                        const int len = Q.pass_p0[size_t(r) + 1] - Q.pass_p0[size_t(r)];
+                        CHECK(len >= 1 && len <= merge, "plan (%d, %d, %d): pass %d of %d pages", n, merge, db, r, len);
+                    }
+                    for (int g = 0; g < Q.groups(); g++) {
+                        const int a = Q.group_p0[size_t(g)], b = Q.group_p0[size_t(g) + 1];
+                        CHECK(b > a && b - a <= db, "plan (%d, %d, %d): group %d of %d pages", n, merge, db, g, b - a);
+                        CHECK(Q.pass_of[size_t(a)] == Q.pass_of[size_t(b - 1)], "plan (%d, %d, %d): group %d straddles a pass",
+                              n, merge, db, g);
+                    }
+                }
         CHECK(plan_pipeline(0, 2, 4).passes() == 0, "plan: no pages");
     }
     // The bounded wait itself: it returns once ready() holds, passes ready()'s own errors through,

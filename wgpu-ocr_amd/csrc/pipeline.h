@@ -17,7 +17,7 @@ struct PipelineOpts {
     float relend = 0.1f;  // line padding at the ends (RELEND)
     float thr = 0.5f;     // detection threshold
     int threads = 0;      // host worker threads (0: hardware concurrency, at most 16)
-    int det_batch = 4;    // pages per detection pass
+    int det_batch = 3;    // pages per detection pass
     bool lookahead = true;  // a recognition pass waits for the next pass's detections to be queued
     // Capacities of the GPU labelling of a page's mask (0: 2^17 runs, 16384 components, 65536
     // row slots); a page that needs more, or is wider or taller than 65536 pixels, is labelled

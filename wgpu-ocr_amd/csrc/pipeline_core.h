@@ -30,11 +30,14 @@
 
 namespace ocr {
 
-// Recognition passes of `merge` pages and detection groups of at most det_batch pages that
-// never straddle a pass. The first group is a third of det_batch (at least one page), so the
-// host starts on layouts while the GPU detects the rest of the first pass; the last pass's last
-// group is half of det_batch (at least one page), so that its other pages are detected and laid
-// out while those last pages still upload, and less detection and layout follows the last upload.
+// Recognition passes of at most `merge` pages, and detection groups of at most det_batch pages
+// that never straddle a pass. With more than `merge` pages the first pass holds ceil(merge / 2)
+// and the others share the rest evenly: the first pass is laid out and recognised while later
+// pages still upload, where a full one would leave the GPU idle until more pages had arrived.
+// The first group is a third of det_batch (at least one page), so the host starts on layouts
+// while the GPU detects the rest of the first pass; the last pass's last group is half of
+// det_batch rounded up, so that its other pages are detected and laid out while those last pages
+// still upload, and less detection and layout follows the last upload.
 struct PipelinePlan {
     int npages = 0;
     std::vector<int> pass_p0;   // pass r covers pages [pass_p0[r], pass_p0[r + 1])
@@ -48,7 +51,11 @@ inline PipelinePlan plan_pipeline(int npages, int merge, int det_batch) {
     PipelinePlan P;
     P.npages = std::max(npages, 0);
     merge = std::max(merge, 1), det_batch = std::max(det_batch, 1);
-    for (int p = 0; p < P.npages; p += merge) P.pass_p0.push_back(p);
+    if (P.npages > 0) P.pass_p0.push_back(0);
+    if (P.npages > merge) {
+        const int first = (merge + 1) / 2, rest = P.npages - first, nr = (rest + merge - 1) / merge;
+        for (int k = 0; k < nr; k++) P.pass_p0.push_back(first + int(long(rest) * k / nr));
+    }
     P.pass_p0.push_back(P.npages);
     P.group_of.assign(size_t(P.npages), 0);
     P.pass_of.assign(size_t(P.npages), 0);
@@ -61,7 +68,7 @@ inline PipelinePlan plan_pipeline(int npages, int merge, int det_batch) {
             P.group_p0.push_back(q0);
             q0 += first;
         }
-        const int last = std::max(1, det_batch / 2);
+        const int last = std::max(1, (det_batch + 1) / 2);
         const int tail = (r + 1 == P.passes() && r1 - q0 > last) ? last : 0;
         const int b1 = r1 - tail;
         const int ng = (b1 - q0 + det_batch - 1) / det_batch;

@@ -697,7 +697,7 @@ class Pipeline:
     """The whole-page pipeline (ocr-bench.rs:133-310, 458-585)."""
 
     def __init__(self, det: Detector, rec: Recognizer, merge=2, relv=0.15, relend=0.1, thr=0.5, threads=0,
-                 det_batch=4, label_runs=0, label_comps=0, label_slots=0):
+                 det_batch=3, label_runs=0, label_comps=0, label_slots=0):
         self.ctx = det.ctx
         self._keep = (det, rec)
         opts = ocr_pipeline_opts(merge, relv, relend, thr, threads, det_batch, label_runs, label_comps, label_slots)
