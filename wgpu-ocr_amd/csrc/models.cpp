@@ -181,7 +181,7 @@ Recognizer::Dims Recognizer::dims(const Batch *batches, int count) const {
 }
 
 void Recognizer::recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens,
-                                  const std::function<void()> &between) {
+                                  const std::function<void()> &between, hipStream_t gru_stream) {
     const hipStream_t st = ctx_.stream();
     const Dims d = dims(batches, count);
     if (d.ntot == 0) return;
@@ -255,7 +255,41 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     DBuf Y[2] = {DBuf(&ctx_, size_t(M) * 512 * sizeof(float)), DBuf(&ctx_, size_t(M) * 512 * sizeof(float))};
     const float *in = X.as<float>();
     int in_c = 256;
+    // With a stream for the recurrences: each waits for its projection, and the context's stream
+    // waits for it (join) before the next projection reads its output. Every buffer it touches is
+    // released on the context's stream after the last join, so none is reused under it.
+    const hipStream_t gs = gru_stream ? gru_stream : st;
+    hipEvent_t join = nullptr;
+    auto fork = [&]() {
+        if (gs == st) return;
+        hipEvent_t e = nullptr;
+        OCR_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        OCR_HIP(hipEventRecord(e, st));
+        OCR_HIP(hipStreamWaitEvent(gs, e, 0));
+        OCR_HIP(hipEventDestroy(e));  // the wait holds what it needs
+    };
+    auto join_back = [&]() {
+        if (!join) return;
+        OCR_HIP(hipStreamWaitEvent(st, join, 0));
+        OCR_HIP(hipEventDestroy(join));
+        join = nullptr;
+    };
+    // If anything throws before the last join, the context's stream still waits for the
+    // recurrence stream before G and Y (declared above, so released after this) go back.
+    struct Unwind {
+        hipStream_t st, gs;
+        hipEvent_t &join;
+        ~Unwind() {
+            if (join) (void)hipEventDestroy(join);
+            if (gs == st) return;
+            hipEvent_t e = nullptr;
+            if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return;
+            if (hipEventRecord(e, gs) == hipSuccess) (void)hipStreamWaitEvent(st, e, 0);
+            (void)hipEventDestroy(e);
+        }
+    } unwind{st, gs, join};
     for (int l = 0; l < 2; l++) {
+        join_back();
         const Layer &L = layers_[l];
         if (in_c != L.input) fail("GRU layer input size");
         ConvArgs ca;
@@ -268,12 +302,18 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         ca.bias = L.wb;
         ca.pk = L.pk;
         conv_mfma(ca, st);
-        if (L.r32) gru_recurrence_f32(G.as<float>(), L.r32, L.rb, Y[l].as<float>(), lensd, ntot, steps, st);
-        else gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd, ntot, tmax, steps, st);
+        fork();
+        if (L.r32) gru_recurrence_f32(G.as<float>(), L.r32, L.rb, Y[l].as<float>(), lensd, ntot, steps, gs);
+        else gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd, ntot, tmax, steps, gs);
+        if (gs != st) {
+            OCR_HIP(hipEventCreateWithFlags(&join, hipEventDisableTiming));
+            OCR_HIP(hipEventRecord(join, gs));
+        }
         in = Y[l].as<float>();
         in_c = 512;
         if (between) between();
     }
+    join_back();
     ConvArgs ca;
     ca.x = Act{const_cast<float *>(in), 1, 1, P, 512, 512};
     ca.y = Act{logits, 1, 1, P, classes_, classes_};

@@ -47,9 +47,12 @@ class Recognizer {
     // best: device [tmax][ntot] arg-max per row (last index on ties), may be null; lens: host
     // [ntot], every line's step count (its batch's trunk width, gpu.rs:1552). between, if given,
     // is called after the trunk's and after each GRU layer's kernels are queued (a caller that
-    // interleaves other work on the stream).
+    // interleaves other work on the stream). gru_stream, if given, runs the two recurrences: each
+    // waits for its input projection on the context's stream, which waits for it only where its
+    // output is read (the next projection), so what the caller queues from between() runs beside
+    // the recurrence, whose workgroups occupy one CU per 8 lines and direction.
     void recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens,
-                          const std::function<void()> &between = {});
+                          const std::function<void()> &between = {}, hipStream_t gru_stream = nullptr);
     int classes() const { return classes_; }
     bool recurrent_exact() const { return r_exact_; }
     uint32_t lines() const { return lines_; }

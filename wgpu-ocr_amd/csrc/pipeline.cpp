@@ -76,6 +76,11 @@ struct Pipeline::Impl {
     // kernels take every CU (persistent workgroups), so running them side by side only slows
     // both.
     hipStream_t copy = nullptr;
+    // The recurrences of a recognition pass run on a stream of their own when pages come from host
+    // memory: a recurrence occupies one CU per 8 lines and direction (a third to a half of the GPU
+    // at the bench's passes), and the detection groups queued between the pass's stages run on
+    // the rest of the CUs meanwhile.
+    hipStream_t gru = nullptr;
     PageUploader upl;
     hipStream_t up;
     // Host threads the layouts of one recognition pass share (a page's word boxes in row bands,
@@ -86,8 +91,13 @@ struct Pipeline::Impl {
           host_threads(std::max(1, int(std::thread::hardware_concurrency()))) {
         ctx.bind();
         OCR_HIP(hipStreamCreateWithFlags(&copy, hipStreamNonBlocking));
+        OCR_HIP(hipStreamCreateWithFlags(&gru, hipStreamNonBlocking));
     }
     ~Impl() {
+        if (gru) {
+            drain_stream(gru, "the pipeline's recurrence stream");
+            (void)hipStreamDestroy(gru);
+        }
         if (copy) {
             drain_stream(copy, "the pipeline's copy stream");
             ctx.pool().retire_stream(copy);
@@ -481,7 +491,7 @@ struct PipelineRun final : PipelineHooks {
                 });
         };
         I.rec.recognize_device(rb.data(), int(rb.size()), logits.as<float>(), R.best.as<uint32_t>(), R.lens.data(),
-                               between);
+                               between, interleave ? I.gru : nullptr);
         for (hipEvent_t e : stage_ev) OCR_HIP(hipEventDestroy(e));
         gpu_span("recognize " + std::to_string(r), ga, gpu_event(st));
         mark("rec " + std::to_string(r) + " queued");
