@@ -701,18 +701,18 @@ Graph::Out Graph::run(Ctx &ctx, const Act &x) const {
 
 std::vector<Graph::Out> Graph::run_multi(Ctx &ctx, const std::vector<Act> &xs) const {
     std::vector<Out> outs;
-    run_multi_tm(ctx, xs, 0, nullptr, 0, outs);
+    run_multi_tm(ctx, xs, 0, nullptr, 0, outs, {});
     return outs;
 }
 
 bool Graph::run_multi_time_major(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot,
-                                 std::vector<Out> &outs) const {
+                                 std::vector<Out> &outs, const std::function<void(int)> &after_step) const {
     if (!X || kh != 2) fail("run_multi_time_major: X and an average pool over 2 rows");
-    return run_multi_tm(ctx, xs, kh, X, ntot, outs);
+    return run_multi_tm(ctx, xs, kh, X, ntot, outs, after_step);
 }
 
 bool Graph::run_multi_tm(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot,
-                         std::vector<Out> &outs) const {
+                         std::vector<Out> &outs, const std::function<void(int)> &after_step) const {
     std::vector<std::unique_ptr<Exec>> es;
     for (const Act &x : xs) es.emplace_back(new Exec(*this, ctx, x));
     std::vector<ConvArgs> cas;
@@ -784,6 +784,7 @@ bool Graph::run_multi_tm(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X,
         } else {
             for (auto &e : es) e->step(i);
         }
+        if (after_step) after_step(int(i));
     }
     for (auto &e : es) outs.push_back(e->result());
     return false;

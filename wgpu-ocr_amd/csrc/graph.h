@@ -2,6 +2,7 @@
 #pragma once
 
 #include <array>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -71,15 +72,18 @@ class Graph {
     // followed by an AveragePool (kh, 1) to one row written time-major into X[t][ntot][c] at line
     // offsets 0, n0, n0 + n1, ...: when the last layer can do that in its own epilogue it does,
     // returns true and the outputs are left empty; otherwise returns false with the outputs.
+    // after_step, if given, is called with each step's index once its kernels are queued (the
+    // fused last layer excepted).
     bool run_multi_time_major(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot,
-                              std::vector<Out> &outs) const;
+                              std::vector<Out> &outs, const std::function<void(int)> &after_step = {}) const;
 
     std::string input, output;
     std::vector<Step> steps;
 
   private:
     struct Exec;
-    bool run_multi_tm(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot, std::vector<Out> &outs) const;
+    bool run_multi_tm(Ctx &ctx, const std::vector<Act> &xs, int kh, float *X, int ntot, std::vector<Out> &outs,
+                      const std::function<void(int)> &after_step) const;
     std::vector<Shape> shapes(const Shape &in) const;  // output shape of every step
 };
 

@@ -242,7 +242,14 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     const uint32_t *lensd = reinterpret_cast<const uint32_t *>(tabd.as<char>());
     const int32_t *rowsd = reinterpret_cast<const int32_t *>(tabd.as<char>() + rows_at);
     std::vector<Graph::Out> trunks;
-    const bool fused = pool_kh_ == 2 && trunk_.run_multi_time_major(ctx_, xs, pool_kh_, X.as<float>(), d.ntot, trunks);
+    // A stage boundary also in the middle of the trunk (its five layers carry similar work), so a
+    // caller's work queued from between() waits for half the trunk rather than all of it.
+    const int mid = (int(trunk_.steps.size()) + 1) / 2;
+    auto after = [&](int i) {
+        if (between && i + 1 == mid) between();
+    };
+    const bool fused = pool_kh_ == 2 && trunk_.run_multi_time_major(ctx_, xs, pool_kh_, X.as<float>(), d.ntot, trunks,
+                                                                    after);
     if (!fused) {
         if (pool_kh_ != 2) trunks = trunk_.run_multi(ctx_, xs);
         std::vector<Act> feats;

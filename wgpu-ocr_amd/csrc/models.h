@@ -46,8 +46,8 @@ class Recognizer {
     // logits: device [tmax][ntot][classes] raw logits (rows t >= lens[line] are not defined);
     // best: device [tmax][ntot] arg-max per row (last index on ties), may be null; lens: host
     // [ntot], every line's step count (its batch's trunk width, gpu.rs:1552). between, if given,
-    // is called after the trunk's and after each GRU layer's kernels are queued (a caller that
-    // interleaves other work on the stream). gru_stream, if given, runs the two recurrences: each
+    // is called after the first half of the trunk's layers, after the trunk's and after each GRU
+    // layer's kernels are queued (a caller that interleaves other work on the stream). gru_stream, if given, runs the two recurrences: each
     // waits for its input projection on the context's stream, which waits for it only where its
     // output is read (the next projection), so what the caller queues from between() runs beside
     // the recurrence, whose workgroups occupy one CU per 8 lines and direction.
