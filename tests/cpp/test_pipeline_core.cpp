@@ -225,7 +225,8 @@ std::vector<char> expected_failed(const PipelinePlan &P, const Faults &f) {
 int run_case(const char *name, int npages, int merge, int det_batch, int workers, Faults f, unsigned seed,
              bool jitter, bool lookahead = false, bool interleave = false, int land_us = -1,
              int never_lands = -1) {
-    const PipelinePlan P = plan_pipeline(npages, merge, det_batch);
+    // The interleaved cases stand for pages from host memory, and take their plan.
+    const PipelinePlan P = plan_pipeline(npages, merge, det_batch, interleave);
     Hooks H(P, f, seed, jitter);
     H.land_us = land_us, H.never_lands = never_lands;
     H.lookahead = lookahead;
@@ -287,6 +288,14 @@ int main() {
         const int bg[] = {0, 1, 3, 5, 7, 10, 12};
         CHECK(B.groups() == 6, "plan: bench groups %d", B.groups());
         for (int g = 0; g <= 6 && g <= B.groups(); g++) CHECK(B.group_p0[size_t(g)] == bg[g], "plan: bench group %d", g);
+        // Pages from host memory: the first pass's pages one group each, the rest as above.
+        const PipelinePlan H = plan_pipeline(12, 6, 3, true);
+        const int hg[] = {0, 1, 2, 3, 5, 7, 10, 12};
+        CHECK(H.groups() == 7 && H.passes() == 3, "plan: host groups %d", H.groups());
+        for (int g = 0; g <= 7 && g <= H.groups(); g++) CHECK(H.group_p0[size_t(g)] == hg[g], "plan: host group %d", g);
+        // One pass: the option changes nothing (the first and last rules apply).
+        const PipelinePlan H1 = plan_pipeline(6, 6, 4, true);
+        CHECK(H1.groups() == 3 && H1.group_p0[1] == 1 && H1.group_p0[2] == 4, "plan: host, one pass");
         // Passes share the pages after the first evenly: 3, then 5, 5, 5, 6 for 24 pages.
         const PipelinePlan L = plan_pipeline(24, 6, 3);
         const int lp[] = {0, 3, 8, 13, 18, 24};
@@ -300,8 +309,9 @@ int main() {
         CHECK(plan_pipeline(5, 1, 4).passes() == 5, "plan: merge 1");
         for (int n = 1; n <= 40; n++)
             for (int merge = 1; merge <= 8; merge++)
-                for (int db = 1; db <= 6; db++) {
-                    const PipelinePlan Q = plan_pipeline(n, merge, db);
+                for (int db = 1; db <= 12; db++) {
+                    const PipelinePlan Q = plan_pipeline(n, merge, db > 6 ? db - 6 : db, db > 6);
+                    const int dbq = db > 6 ? db - 6 : db;
                     CHECK(Q.pass_p0.front() == 0 && Q.pass_p0.back() == n && Q.group_p0.front() == 0 &&
                               Q.group_p0.back() == n,
                           "plan (%d, %d, %d): ends", n, merge, db);
@@ -311,7 +321,7 @@ int main() {
                     }
                     for (int g = 0; g < Q.groups(); g++) {
                         const int a = Q.group_p0[size_t(g)], b = Q.group_p0[size_t(g) + 1];
-                        CHECK(b > a && b - a <= db, "plan (%d, %d, %d): group %d of %d pages", n, merge, db, g, b - a);
+                        CHECK(b > a && b - a <= dbq, "plan (%d, %d, %d): group %d of %d pages", n, merge, db, g, b - a);
                         CHECK(Q.pass_of[size_t(a)] == Q.pass_of[size_t(b - 1)], "plan (%d, %d, %d): group %d straddles a pass",
                               n, merge, db, g);
                     }

@@ -542,7 +542,7 @@ void Pipeline::run_pages(const uint8_t *const *src, bool on_host, const int *w, 
         if (w[p] <= 0 || h[p] <= 0) fail("pipeline: empty page " + std::to_string(p));
     }
     I.ctx.bind();
-    const PipelinePlan plan = plan_pipeline(npages, I.opts.merge, I.opts.det_batch);
+    const PipelinePlan plan = plan_pipeline(npages, I.opts.merge, I.opts.det_batch, on_host);
     std::vector<std::string> errs;
     double busy = 0;
     int failed = 0;

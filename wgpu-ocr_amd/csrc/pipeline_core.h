@@ -37,7 +37,9 @@ namespace ocr {
 // The first group is a third of det_batch (at least one page), so the host starts on layouts
 // while the GPU detects the rest of the first pass; the last pass's last group is half of
 // det_batch rounded up, so that its other pages are detected and laid out while those last pages
-// still upload, and less detection and layout follows the last upload.
+// still upload, and less detection and layout follows the last upload. With first_singles (pages
+// that arrive from host memory one upload at a time) every page of the first pass is a group of
+// its own instead: each is detected as soon as it has landed, and the first pass is ready sooner.
 struct PipelinePlan {
     int npages = 0;
     std::vector<int> pass_p0;   // pass r covers pages [pass_p0[r], pass_p0[r + 1])
@@ -47,7 +49,7 @@ struct PipelinePlan {
     int groups() const { return int(group_p0.size()) - 1; }
 };
 
-inline PipelinePlan plan_pipeline(int npages, int merge, int det_batch) {
+inline PipelinePlan plan_pipeline(int npages, int merge, int det_batch, bool first_singles = false) {
     PipelinePlan P;
     P.npages = std::max(npages, 0);
     merge = std::max(merge, 1), det_batch = std::max(det_batch, 1);
@@ -63,6 +65,10 @@ inline PipelinePlan plan_pipeline(int npages, int merge, int det_batch) {
         int q0 = P.pass_p0[size_t(r)];
         const int r1 = P.pass_p0[size_t(r) + 1];
         for (int p = q0; p < r1; p++) P.pass_of[size_t(p)] = r;
+        if (r == 0 && first_singles && P.passes() > 1) {
+            for (int p = q0; p < r1; p++) P.group_p0.push_back(p);
+            continue;
+        }
         if (r == 0 && r1 - q0 > 1) {
             const int first = std::min(r1 - q0, std::max(1, det_batch / 3));
             P.group_p0.push_back(q0);
