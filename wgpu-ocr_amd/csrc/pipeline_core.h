@@ -291,15 +291,19 @@ inline std::vector<std::string> run_schedule(const PipelinePlan &P, PipelineHook
                 return q >= np ? ng : P.group_of[size_t(q)];
             };
             // A staged group goes first once it has landed; a ready pass goes ahead of a group
-            // still in flight. While a group is in flight and no pass is ready, look again every
-            // 20 us, for at most 100 ms (then the group is queued anyway, and the stream's own
-            // bounded waits report a copy that never ends).
+            // still in flight (one the next pass does not need). While such a group is in flight
+            // and no pass is ready, look again every 20 us, for at most 100 ms (then the group is
+            // queued anyway, and the stream's own bounded waits report a copy that never ends).
             auto staged_next = [&] { return next_det < ng && staged > next_det; };
             auto rec_now = [&] { return pass_ready(next_rec) && next_det >= groups_before(next_rec); };
+            // A group the next pass still needs goes at once, landed or not: no pass can run
+            // before it, and the stream's own wait for its copy starts it the moment it lands.
+            auto needed = [&] { return next_rec >= nr || next_det < groups_before(next_rec); };
             bool take_det = false;
             const auto t_in = clk::now();
             for (;;) {
-                if (staged_next() && (H.landed(next_det) || clk::now() - t_in > std::chrono::milliseconds(100))) {
+                if (staged_next() && (needed() || H.landed(next_det) ||
+                                      clk::now() - t_in > std::chrono::milliseconds(100))) {
                     take_det = true;
                     break;
                 }
