@@ -262,10 +262,18 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     DBuf Y[2] = {DBuf(&ctx_, size_t(M) * 512 * sizeof(float)), DBuf(&ctx_, size_t(M) * 512 * sizeof(float))};
     const float *in = X.as<float>();
     int in_c = 256;
-    // With a stream for the recurrences: each waits for its projection, and the context's stream
-    // waits for it (join) before the next projection reads its output. Every buffer it touches is
-    // released on the context's stream after the last join, so none is reused under it.
+    // With a stream for the recurrences: each waits for its projection; the context's stream
+    // waits for the first (join) before the second projection reads its output, and the second
+    // recurrence, the output layer and the arg-max stay on the recurrence stream (the caller
+    // orders its reads of logits and best after that stream). The buffers the recurrence stream
+    // touches are marked as used on it, so the pool hands them out again only after its work.
     const hipStream_t gs = gru_stream ? gru_stream : st;
+    if (gs != st) {
+        G.used_on(gs);
+        Y[0].used_on(gs);
+        Y[1].used_on(gs);
+        tabd.used_on(gs);
+    }
     hipEvent_t join = nullptr;
     auto fork = [&]() {
         if (gs == st) return;
@@ -281,14 +289,15 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         OCR_HIP(hipEventDestroy(join));
         join = nullptr;
     };
-    // If anything throws before the last join, the context's stream still waits for the
-    // recurrence stream before G and Y (declared above, so released after this) go back.
+    // If anything throws, the context's stream still waits for the recurrence stream before the
+    // buffers (declared above, so released after this) go back.
     struct Unwind {
         hipStream_t st, gs;
         hipEvent_t &join;
+        bool settled = false;
         ~Unwind() {
             if (join) (void)hipEventDestroy(join);
-            if (gs == st) return;
+            if (settled || gs == st) return;
             hipEvent_t e = nullptr;
             if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return;
             if (hipEventRecord(e, gs) == hipSuccess) (void)hipStreamWaitEvent(st, e, 0);
@@ -312,7 +321,7 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         fork();
         if (L.r32) gru_recurrence_f32(G.as<float>(), L.r32, L.rb, Y[l].as<float>(), lensd, ntot, steps, gs);
         else gru_recurrence(G.as<float>(), L.r, L.rb, Y[l].as<float>(), lensd, ntot, tmax, steps, gs);
-        if (gs != st) {
+        if (gs != st && l == 0) {
             OCR_HIP(hipEventCreateWithFlags(&join, hipEventDisableTiming));
             OCR_HIP(hipEventRecord(join, gs));
         }
@@ -320,7 +329,6 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
         in_c = 512;
         if (between) between();
     }
-    join_back();
     ConvArgs ca;
     ca.x = Act{const_cast<float *>(in), 1, 1, P, 512, 512};
     ca.y = Act{logits, 1, 1, P, classes_, classes_};
@@ -330,8 +338,9 @@ void Recognizer::recognize_device(const Batch *batches, int count, float *logits
     ca.wt_frag = lin_frag_;
     ca.bias = lin_b_;
     ca.pk = lin_pk_;
-    conv_mfma(ca, st);
-    if (best) argmax_rows(logits, P, classes_, best, st, rowsd);
+    conv_mfma(ca, gs);
+    if (best) argmax_rows(logits, P, classes_, best, gs, rowsd);
+    unwind.settled = true;
 }
 
 }  // namespace ocr

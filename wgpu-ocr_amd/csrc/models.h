@@ -47,10 +47,14 @@ class Recognizer {
     // best: device [tmax][ntot] arg-max per row (last index on ties), may be null; lens: host
     // [ntot], every line's step count (its batch's trunk width, gpu.rs:1552). between, if given,
     // is called after the first half of the trunk's layers, after the trunk's and after each GRU
-    // layer's kernels are queued (a caller that interleaves other work on the stream). gru_stream, if given, runs the two recurrences: each
-    // waits for its input projection on the context's stream, which waits for it only where its
-    // output is read (the next projection), so what the caller queues from between() runs beside
-    // the recurrence, whose workgroups occupy one CU per 8 lines and direction.
+    // layer's kernels are queued (a caller that interleaves other work on the stream).
+    // gru_stream, if given, runs the two recurrences and everything after the second (the output
+    // layer and the arg-max): each recurrence waits for its input projection on the context's
+    // stream, which waits for the first only before the second projection and returns without
+    // waiting for the second. What the caller queues meanwhile (from between(), or its next
+    // pass's trunk) runs beside the recurrence, whose workgroups occupy one CU per 8 lines and
+    // direction. logits and best are then written in gru_stream's order: the caller orders its
+    // reads after that stream and marks the buffers as used on it.
     void recognize_device(const Batch *batches, int count, float *logits, uint32_t *best, uint32_t *lens,
                           const std::function<void()> &between = {}, hipStream_t gru_stream = nullptr);
     int classes() const { return classes_; }

@@ -490,17 +490,24 @@ struct PipelineRun final : PipelineHooks {
                            " on the compute stream";
                 });
         };
+        // With host pages the pass ends on the recurrence stream (its second recurrence, output
+        // layer and arg-max), and the next pass's trunk may start beside it.
+        const hipStream_t tail = interleave ? I.gru : st;
+        if (tail != st) {
+            logits.used_on(tail);
+            R.best.used_on(tail);
+        }
         I.rec.recognize_device(rb.data(), int(rb.size()), logits.as<float>(), R.best.as<uint32_t>(), R.lens.data(),
                                between, interleave ? I.gru : nullptr);
         for (hipEvent_t e : stage_ev) OCR_HIP(hipEventDestroy(e));
-        gpu_span("recognize " + std::to_string(r), ga, gpu_event(st));
+        gpu_span("recognize " + std::to_string(r), ga, gpu_event(tail));
         mark("rec " + std::to_string(r) + " queued");
         // The arg-max goes to the host on the copy stream, so the next pass's kernels do not
         // wait for the copy.
         I.best_host[size_t(r)].ensure(size_t(d.tmax) * d.ntot * sizeof(uint32_t));
         hipEvent_t am = nullptr;
         OCR_HIP(hipEventCreateWithFlags(&am, hipEventDisableTiming));
-        OCR_HIP(hipEventRecord(am, st));
+        OCR_HIP(hipEventRecord(am, tail));
         OCR_HIP(hipStreamWaitEvent(I.copy, am, 0));
         OCR_HIP(hipEventDestroy(am));
         OCR_HIP(hipMemcpyAsync(I.best_host[size_t(r)].p, R.best.get(), size_t(d.tmax) * d.ntot * sizeof(uint32_t),

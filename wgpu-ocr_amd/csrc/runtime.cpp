@@ -189,16 +189,28 @@ void *Pool::get(size_t bytes, hipStream_t s) {
         auto it = free_.find(sz);
         if (it != free_.end() && !it->second.empty()) {
             std::vector<Block> &v = it->second;
-            // The newest buffer whose home is s (stream order covers its earlier uses there),
-            // else the newest idle one. A buffer still homed on another stream is not taken: an
-            // event recorded on that stream now would also wait for everything queued there
-            // since, and serialise the streams.
+            // The newest buffer whose home is s (stream order covers its earlier uses there) and
+            // whose uses on other streams have finished, else the newest whose home is s (s then
+            // waits for those uses on the GPU), else the newest idle one. A buffer still homed on
+            // another stream is not taken: an event recorded on that stream now would also wait
+            // for everything queued there since, and serialise the streams.
+            auto settled = [](const Block &b) {
+                for (hipEvent_t e : b.pending)
+                    if (hipEventQuery(e) != hipSuccess) return false;
+                return true;
+            };
             long pick = -1;
             for (size_t k = v.size(); k-- > 0;)
-                if (v[k].home == s) {
+                if (v[k].home == s && settled(v[k])) {
                     pick = long(k);
                     break;
                 }
+            if (pick < 0)
+                for (size_t k = v.size(); k-- > 0;)
+                    if (v[k].home == s) {
+                        pick = long(k);
+                        break;
+                    }
             if (pick < 0)
                 for (size_t k = v.size(); k-- > 0;)
                     if (v[k].home == nullptr) {
