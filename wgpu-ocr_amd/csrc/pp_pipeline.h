@@ -21,7 +21,7 @@ struct PpPipelineOpts {
     int max_side = 960;     // detection input's long side (DETMAX)
     int per_batch = 16;     // lines per recognition batch (PPBATCH)
     int threads = 0;        // host worker threads (0: hardware concurrency, at most 16)
-    int det_batch = 4;      // same-size pages per detection pass
+    int det_batch = 2;      // same-size pages per detection pass
     DbParams db;
 };
 
