@@ -45,16 +45,17 @@ def test_pipeline_text_matches_cpu(pipeline, detector, det_oracle, rec_oracle):
 
 
 def test_bench_configuration_text_matches_cpu(detector, recognizer, det_oracle, rec_oracle):
-    # The benchmark's workload and plan (bench.py's defaults): 12 pages from host memory, 6 pages
-    # a recognition pass, 4 a detection group. Every page's text equals the CPU pipeline's (oracle
-    # detection, layout, line images, recognition, CTC) on the same mask; detection groups of 2
-    # and 6 give the same text.
+    # The benchmark's workload and plan (bench.py's defaults): 12 pages from host memory, merge 6
+    # (recognition passes of 3, 4 and 5 pages), detection groups of 3 (the first pass's pages one
+    # a group, as pages from host memory are), the recurrences and each pass's tail on their own
+    # stream. Every page's text equals the CPU pipeline's (oracle detection, layout, line images,
+    # recognition, CTC) on the same mask; detection groups of 2, 4 and 6 give the same text.
     pages = [synth.page(i) for i in range(12)]
-    p = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=4)
-    print("bench configuration: 12 pages, merge 6, detection groups of 4", flush=True)
+    p = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=3)
+    print("bench configuration: 12 pages, merge 6, detection groups of 3", flush=True)
     p.run(pages)
     others = []
-    for db in (2, 6):
+    for db in (2, 4, 6):
         q = ocrhip.Pipeline(detector, recognizer, merge=6, det_batch=db)
         print(f"bench configuration: detection groups of {db}", flush=True)
         q.run(pages)
