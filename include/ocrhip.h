@@ -351,7 +351,7 @@ typedef struct ocr_pp_pipeline ocr_pp_pipeline;
  * relv: box padding across (RELV, 0.1 with DET=ppocr, ocr-bench.rs:540); max_side: detection
  * input's long side (DETMAX); per_batch: lines per batch (PPBATCH); threads: host workers;
  * det_batch: same-size pages per detection pass; box_thresh, unclip_ratio, min_size: DB
- * post-processing (ppdet.rs:55-60). Zeros take the defaults 2, 0.3, 0.1, 960, 16, 0, 2, 0.45,
+ * post-processing (ppdet.rs:55-60). Zeros take the defaults 2, 0.3, 0.1, 960, 16, 0, 4, 0.45,
  * 1.4, 3. */
 typedef struct ocr_pp_opts {
     uint32_t merge;

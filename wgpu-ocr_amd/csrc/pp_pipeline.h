@@ -21,7 +21,7 @@ struct PpPipelineOpts {
     int max_side = 960;     // detection input's long side (DETMAX)
     int per_batch = 16;     // lines per recognition batch (PPBATCH)
     int threads = 0;        // host worker threads (0: hardware concurrency, at most 16)
-    int det_batch = 2;      // same-size pages per detection pass
+    int det_batch = 4;      // same-size pages per detection pass
     DbParams db;
 };
 
@@ -31,19 +31,20 @@ class PpPipeline {
     ~PpPipeline();
     // All pages' RGB bytes already in device memory.
     void run(const uint8_t *const *d_rgb, const int *w, const int *h, int npages);
-    // Pages in host memory (page-locked or pageable): each detection pass's pages go up on the
-    // uploader's stream right before the pass, so later pages upload while earlier ones are
-    // detected (the reference uploads each page in its detection path, src/nd.rs:1353-1369).
+    // Pages in host memory (page-locked or pageable): a detection group's pages go up on the
+    // uploader's stream as the schedule stages them, so later pages upload while earlier ones are
+    // detected and recognised (the reference uploads each page in its detection path,
+    // src/nd.rs:1353-1369).
     void run_host(const uint8_t *const *rgb, const int *w, const int *h, int npages);
     const std::vector<PageText> &pages() const { return pages_; }
     const PipelineStats &stats() const { return stats_; }
 
-  private:
     struct Impl;
+
+  private:
     Impl *impl_;
-    // before_pass(p, q): called before the detection pass of pages [p, q) is queued.
-    void run_pages(const uint8_t *const *d_rgb, const int *w, const int *h, int npages,
-                   const std::function<void(int, int)> &before_pass);
+    // Both entry points: the page pipeline's schedule (pipeline_core.h) over this run's hooks.
+    void run_pages(const uint8_t *const *src, bool on_host, const int *w, const int *h, int npages);
     std::vector<PageText> pages_;
     PipelineStats stats_;
 };

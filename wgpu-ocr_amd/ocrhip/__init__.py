@@ -764,7 +764,7 @@ class PpPipeline:
     SVTR recognition with the fused arg-max head, host CTC."""
 
     def __init__(self, det: NdGraph, rec: NdGraph, merge=2, thr=0.3, relv=0.1, max_side=960, per_batch=16,
-                 threads=0, det_batch=2):
+                 threads=0, det_batch=4):
         self.ctx = det.ctx
         self._keep = (det, rec)
         opts = ocr_pp_opts(merge, thr, relv, max_side, per_batch, threads, det_batch, 0.0, 0.0, 0.0)
