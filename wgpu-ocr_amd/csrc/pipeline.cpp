@@ -296,7 +296,7 @@ struct PipelineRun final : PipelineHooks {
 
     bool landed(int g) override {
         const hipEvent_t e = up_ev[size_t(g)];
-        return !e || hipEventQuery(e) != hipErrorNotReady;
+        return !e || event_query(e, true);
     }
 
     // Detection of a group's pages, the labelling of their masks, and the copies of masks and

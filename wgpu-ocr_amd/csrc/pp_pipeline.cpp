@@ -153,7 +153,7 @@ struct PpRun final : PipelineHooks {
     }
     bool landed(int g) override {
         const hipEvent_t e = up_ev[size_t(g)];
-        return !e || hipEventQuery(e) != hipErrorNotReady;
+        return !e || event_query(e, true);
     }
     void detect(int g) override {
         const int p = P.group_p0[size_t(g)], q = P.group_p0[size_t(g) + 1], n = q - p;

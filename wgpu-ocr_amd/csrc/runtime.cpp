@@ -196,7 +196,7 @@ void *Pool::get(size_t bytes, hipStream_t s) {
             // for everything queued there since, and serialise the streams.
             auto settled = [](const Block &b) {
                 for (hipEvent_t e : b.pending)
-                    if (hipEventQuery(e) != hipSuccess) return false;
+                    if (!event_query(e, false)) return false;
                 return true;
             };
             long pick = -1;

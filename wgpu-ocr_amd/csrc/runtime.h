@@ -30,6 +30,17 @@ void wait_stream(hipStream_t s, const std::string &what, bool spin = true);
 // reported on stderr and the wait goes on (the buffers the stream uses must not be reused before
 // it ends). GPU errors are ignored here.
 void drain_stream(hipStream_t s, const std::string &what) noexcept;
+// Whether an event's work has finished, for callers that only poll (no error is raised here):
+// hipErrorNotReady reads as false, any other error as on_error, and such an error is cleared
+// from the thread's last error when it is the one this query left (a later launch check would
+// otherwise report it as its own).
+inline bool event_query(hipEvent_t e, bool on_error) {
+    const hipError_t r = hipEventQuery(e);
+    if (r == hipSuccess) return true;
+    if (r == hipErrorNotReady) return false;
+    if (hipPeekAtLastError() == r) (void)hipGetLastError();
+    return on_error;
+}
 
 // 64 zero bytes on the current device (allocated once per device, kept until the process ends):
 // the kernels' source for out-of-range taps.
